@@ -1,0 +1,267 @@
+"""Benchmark: delta-rule forward on one MI355X (BASELINE cfg1), plus the decode step.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A "step" is one call of the forward (``pm_delta_fwd``, the C ABI behind
+``prometheus_amd.kernels.chunked_delta_rule``) over the cfg1 batch:
+B=4 H=16 T=4096 d_k=d_v=128, bf16 q/k/v (q, k L2-normalised), fp32 beta,
+zero initial state, fp32 O and final S, chunk 64. Inputs are resident in
+HBM before timing starts; two input sets alternate so that consecutive
+steps never find their 201 MB of inputs in the 256 MB Infinity Cache.
+
+Prints ONE JSON line (the driver's contract) with ``roofline`` for the
+forward kernel (HBM-bound at this shape: 340.8 MB vs 47.6 GFLOP) and
+``cpu_baseline`` (the C restatement of the reference's per-token CPU
+algorithm, OpenMP over the 64 (b, h) sequences, on this host). The decode
+step (cfg4: B=256 H=32 D=128, fp32 state updated in place) is measured in
+the same run and reported under ``decode``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, vendor figure
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, vendor figure
+CHUNK = 64
+
+
+def fwd_flops(B, T, H, D, chunk=CHUNK) -> float:
+    """Algorithmic flops of the chunked form: 10 c^2 D + 6 c D^2 + c^3/3 per (b, h) chunk."""
+    n_full, rem = divmod(T, chunk)
+    per = lambda c: 10 * c * c * D + 6 * c * D * D + c ** 3 / 3.0  # noqa: E731
+    return B * H * (n_full * per(chunk) + (per(rem) if rem else 0.0))
+
+
+def fwd_bytes(B, T, H, D, s_in=2, s_out=4, s0=False) -> float:
+    """Algorithmic HBM bytes: q, k, v in + beta + O out + S out (+ S0 in)."""
+    E = B * T * H * D
+    S = 4 * B * H * D * D
+    return 3 * E * s_in + 4 * B * T * H + E * s_out + S + (S if s0 else 0)
+
+
+def step_bytes(B, H, D, s_in=2) -> float:
+    """Decode step: S read + written, q, k, v in, beta in, o out."""
+    S = 4 * B * H * D * D
+    return 2 * S + 3 * B * H * D * s_in + 4 * B * H + 4 * B * H * D
+
+
+def make_inputs(torch, B, T, H, D, seed, device):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+
+    def unit(shape):
+        x = torch.randn(shape, generator=g, device=device, dtype=torch.float32)
+        x = x / torch.clamp(torch.linalg.vector_norm(x, dim=-1, keepdim=True), min=1e-6)
+        return x.to(torch.bfloat16).contiguous()
+
+    q = unit((B, T, H, D))
+    k = unit((B, T, H, D))
+    v = torch.randn((B, T, H, D), generator=g, device=device).to(torch.bfloat16).contiguous()
+    beta = torch.sigmoid(torch.randn((B, T, H), generator=g, device=device)).contiguous()
+    return q, k, v, beta
+
+
+def bits(t) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(dtype=__import__("torch").int16).numpy().view(np.uint16)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--decode-steps", type=int, default=64)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_cfg1.json"),
+                    help="JSON with measured HBM bytes per launch (from rocprofv3 --pmc)")
+    ap.add_argument("--tile", type=int, default=0, help="d_v tile of the chunked kernel (0 auto)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"--gpus {args.gpus}); the forward shards over (b, h) with no exchange", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from prometheus_amd import _native
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    lib = _native.lib()
+    if args.tile:
+        _native.set_tile(args.tile)
+
+    B, T, H, D = 4, 4096, 16, 128
+    print(f"[bench] cfg1 inputs B{B} T{T} H{H} D{D}", file=sys.stderr, flush=True)
+    sets = [make_inputs(torch, B, T, H, D, seed, dev) for seed in (1, 2)]
+    o = torch.empty((B, T, H, D), dtype=torch.float32, device=dev)
+    s = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def launch(i):
+        q, k, v, beta = sets[i % 2]
+        rc = lib.pm_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), None,
+                              o.data_ptr(), s.data_ptr(), B, T, H, D, _native.DTYPE_BF16,
+                              _native.DTYPE_F32, CHUNK, None, 0, stream.cuda_stream)
+        _native.check(rc)
+
+    for i in range(args.warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    print(f"[bench] warmup {args.warmup} done; timing {args.steps} steps", file=sys.stderr,
+          flush=True)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        launch(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_launch_ms = [a.elapsed_time(b) for a, b in ev]
+    kern_ms = float(np.mean(per_launch_ms))
+    ms_per_step = wall * 1e3 / args.steps
+    last = (args.steps - 1) % 2
+
+    tokens = B * T
+    flops = fwd_flops(B, T, H, D)
+    nbytes = fwd_bytes(B, T, H, D)
+    achieved_gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    tflops = flops / (kern_ms * 1e-3) / 1e12
+    traffic = None
+    if os.path.exists(args.traffic):
+        with open(args.traffic) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+
+    # parity of the timed output against the C restatement (which is also the CPU baseline)
+    cpu = None
+    parity = None
+    if not args.no_cpu_baseline:
+        from oracle import cref
+
+        q, k, v, beta = sets[last]
+        hq, hk, hv, hb = bits(q), bits(k), bits(v), beta.cpu().numpy()
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        print(f"[bench] CPU baseline on {threads} threads", file=sys.stderr, flush=True)
+        cref.delta_fwd(hq[:, :64], hk[:, :64], hv[:, :64], hb[:, :64], None, threads=threads)
+        t1 = time.perf_counter()
+        e_o, e_s = cref.delta_fwd(hq, hk, hv, hb, None, threads=threads)
+        cpu_s = time.perf_counter() - t1
+        got_o, got_s = o.cpu().numpy(), s.cpu().numpy()
+        rel = lambda a, b: float(np.linalg.norm((a - b).ravel()) / np.linalg.norm(b.ravel()))  # noqa
+        parity = {"rel_l2_o": rel(got_o, e_o), "rel_l2_s": rel(got_s, e_s), "bound": 2e-2}
+        parity["ok"] = parity["rel_l2_o"] <= 2e-2 and parity["rel_l2_s"] <= 2e-2
+        cpu = {"value": tokens / cpu_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": f"full cfg1 batch (B4 T4096 H16 D128, bf16 inputs upcast to fp32), "
+                         f"{cpu_s:.2f} s; C restatement of the reference's per-token rank-1 "
+                         f"recurrence (oracle/delta_ref.c), OpenMP over 64 (b,h) sequences; "
+                         f"CPU: {cpu_model()}"}
+
+    # decode step, cfg4: B256 H32 D128, fp32 state updated in place, 64 steps
+    Bd, Hd = 256, 32
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    state = (torch.randn((Bd, Hd, D, D), generator=g, device=dev) * 0.02).contiguous()
+    toks = []
+    for _ in range(2):
+        qd = torch.randn((Bd, Hd, D), generator=g, device=dev)
+        qd = (qd / qd.norm(dim=-1, keepdim=True)).to(torch.bfloat16)
+        kd = torch.randn((Bd, Hd, D), generator=g, device=dev)
+        kd = (kd / kd.norm(dim=-1, keepdim=True)).to(torch.bfloat16)
+        vd = torch.randn((Bd, Hd, D), generator=g, device=dev).to(torch.bfloat16)
+        bd = torch.sigmoid(torch.randn((Bd, Hd), generator=g, device=dev))
+        toks.append((qd, kd, vd, bd))
+    od = torch.empty((Bd, Hd, D), dtype=torch.float32, device=dev)
+
+    def step(i):
+        qd, kd, vd, bd = toks[i % 2]
+        rc = lib.pm_delta_step(state.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                               bd.data_ptr(), od.data_ptr(), Bd, Hd, D, _native.DTYPE_BF16,
+                               stream.cuda_stream)
+        _native.check(rc)
+
+    for i in range(4):
+        step(i)
+    torch.cuda.synchronize()
+    dev_ = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(args.decode_steps)]
+    for i in range(args.decode_steps):
+        dev_[i][0].record(stream)
+        step(i)
+        dev_[i][1].record(stream)
+    torch.cuda.synchronize()
+    step_ms = float(np.mean([a.elapsed_time(b) for a, b in dev_]))
+    dbytes = step_bytes(Bd, Hd, D)
+    decode = {
+        "workload": "cfg4 decode step B256 H32 D128, bf16 token, fp32 state in place",
+        "steps": args.decode_steps,
+        "us_per_step": step_ms * 1e3,
+        "tokens_per_s": Bd / (step_ms * 1e-3),
+        "roofline": {"bound": "hbm", "achieved": dbytes / (step_ms * 1e-3) / 1e9,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dbytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+    }
+
+    line = {
+        "metric": "delta-rule fwd tokens/s + % MFMA/HBM roofline, B4·H16·T4096·d128 bf16",
+        "value": tokens / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded torch RNG: q,k L2-normalised N(0,1), v N(0,1), "
+                "beta sigmoid(N(0,1)); two input sets alternate)",
+        "config": {"workload": "cfg1 delta-rule forward", "B": B, "T": T, "H": H, "d_k": D,
+                   "d_v": D, "chunk": CHUNK, "in_dtype": "bf16", "out_dtype": "fp32",
+                   "state0": "zeros"},
+        "roofline": {"bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic},
+        "mfma": {"achieved_tflops": tflops, "peak_tflops": BF16_PEAK_TFLOPS,
+                 "frac": tflops / BF16_PEAK_TFLOPS, "algorithmic_gflop": flops / 1e9},
+        "attainable_roofline_frac": max(flops / (BF16_PEAK_TFLOPS * 1e12),
+                                        nbytes / (HBM_PEAK_GBS * 1e9)) / (kern_ms * 1e-3),
+        "kernel_us": kern_ms * 1e3,
+        "algorithmic_bytes": nbytes,
+        "cpu_baseline": cpu,
+        "parity": parity,
+        "decode": decode,
+    }
+    print(json.dumps(line), flush=True)
+    if parity is not None and not parity["ok"]:
+        sys.exit(3)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,133 @@
+/*
+ * pm_delta.h — C ABI of libpmdelta.so, the MI355X (gfx950) delta-rule
+ * linear-attention forward and its single-token decode step.
+ *
+ * Recurrence (decay gate 1), per (batch b, head h), state S is d_k x d_v:
+ *     S_t = (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T
+ *     o_t = q_t S_t                              (o_t[e] = sum_d q_t[d] S_t[d][e])
+ *
+ * Reference interfaces this ABI stands behind (teddytennant/prometheus):
+ *   kernels/__init__.py:661-689  chunked_delta_rule_fwd   -> pm_delta_fwd
+ *   kernels/__init__.py:591-619  chunked_delta_rule       -> pm_delta_fwd
+ *   kernels/__init__.py:357-376  _delta_step_np/_jax      -> pm_delta_step
+ *   (no reference counterpart)   packed cu_seqlens batch  -> pm_delta_fwd_varlen
+ * The reference has no FFI of its own: its call surface is Python
+ * (kernels/__init__.py).  prometheus_amd/kernels binds these entry points
+ * with ctypes under the reference's names.
+ *
+ * Layouts (all row-major, contiguous, device pointers):
+ *   q, k, v  (B, T, H, D)        element type in_dtype
+ *   beta     (B, T, H)           fp32
+ *   s0/s_out (B, H, D, D)        fp32, [d_k][d_v]
+ *   o        (B, T, H, D)        element type out_dtype
+ * Varlen: q, k, v are (total_T, H, D), beta (total_T, H), cu_seqlens int32
+ * (n_seqs + 1) exclusive prefix with cu_seqlens[0] == 0 and
+ * cu_seqlens[n_seqs] == total_T; s0/s_out are (n_seqs, H, D, D).
+ *
+ * Return codes: 0 on success; a negative PM_E* value for an invalid
+ * argument (nothing was launched); a positive hipError_t when a launch
+ * failed.  pm_last_error() gives a thread-local message for the last
+ * nonzero return on the calling thread.
+ *
+ * All launches are asynchronous on `stream` (a hipStream_t; NULL is the
+ * default stream).  The library holds no device allocations and never
+ * synchronises.  Inputs and outputs must not alias, except that
+ * pm_delta_step updates s_inout in place by design.
+ */
+#ifndef PM_DELTA_H
+#define PM_DELTA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PM_DELTA_ABI_VERSION 1
+
+/* element types */
+#define PM_DTYPE_F32 0
+#define PM_DTYPE_BF16 1
+
+/* negative return codes */
+#define PM_E_NULL (-1)        /* required pointer is NULL               */
+#define PM_E_SHAPE (-2)       /* dimension out of range / inconsistent  */
+#define PM_E_DTYPE (-3)       /* unknown or unsupported element type    */
+#define PM_E_ALIGN (-4)       /* pointer not aligned for vector access  */
+#define PM_E_WORKSPACE (-5)   /* workspace too small                    */
+#define PM_E_UNSUPPORTED (-6) /* valid request this build cannot serve  */
+
+/* Largest head dimension any entry point accepts. */
+#define PM_DELTA_MAX_D 256
+
+/*
+ * Delta-rule forward over (B, T, H, D) inputs.
+ * Replaces kernels/__init__.py:661-689 (chunked_delta_rule_fwd) and
+ * :591-619 (chunked_delta_rule): same inputs, same (O, S) outputs.
+ * s0 may be NULL (zero initial state, as `state=None` at :349-351).
+ * chunk >= 1 is accepted as in the reference (:676-677); like the
+ * reference it does not change the mathematical result (:92).
+ * T == 0 gives no output rows and s_out = s0 (or zeros).
+ * workspace/ws_bytes: pass NULL/0; no kernel of this build needs one
+ * (pm_delta_workspace_bytes returns 0), kept for ABI stability.
+ */
+int pm_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
+                 const float* s0, void* o, float* s_out, int B, int T, int H, int D,
+                 int in_dtype, int out_dtype, int chunk, void* workspace, size_t ws_bytes,
+                 void* stream);
+
+/*
+ * Packed variable-length forward: n_seqs independent sequences
+ * concatenated along the token axis, state reset at every boundary
+ * (each segment equals a B=1 pm_delta_fwd call with s0 = NULL, bit for bit).
+ * No reference counterpart: the reference's equivalent is n_seqs separate
+ * chunked_delta_rule calls (kernels/__init__.py:591-619) with B=1.
+ * s0 may be NULL (zeros) or (n_seqs, H, D, D).
+ */
+int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float* beta,
+                        const int32_t* cu_seqlens, int n_seqs, int total_T,
+                        const float* s0, void* o, float* s_out, int H, int D,
+                        int in_dtype, int out_dtype, int chunk, void* workspace,
+                        size_t ws_bytes, void* stream);
+
+/*
+ * One recurrent decode step for B*H sequences, state updated in place.
+ * Replaces kernels/__init__.py:357-376 (_delta_step_np / _delta_step_jax):
+ *   S' = S - beta k (k^T S) + beta k v^T ;  o = q S'
+ * q, k, v: (B, H, D) in_dtype; beta (B, H) fp32; s_inout (B, H, D, D) fp32;
+ * o: (B, H, D) fp32.
+ */
+int pm_delta_step(float* s_inout, const void* q, const void* k, const void* v,
+                  const float* beta, float* o, int B, int H, int D, int in_dtype,
+                  void* stream);
+
+/* Workspace bytes pm_delta_fwd would need (0 in this build). */
+size_t pm_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype);
+
+/* Thread-local message for the last nonzero return on this thread. */
+const char* pm_last_error(void);
+
+/* PM_DELTA_ABI_VERSION of the loaded library. */
+int pm_abi_version(void);
+
+/*
+ * Kernel selection for pm_delta_fwd / pm_delta_fwd_varlen, for tests and
+ * benchmarks: 0 = automatic (chunked MFMA kernel where the shape and dtype
+ * allow, else the per-token kernel), 1 = always the per-token kernel,
+ * 2 = chunked kernel required (PM_E_UNSUPPORTED when it cannot serve the
+ * call).  The previous value is returned.  Process-wide.
+ */
+int pm_delta_set_path(int path);
+
+/*
+ * Column-tile width (d_v columns per workgroup) the chunked kernel uses:
+ * 0 = automatic, else 16, 32 or 64.  Returns the previous value.
+ */
+int pm_delta_set_tile(int dv_tile);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PM_DELTA_H */

@@ -1,0 +1,157 @@
+// delta_recurrent.hip — K4: per-token delta-rule recurrence for any D <= 256.
+//
+// The reference's own algorithm (kernels/__init__.py:357-376 step,
+// sequential over tokens as in :379-395 / :421-458), in fp32 on the VALU:
+//   kS = k^T S ;  u = beta (v - kS) ;  S += k u^T ;  o = q S
+// It serves fp32 inputs (parity at 1e-5 against the fp32 reference), every
+// head dimension the chunked MFMA kernel does not cover (the reference's
+// own tests use D = 2..8), the varlen form of those, and pm_delta_step for
+// D outside the specialised decode kernel.
+//
+// Mapping: one workgroup per (sequence, head).  Thread (e, r) holds rows
+// [r*RPT, r*RPT + RPT) of column e of S in registers (RS = row slices per
+// column, adjacent lanes, reduced with cross-lane shuffles).  Tokens are
+// staged into LDS STEPS at a time so the inner loop has no barriers.
+// S is read once at the start and written once at the end, so s0 may alias
+// s_out (the decode step runs in place).
+
+#include "pm_common.h"
+#include "pm_internal.h"
+
+namespace pm {
+
+constexpr int kRecSteps = 16;
+
+// D <= 128 runs at most 512 threads (RPT 32, 4 slices); only D > 128 needs
+// 1024 threads, where the 64-row slices do not fit the register budget and
+// part of S spills (a rare shape, kept for generality).
+template <int RPT, typename InT, typename OutT>
+__global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel(
+    const InT* __restrict__ q, const InT* __restrict__ k, const InT* __restrict__ v,
+    const float* __restrict__ beta, const float* s0, OutT* __restrict__ o, float* s_out,
+    const int32_t* __restrict__ cu_seqlens, int T, int H, int D, int RS) {
+    extern __shared__ float lds[];
+    const int DP = RS * RPT;  // padded row count per column
+    float* sk = lds;                          // [kRecSteps][DP]
+    float* sq = sk + kRecSteps * DP;          // [kRecSteps][DP]
+    float* sv = sq + kRecSteps * DP;          // [kRecSteps][DP]
+    float* sb = sv + kRecSteps * DP;          // [kRecSteps]
+
+    const int pair = blockIdx.x;
+    const int seq = pair / H, h = pair % H;
+    long tok0;
+    int len;
+    if (cu_seqlens) {
+        // varlen: T is the packed token count; offsets are clamped into it
+        const int a = min(max(cu_seqlens[seq], 0), T);
+        const int z = min(max(cu_seqlens[seq + 1], a), T);
+        tok0 = a;
+        len = z - a;
+    } else {
+        tok0 = static_cast<long>(seq) * T;
+        len = T;
+    }
+
+    const int tid = threadIdx.x;
+    const int e = tid / RS;
+    const int r = tid % RS;
+    const bool col_ok = e < D;
+    const size_t sbase = static_cast<size_t>(pair) * D * D;
+
+    float S[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+        const int d = r * RPT + i;
+        S[i] = (s0 && col_ok && d < D) ? s0[sbase + static_cast<size_t>(d) * D + e] : 0.0f;
+    }
+
+    for (int t0 = 0; t0 < len; t0 += kRecSteps) {
+        const int nst = min(kRecSteps, len - t0);
+        __syncthreads();
+        for (int idx = tid; idx < kRecSteps * DP; idx += blockDim.x) {
+            const int j = idx / DP, d = idx % DP;
+            float kv = 0.f, qv = 0.f, vv = 0.f;
+            if (j < nst && d < D) {
+                const size_t a = (static_cast<size_t>(tok0 + t0 + j) * H + h) * D + d;
+                kv = to_f32(k[a]);
+                qv = to_f32(q[a]);
+                vv = to_f32(v[a]);
+            }
+            sk[idx] = kv;
+            sq[idx] = qv;
+            sv[idx] = vv;
+        }
+        for (int j = tid; j < kRecSteps; j += blockDim.x)
+            sb[j] = (j < nst) ? beta[static_cast<size_t>(tok0 + t0 + j) * H + h] : 0.f;
+        __syncthreads();
+
+        for (int j = 0; j < nst; ++j) {
+            const float* kr = sk + j * DP + r * RPT;
+            const float* qr = sq + j * DP + r * RPT;
+            float ks = 0.f;
+#pragma unroll
+            for (int i = 0; i < RPT; ++i) ks = fmaf(kr[i], S[i], ks);
+            for (int m = 1; m < RS; m <<= 1) ks += __shfl_xor(ks, m);
+            const float u = sb[j] * ((col_ok ? sv[j * DP + e] : 0.f) - ks);
+#pragma unroll
+            for (int i = 0; i < RPT; ++i) S[i] = fmaf(kr[i], u, S[i]);
+            float os = 0.f;
+#pragma unroll
+            for (int i = 0; i < RPT; ++i) os = fmaf(qr[i], S[i], os);
+            for (int m = 1; m < RS; m <<= 1) os += __shfl_xor(os, m);
+            if (r == 0 && col_ok)
+                o[(static_cast<size_t>(tok0 + t0 + j) * H + h) * D + e] = from_f32<OutT>(os);
+        }
+    }
+
+    if (col_ok) {
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+            const int d = r * RPT + i;
+            if (d < D) s_out[sbase + static_cast<size_t>(d) * D + e] = S[i];
+        }
+    }
+}
+
+// Picks rows-per-thread and the row-slice count for head dimension D.
+static void recurrent_geometry(int D, int* rpt, int* rs) {
+    int r = (D <= 8) ? 8 : (D <= 16) ? 16 : (D <= 128) ? 32 : 64;
+    int s = 1;
+    while (r * s < D) s <<= 1;
+    *rpt = r;
+    *rs = s;
+}
+
+template <int RPT, typename InT, typename OutT>
+static hipError_t launch_rec_t(const RecurrentArgs& a, int rs, hipStream_t st) {
+    const int threads = ((a.D * rs + 63) / 64) * 64;
+    const size_t lds = sizeof(float) * (3 * kRecSteps * rs * RPT + kRecSteps);
+    hipLaunchKernelGGL((delta_recurrent_kernel<RPT, InT, OutT>), dim3(a.n_pairs), dim3(threads),
+                       lds, st, static_cast<const InT*>(a.q), static_cast<const InT*>(a.k),
+                       static_cast<const InT*>(a.v), a.beta, a.s0, static_cast<OutT*>(a.o),
+                       a.s_out, a.cu_seqlens, a.T, a.H, a.D, rs);
+    return hipGetLastError();
+}
+
+template <typename InT, typename OutT>
+static hipError_t launch_rec_io(const RecurrentArgs& a, hipStream_t st) {
+    int rpt, rs;
+    recurrent_geometry(a.D, &rpt, &rs);
+    switch (rpt) {
+        case 8: return launch_rec_t<8, InT, OutT>(a, rs, st);
+        case 16: return launch_rec_t<16, InT, OutT>(a, rs, st);
+        case 32: return launch_rec_t<32, InT, OutT>(a, rs, st);
+        default: return launch_rec_t<64, InT, OutT>(a, rs, st);
+    }
+}
+
+hipError_t launch_recurrent(const RecurrentArgs& a, hipStream_t st) {
+    if (a.n_pairs == 0) return hipSuccess;
+    if (a.in_bf16) {
+        return a.out_bf16 ? launch_rec_io<uint16_t, uint16_t>(a, st)
+                          : launch_rec_io<uint16_t, float>(a, st);
+    }
+    return a.out_bf16 ? launch_rec_io<float, uint16_t>(a, st) : launch_rec_io<float, float>(a, st);
+}
+
+}  // namespace pm

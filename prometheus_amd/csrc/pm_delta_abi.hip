@@ -1,0 +1,224 @@
+// pm_delta_abi.hip — the extern "C" boundary of libpmdelta.so.
+//
+// Validates every argument before anything is launched (negative PM_E_*
+// codes, thread-local message), then dispatches to the gfx950 kernels:
+//   K1/K2 delta_chunked.hip    chunked WY/UT forward on bf16 MFMA
+//   K3    delta_step.hip       decode step, HBM-streaming
+//   K4    delta_recurrent.hip  per-token fp32 recurrence (generic shapes)
+// Mirrors the checks of kernels/__init__.py:308-338 (shapes), :613-614 and
+// :676-677 (chunk >= 1); shapes arrive as integers, so the Python layer
+// (prometheus_amd/kernels) raises KernelError for the tensor-level checks
+// before it calls in.
+
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <atomic>
+
+#include "pm_common.h"
+#include "pm_internal.h"
+#include "../../include/pm_delta.h"
+
+namespace pm {
+
+__global__ void fill_zero_kernel(float* __restrict__ p, size_t n) {
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (; i < n; i += stride) p[i] = 0.f;
+}
+
+__global__ void copy_f32_kernel(float* __restrict__ d, const float* __restrict__ s, size_t n) {
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (; i < n; i += stride) d[i] = s[i];
+}
+
+static unsigned grid_for(size_t n) {
+    size_t g = (n + 255) / 256;
+    if (g > 65536) g = 65536;
+    return static_cast<unsigned>(g < 1 ? 1 : g);
+}
+
+hipError_t launch_fill_zero(float* p, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_for(n)), dim3(256), 0, st, p, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_f32(float* dst, const float* src, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(copy_f32_kernel, dim3(grid_for(n)), dim3(256), 0, st, dst, src, n);
+    return hipGetLastError();
+}
+
+}  // namespace pm
+
+namespace {
+
+thread_local char g_err[512] = "";
+std::atomic<int> g_path{0};
+std::atomic<int> g_tile{0};
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(static_cast<int>(e), "%s: HIP error %d (%s)", what, static_cast<int>(e),
+                hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_dtypes(int in_dtype, int out_dtype) {
+    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16)
+        return fail(PM_E_DTYPE, "in_dtype %d is not PM_DTYPE_F32 or PM_DTYPE_BF16", in_dtype);
+    if (out_dtype != PM_DTYPE_F32 && out_dtype != PM_DTYPE_BF16)
+        return fail(PM_E_DTYPE, "out_dtype %d is not PM_DTYPE_F32 or PM_DTYPE_BF16", out_dtype);
+    return 0;
+}
+
+// Common forward dispatch. cu == nullptr: fixed length (n_seq = B, T).
+int forward(const void* q, const void* k, const void* v, const float* beta, const float* s0,
+            void* o, float* s_out, const int32_t* cu, int n_seq, int T, int total_T, int H,
+            int D, int in_dtype, int out_dtype, int chunk, hipStream_t st) {
+    const bool varlen = cu != nullptr;
+    const long n_pairs = static_cast<long>(n_seq) * H;
+    const long n_tok = varlen ? static_cast<long>(total_T) : static_cast<long>(n_seq) * T;
+    if (n_pairs == 0) return 0;
+    if (!s_out) return fail(PM_E_NULL, "s_out is NULL");
+    if (n_tok > 0 && (!q || !k || !v || !beta || !o))
+        return fail(PM_E_NULL, "q, k, v, beta and o must be non-NULL");
+    if (!aligned(s_out, 4) || (s0 && !aligned(s0, 4)) || (beta && !aligned(beta, 4)))
+        return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
+    if (n_pairs > (1L << 30) || n_tok > (1L << 40))
+        return fail(PM_E_SHAPE, "problem too large");
+
+    const size_t s_elems = static_cast<size_t>(n_pairs) * D * D;
+    if (n_tok == 0) {
+        // no tokens: every state passes through unchanged (reference :456-457)
+        hipError_t e = s0 ? pm::launch_copy_f32(s_out, s0, s_elems, st)
+                          : pm::launch_fill_zero(s_out, s_elems, st);
+        return e == hipSuccess ? 0 : hip_fail(e, "state copy");
+    }
+
+    const int path = g_path.load();
+    const bool in_bf16 = in_dtype == PM_DTYPE_BF16;
+    const bool want_chunked = path != 1;
+    const bool can_chunked = in_bf16 && pm::chunked_supported(D) && aligned(q, 16) &&
+                             aligned(k, 16) && aligned(v, 16) &&
+                             (out_dtype == PM_DTYPE_F32 ? aligned(o, 16) : aligned(o, 8));
+    if (path == 2 && !can_chunked)
+        return fail(PM_E_UNSUPPORTED,
+                    "chunked kernel needs bf16 inputs, D in {64, 128} and 16-byte aligned "
+                    "q/k/v/o (got in_dtype %d, D %d)",
+                    in_dtype, D);
+    if (want_chunked && can_chunked) {
+        pm::ChunkedArgs a{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                          static_cast<const uint16_t*>(v), beta, s0, o, s_out, cu, n_seq,
+                          varlen ? total_T : T, H, D,
+                          out_dtype == PM_DTYPE_BF16, g_tile.load()};
+        hipError_t e = pm::launch_chunked(a, st);
+        return e == hipSuccess ? 0 : hip_fail(e, "chunked forward launch");
+    }
+    (void)chunk;
+    pm::RecurrentArgs a{q, k, v, beta, s0, o, s_out, cu, static_cast<int>(n_pairs),
+                        varlen ? total_T : T, H, D,
+                        in_bf16, out_dtype == PM_DTYPE_BF16};
+    hipError_t e = pm::launch_recurrent(a, st);
+    return e == hipSuccess ? 0 : hip_fail(e, "recurrent forward launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int pm_abi_version(void) { return PM_DELTA_ABI_VERSION; }
+
+const char* pm_last_error(void) { return g_err; }
+
+size_t pm_delta_workspace_bytes(int, int, int, int, int) { return 0; }
+
+int pm_delta_set_path(int path) {
+    if (path < 0 || path > 2) return fail(PM_E_UNSUPPORTED, "path %d not in {0, 1, 2}", path);
+    return g_path.exchange(path);
+}
+
+int pm_delta_set_tile(int dv_tile) {
+    if (dv_tile != 0 && dv_tile != 16 && dv_tile != 32 && dv_tile != 64)
+        return fail(PM_E_UNSUPPORTED, "dv_tile %d not in {0, 16, 32, 64}", dv_tile);
+    return g_tile.exchange(dv_tile);
+}
+
+int pm_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
+                 const float* s0, void* o, float* s_out, int B, int T, int H, int D,
+                 int in_dtype, int out_dtype, int chunk, void* workspace, size_t ws_bytes,
+                 void* stream) {
+    (void)workspace;
+    (void)ws_bytes;
+    g_err[0] = '\0';
+    if (B < 0 || T < 0 || H < 0)
+        return fail(PM_E_SHAPE, "B, T, H must be >= 0 (got %d, %d, %d)", B, T, H);
+    if (D < 1 || D > PM_DELTA_MAX_D)
+        return fail(PM_E_SHAPE, "D must be in [1, %d] (got %d)", PM_DELTA_MAX_D, D);
+    if (chunk < 1) return fail(PM_E_SHAPE, "chunk must be >= 1, got %d", chunk);
+    if (int rc = check_dtypes(in_dtype, out_dtype)) return rc;
+    return forward(q, k, v, beta, s0, o, s_out, nullptr, B, T, 0, H, D, in_dtype, out_dtype,
+                   chunk, static_cast<hipStream_t>(stream));
+}
+
+int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float* beta,
+                        const int32_t* cu_seqlens, int n_seqs, int total_T, const float* s0,
+                        void* o, float* s_out, int H, int D, int in_dtype, int out_dtype,
+                        int chunk, void* workspace, size_t ws_bytes, void* stream) {
+    (void)workspace;
+    (void)ws_bytes;
+    g_err[0] = '\0';
+    if (n_seqs < 0 || total_T < 0 || H < 0)
+        return fail(PM_E_SHAPE, "n_seqs, total_T, H must be >= 0 (got %d, %d, %d)", n_seqs,
+                    total_T, H);
+    if (D < 1 || D > PM_DELTA_MAX_D)
+        return fail(PM_E_SHAPE, "D must be in [1, %d] (got %d)", PM_DELTA_MAX_D, D);
+    if (chunk < 1) return fail(PM_E_SHAPE, "chunk must be >= 1, got %d", chunk);
+    if (int rc = check_dtypes(in_dtype, out_dtype)) return rc;
+    if (n_seqs > 0 && !cu_seqlens) return fail(PM_E_NULL, "cu_seqlens is NULL");
+    if (cu_seqlens && !aligned(cu_seqlens, 4))
+        return fail(PM_E_ALIGN, "cu_seqlens must be 4-byte aligned");
+    return forward(q, k, v, beta, s0, o, s_out, cu_seqlens, n_seqs, 0, total_T, H, D, in_dtype,
+                   out_dtype, chunk, static_cast<hipStream_t>(stream));
+}
+
+int pm_delta_step(float* s_inout, const void* q, const void* k, const void* v,
+                  const float* beta, float* o, int B, int H, int D, int in_dtype, void* stream) {
+    g_err[0] = '\0';
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (B < 0 || H < 0) return fail(PM_E_SHAPE, "B, H must be >= 0 (got %d, %d)", B, H);
+    if (D < 1 || D > PM_DELTA_MAX_D)
+        return fail(PM_E_SHAPE, "D must be in [1, %d] (got %d)", PM_DELTA_MAX_D, D);
+    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16)
+        return fail(PM_E_DTYPE, "in_dtype %d is not PM_DTYPE_F32 or PM_DTYPE_BF16", in_dtype);
+    const long n_pairs = static_cast<long>(B) * H;
+    if (n_pairs == 0) return 0;
+    if (n_pairs > (1L << 30)) return fail(PM_E_SHAPE, "problem too large");
+    if (!s_inout || !q || !k || !v || !beta || !o)
+        return fail(PM_E_NULL, "s_inout, q, k, v, beta and o must be non-NULL");
+    if (pm::step_supported(D) && aligned(s_inout, 16) && aligned(o, 16)) {
+        pm::StepArgs a{s_inout, q, k, v, beta, o, static_cast<int>(n_pairs), D,
+                       in_dtype == PM_DTYPE_BF16};
+        hipError_t e = pm::launch_step(a, st);
+        return e == hipSuccess ? 0 : hip_fail(e, "decode step launch");
+    }
+    if (!aligned(s_inout, 4) || !aligned(o, 4))
+        return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
+    // a (B, H, D) token is a length-1 (B, 1, H, D) sequence; K4 runs it in place
+    pm::RecurrentArgs a{q, k, v, beta, s_inout, o, s_inout, nullptr, static_cast<int>(n_pairs), 1,
+                        H, D, in_dtype == PM_DTYPE_BF16, false};
+    hipError_t e = pm::launch_recurrent(a, st);
+    return e == hipSuccess ? 0 : hip_fail(e, "decode step launch");
+}
+
+}  // extern "C"

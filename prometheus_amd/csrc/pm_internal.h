@@ -1,0 +1,64 @@
+// pm_internal.h — launcher interfaces between the C ABI layer and kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace pm {
+
+// Per-token kernel (K4). Fixed-length mode: n_pairs = B*H sequences of T
+// tokens. Varlen mode (cu_seqlens != nullptr): n_pairs = n_seqs*H and T is
+// the packed token count (segment offsets are clamped into [0, T]).
+struct RecurrentArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* beta;
+    const float* s0;  // nullable; may alias s_out
+    void* o;
+    float* s_out;
+    const int32_t* cu_seqlens;  // nullable
+    int n_pairs;
+    int T, H, D;
+    bool in_bf16, out_bf16;
+};
+hipError_t launch_recurrent(const RecurrentArgs& a, hipStream_t st);
+
+// Decode step (K3) for D in {32, 64, 128}: s updated in place.
+struct StepArgs {
+    float* s;
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* beta;
+    float* o;
+    int n_pairs, D;
+    bool in_bf16;
+};
+bool step_supported(int D);
+hipError_t launch_step(const StepArgs& a, hipStream_t st);
+
+// Chunked WY/UT forward (K1 / K2 when cu_seqlens != nullptr), bf16 inputs.
+struct ChunkedArgs {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const float* beta;
+    const float* s0;  // nullable
+    void* o;
+    float* s_out;
+    const int32_t* cu_seqlens;  // nullable
+    int n_seq;                  // B, or n_seqs in varlen mode
+    int T, H, D;                // varlen: T = packed token count
+    bool out_bf16;
+    int dv_tile;  // 0 = automatic
+};
+bool chunked_supported(int D);
+hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st);
+
+// Zero fill (used instead of hipMemsetAsync so callers may graph-capture).
+hipError_t launch_fill_zero(float* p, size_t n, hipStream_t st);
+hipError_t launch_copy_f32(float* dst, const float* src, size_t n, hipStream_t st);
+
+}  // namespace pm

@@ -1,0 +1,409 @@
+"""Delta-rule linear attention on MI355X — the reference's ``kernels`` call surface.
+
+Drop-in for the delta-rule forward of teddytennant/prometheus
+(``kernels/__init__.py``): same names, same positional order
+``(q, k, v, beta, state, config)``, same shapes, fp32 outputs, the same
+``_DeltaResidual`` fields and the same ``KernelError`` checks. The work runs
+in hand-written HIP kernels for gfx950 behind the C ABI of
+``include/pm_delta.h`` (``libpmdelta.so``); torch tensors are only device
+buffers and streams. There is no CPU fallback: without the built library
+or a GPU every call that reaches compute raises.
+
+Recurrence (decay gate 1), per batch b and head h::
+
+    S_t = (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T,    o_t = q_t S_t
+
+Inputs may be torch tensors (any device; CUDA/HIP tensors are used in
+place, CPU tensors are copied over and results copied back) or NumPy arrays
+(the reference's NumPy path: copied to the GPU, results returned as NumPy).
+bf16 q/k/v run the chunked MFMA kernel; every other dtype is cast to fp32,
+as the reference does (``kernels/__init__.py:344-347``), and runs the fp32
+per-token kernel.
+
+Beyond the reference surface: ``chunked_delta_rule_varlen`` (packed batch
+with ``cu_seqlens``), ``delta_rule_step`` (public single-token decode step)
+and the keyword ``out_dtype`` (bf16 output, opt-in; fp32 by default).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any
+
+import numpy as np
+import torch
+
+from prometheus_amd import _native
+
+Array = Any  # torch.Tensor or numpy.ndarray
+
+# Chunk width for the delta-rule tiling (kernels/__init__.py:80).
+DEFAULT_CHUNK = 64
+
+
+class KernelError(ValueError):
+    """Shape, dtype, or routing invariant failed before the kernel ran.
+
+    Same class as ``kernels/__init__.py:68-69``.
+    """
+
+
+@dataclass(frozen=True)
+class LinearAttnConfig:
+    """Chunked delta-rule knobs. ``chunk`` does not change the mathematical result.
+
+    Same fields and defaults as ``kernels/__init__.py:90-95``; ``eps`` is
+    unused there and here. The GPU kernel tiles by 64 tokens whatever
+    ``chunk`` says; ``chunk`` is validated (>= 1) and kept in the residual.
+    """
+
+    chunk: int = DEFAULT_CHUNK
+    eps: float = 1e-6
+
+
+@dataclass(frozen=True)
+class _DeltaResidual:
+    """Residual of ``chunked_delta_rule_fwd`` (``kernels/__init__.py:148-163``).
+
+    ``q, k, v, beta, state0`` are the arrays the kernel consumed (not
+    copied: bf16 inputs stay bf16, a documented difference from the
+    reference's fp32 copies); ``state0`` is fp32, zeros when ``state`` was
+    None; ``chunk`` is a Python int.
+    """
+
+    q: Array
+    k: Array
+    v: Array
+    beta: Array
+    state0: Array
+    chunk: int
+
+
+# ---------------------------------------------------------------------------
+# argument normalisation
+# ---------------------------------------------------------------------------
+
+
+def _on_host(*xs) -> bool:
+    """True when no argument is a GPU tensor (the reference's host-array path)."""
+    return not any(isinstance(x, torch.Tensor) and x.device.type == "cuda" for x in xs)
+
+
+def _shape(x) -> tuple:
+    return tuple(x.shape) if hasattr(x, "shape") else tuple(np.shape(x))
+
+
+def _check_chunk(config: LinearAttnConfig) -> int:
+    if config.chunk < 1:
+        raise KernelError(f"chunk must be >= 1, got {config.chunk}")
+    return int(config.chunk)
+
+
+def _validate(q, k, v, beta, state) -> tuple[int, int, int, int]:
+    """Shape checks of ``kernels/__init__.py:308-338`` on any array type."""
+    qs, ks, vs, bs = _shape(q), _shape(k), _shape(v), _shape(beta)
+    if len(qs) != 4 or ks != qs or vs != qs:
+        raise KernelError(f"q, k, v must all have shape (B, S, H, D); got {qs}")
+    batch, seq, heads, dim = qs
+    if bs != (batch, seq, heads):
+        raise KernelError(f"beta shape {bs} != {(batch, seq, heads)}")
+    if state is not None and _shape(state) != (batch, heads, dim, dim):
+        raise KernelError(f"state shape {_shape(state)} != {(batch, heads, dim, dim)}")
+    if dim > _native.MAX_D:
+        raise KernelError(f"head dimension {dim} exceeds the supported maximum {_native.MAX_D}")
+    return batch, seq, heads, dim
+
+
+def _check_beta_host(beta) -> None:
+    """``beta < 0`` check of the reference's host path (kernels/__init__.py:317-318)."""
+    if isinstance(beta, torch.Tensor):
+        b = beta.detach().cpu().float().numpy()
+    else:
+        b = np.asarray(beta, dtype=np.float32)
+    if np.any(b < 0):
+        raise KernelError("beta must be in (0, 1]")
+
+
+def _device() -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError("prometheus_amd.kernels needs a HIP GPU; none is visible")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+class _Call:
+    """Moves a call's arrays onto one GPU and remembers how to give results back."""
+
+    def __init__(self, *xs):
+        tensors = [x for x in xs if isinstance(x, torch.Tensor)]
+        dev_tensors = [t for t in tensors if t.device.type == "cuda"]
+        self.host_numpy = not tensors
+        self.host_torch = bool(tensors) and not dev_tensors
+        if dev_tensors:
+            self.device = dev_tensors[0].device
+            for t in dev_tensors:
+                if t.device != self.device:
+                    raise KernelError("all tensors must be on the same device")
+        else:
+            self.device = _device()
+
+    def dev(self, x, dtype=None):
+        if x is None:
+            return None
+        if isinstance(x, torch.Tensor):
+            t = x
+        else:
+            t = torch.from_numpy(np.ascontiguousarray(np.asarray(x, dtype=np.float32)))
+        if dtype is not None and t.dtype != dtype:
+            t = t.to(dtype)
+        return t.to(self.device, non_blocking=False).contiguous()
+
+    def out(self, t):
+        if self.host_numpy:
+            return t.cpu().numpy()
+        if self.host_torch:
+            return t.cpu()
+        return t
+
+
+def _qkv_dtype(q, k, v) -> torch.dtype:
+    dts = {x.dtype for x in (q, k, v) if isinstance(x, torch.Tensor)}
+    if dts == {torch.bfloat16} and all(isinstance(x, torch.Tensor) for x in (q, k, v)):
+        return torch.bfloat16
+    return torch.float32
+
+
+def _out_dtype(out_dtype) -> torch.dtype:
+    if out_dtype is None or out_dtype in (torch.float32, np.float32, "fp32", "float32"):
+        return torch.float32
+    if out_dtype in (torch.bfloat16, "bf16", "bfloat16"):
+        return torch.bfloat16
+    raise KernelError(f"out_dtype must be fp32 (default) or bf16, got {out_dtype!r}")
+
+
+def _code(dt: torch.dtype) -> int:
+    return _native.DTYPE_BF16 if dt == torch.bfloat16 else _native.DTYPE_F32
+
+
+def _ptr(t) -> int | None:
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+# ---------------------------------------------------------------------------
+# forward
+# ---------------------------------------------------------------------------
+
+
+def _forward(q, k, v, beta, state, chunk: int, out_dtype):
+    batch, seq, heads, dim = _validate(q, k, v, beta, state)
+    odt = _out_dtype(out_dtype)
+    if _on_host(q, k, v, beta, state):
+        _check_beta_host(beta)
+    call = _Call(q, k, v, beta, state)
+    cdt = _qkv_dtype(q, k, v)
+    with torch.cuda.device(call.device):
+        qd, kd, vd = call.dev(q, cdt), call.dev(k, cdt), call.dev(v, cdt)
+        bd = call.dev(beta, torch.float32)
+        sd = call.dev(state, torch.float32)
+        o = torch.empty((batch, seq, heads, dim), dtype=odt, device=call.device)
+        s_out = torch.empty((batch, heads, dim, dim), dtype=torch.float32, device=call.device)
+        rc = _native.lib().pm_delta_fwd(
+            _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(sd), _ptr(o), _ptr(s_out),
+            batch, seq, heads, dim, _code(cdt), _code(odt), chunk, None, 0,
+            _stream(call.device),
+        )
+        _native.check(rc)
+        if sd is None:
+            sd = torch.zeros((batch, heads, dim, dim), dtype=torch.float32, device=call.device)
+    return call, (qd, kd, vd, bd, sd), o, s_out
+
+
+def chunked_delta_rule(q, k, v, beta, state=None, config=None, *, out_dtype=None):
+    """Gated delta-rule linear attention (``kernels/__init__.py:591-619``).
+
+    q, k, v: (batch, seq, heads, dim). beta: (batch, seq, heads) gate in (0, 1].
+    state: (batch, heads, dim, dim) recurrent state, zeros if None.
+    Returns ``(output, next_state)``; output shaped like v (fp32 unless
+    ``out_dtype`` asks for bf16), next_state fp32.
+    """
+    cfg = LinearAttnConfig() if config is None else config
+    chunk = _check_chunk(cfg)
+    call, _, o, s = _forward(q, k, v, beta, state, chunk, out_dtype)
+    return call.out(o), call.out(s)
+
+
+def chunked_delta_rule_fwd(q, k, v, beta, state, config, *, out_dtype=None):
+    """Explicit forward of the VJP pair (``kernels/__init__.py:661-689``).
+
+    Returns ``((output, next_state), _DeltaResidual)``.
+    """
+    chunk = _check_chunk(config)
+    call, (qd, kd, vd, bd, sd), o, s = _forward(q, k, v, beta, state, chunk, out_dtype)
+    if call.host_numpy:
+        residual = _DeltaResidual(
+            q=np.asarray(q, dtype=np.float32), k=np.asarray(k, dtype=np.float32),
+            v=np.asarray(v, dtype=np.float32), beta=np.asarray(beta, dtype=np.float32),
+            state0=sd.cpu().numpy(), chunk=chunk,
+        )
+    else:
+        residual = _DeltaResidual(q=call.out(qd), k=call.out(kd), v=call.out(vd),
+                                  beta=call.out(bd), state0=call.out(sd), chunk=chunk)
+    return (call.out(o), call.out(s)), residual
+
+
+def chunked_delta_rule_bwd(residual: _DeltaResidual, grads):
+    """Backward of the VJP pair (``kernels/__init__.py:692-719``): not built yet.
+
+    The MI355X build covers the forward and the decode step; the chunked
+    recompute backward is the next item of the roadmap.
+    """
+    raise NotImplementedError("chunked_delta_rule_bwd: the MI355X backward is not built yet")
+
+
+# ---------------------------------------------------------------------------
+# packed variable-length forward (no reference counterpart)
+# ---------------------------------------------------------------------------
+
+
+def _validate_cu(cu_host: np.ndarray, total: int) -> None:
+    if cu_host.ndim != 1 or cu_host.size < 1:
+        raise KernelError("cu_seqlens must be a 1-D array of n_seqs + 1 offsets")
+    if cu_host[0] != 0 or cu_host[-1] != total:
+        raise KernelError(f"cu_seqlens must start at 0 and end at {total}; got "
+                          f"{int(cu_host[0])}..{int(cu_host[-1])}")
+    if np.any(np.diff(cu_host) < 0):
+        raise KernelError("cu_seqlens must be non-decreasing")
+
+
+def chunked_delta_rule_varlen(q, k, v, beta, cu_seqlens, state=None, config=None, *,
+                              out_dtype=None):
+    """Packed batch of independent sequences, state reset at every boundary.
+
+    q, k, v: (N, H, D) or (1, N, H, D); beta: (N, H) or (1, N, H);
+    cu_seqlens: int32 (n_seqs + 1,) exclusive prefix, 0 .. N;
+    state: None (zeros) or (n_seqs, H, D, D) initial states.
+    Returns ``(output, final_states)`` with output shaped like q and
+    final_states (n_seqs, H, D, D) fp32. Each segment equals a B=1
+    ``chunked_delta_rule`` call on that segment alone, bit for bit.
+    """
+    cfg = LinearAttnConfig() if config is None else config
+    chunk = _check_chunk(cfg)
+    qs = _shape(q)
+    lead4 = len(qs) == 4
+    if lead4:
+        if qs[0] != 1:
+            raise KernelError(f"packed q must be (N, H, D) or (1, N, H, D); got {qs}")
+        qs = qs[1:]
+    if len(qs) != 3 or _shape(k)[-3:] != qs or _shape(v)[-3:] != qs:
+        raise KernelError(f"q, k, v must all have shape (N, H, D); got {_shape(q)}")
+    n_tok, heads, dim = qs
+    bs = _shape(beta)
+    if bs not in ((n_tok, heads), (1, n_tok, heads)):
+        raise KernelError(f"beta shape {bs} != {(n_tok, heads)}")
+    if dim > _native.MAX_D:
+        raise KernelError(f"head dimension {dim} exceeds the supported maximum {_native.MAX_D}")
+    if isinstance(cu_seqlens, torch.Tensor):
+        cu_host = cu_seqlens.detach().cpu().numpy()
+    else:
+        cu_host = np.asarray(cu_seqlens)
+    if not np.issubdtype(cu_host.dtype, np.integer):
+        raise KernelError(f"cu_seqlens must be an integer array, got {cu_host.dtype}")
+    cu_host = cu_host.astype(np.int64)
+    _validate_cu(cu_host, n_tok)
+    if cu_host[-1] >= 2**31:
+        raise KernelError("cu_seqlens exceeds int32")
+    n_seqs = cu_host.size - 1
+    if state is not None and _shape(state) != (n_seqs, heads, dim, dim):
+        raise KernelError(f"state shape {_shape(state)} != {(n_seqs, heads, dim, dim)}")
+
+    odt = _out_dtype(out_dtype)
+    if _on_host(q, k, v, beta, state):
+        _check_beta_host(beta)
+    call = _Call(q, k, v, beta, state, cu_seqlens)
+    cdt = _qkv_dtype(q, k, v)
+    with torch.cuda.device(call.device):
+        qd = call.dev(q, cdt).reshape(n_tok, heads, dim)
+        kd = call.dev(k, cdt).reshape(n_tok, heads, dim)
+        vd = call.dev(v, cdt).reshape(n_tok, heads, dim)
+        bd = call.dev(beta, torch.float32).reshape(n_tok, heads)
+        sd = call.dev(state, torch.float32)
+        cu = torch.from_numpy(cu_host.astype(np.int32)).to(call.device)
+        o = torch.empty((n_tok, heads, dim), dtype=odt, device=call.device)
+        s_out = torch.empty((n_seqs, heads, dim, dim), dtype=torch.float32, device=call.device)
+        rc = _native.lib().pm_delta_fwd_varlen(
+            _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(cu), n_seqs, n_tok, _ptr(sd),
+            _ptr(o), _ptr(s_out), heads, dim, _code(cdt), _code(odt), chunk, None, 0,
+            _stream(call.device),
+        )
+        _native.check(rc)
+    if lead4:
+        o = o.reshape(1, n_tok, heads, dim)
+    return call.out(o), call.out(s_out)
+
+
+# ---------------------------------------------------------------------------
+# single-token decode step (public form of kernels/__init__.py:357-376)
+# ---------------------------------------------------------------------------
+
+
+def delta_rule_step(q, k, v, beta, state):
+    """One recurrent step for (B, H, D) tokens; ``state`` (B, H, D, D) updated in place.
+
+    Same algebra as ``_delta_step_np`` / ``_delta_step_jax``
+    (``kernels/__init__.py:357-376``): ``S' = S - beta k (k^T S) + beta k v^T``
+    and ``o = q S'``. ``state`` must be fp32: a contiguous GPU tensor is
+    updated on the device, a NumPy array or CPU tensor is updated through a
+    copy. Returns o (B, H, D) fp32.
+    """
+    qs = _shape(q)
+    if len(qs) != 3 or _shape(k) != qs or _shape(v) != qs:
+        raise KernelError(f"q, k, v must all have shape (B, H, D); got {qs}")
+    batch, heads, dim = qs
+    if _shape(beta) != (batch, heads):
+        raise KernelError(f"beta shape {_shape(beta)} != {(batch, heads)}")
+    if state is None or _shape(state) != (batch, heads, dim, dim):
+        raise KernelError(f"state shape {_shape(state) if state is not None else None} != "
+                          f"{(batch, heads, dim, dim)}")
+    if dim > _native.MAX_D:
+        raise KernelError(f"head dimension {dim} exceeds the supported maximum {_native.MAX_D}")
+    in_place = isinstance(state, torch.Tensor) and state.device.type == "cuda"
+    if in_place and (state.dtype != torch.float32 or not state.is_contiguous()):
+        raise KernelError("state must be a contiguous fp32 tensor to be updated in place")
+    if isinstance(state, np.ndarray) and state.dtype != np.float32:
+        raise KernelError("state must be fp32 to be updated in place")
+    if _on_host(q, k, v, beta, state):
+        _check_beta_host(beta)
+    call = _Call(q, k, v, beta, state)
+    cdt = _qkv_dtype(q, k, v)
+    with torch.cuda.device(call.device):
+        qd, kd, vd = call.dev(q, cdt), call.dev(k, cdt), call.dev(v, cdt)
+        bd = call.dev(beta, torch.float32)
+        sd = state if in_place else call.dev(state, torch.float32)
+        o = torch.empty((batch, heads, dim), dtype=torch.float32, device=call.device)
+        rc = _native.lib().pm_delta_step(_ptr(sd), _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd),
+                                         _ptr(o), batch, heads, dim, _code(cdt),
+                                         _stream(call.device))
+        _native.check(rc)
+        if not in_place:
+            host = sd.cpu()
+            if isinstance(state, np.ndarray):
+                state[...] = host.numpy()
+            else:
+                state.copy_(host)
+    return call.out(o)
+
+
+__all__ = [
+    "DEFAULT_CHUNK",
+    "KernelError",
+    "LinearAttnConfig",
+    "_DeltaResidual",
+    "chunked_delta_rule",
+    "chunked_delta_rule_fwd",
+    "chunked_delta_rule_bwd",
+    "chunked_delta_rule_varlen",
+    "delta_rule_step",
+]

@@ -1,0 +1,213 @@
+"""CPU tests of the host side: the reference call surface, its checks, and the C ABI.
+
+Nothing here launches a kernel: the checks mirrored from the reference
+(kernels/__init__.py:308-338, :613-614, :676-677; tests/test_kernels.py:
+218-241, :464-481) all fire before any device work, and the C ABI's
+argument validation returns before touching the GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from prometheus_amd import _native, kernels, synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _inputs(rng, batch=2, seq=5, heads=2, dim=4):
+    return synth.reference_test_inputs(rng, batch, seq, heads, dim)
+
+
+# --- constants and dataclasses (tests/test_kernels.py:218-241) ---
+
+
+def test_default_chunk_is_64():
+    assert kernels.DEFAULT_CHUNK == 64
+
+
+def test_linear_attn_config_defaults():
+    cfg = kernels.LinearAttnConfig()
+    assert cfg.chunk == 64
+    assert cfg.eps == pytest.approx(1e-6)
+    with pytest.raises(Exception):
+        cfg.chunk = 3  # frozen
+
+
+def test_kernel_error_is_value_error():
+    assert issubclass(kernels.KernelError, ValueError)
+    assert isinstance(kernels.KernelError("shape"), ValueError)
+
+
+def test_delta_residual_fields():
+    fields = [f for f in kernels._DeltaResidual.__dataclass_fields__]
+    assert fields == ["q", "k", "v", "beta", "state0", "chunk"]
+
+
+# --- KernelError before any device work (tests/test_kernels.py:464-481) ---
+
+
+def test_bad_shapes_raise_kernel_error():
+    q, k, v, beta = _inputs(np.random.default_rng(21), batch=1, seq=3, heads=1, dim=4)
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule(q[:, :, :, :3], k, v, beta)
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule(q, k, v, beta[:, :2])
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule(q, k, v, beta, state=np.zeros((1, 1, 3, 3), np.float32))
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule(q[0], k[0], v[0], beta[0])
+
+
+def test_negative_beta_raises_kernel_error():
+    q, k, v, beta = _inputs(np.random.default_rng(22), batch=1, seq=2, heads=1, dim=2)
+    beta = beta.copy()
+    beta[0, 0, 0] = -0.1
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule(q, k, v, beta)
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule_fwd(q, k, v, beta, None, kernels.LinearAttnConfig())
+
+
+def test_chunk_below_one_raises_kernel_error():
+    q, k, v, beta = _inputs(np.random.default_rng(23))
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule(q, k, v, beta, config=kernels.LinearAttnConfig(chunk=0))
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule_fwd(q, k, v, beta, None, kernels.LinearAttnConfig(chunk=-2))
+
+
+def test_head_dim_limit_raises_kernel_error():
+    z = np.zeros((1, 1, 1, 257), np.float32)
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule(z, z, z, np.zeros((1, 1, 1), np.float32))
+
+
+def test_bwd_is_not_built_yet():
+    with pytest.raises(NotImplementedError):
+        kernels.chunked_delta_rule_bwd(None, (None, None))
+
+
+def test_varlen_checks():
+    q = np.zeros((10, 2, 4), np.float32)
+    b = np.zeros((10, 2), np.float32)
+    for cu in ([0, 5, 9], [1, 5, 10], [0, 6, 5, 10], [0.0, 10.0]):
+        with pytest.raises(kernels.KernelError):
+            kernels.chunked_delta_rule_varlen(q, q, q, b, np.asarray(cu))
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule_varlen(q, q, q, b[:5], np.array([0, 10]))
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule_varlen(q, q, q, b, np.array([0, 4, 10]),
+                                          state=np.zeros((3, 2, 4, 4), np.float32))
+
+
+def test_step_checks():
+    q = np.zeros((2, 3, 4), np.float32)
+    b = np.zeros((2, 3), np.float32)
+    with pytest.raises(kernels.KernelError):
+        kernels.delta_rule_step(q, q, q, b, np.zeros((2, 3, 4, 5), np.float32))
+    with pytest.raises(kernels.KernelError):
+        kernels.delta_rule_step(q, q, q, b, np.zeros((2, 3, 4, 4), np.float64))
+    with pytest.raises(kernels.KernelError):
+        kernels.delta_rule_step(q, q, q, b[:1], np.zeros((2, 3, 4, 4), np.float32))
+
+
+def test_out_dtype_check():
+    q, k, v, beta = _inputs(np.random.default_rng(24))
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule(q, k, v, beta, out_dtype="fp16")
+
+
+# --- the C ABI library: loads, exports what include/pm_delta.h declares ---
+
+
+def _header_functions():
+    text = open(os.path.join(ROOT, "include", "pm_delta.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pm_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    declared = _header_functions()
+    assert declared == sorted(_native.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.pm_abi_version() == _native.ABI_VERSION
+
+
+def test_abi_argument_validation_without_gpu():
+    lib = _native.lib()
+    f = lib.pm_delta_fwd
+    dummy = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    # D out of range
+    assert f(dummy, dummy, dummy, dummy, None, dummy, dummy, 1, 4, 1, 0, 0, 0, 64, None, 0,
+             None) == _native.E_SHAPE
+    assert b"D must be" in lib.pm_last_error()
+    assert f(dummy, dummy, dummy, dummy, None, dummy, dummy, 1, 4, 1, 300, 0, 0, 64, None, 0,
+             None) == _native.E_SHAPE
+    # chunk < 1
+    assert f(dummy, dummy, dummy, dummy, None, dummy, dummy, 1, 4, 1, 8, 0, 0, 0, None, 0,
+             None) == _native.E_SHAPE
+    # dtype
+    assert f(dummy, dummy, dummy, dummy, None, dummy, dummy, 1, 4, 1, 8, 7, 0, 64, None, 0,
+             None) == _native.E_DTYPE
+    assert f(dummy, dummy, dummy, dummy, None, dummy, dummy, 1, 4, 1, 8, 0, 5, 64, None, 0,
+             None) == _native.E_DTYPE
+    # NULL inputs with tokens to process
+    assert f(None, dummy, dummy, dummy, None, dummy, dummy, 1, 4, 1, 8, 0, 0, 64, None, 0,
+             None) == _native.E_NULL
+    assert f(dummy, dummy, dummy, dummy, None, dummy, None, 1, 4, 1, 8, 0, 0, 64, None, 0,
+             None) == _native.E_NULL
+    # negative sizes
+    assert f(dummy, dummy, dummy, dummy, None, dummy, dummy, -1, 4, 1, 8, 0, 0, 64, None, 0,
+             None) == _native.E_SHAPE
+    # nothing to do: B*H == 0 returns success without touching anything
+    assert f(None, None, None, None, None, None, None, 0, 4, 3, 8, 0, 0, 64, None, 0, None) == 0
+    # varlen: NULL cu_seqlens, misaligned cu_seqlens
+    g = lib.pm_delta_fwd_varlen
+    assert g(dummy, dummy, dummy, dummy, None, 2, 10, None, dummy, dummy, 1, 8, 0, 0, 64, None, 0,
+             None) == _native.E_NULL
+    assert g(dummy, dummy, dummy, dummy, ctypes.c_void_p(18), 2, 10, None, dummy, dummy, 1, 8, 0,
+             0, 64, None, 0, None) == _native.E_ALIGN
+    # step
+    h = lib.pm_delta_step
+    assert h(None, dummy, dummy, dummy, dummy, dummy, 2, 2, 8, 0, None) == _native.E_NULL
+    assert h(dummy, dummy, dummy, dummy, dummy, dummy, 2, 2, 0, 0, None) == _native.E_SHAPE
+    assert h(dummy, dummy, dummy, dummy, dummy, dummy, 2, 2, 8, 3, None) == _native.E_DTYPE
+    assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, 1) == 0
+
+
+def test_path_and_tile_switches():
+    old = _native.set_path(1)
+    try:
+        assert _native.set_path(2) == 1
+    finally:
+        _native.set_path(old)
+    with pytest.raises(_native.NativeError):
+        _native.set_path(3)
+    old = _native.set_tile(32)
+    try:
+        assert _native.set_tile(16) == 32
+    finally:
+        _native.set_tile(old)
+    with pytest.raises(_native.NativeError):
+        _native.set_tile(48)
+
+
+def test_synth_configs_and_lengths():
+    c = synth.CONFIGS[2]
+    lens = synth.varlen_lengths(c["total"], c["lo"], c["hi"], seed=0)
+    assert int(lens.sum()) == c["total"]
+    assert np.all(lens[:-1] >= 64) and np.all(lens <= 4096)
+    cu = synth.cu_seqlens(lens)
+    assert cu.dtype == np.int32 and cu[0] == 0 and cu[-1] == c["total"]
+    x = synth.fwd_inputs((1, 8, 2, 16), seed=1, dtype="bf16", s0_std=0.02)
+    np.testing.assert_allclose(np.linalg.norm(x.q, axis=-1), 1.0, atol=1e-2)
+    assert x.q_bits.dtype == np.uint16 and x.s0.shape == (1, 2, 16, 16)
+    assert np.all((x.beta > 0) & (x.beta < 1))

@@ -52,21 +52,29 @@ constexpr int kC = 64;  // chunk length (tokens)
 __device__ __forceinline__ f32x4_t mfma32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f32x4_t mfma16(bf16x4_t a, bf16x4_t b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x4_t mfma16(u32x2_t a, u32x2_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, a),
+                                                     __builtin_bit_cast(bf16x4_t, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ bf16x4_t cvt4(f32x4_t x) {
-    bf16x4_t r = {(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w};
-    return r;
+__device__ __forceinline__ uint16_t bf16_bits(float x) {
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
 }
-__device__ __forceinline__ bf16x8_t cat8(bf16x4_t lo, bf16x4_t hi) {
-    bf16x8_t r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+// bf16 operands are assembled from 16-bit patterns packed into 32-bit
+// words and bit-cast to the MFMA vector type only at the call: element
+// access on bf16 vectors (extract or insert) is avoided on purpose, since
+// hipcc (ROCm 7.2) miscompiled an element extract feeding a 16-bit LDS store.
+__device__ __forceinline__ unsigned pack2(float a, float b) {
+    return static_cast<unsigned>(bf16_bits(a)) | (static_cast<unsigned>(bf16_bits(b)) << 16);
+}
+__device__ __forceinline__ u32x2_t cvt4(f32x4_t x) {
+    const u32x2_t r = {pack2(x.x, x.y), pack2(x.z, x.w)};
     return r;
 }
 // Two stacked accumulator tiles (rows 0-15 and 16-31 of a 32-block) as a B operand.
 __device__ __forceinline__ bf16x8_t acc_to_b(f32x4_t lo, f32x4_t hi) {
-    return cat8(cvt4(lo), cvt4(hi));
+    const u32x4_t r = {pack2(lo.x, lo.y), pack2(lo.z, lo.w), pack2(hi.x, hi.y), pack2(hi.z, hi.w)};
+    return __builtin_bit_cast(bf16x8_t, r);
 }
 
 // A operand of a 16x16x32 product from a row-major bf16 LDS matrix:
@@ -84,9 +92,6 @@ __device__ __forceinline__ void wave_lds_fence() {
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
-__device__ __forceinline__ uint16_t bf16_bits(float x) {
-    return __builtin_bit_cast(uint16_t, (__bf16)x);
-}
 __device__ __forceinline__ uint16_t half_of(u32x4_t v, int j) {
     const unsigned w = v[j >> 1];
     return static_cast<uint16_t>((j & 1) ? (w >> 16) : (w & 0xffffu));
@@ -344,12 +349,11 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
             // xb[i] holds X_i as a 16x16x16 B operand (slot s <-> row 4g+s);
             // every slot starts as X_j and slots i > j are overwritten in order.
             const int j = w;
-            bf16x4_t xb[4];
+            u32x2_t xb[4];
             {
-                const uint16_t* dj = Dw + ((w * 4 + j) * 16) * G::PD;
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
-                    xb[0][jj] = __builtin_bit_cast(__bf16, dj[(4 * lg + jj) * G::PD + l16]);
+                const uint16_t* dj = Dw + ((w * 4 + j) * 16) * G::PD + l16;
+                xb[0].x = dj[(4 * lg) * G::PD] | (static_cast<unsigned>(dj[(4 * lg + 1) * G::PD]) << 16);
+                xb[0].y = dj[(4 * lg + 2) * G::PD] | (static_cast<unsigned>(dj[(4 * lg + 3) * G::PD]) << 16);
 #pragma unroll
                 for (int i = 1; i < 4; ++i) xb[i] = xb[0];
             }
@@ -367,12 +371,13 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
                 const uint16_t* di = Dw + ((w * 4 + i) * 16 + l16) * G::PD + 4 * lg;
                 const u32x2_t dv = *reinterpret_cast<const u32x2_t*>(di);
                 const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-                const f32x4_t x = -mfma16(__builtin_bit_cast(bf16x4_t, dv), cvt4(z), zero);
+                const f32x4_t x = -mfma16(dv, cvt4(z), zero);
                 xb[i] = cvt4(x);
-#pragma unroll
-                for (int ii = 0; ii < 4; ++ii)
-                    Tm[(16 * i + 4 * lg + ii) * G::PT + 16 * j + l16] =
-                        __builtin_bit_cast(uint16_t, xb[i][ii]);
+                uint16_t* tcol = Tm + (16 * i + 4 * lg) * G::PT + 16 * j + l16;
+                tcol[0] = static_cast<uint16_t>(xb[i].x & 0xffffu);
+                tcol[G::PT] = static_cast<uint16_t>(xb[i].x >> 16);
+                tcol[2 * G::PT] = static_cast<uint16_t>(xb[i].y & 0xffffu);
+                tcol[3 * G::PT] = static_cast<uint16_t>(xb[i].y >> 16);
             }
         }
         __syncthreads();

@@ -34,6 +34,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, vendor figure
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, vendor figure
 CHUNK = 64
+CALIB_COPY_BYTES = 1 << 30  # bytes read (and written) by one calibration copy launch
 
 
 def fwd_flops(B, T, H, D, chunk=CHUNK) -> float:
@@ -97,6 +98,10 @@ def main():
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_cfg1.json"),
                     help="JSON with measured HBM bytes per launch (from rocprofv3 --pmc)")
     ap.add_argument("--tile", type=int, default=0, help="d_v tile of the chunked kernel (0 auto)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run 3 launches of a plain 1 GiB fp32 elementwise copy (torch.neg, "
+                         "4 GiB read+written in all) so that rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE "
+                         "runs can be scaled to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
@@ -228,6 +233,15 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": dbytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
     }
+
+    if args.calib_copy:
+        n = CALIB_COPY_BYTES // 4
+        x = torch.randn(n, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            torch.neg(x, out=y)
+        torch.cuda.synchronize()
+        del x, y
 
     line = {
         "metric": "delta-rule fwd tokens/s + % MFMA/HBM roofline, B4·H16·T4096·d128 bf16",

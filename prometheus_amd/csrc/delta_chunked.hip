@@ -148,9 +148,13 @@ __device__ __forceinline__ void zero_upper_half(uint16_t* buf, int q, int lane) 
     *reinterpret_cast<u32x2_t*>(buf + q * 512 + lane * 8 + 4) = z;
 }
 
-__device__ __forceinline__ uint16_t half_of(u32x4_t v, int j) {
-    const unsigned w = v[j >> 1];
-    return static_cast<uint16_t>((j & 1) ? (w >> 16) : (w & 0xffffu));
+// Element j of four 8-element rows r[0..3], packed as 4 consecutive bf16
+// (a column of a 4x8 block), with v_perm_b32 selecting 16-bit halves.
+__device__ __forceinline__ u32x2_t column4(const u32x4_t* r, int j) {
+    const unsigned sel = (j & 1) ? 0x07060302u : 0x05040100u;
+    const u32x2_t out = {__builtin_amdgcn_perm(r[1][j >> 1], r[0][j >> 1], sel),
+                         __builtin_amdgcn_perm(r[3][j >> 1], r[2][j >> 1], sel)};
+    return out;
 }
 
 // LDS-only workgroup barrier: waits for this wave's LDS traffic, never for
@@ -293,10 +297,7 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int d = dg * 8 + j;
-                    const u32x2_t pk = {
-                        half_of(kr[u][0], j) | (static_cast<unsigned>(half_of(kr[u][1], j)) << 16),
-                        half_of(kr[u][2], j) | (static_cast<unsigned>(half_of(kr[u][3], j)) << 16)};
-                    *reinterpret_cast<u32x2_t*>(Kt + d * G::PT + 4 * (tg ^ swz_t(d))) = pk;
+                    *reinterpret_cast<u32x2_t*>(Kt + d * G::PT + 4 * (tg ^ swz_t(d))) = column4(kr[u], j);
                 }
             }
         }
@@ -308,10 +309,7 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int e = cv * 8 + j;
-                    const u32x2_t pk = {
-                        half_of(vr[u][0], j) | (static_cast<unsigned>(half_of(vr[u][1], j)) << 16),
-                        half_of(vr[u][2], j) | (static_cast<unsigned>(half_of(vr[u][3], j)) << 16)};
-                    *reinterpret_cast<u32x2_t*>(Vt + e * G::PT + 4 * (tg ^ swz_t(e))) = pk;
+                    *reinterpret_cast<u32x2_t*>(Vt + e * G::PT + 4 * (tg ^ swz_t(e))) = column4(vr[u], j);
                 }
             }
         }

@@ -1,0 +1,160 @@
+"""Summaries of rocprofv3 CSV output for the committed profiles.
+
+    python -m prometheus_amd.rocprof_summary stats DIR --cmd "..." [--bench-log LOG] -o OUT.md
+    python -m prometheus_amd.rocprof_summary traffic FETCH_DIR WRITE_DIR --kernel NAME
+        --cmd-fetch "..." --cmd-write "..." -o OUT.json
+
+``stats`` turns ``*_kernel_stats.csv`` (from ``--kernel-trace --stats``) into a
+short markdown table.  ``traffic`` reads two ``--pmc`` runs (``FETCH_SIZE``,
+then ``WRITE_SIZE``; both in KiB per dispatch) of a command that also ran
+``bench.py --calib-copy`` (a plain elementwise fp32 copy of a known 1 GiB), and
+scales the kernel's per-dispatch counters by ``known bytes / counted bytes``
+of that copy, giving the HBM bytes one launch of the kernel moves.
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import os
+import re
+import statistics
+import sys
+
+CALIB_COPY_BYTES = 1 << 30
+CALIB_KERNEL = "neg"  # torch.neg elementwise kernel launched by bench.py --calib-copy
+
+
+def _one(pattern: str) -> str:
+    hits = sorted(glob.glob(pattern, recursive=True))
+    if not hits:
+        raise FileNotFoundError(pattern)
+    return hits[0]
+
+
+def short_name(name: str) -> str:
+    """Kernel name without return type and argument list (templates kept)."""
+    name = re.sub(r"^void\s+", "", name).replace("(anonymous namespace)", "{anon}")
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            name = name[:i]
+            break
+    return name if len(name) <= 110 else name[:107] + "..."
+
+
+def stats(args) -> None:
+    path = _one(os.path.join(args.dir, "**", "*kernel_stats.csv"))
+    with open(path) as f:
+        rows = list(csv.DictReader(f))
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    out = ["# rocprofv3 kernel statistics", "", "Command:", "", "```", args.cmd, "```", ""]
+    if args.bench_log:
+        for ln in open(args.bench_log):
+            if ln.startswith("{"):
+                d = json.loads(ln)
+                out += [f"bench.py line from the same run: kernel_us (HIP events, mean per launch) = "
+                        f"{d['kernel_us']:.1f}; decode us_per_step = "
+                        f"{d['decode']['us_per_step']:.1f}; value = {d['value']:.4g} {d['unit']}", ""]
+    out += ["| kernel | calls | avg us | min us | max us | total % |",
+            "|---|---:|---:|---:|---:|---:|"]
+    for r in rows[: args.top]:
+        out.append(f"| `{short_name(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                   f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
+                   f"{float(r['Percentage']):.1f} |")
+    text = "\n".join(out) + "\n"
+    with open(args.out, "w") as f:
+        f.write(text)
+    print(text)
+
+
+def _per_dispatch(dir_: str, counter: str) -> dict[str, list[float]]:
+    """Kernel short name -> list of per-dispatch values of ``counter``."""
+    path = _one(os.path.join(dir_, "**", "*counter_collection.csv"))
+    acc: dict[tuple[str, str], float] = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            key = (r["Dispatch_Id"], r["Kernel_Name"])
+            acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"])
+    out: dict[str, list[float]] = {}
+    for (_, name), v in acc.items():
+        out.setdefault(short_name(name), []).append(v)
+    return out
+
+
+def _pick(table: dict[str, list[float]], needle: str) -> tuple[str, list[float]]:
+    hits = [(k, v) for k, v in table.items() if needle in k]
+    if not hits:
+        raise KeyError(f"no kernel matching {needle!r} in {sorted(table)}")
+    hits.sort(key=lambda kv: -len(kv[1]))
+    return hits[0]
+
+
+def traffic(args) -> None:
+    fetch = _per_dispatch(args.fetch_dir, "FETCH_SIZE")
+    write = _per_dispatch(args.write_dir, "WRITE_SIZE")
+    kname, kf = _pick(fetch, args.kernel)
+    _, kw = _pick(write, args.kernel)
+    cname, cf = _pick(fetch, CALIB_KERNEL)
+    _, cw = _pick(write, CALIB_KERNEL)
+    kib = CALIB_COPY_BYTES / 1024.0
+    f_scale = kib / statistics.median(cf)
+    w_scale = kib / statistics.median(cw)
+    k_fetch = statistics.median(kf) * f_scale * 1024.0
+    k_write = statistics.median(kw) * w_scale * 1024.0
+    res = {
+        "kernel": kname,
+        "dispatches": {"fetch": len(kf), "write": len(kw)},
+        "fetch_kib_per_dispatch": statistics.median(kf),
+        "write_kib_per_dispatch": statistics.median(kw),
+        "calib_kernel": cname,
+        "calib_bytes_each_way": CALIB_COPY_BYTES,
+        "calib_fetch_kib": statistics.median(cf),
+        "calib_write_kib": statistics.median(cw),
+        "fetch_scale": f_scale,
+        "write_scale": w_scale,
+        "fetch_bytes_per_launch": k_fetch,
+        "write_bytes_per_launch": k_write,
+        "bytes_per_launch": k_fetch + k_write,
+        "algorithmic_bytes": args.algorithmic_bytes,
+        "commands": {"fetch": args.cmd_fetch, "write": args.cmd_write},
+    }
+    if args.algorithmic_bytes:
+        res["traffic_over_algorithmic"] = res["bytes_per_launch"] / args.algorithmic_bytes
+    with open(args.out, "w") as f:
+        json.dump(res, f, indent=1)
+        f.write("\n")
+    print(json.dumps(res, indent=1))
+
+
+def main(argv=None) -> None:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd_name", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("dir")
+    s.add_argument("--cmd", required=True)
+    s.add_argument("--bench-log")
+    s.add_argument("--top", type=int, default=8)
+    s.add_argument("-o", "--out", required=True)
+    t = sub.add_parser("traffic")
+    t.add_argument("fetch_dir")
+    t.add_argument("write_dir")
+    t.add_argument("--kernel", required=True)
+    t.add_argument("--cmd-fetch", required=True)
+    t.add_argument("--cmd-write", required=True)
+    t.add_argument("--algorithmic-bytes", type=float, default=None)
+    t.add_argument("-o", "--out", required=True)
+    args = ap.parse_args(argv)
+    (stats if args.cmd_name == "stats" else traffic)(args)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])

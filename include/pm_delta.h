@@ -122,7 +122,9 @@ int pm_delta_set_path(int path);
 
 /*
  * Column-tile width (d_v columns per workgroup) the chunked kernel uses:
- * 0 = automatic, else 16, 32 or 64.  Returns the previous value.
+ * 0 = automatic (32 when B*H*(D/32) >= 256, else 16), else 16, 32 or 64;
+ * 64 is accepted and served with 32-column workgroups (a 64-column
+ * workgroup would leave no producer waves).  Returns the previous value.
  */
 int pm_delta_set_tile(int dv_tile);
 

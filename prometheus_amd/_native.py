@@ -103,7 +103,7 @@ def set_path(path: int) -> int:
 
 
 def set_tile(dv_tile: int) -> int:
-    """Chunked kernel d_v tile width (0 auto, 16, 32, 64); returns old value."""
+    """Chunked kernel d_v tile width (0 auto, 16, 32; 64 runs as 32); returns old value."""
     old = lib().pm_delta_set_tile(int(dv_tile))
     if old < 0:
         check(old)

@@ -15,14 +15,20 @@
 //
 // Work split.  The recurrence is separable along d_v.  A 256-thread
 // workgroup owns (sequence, head, d_v tile of DV columns) and walks the
-// sequence's chunks in order, as a three-stage software pipeline:
+// sequence's chunks in order, as a three-stage software pipeline with one
+// LDS barrier per chunk:
 //   * DV/16 "chain" waves own 16 columns of S each (fp32 MFMA
-//     accumulators) and run chunk c: K S, Q S, R, U = T R, O = Q S + P U,
-//     S += K^T U;
-//   * "producer" waves build chunk c+1's T (producer 0) and P (producer 1)
-//     in registers and stage chunk c+2 from HBM into LDS.
-// Two LDS-only barriers per chunk; only producers touch global loads, so
-// no barrier waits on memory traffic.  The workgroups of one (sequence,
+//     accumulators) and run chunk c-1: K S, Q S, R, U = T R,
+//     O = Q S + P U, S += K^T U;
+//   * producer 0 builds chunk c's T and producer 1 chunk c's P, in
+//     registers, into LDS in MFMA operand order;
+//   * the last producer also issues chunk c+1's HBM -> LDS copies
+//     (buffer_load ... lds: no registers, no LDS write instructions).
+// K, Q, V and beta stay in LDS exactly as in HBM (token rows), in three
+// rotating buffers; the K^T and V operands the chain needs come from the
+// same token rows through the gfx950 LDS transpose read
+// (ds_read_b64_tr_b16).  Rows past the end of a sequence are read as
+// zeros by the buffer range check.  The workgroups of one (sequence,
 // head) share bid % 8, i.e. one XCD and its L2 (blocks go round-robin
 // over the 8 XCDs), so their common Q/K reads are served by that L2.
 //
@@ -57,8 +63,11 @@ typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kC = 64;  // chunk length (tokens)
+// Buffer descriptor word 3 for raw (untyped, unswizzled) gfx9 buffer access.
+constexpr int kRsrcWord3 = 0x00020000;
 
 __device__ __forceinline__ f32x4_t mfma32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -68,9 +77,6 @@ __device__ __forceinline__ f32x4_t mfma16(u32x2_t a, u32x2_t b, f32x4_t c) {
                                                      __builtin_bit_cast(bf16x4_t, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint16_t bf16_bits(float x) {
-    return __builtin_bit_cast(uint16_t, (__bf16)x);
-}
 // bf16 operands are assembled from 16-bit patterns packed into 32-bit
 // words and bit-cast to the MFMA vector type only at the call: element
 // access on bf16 vectors (extract or insert) is avoided on purpose, since
@@ -94,35 +100,67 @@ __device__ __forceinline__ bf16x8_t acc_to_b(f32x4_t lo, f32x4_t hi) {
     const u32x4_t r = {pack2(lo.x, lo.y), pack2(lo.z, lo.w), pack2(hi.x, hi.y), pack2(hi.z, hi.w)};
     return __builtin_bit_cast(bf16x8_t, r);
 }
+__device__ __forceinline__ f32x4_t widen4(u32x2_t v) {
+    const f32x4_t r = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
+    return r;
+}
 
-// LDS swizzles (bank-conflict-free 8-byte accesses).  Rows are stored in
-// 8-byte blocks of 4 bf16; the physical block is the logical block XORed
-// with a per-row value:
-//   K/Q rows (token-major):      block ^ ((row >> 3) & 1)   -- rows r and r+8
-//                                land on different banks; a 16-byte chunk keeps
-//                                its place with its two halves swapped;
-//   K^T / V^T rows (d/e-major):  block ^ ((row >> 3) & 15)  -- the staging
-//                                writes of 16 lanes (16 different rows 8
-//                                apart, one token block) hit 16 different banks.
-__device__ __forceinline__ int swz_kq(int row) { return (row >> 3) & 1; }
-__device__ __forceinline__ int swz_t(int row) { return (row >> 3) & 15; }
+// LDS layout of a token-major tile (K or Q: D bf16 per row, V: DV per row).
+// Rows have no padding; the 16-byte chunk c of row r is stored at chunk
+// c ^ f(r).  With 64 banks served 32 lanes at a time, f makes every access
+// pattern below conflict-free: the A-operand reads (16 rows, two 8-byte
+// blocks of one chunk), the transpose reads (8 rows, two chunks) and the
+// copies (1 KiB contiguous per instruction).
+template <int D>
+__device__ __forceinline__ int kq_f(int r) {
+    if constexpr (D == 128) return 2 * (r & 7) + ((r >> 3) & 1);  // 16 chunks, rows share banks
+    else return 2 * ((r >> 1) & 3) + ((r >> 3) & 1);              // 8 chunks, odd rows offset
+}
+template <int DV>
+__device__ __forceinline__ int v_f(int r) {
+    if constexpr (DV == 32) return 2 * ((r >> 2) & 1);  // rows r and r+4 share banks
+    else return 0;                                       // 8 rows of 32 bytes cover all banks
+}
 
-// A operand of a 16x16x32 product from a swizzled bf16 LDS matrix:
-// row `row`, contraction block starting at k0 (multiple of 32), lane group g.
-__device__ __forceinline__ bf16x8_t lds_a_sw(const uint16_t* m, int pitch, int row, int k0, int g,
-                                             int sw) {
-    const uint16_t* r = m + row * pitch;
-    const int b = (k0 >> 2) + g;
-    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(r + 4 * (b ^ sw));
-    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(r + 4 * ((b + 4) ^ sw));
+// A operand of a 16x16x32 product from a swizzled K/Q tile: row `row`,
+// contraction block starting at k0 (multiple of 32), lane group g.
+template <int D>
+__device__ __forceinline__ bf16x8_t lds_a_kq(const uint16_t* m, int row, int k0, int g) {
+    const uint16_t* r = m + row * D;
+    const int f = kq_f<D>(row);
+    const int b = (k0 >> 2) + g;  // 8-byte block: chunk b >> 1, half b & 1
+    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(r + 8 * ((b >> 1) ^ f) + 4 * (b & 1));
+    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(r + 8 * (((b >> 1) + 2) ^ f) + 4 * (b & 1));
     const u32x4_t v = {lo.x, lo.y, hi.x, hi.y};
     return __builtin_bit_cast(bf16x8_t, v);
 }
-__device__ __forceinline__ bf16x8_t lds_a_kq(const uint16_t* m, int pitch, int row, int k0, int g) {
-    return lds_a_sw(m, pitch, row, k0, g, swz_kq(row));
+
+// ds_read_b64_tr_b16: within each 16-lane group, the four 4-element rows
+// addressed by lanes 4j..4j+3 (16 consecutive elements of row j) are
+// transposed: lane i receives element i of rows 0..3.
+__device__ __forceinline__ u32x2_t lds_tr16(const uint16_t* p) {
+    typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+    const i16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
+    return __builtin_bit_cast(u32x2_t, r);
 }
-__device__ __forceinline__ bf16x8_t lds_a_t(const uint16_t* m, int pitch, int row, int k0, int g) {
-    return lds_a_sw(m, pitch, row, k0, g, swz_t(row));
+// A operand of K^T (rows d = 16 md + l16, contraction over tokens
+// k0 + {4g..4g+3, 16+4g..16+4g+3}) read from the token-major K tile.
+template <int D>
+__device__ __forceinline__ bf16x8_t lds_kt(const uint16_t* Ks, int md, int k0, int lane) {
+    const int g = lane >> 4, j = (lane >> 2) & 3, cc = lane & 3;
+    const int t = k0 + 4 * g + j;  // kq_f(t + 16) == kq_f(t)
+    const uint16_t* p = Ks + t * D + 8 * ((2 * md + (cc >> 1)) ^ kq_f<D>(t)) + 4 * (cc & 1);
+    const u32x2_t lo = lds_tr16(p), hi = lds_tr16(p + 16 * D);
+    const u32x4_t v = {lo.x, lo.y, hi.x, hi.y};
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+// V in accumulator layout: lane (g, l16) gets V[16m + 4g + i][16w + l16], i < 4.
+template <int DV>
+__device__ __forceinline__ f32x4_t lds_v_acc(const uint16_t* Vs, int m, int w, int lane) {
+    const int g = lane >> 4, j = (lane >> 2) & 3, cc = lane & 3;
+    const int t = 16 * m + 4 * g + j;
+    return widen4(lds_tr16(Vs + t * DV + 8 * ((2 * w + (cc >> 1)) ^ v_f<DV>(t)) + 4 * (cc & 1)));
 }
 
 // Packed operand layout of the 64x64 lower-triangular T and P: operand
@@ -148,13 +186,15 @@ __device__ __forceinline__ void zero_upper_half(uint16_t* buf, int q, int lane) 
     *reinterpret_cast<u32x2_t*>(buf + q * 512 + lane * 8 + 4) = z;
 }
 
-// Element j of four 8-element rows r[0..3], packed as 4 consecutive bf16
-// (a column of a 4x8 block), with v_perm_b32 selecting 16-bit halves.
-__device__ __forceinline__ u32x2_t column4(const u32x4_t* r, int j) {
-    const unsigned sel = (j & 1) ? 0x07060302u : 0x05040100u;
-    const u32x2_t out = {__builtin_amdgcn_perm(r[1][j >> 1], r[0][j >> 1], sel),
-                         __builtin_amdgcn_perm(r[3][j >> 1], r[2][j >> 1], sel)};
-    return out;
+// Asynchronous copy of 16 (or 4) bytes per lane from a buffer to LDS:
+// lane L's bytes land at dst + L * size (dst wave-uniform).
+__device__ __forceinline__ void copy_to_lds(__amdgpu_buffer_rsrc_t rsrc, void* dst, int size,
+                                            unsigned voffset) {
+    typedef __attribute__((address_space(3))) void lds_void_t;
+    if (size == 16)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(dst), 16, voffset, 0, 0, 0);
+    else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(dst), 4, voffset, 0, 0, 0);
 }
 
 // LDS-only workgroup barrier: waits for this wave's LDS traffic, never for
@@ -162,32 +202,29 @@ __device__ __forceinline__ u32x2_t column4(const u32x4_t* r, int j) {
 __device__ __forceinline__ void lds_barrier() {
     __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
+// Wait for this wave's outstanding buffer loads (and so its LDS copies).
+__device__ __forceinline__ void wait_copies() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 template <int D, int DV>
 struct Geo {
-    static constexpr int NCW = DV / 16;   // chain waves
-    static constexpr int NPW = 4 - NCW;   // producer waves
-    static constexpr int PK = D + 8;      // Ks/Qs pitch (bf16)
-    static constexpr int PT = kC + 8;     // Kt/Vt pitch (bf16)
-    static constexpr int DG = D / 8;      // 16-byte groups per token row
-    static constexpr int VG = DV / 8;     // 16-byte groups per V tile row
-    static constexpr int NU = 16 * DG;    // K/Q staging units (4 tokens x 8 d)
-    static constexpr int NVU = 16 * VG;   // V staging units (4 tokens x 8 columns)
-    static constexpr int UPL = (NU + NPW * 64 - 1) / (NPW * 64);   // units per producer lane
-    static constexpr int VPL = (NVU + NPW * 64 - 1) / (NPW * 64);
-    // one RAW buffer: Ks, Qs, Kt, Vt (bf16), Bs (fp32)
+    static constexpr int NCW = DV / 16;        // chain waves
+    static constexpr int NPW = 4 - NCW;        // producer waves
+    static constexpr int LOADER = NPW - 1;     // producer that issues the HBM -> LDS copies
+    static constexpr int NI_KQ = kC * D * 2 / 1024;   // 1 KiB copy instructions per K or Q tile
+    static constexpr int NI_V = kC * DV * 2 / 1024;   // ... per V tile
+    // one RAW buffer: Ks, Qs, Vs (bf16 token rows, swizzled), Bs (fp32)
     static constexpr int R_KS = 0;
-    static constexpr int R_QS = R_KS + kC * PK * 2;
-    static constexpr int R_KT = R_QS + kC * PK * 2;
-    static constexpr int R_VT = R_KT + D * PT * 2;
-    static constexpr int R_BS = R_VT + DV * PT * 2;
+    static constexpr int R_QS = R_KS + kC * D * 2;
+    static constexpr int R_VS = R_QS + kC * D * 2;
+    static constexpr int R_BS = R_VS + kC * DV * 2;
     static constexpr int RAW = R_BS + kC * 4;
+    static constexpr int NRAW = 3;
     // one TP buffer: T and P, 6 operand blocks of 1 KiB each
     static constexpr int TP = 2 * 6 * 1024;
-    static constexpr int BYTES = 2 * RAW + 2 * TP;
-    static_assert(D % 32 == 0 && D <= 128, "D");
+    static constexpr int BYTES = NRAW * RAW + 2 * TP;
+    static_assert(D == 64 || D == 128, "D");
     static_assert(DV == 16 || DV == 32, "DV");
-    static_assert(RAW % 16 == 0, "RAW alignment");
+    static_assert(NI_V >= 1 && RAW % 16 == 0, "RAW layout");
     static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
@@ -226,94 +263,50 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
     const int l16 = lane & 15, lg = lane >> 4;
     const bool chain = w < G::NCW;
     const int pw = w - G::NCW;  // producer index (valid when !chain)
-    const int plane = pw * 64 + lane;
     const size_t sbase = static_cast<size_t>(pair) * D * D;
     const size_t tstride = static_cast<size_t>(H) * D;  // elements between tokens
 
-    auto raw = [&](int c) { return smem + (c & 1) * G::RAW; };
-    auto tpb = [&](int c) { return reinterpret_cast<uint16_t*>(smem + 2 * G::RAW + (c & 1) * G::TP); };
+    auto raw = [&](int c) { return smem + (c % G::NRAW) * G::RAW; };
+    auto tpb = [&](int c) {
+        return reinterpret_cast<uint16_t*>(smem + G::NRAW * G::RAW + (c & 1) * G::TP);
+    };
 
-    // ---------------- producer state: staged chunk in registers ----------------
-    u32x4_t kr[G::UPL][4], qr[G::UPL][4], vr[G::VPL][4];
-    float br = 0.f;
-    auto stage_load = [&](int c) {
+    // ---------------- loader: chunk c's K, Q, V tile and beta, HBM -> LDS ----------------
+    // Copy instruction i, lane L fills LDS bytes [1024 i + 16 L, +16) of the tile: row r,
+    // stored chunk p, i.e. logical chunk p ^ f(r) of token row r.
+    auto issue_copies = [&](int c) {
         const int base = c * kC;
         const int clen = min(kC, len - base);
-        const u32x4_t z = {0u, 0u, 0u, 0u};
+        const size_t row0 = static_cast<size_t>(tok0 + base) * tstride + static_cast<size_t>(h) * D;
+        // bytes up to the end of the last valid token's row: later rows read as zeros
+        const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
+        const unsigned n_v = static_cast<unsigned>(((clen - 1) * tstride + DV) * 2);
+        const unsigned n_b = static_cast<unsigned>(((clen - 1) * H + 1) * 4);
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(k + row0), 0, n_kq, kRsrcWord3);
+        const __amdgpu_buffer_rsrc_t rq =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(q + row0), 0, n_kq, kRsrcWord3);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(v + row0 + col0), 0, n_v, kRsrcWord3);
+        const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(beta + (tok0 + base) * H + h), 0, n_b, kRsrcWord3);
+        unsigned char* rbuf = raw(c);
 #pragma unroll
-        for (int u = 0; u < G::UPL; ++u) {
-            const int unit = plane + u * G::NPW * 64;
-            const int dg = unit % G::DG, tg = unit / G::DG;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 4 * tg + i;
-                kr[u][i] = z;
-                qr[u][i] = z;
-                if (unit < G::NU && t < clen) {
-                    const size_t a = (tok0 + base + t) * tstride + static_cast<size_t>(h) * D + dg * 8;
-                    kr[u][i] = *reinterpret_cast<const u32x4_t*>(k + a);
-                    qr[u][i] = *reinterpret_cast<const u32x4_t*>(q + a);
-                }
-            }
+        for (int i = 0; i < G::NI_KQ; ++i) {
+            const int pos = 512 * i + 8 * lane;  // element position in the tile
+            const int r = pos / D, p = (pos % D) / 8;
+            const unsigned vo = static_cast<unsigned>(r * tstride * 2) + 16u * (p ^ kq_f<D>(r));
+            copy_to_lds(rk, rbuf + G::R_KS + 1024 * i, 16, vo);
+            copy_to_lds(rq, rbuf + G::R_QS + 1024 * i, 16, vo);
         }
 #pragma unroll
-        for (int u = 0; u < G::VPL; ++u) {
-            const int unit = plane + u * G::NPW * 64;
-            const int tg = unit % 16, cv = unit / 16;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 4 * tg + i;
-                vr[u][i] = z;
-                if (unit < G::NVU && t < clen) {
-                    const size_t a =
-                        (tok0 + base + t) * tstride + static_cast<size_t>(h) * D + col0 + cv * 8;
-                    vr[u][i] = *reinterpret_cast<const u32x4_t*>(v + a);
-                }
-            }
+        for (int i = 0; i < G::NI_V; ++i) {
+            const int pos = 512 * i + 8 * lane;
+            const int r = pos / DV, p = (pos % DV) / 8;
+            const unsigned vo = static_cast<unsigned>(r * tstride * 2) + 16u * (p ^ v_f<DV>(r));
+            copy_to_lds(rv, rbuf + G::R_VS + 1024 * i, 16, vo);
         }
-        br = (plane < clen) ? beta[(tok0 + base + plane) * H + h] : 0.f;
-    };
-    auto stage_store = [&](int c) {
-        unsigned char* rb = raw(c);
-        uint16_t* Ks = reinterpret_cast<uint16_t*>(rb + G::R_KS);
-        uint16_t* Qs = reinterpret_cast<uint16_t*>(rb + G::R_QS);
-        uint16_t* Kt = reinterpret_cast<uint16_t*>(rb + G::R_KT);
-        uint16_t* Vt = reinterpret_cast<uint16_t*>(rb + G::R_VT);
-        float* Bs = reinterpret_cast<float*>(rb + G::R_BS);
-#pragma unroll
-        for (int u = 0; u < G::UPL; ++u) {
-            const int unit = plane + u * G::NPW * 64;
-            if (unit < G::NU) {
-                const int dg = unit % G::DG, tg = unit / G::DG;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = 4 * tg + i;
-                    const bool swap = swz_kq(r) != 0;  // 16-byte chunk with its halves swapped
-                    const u32x4_t kv = swap ? u32x4_t{kr[u][i].z, kr[u][i].w, kr[u][i].x, kr[u][i].y} : kr[u][i];
-                    const u32x4_t qv = swap ? u32x4_t{qr[u][i].z, qr[u][i].w, qr[u][i].x, qr[u][i].y} : qr[u][i];
-                    *reinterpret_cast<u32x4_t*>(Ks + r * G::PK + dg * 8) = kv;
-                    *reinterpret_cast<u32x4_t*>(Qs + r * G::PK + dg * 8) = qv;
-                }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int d = dg * 8 + j;
-                    *reinterpret_cast<u32x2_t*>(Kt + d * G::PT + 4 * (tg ^ swz_t(d))) = column4(kr[u], j);
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < G::VPL; ++u) {
-            const int unit = plane + u * G::NPW * 64;
-            if (unit < G::NVU) {
-                const int tg = unit % 16, cv = unit / 16;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int e = cv * 8 + j;
-                    *reinterpret_cast<u32x2_t*>(Vt + e * G::PT + 4 * (tg ^ swz_t(e))) = column4(vr[u], j);
-                }
-            }
-        }
-        if (plane < kC) Bs[plane] = br;
+        copy_to_lds(rb, rbuf + G::R_BS, 4, static_cast<unsigned>(lane * H * 4));
     };
 
     // ---------------- producer 0: T = (I + A)^-1 in packed operand order ----------------
@@ -333,7 +326,7 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
         for (int kb = 0; kb < D / 32; ++kb) {
             bf16x8_t f[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) f[r] = lds_a_kq(Ks, G::PK, 16 * r + l16, 32 * kb, lg);
+            for (int r = 0; r < 4; ++r) f[r] = lds_a_kq<D>(Ks, 16 * r + l16, 32 * kb, lg);
 #pragma unroll
             for (int b = 0; b < 4; ++b) gd[b] = mfma32(f[b], f[b], gd[b]);
             gu[0] = mfma32(f[0], f[1], gu[0]);  // (0,1)
@@ -470,8 +463,8 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
             bf16x8_t fk[4], fq[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                fk[r] = lds_a_kq(Ks, G::PK, 16 * r + l16, 32 * kb, lg);
-                fq[r] = lds_a_kq(Qs, G::PK, 16 * r + l16, 32 * kb, lg);
+                fk[r] = lds_a_kq<D>(Ks, 16 * r + l16, 32 * kb, lg);
+                fq[r] = lds_a_kq<D>(Qs, 16 * r + l16, 32 * kb, lg);
             }
             // accumulator of (P_ij)^T = K_j Q_i^T: lane holds P[16i+l16][16j+4g+r]
             int x = 0;
@@ -515,8 +508,7 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
         unsigned char* rb = raw(c);
         const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + G::R_KS);
         const uint16_t* Qs = reinterpret_cast<const uint16_t*>(rb + G::R_QS);
-        const uint16_t* Kt = reinterpret_cast<const uint16_t*>(rb + G::R_KT);
-        const uint16_t* Vt = reinterpret_cast<const uint16_t*>(rb + G::R_VT);
+        const uint16_t* Vs = reinterpret_cast<const uint16_t*>(rb + G::R_VS);
         const float* Bs = reinterpret_cast<const float*>(rb + G::R_BS);
         const uint16_t* Tp = tpb(c);
         const uint16_t* Pp = Tp + 6 * 512;
@@ -535,8 +527,8 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
             bf16x8_t fk[4], fq[4];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                fk[m] = lds_a_kq(Ks, G::PK, 16 * m + l16, 32 * kb, lg);
-                fq[m] = lds_a_kq(Qs, G::PK, 16 * m + l16, 32 * kb, lg);
+                fk[m] = lds_a_kq<D>(Ks, 16 * m + l16, 32 * kb, lg);
+                fq[m] = lds_a_kq<D>(Qs, 16 * m + l16, 32 * kb, lg);
             }
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
@@ -545,16 +537,11 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
             }
         }
         // R = beta (V - X)
-        const int lc = 16 * w + l16;
         f32x4_t R[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            const u32x2_t vv =
-                *reinterpret_cast<const u32x2_t*>(Vt + lc * G::PT + 4 * ((4 * m + lg) ^ swz_t(lc)));
             const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + 16 * m + 4 * lg);
-            const f32x4_t vf = {bf16_to_f32(vv.x & 0xffffu), bf16_to_f32(vv.x >> 16),
-                                bf16_to_f32(vv.y & 0xffffu), bf16_to_f32(vv.y >> 16)};
-            R[m] = bs * (vf - X[m]);
+            R[m] = bs * (lds_v_acc<DV>(Vs, m, w, lane) - X[m]);
         }
         const bf16x8_t Rb0 = acc_to_b(R[0], R[1]), Rb1 = acc_to_b(R[2], R[3]);
         // U = T R
@@ -564,14 +551,14 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
         U[2] = mfma32(packed_a(Tp, 3, lane), Rb1, mfma32(packed_a(Tp, 2, lane), Rb0, zero));
         U[3] = mfma32(packed_a(Tp, 5, lane), Rb1, mfma32(packed_a(Tp, 4, lane), Rb0, zero));
         const bf16x8_t Ub0 = acc_to_b(U[0], U[1]), Ub1 = acc_to_b(U[2], U[3]);
-        // S += K^T U
+        // S += K^T U (K^T operands by transpose reads of the token rows)
 #pragma unroll
         for (int h4 = 0; h4 < D / 64; ++h4) {
             bf16x8_t f0[4], f1[4];
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
-                f0[x] = lds_a_t(Kt, G::PT, 16 * (4 * h4 + x) + l16, 0, lg);
-                f1[x] = lds_a_t(Kt, G::PT, 16 * (4 * h4 + x) + l16, 32, lg);
+                f0[x] = lds_kt<D>(Ks, 4 * h4 + x, 0, lane);
+                f1[x] = lds_kt<D>(Ks, 4 * h4 + x, 32, lane);
             }
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
@@ -604,41 +591,36 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
         }
     };
 
-    // ---------------- pipeline: chain(c) || prep(c+1), staging c+2 ----------------
-    // Each role runs its own loop (so registers are allocated per role) with
-    // the same sequence of barriers: one after the prologue, two per chunk.
+    // ---------------- pipeline: one barrier per chunk ----------------
+    // Between barriers i and i+1: the loader copies chunk i+1 into RAW[(i+1)%3],
+    // the producers build chunk i's T and P from RAW[i%3] into TP[i%2], and the
+    // chain runs chunk i-1 from RAW[(i-1)%3] and TP[(i-1)%2].  Barrier i+1
+    // publishes all three, and frees RAW[(i-1)%3] and TP[(i-1)%2] for reuse.
+    // Every role passes the same n_chunks + 1 barriers.
     if (n_chunks > 0) {
         if (chain) {
-            lds_barrier();
+            lds_barrier();  // chunk 0 copied
+            lds_barrier();  // chunk 0's T and P built
             for (int c = 0; c < n_chunks; ++c) {
-                lds_barrier();  // T/P of chunk c ready; chunk c-1 no longer read
-                lds_barrier();  // chunk c+1 staged
                 run_chunk(c);
+                if (c + 1 < n_chunks) lds_barrier();
             }
         } else {
-            stage_load(0);
-            stage_store(0);
-            if (n_chunks > 1) stage_load(1);
-            lds_barrier();
-            if (pw == 0) {
-                build_t(0);
-            } else if (pw == 1) {
-                build_p(0);
+            const bool loader = pw == G::LOADER;
+            if (loader) {
+                issue_copies(0);
+                wait_copies();
             }
+            lds_barrier();
             for (int c = 0; c < n_chunks; ++c) {
-                lds_barrier();
-                if (c + 1 < n_chunks) {
-                    stage_store(c + 1);
-                    if (c + 2 < n_chunks) stage_load(c + 2);
+                if (loader && c + 1 < n_chunks) issue_copies(c + 1);
+                if (pw == 0) {
+                    build_t(c);
+                } else if (pw == 1) {
+                    build_p(c);
                 }
+                if (loader) wait_copies();
                 lds_barrier();
-                if (c + 1 < n_chunks) {
-                    if (pw == 0) {
-                        build_t(c + 1);
-                    } else if (pw == 1) {
-                        build_p(c + 1);
-                    }
-                }
             }
         }
     }
@@ -659,12 +641,16 @@ template <int D, int DV, bool OB>
 hipError_t launch_t(const ChunkedArgs& a, hipStream_t st) {
     using G = Geo<D, DV>;
     auto kern = delta_chunked_kernel<D, DV, OB>;
-    static bool attr_set = false;  // per instantiation
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, G::BYTES);
+    // the dynamic-LDS limit is a per-device function attribute
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    static bool attr_set[64] = {};
+    if (dev < 0 || dev >= 64 || !attr_set[dev]) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, G::BYTES);
         if (e != hipSuccess) return e;
-        attr_set = true;
+        if (dev >= 0 && dev < 64) attr_set[dev] = true;
     }
     const int n_pairs = a.n_seq * a.H;
     const int n_tiles = D / DV;
@@ -689,15 +675,18 @@ int pick_tile(int D, long n_pairs, int requested) {
 
 }  // namespace
 
-bool chunked_supported(int D) { return D == 64 || D == 128; }
+// 32-bit buffer offsets: a chunk spans 64 token rows of H*D elements.
+bool chunked_supported(int D, int H) {
+    return (D == 64 || D == 128) && H >= 1 && static_cast<long>(H) * D <= (1L << 24);
+}
 
 hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st) {
     const long n_pairs = static_cast<long>(a.n_seq) * a.H;
     if (n_pairs == 0) return hipSuccess;
+    if (!chunked_supported(a.D, a.H)) return hipErrorInvalidValue;
     const int dv = pick_tile(a.D, n_pairs, a.dv_tile);
     if (a.D == 128) return dv == 16 ? launch_dv<128, 16>(a, st) : launch_dv<128, 32>(a, st);
-    if (a.D == 64) return dv == 16 ? launch_dv<64, 16>(a, st) : launch_dv<64, 32>(a, st);
-    return hipErrorInvalidValue;
+    return dv == 16 ? launch_dv<64, 16>(a, st) : launch_dv<64, 32>(a, st);
 }
 
 }  // namespace pm

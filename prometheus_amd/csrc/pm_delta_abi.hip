@@ -109,7 +109,7 @@ int forward(const void* q, const void* k, const void* v, const float* beta, cons
     const int path = g_path.load();
     const bool in_bf16 = in_dtype == PM_DTYPE_BF16;
     const bool want_chunked = path != 1;
-    const bool can_chunked = in_bf16 && pm::chunked_supported(D) && aligned(q, 16) &&
+    const bool can_chunked = in_bf16 && pm::chunked_supported(D, H) && aligned(q, 16) &&
                              aligned(k, 16) && aligned(v, 16) &&
                              (out_dtype == PM_DTYPE_F32 ? aligned(o, 16) : aligned(o, 8));
     if (path == 2 && !can_chunked)

@@ -54,7 +54,7 @@ struct ChunkedArgs {
     bool out_bf16;
     int dv_tile;  // 0 = automatic
 };
-bool chunked_supported(int D);
+bool chunked_supported(int D, int H);  // D in {64, 128}, H*D <= 2^24
 hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st);
 
 // Zero fill (used instead of hipMemsetAsync so callers may graph-capture).

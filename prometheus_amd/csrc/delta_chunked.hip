@@ -139,28 +139,52 @@ __device__ __forceinline__ bf16x8_t lds_a_kq(const uint16_t* m, int row, int k0,
 // ds_read_b64_tr_b16: within each 16-lane group, the four 4-element rows
 // addressed by lanes 4j..4j+3 (16 consecutive elements of row j) are
 // transposed: lane i receives element i of rows 0..3.
-__device__ __forceinline__ u32x2_t lds_tr16(const uint16_t* p) {
-    typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
-    const i16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
-    return __builtin_bit_cast(u32x2_t, r);
+//
+// Issued as inline asm: the compiler's intrinsic for it carries no LDS
+// memory operand, so hipcc (ROCm 7.2) puts a vmcnt(0) wait -- for every
+// pending global store -- in front of it.  The asm form is asynchronous:
+// results are valid only after lds_wait() takes them as operands.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    typedef __attribute__((address_space(3))) const void lds_cvoid_t;
+    return static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_cvoid_t*)(p)));
+}
+template <int OFFSET>
+__device__ __forceinline__ u32x2_t lds_tr16_issue(unsigned addr) {
+    u32x2_t r;
+    __asm__ volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFFSET) : "memory");
+    return r;
+}
+// Wait for all of this wave's LDS reads; x's registers are tied to the wait
+// so that no use of them is scheduled before it.
+__device__ __forceinline__ void lds_wait(u32x2_t& a, u32x2_t& b, u32x2_t& c, u32x2_t& d) {
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : : "memory");
+}
+__device__ __forceinline__ void lds_wait(u32x4_t& a, u32x4_t& b, u32x4_t& c, u32x4_t& d, u32x4_t& e,
+                                         u32x4_t& f, u32x4_t& g, u32x4_t& h) {
+    __asm__ volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f), "+v"(g), "+v"(h)
+                     :
+                     : "memory");
 }
 // A operand of K^T (rows d = 16 md + l16, contraction over tokens
-// k0 + {4g..4g+3, 16+4g..16+4g+3}) read from the token-major K tile.
-template <int D>
-__device__ __forceinline__ bf16x8_t lds_kt(const uint16_t* Ks, int md, int k0, int lane) {
+// k0 + {4g..4g+3, 16+4g..16+4g+3}) from the token-major K tile: two
+// transpose reads, 16 rows apart (kq_f(t + 16) == kq_f(t)).
+template <int D, int K0>
+__device__ __forceinline__ u32x4_t lds_kt_issue(const uint16_t* Ks, int md, int lane) {
     const int g = lane >> 4, j = (lane >> 2) & 3, cc = lane & 3;
-    const int t = k0 + 4 * g + j;  // kq_f(t + 16) == kq_f(t)
-    const uint16_t* p = Ks + t * D + 8 * ((2 * md + (cc >> 1)) ^ kq_f<D>(t)) + 4 * (cc & 1);
-    const u32x2_t lo = lds_tr16(p), hi = lds_tr16(p + 16 * D);
+    const int t = K0 + 4 * g + j;
+    const unsigned a = lds_addr(Ks + t * D + 8 * ((2 * md + (cc >> 1)) ^ kq_f<D>(t)) + 4 * (cc & 1));
+    const u32x2_t lo = lds_tr16_issue<0>(a), hi = lds_tr16_issue<16 * D * 2>(a);
     const u32x4_t v = {lo.x, lo.y, hi.x, hi.y};
-    return __builtin_bit_cast(bf16x8_t, v);
+    return v;
 }
-// V in accumulator layout: lane (g, l16) gets V[16m + 4g + i][16w + l16], i < 4.
+// V in accumulator layout: lane (g, l16) gets V[16m + 4g + i][16w + l16], i < 4
+// (bf16 pairs; widen4 after lds_wait).
 template <int DV>
-__device__ __forceinline__ f32x4_t lds_v_acc(const uint16_t* Vs, int m, int w, int lane) {
+__device__ __forceinline__ u32x2_t lds_v_issue(const uint16_t* Vs, int m, int w, int lane) {
     const int g = lane >> 4, j = (lane >> 2) & 3, cc = lane & 3;
     const int t = 16 * m + 4 * g + j;
-    return widen4(lds_tr16(Vs + t * DV + 8 * ((2 * w + (cc >> 1)) ^ v_f<DV>(t)) + 4 * (cc & 1)));
+    return lds_tr16_issue<0>(lds_addr(Vs + t * DV + 8 * ((2 * w + (cc >> 1)) ^ v_f<DV>(t)) + 4 * (cc & 1)));
 }
 
 // Packed operand layout of the 64x64 lower-triangular T and P: operand
@@ -184,6 +208,21 @@ __device__ __forceinline__ void store_packed_t(uint16_t* buf, int i, int j, f32x
 __device__ __forceinline__ void zero_upper_half(uint16_t* buf, int q, int lane) {
     const u32x2_t z = {0u, 0u};
     *reinterpret_cast<u32x2_t*>(buf + q * 512 + lane * 8 + 4) = z;
+}
+
+// Wave-uniform values made visibly uniform (SGPRs), so that buffer
+// descriptors and role branches are scalar rather than per-lane.
+__device__ __forceinline__ unsigned uniform(unsigned x) { return __builtin_amdgcn_readfirstlane(x); }
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+    const unsigned long long u = reinterpret_cast<unsigned long long>(p);
+    const unsigned long long lo = uniform(static_cast<unsigned>(u));
+    const unsigned long long hi = uniform(static_cast<unsigned>(u >> 32));
+    return reinterpret_cast<T*>((hi << 32) | lo);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(const_cast<void*>(base)), 0, uniform(bytes),
+                                             kRsrcWord3);
 }
 
 // Asynchronous copy of 16 (or 4) bytes per lane from a buffer to LDS:
@@ -259,7 +298,8 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
     const int n_chunks = (len + kC - 1) / kC;
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6;
+    const int lane = tid & 63;
+    const int w = static_cast<int>(uniform(static_cast<unsigned>(tid >> 6)));  // wave index
     const int l16 = lane & 15, lg = lane >> 4;
     const bool chain = w < G::NCW;
     const int pw = w - G::NCW;  // producer index (valid when !chain)
@@ -282,15 +322,11 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
         const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
         const unsigned n_v = static_cast<unsigned>(((clen - 1) * tstride + DV) * 2);
         const unsigned n_b = static_cast<unsigned>(((clen - 1) * H + 1) * 4);
-        const __amdgpu_buffer_rsrc_t rk =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(k + row0), 0, n_kq, kRsrcWord3);
-        const __amdgpu_buffer_rsrc_t rq =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(q + row0), 0, n_kq, kRsrcWord3);
-        const __amdgpu_buffer_rsrc_t rv =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(v + row0 + col0), 0, n_v, kRsrcWord3);
-        const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(beta + (tok0 + base) * H + h), 0, n_b, kRsrcWord3);
-        unsigned char* rbuf = raw(c);
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(k + row0, n_kq);
+        const __amdgpu_buffer_rsrc_t rq = make_rsrc(q + row0, n_kq);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(v + row0 + col0, n_v);
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(beta + (tok0 + base) * H + h, n_b);
+        unsigned char* rbuf = uniform_ptr(raw(c));
 #pragma unroll
         for (int i = 0; i < G::NI_KQ; ++i) {
             const int pos = 512 * i + 8 * lane;  // element position in the tile
@@ -537,11 +573,15 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
             }
         }
         // R = beta (V - X)
+        u32x2_t vv0 = lds_v_issue<DV>(Vs, 0, w, lane), vv1 = lds_v_issue<DV>(Vs, 1, w, lane);
+        u32x2_t vv2 = lds_v_issue<DV>(Vs, 2, w, lane), vv3 = lds_v_issue<DV>(Vs, 3, w, lane);
+        lds_wait(vv0, vv1, vv2, vv3);
+        const u32x2_t vv[4] = {vv0, vv1, vv2, vv3};
         f32x4_t R[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + 16 * m + 4 * lg);
-            R[m] = bs * (lds_v_acc<DV>(Vs, m, w, lane) - X[m]);
+            R[m] = bs * (widen4(vv[m]) - X[m]);
         }
         const bf16x8_t Rb0 = acc_to_b(R[0], R[1]), Rb1 = acc_to_b(R[2], R[3]);
         // U = T R
@@ -554,16 +594,16 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
         // S += K^T U (K^T operands by transpose reads of the token rows)
 #pragma unroll
         for (int h4 = 0; h4 < D / 64; ++h4) {
-            bf16x8_t f0[4], f1[4];
+            u32x4_t a0 = lds_kt_issue<D, 0>(Ks, 4 * h4 + 0, lane), b0 = lds_kt_issue<D, 32>(Ks, 4 * h4 + 0, lane);
+            u32x4_t a1 = lds_kt_issue<D, 0>(Ks, 4 * h4 + 1, lane), b1 = lds_kt_issue<D, 32>(Ks, 4 * h4 + 1, lane);
+            u32x4_t a2 = lds_kt_issue<D, 0>(Ks, 4 * h4 + 2, lane), b2 = lds_kt_issue<D, 32>(Ks, 4 * h4 + 2, lane);
+            u32x4_t a3 = lds_kt_issue<D, 0>(Ks, 4 * h4 + 3, lane), b3 = lds_kt_issue<D, 32>(Ks, 4 * h4 + 3, lane);
+            lds_wait(a0, b0, a1, b1, a2, b2, a3, b3);
+            const u32x4_t f0[4] = {a0, a1, a2, a3}, f1[4] = {b0, b1, b2, b3};
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
-                f0[x] = lds_kt<D>(Ks, 4 * h4 + x, 0, lane);
-                f1[x] = lds_kt<D>(Ks, 4 * h4 + x, 32, lane);
-            }
-#pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                S[4 * h4 + x] = mfma32(f0[x], Ub0, S[4 * h4 + x]);
-                S[4 * h4 + x] = mfma32(f1[x], Ub1, S[4 * h4 + x]);
+                S[4 * h4 + x] = mfma32(__builtin_bit_cast(bf16x8_t, f0[x]), Ub0, S[4 * h4 + x]);
+                S[4 * h4 + x] = mfma32(__builtin_bit_cast(bf16x8_t, f1[x]), Ub1, S[4 * h4 + x]);
             }
         }
         // O^T = Y^T + U^T P^T (U tiles as the A operand give U^T; the packed P rows are the

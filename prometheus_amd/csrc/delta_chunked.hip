@@ -109,9 +109,9 @@ __device__ __forceinline__ f32x4_t widen4(u32x2_t v) {
 // LDS layout of a token-major tile (K or Q: D bf16 per row, V: DV per row).
 // Rows have no padding; the 16-byte chunk c of row r is stored at chunk
 // c ^ f(r).  With 64 banks served 32 lanes at a time, f makes every access
-// pattern below conflict-free: the A-operand reads (16 rows, two 8-byte
-// blocks of one chunk), the transpose reads (8 rows, two chunks) and the
-// copies (1 KiB contiguous per instruction).
+// pattern below conflict-free: the 16-byte operand reads (16 rows, one
+// chunk each), the copies (1 KiB contiguous per instruction) and, up to
+// two-way, the transpose reads (8 rows, 8-byte halves of four chunks).
 template <int D>
 __device__ __forceinline__ int kq_f(int r) {
     if constexpr (D == 128) return 2 * (r & 7) + ((r >> 3) & 1);  // 16 chunks, rows share banks
@@ -123,17 +123,20 @@ __device__ __forceinline__ int v_f(int r) {
     else return 0;                                       // 8 rows of 32 bytes cover all banks
 }
 
-// A operand of a 16x16x32 product from a swizzled K/Q tile: row `row`,
-// contraction block starting at k0 (multiple of 32), lane group g.
+// Contraction over d.  In every product that contracts over d (X = K S,
+// Y^T = S^T Q^T, K K^T, Q K^T) lane group g's 8 slots of 32-block kb are
+// d = 32 kb + 8 g + [0, 8): one 16-byte chunk of a K/Q row.  To match,
+// accumulator tile md = 2 kb + h of S holds the rows
+//     d = 32 kb + 8 (r / 4) + 4 h + r % 4,   r = 0..15,
+// so that acc_to_b(S[2 kb], S[2 kb + 1]) puts exactly those d in the slots.
+__device__ __forceinline__ int s_row_d(int md, int r) {
+    return 32 * (md >> 1) + 8 * (r >> 2) + 4 * (md & 1) + (r & 3);
+}
+// Operand (A or B) over d from a swizzled K/Q tile: row `row`, 32-block kb, lane group g.
 template <int D>
-__device__ __forceinline__ bf16x8_t lds_a_kq(const uint16_t* m, int row, int k0, int g) {
-    const uint16_t* r = m + row * D;
-    const int f = kq_f<D>(row);
-    const int b = (k0 >> 2) + g;  // 8-byte block: chunk b >> 1, half b & 1
-    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(r + 8 * ((b >> 1) ^ f) + 4 * (b & 1));
-    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(r + 8 * (((b >> 1) + 2) ^ f) + 4 * (b & 1));
-    const u32x4_t v = {lo.x, lo.y, hi.x, hi.y};
-    return __builtin_bit_cast(bf16x8_t, v);
+__device__ __forceinline__ bf16x8_t lds_op_kq(const uint16_t* m, int row, int kb, int g) {
+    return __builtin_bit_cast(bf16x8_t,
+                              *reinterpret_cast<const u32x4_t*>(m + row * D + 8 * ((4 * kb + g) ^ kq_f<D>(row))));
 }
 
 // ds_read_b64_tr_b16: within each 16-lane group, the four 4-element rows
@@ -166,14 +169,15 @@ __device__ __forceinline__ void lds_wait(u32x4_t& a, u32x4_t& b, u32x4_t& c, u32
                      :
                      : "memory");
 }
-// A operand of K^T (rows d = 16 md + l16, contraction over tokens
-// k0 + {4g..4g+3, 16+4g..16+4g+3}) from the token-major K tile: two
-// transpose reads, 16 rows apart (kq_f(t + 16) == kq_f(t)).
+// A operand of K^T for S tile md (rows d = s_row_d(md, l16), contraction
+// over tokens K0 + {4g..4g+3, 16+4g..16+4g+3}) from the token-major K
+// tile: two transpose reads, 16 rows apart (kq_f(t + 16) == kq_f(t)); the
+// four lanes 4j + cc of a group address d = 32 kb + 8 cc + 4 h + [0, 4).
 template <int D, int K0>
 __device__ __forceinline__ u32x4_t lds_kt_issue(const uint16_t* Ks, int md, int lane) {
     const int g = lane >> 4, j = (lane >> 2) & 3, cc = lane & 3;
     const int t = K0 + 4 * g + j;
-    const unsigned a = lds_addr(Ks + t * D + 8 * ((2 * md + (cc >> 1)) ^ kq_f<D>(t)) + 4 * (cc & 1));
+    const unsigned a = lds_addr(Ks + t * D + 8 * ((4 * (md >> 1) + cc) ^ kq_f<D>(t)) + 4 * (md & 1));
     const u32x2_t lo = lds_tr16_issue<0>(a), hi = lds_tr16_issue<16 * D * 2>(a);
     const u32x4_t v = {lo.x, lo.y, hi.x, hi.y};
     return v;
@@ -362,7 +366,7 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
         for (int kb = 0; kb < D / 32; ++kb) {
             bf16x8_t f[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) f[r] = lds_a_kq<D>(Ks, 16 * r + l16, 32 * kb, lg);
+            for (int r = 0; r < 4; ++r) f[r] = lds_op_kq<D>(Ks, 16 * r + l16, kb, lg);
 #pragma unroll
             for (int b = 0; b < 4; ++b) gd[b] = mfma32(f[b], f[b], gd[b]);
             gu[0] = mfma32(f[0], f[1], gu[0]);  // (0,1)
@@ -499,8 +503,8 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
             bf16x8_t fk[4], fq[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                fk[r] = lds_a_kq<D>(Ks, 16 * r + l16, 32 * kb, lg);
-                fq[r] = lds_a_kq<D>(Qs, 16 * r + l16, 32 * kb, lg);
+                fk[r] = lds_op_kq<D>(Ks, 16 * r + l16, kb, lg);
+                fq[r] = lds_op_kq<D>(Qs, 16 * r + l16, kb, lg);
             }
             // accumulator of (P_ij)^T = K_j Q_i^T: lane holds P[16i+l16][16j+4g+r]
             int x = 0;
@@ -532,7 +536,7 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
     for (int md = 0; md < D / 16; ++md) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int d = 16 * md + 4 * lg + r;
+            const int d = s_row_d(md, 4 * lg + r);
             S[md][r] = (chain && s0) ? s0[sbase + static_cast<size_t>(d) * D + ecol] : 0.f;
         }
     }
@@ -563,8 +567,8 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
             bf16x8_t fk[4], fq[4];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                fk[m] = lds_a_kq<D>(Ks, 16 * m + l16, 32 * kb, lg);
-                fq[m] = lds_a_kq<D>(Qs, 16 * m + l16, 32 * kb, lg);
+                fk[m] = lds_op_kq<D>(Ks, 16 * m + l16, kb, lg);
+                fq[m] = lds_op_kq<D>(Qs, 16 * m + l16, kb, lg);
             }
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
@@ -670,7 +674,7 @@ __global__ __launch_bounds__(256) void delta_chunked_kernel(
         for (int md = 0; md < D / 16; ++md) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int d = 16 * md + 4 * lg + r;
+                const int d = s_row_d(md, 4 * lg + r);
                 s_out[sbase + static_cast<size_t>(d) * D + ecol] = S[md][r];
             }
         }

@@ -29,6 +29,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
     # keep packed-fp32 VALU forms out of the generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: the kernels convert and combine
+    # accumulator tiles with VALU ops, which cannot read AGPRs directly
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(ROOT, "include"),
     "-I", CSRC,
 ]

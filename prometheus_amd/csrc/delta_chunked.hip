@@ -272,7 +272,7 @@ struct Geo {
 };
 
 template <int D, int DV, bool OUT_BF16>
-__global__ __launch_bounds__(256) void delta_chunked_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void delta_chunked_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ beta,
     const float* __restrict__ s0, void* __restrict__ o_out, float* __restrict__ s_out,

@@ -152,6 +152,104 @@ def varlen_fwd(q, k, v, beta, cu_seqlens, state=None, dtype=np.float32):
     return out, states
 
 
+def delta_vjp(q, k, v, beta, go, gs, state=None, dtype=np.float64):
+    """Reverse mode of the recurrence with the full state history.
+
+    Follows the reference's ``_delta_vjp_np`` (``kernels/__init__.py:460-527``)
+    and its oracle ``gated_delta_rule_vjp`` (``tests/reference/kernels.py:174-251``):
+    a forward pass keeps every S_t, then a reverse pass per token
+
+        gq_t = S_t go_t             g_S += q_t go_t^T
+        g_A  = g_S S_{t-1}^T        gv_t = beta_t g_S^T k_t
+        gk_t = beta_t (g_S v_t - g_A k_t - g_A^T k_t)
+        gbeta_t = k_t^T g_S v_t - k_t^T g_A k_t
+        g_S <- (I - beta_t k_t k_t^T) g_S
+
+    ``go`` is dL/dO (B, T, H, D), ``gs`` dL/dS_T (B, H, D, D), either may be
+    None (zeros).  Returns (gq, gk, gv, gbeta, gstate0).
+    """
+    q, k, v, beta = (_as(x, dtype) for x in (q, k, v, beta))
+    st = None if state is None else _as(state, dtype)
+    _check(q, k, v, beta, st)
+    b, t, h, d = q.shape
+    go = np.zeros((b, t, h, d), dtype) if go is None else _as(go, dtype)
+    g_s = np.zeros((b, h, d, d), dtype) if gs is None else _as(gs, dtype).copy()
+    s = np.zeros((b, h, d, d), dtype=dtype) if st is None else st.copy()
+    eye = np.eye(d, dtype=dtype)
+    hist = [s]
+    for i in range(t):
+        bt = beta[:, i, :, None, None]
+        decay = eye[None, None] - bt * np.einsum("bhd,bhe->bhde", k[:, i], k[:, i])
+        s = np.einsum("bhij,bhjk->bhik", decay, s) + bt * np.einsum("bhd,bhe->bhde", k[:, i], v[:, i])
+        hist.append(s)
+    gq, gk, gv = (np.zeros((b, t, h, d), dtype) for _ in range(3))
+    gbeta = np.zeros((b, t, h), dtype)
+    for i in range(t - 1, -1, -1):
+        qt, kt, vt, bt, g_o = q[:, i], k[:, i], v[:, i], beta[:, i], go[:, i]
+        s_t, s_prev = hist[i + 1], hist[i]
+        gq[:, i] = np.einsum("bhe,bhde->bhd", g_o, s_t)
+        g_s = g_s + np.einsum("bhd,bhe->bhde", qt, g_o)
+        g_a = np.einsum("bhik,bhjk->bhij", g_s, s_prev)
+        gv[:, i] = np.einsum("bhde,bhd->bhe", g_s, kt) * bt[..., None]
+        gk[:, i] = bt[..., None] * (np.einsum("bhde,bhe->bhd", g_s, vt)
+                                    - np.einsum("bhde,bhe->bhd", g_a, kt)
+                                    - np.einsum("bhed,bhe->bhd", g_a, kt))
+        gbeta[:, i] = (np.einsum("bhde,bhd,bhe->bh", g_s, kt, vt)
+                       - np.einsum("bhde,bhd,bhe->bh", g_a, kt, kt))
+        a_t = eye[None, None] - bt[..., None, None] * np.einsum("bhd,bhe->bhde", kt, kt)
+        g_s = np.einsum("bhij,bhik->bhjk", a_t, g_s)
+    return gq, gk, gv, gbeta, g_s
+
+
+def delta_vjp_downdate(q, k, v, beta, go, gs, state=None, ckpt=64, dtype=np.float64):
+    """The same gradients in the form the GPU backward computes them.
+
+    Not in the reference: a restatement that keeps no state history.  A
+    forward pass stores u_t = v_t - S_{t-1}^T k_t per token and the state at
+    the end of every ``ckpt`` tokens; the reverse pass restarts from those
+    checkpoints and walks the state back exactly, S_{t-1} = S_t - beta_t k_t
+    u_t^T, with (w_t = g_S^T k_t after g_S += q_t go_t^T)
+
+        gq_t = S_t go_t          gv_t = beta_t w_t
+        gk_t = beta_t (g_S u_t - S_{t-1} w_t)      gbeta_t = k_t^T g_S u_t
+        g_S <- g_S - beta_t k_t w_t^T
+
+    (g_A k_t = g_S S_{t-1}^T k_t = g_S (v_t - u_t) folds the reference's
+    three k-terms into these two.)
+    """
+    q, k, v, beta = (_as(x, dtype) for x in (q, k, v, beta))
+    st = None if state is None else _as(state, dtype)
+    _check(q, k, v, beta, st)
+    b, t, h, d = q.shape
+    go = np.zeros((b, t, h, d), dtype) if go is None else _as(go, dtype)
+    g_s = np.zeros((b, h, d, d), dtype) if gs is None else _as(gs, dtype).copy()
+    s = np.zeros((b, h, d, d), dtype=dtype) if st is None else st.copy()
+    u = np.zeros((b, t, h, d), dtype)
+    ends = {}
+    for i in range(t):
+        u[:, i] = v[:, i] - np.einsum("bhd,bhde->bhe", k[:, i], s)
+        s = s + beta[:, i, :, None, None] * np.einsum("bhd,bhe->bhde", k[:, i], u[:, i])
+        if (i + 1) % ckpt == 0 or i + 1 == t:
+            ends[i] = s.copy()
+    gq, gk, gv = (np.zeros((b, t, h, d), dtype) for _ in range(3))
+    gbeta = np.zeros((b, t, h), dtype)
+    for i in range(t - 1, -1, -1):
+        if i in ends:
+            s = ends[i].copy()
+        kt, bt, g_o = k[:, i], beta[:, i], go[:, i]
+        gq[:, i] = np.einsum("bhde,bhe->bhd", s, g_o)
+        g_s = g_s + np.einsum("bhd,bhe->bhde", q[:, i], g_o)
+        w = np.einsum("bhde,bhd->bhe", g_s, kt)
+        x = np.einsum("bhde,bhe->bhd", g_s, u[:, i])
+        s = s - bt[..., None, None] * np.einsum("bhd,bhe->bhde", kt, u[:, i])
+        y = np.einsum("bhde,bhe->bhd", s, w)
+        gv[:, i] = bt[..., None] * w
+        gk[:, i] = bt[..., None] * (x - y)
+        gbeta[:, i] = np.einsum("bhd,bhd->bh", kt, x)
+        g_s = g_s - bt[..., None, None] * np.einsum("bhd,bhe->bhde", kt, w)
+    return gq, gk, gv, gbeta, g_s
+
+
 def rel_l2(got, exp) -> float:
     """||got - exp||_2 / ||exp||_2 over all elements (0/0 -> 0)."""
     got = np.asarray(got, dtype=np.float64)

@@ -10,6 +10,7 @@
  *   kernels/__init__.py:661-689  chunked_delta_rule_fwd   -> pm_delta_fwd
  *   kernels/__init__.py:591-619  chunked_delta_rule       -> pm_delta_fwd
  *   kernels/__init__.py:357-376  _delta_step_np/_jax      -> pm_delta_step
+ *   kernels/__init__.py:692-719  chunked_delta_rule_bwd   -> pm_delta_bwd
  *   (no reference counterpart)   packed cu_seqlens batch  -> pm_delta_fwd_varlen
  * The reference has no FFI of its own: its call surface is Python
  * (kernels/__init__.py).  prometheus_amd/kernels binds these entry points
@@ -104,6 +105,31 @@ int pm_delta_step(float* s_inout, const void* q, const void* k, const void* v,
 
 /* Workspace bytes pm_delta_fwd would need (0 in this build). */
 size_t pm_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype);
+
+/*
+ * Reverse mode of the forward: gradients of L with respect to (q, k, v,
+ * beta, s0) given go = dL/dO and gs = dL/dS_T.
+ * Replaces kernels/__init__.py:692-719 (chunked_delta_rule_bwd, which runs
+ * _delta_vjp_np :460-527 / _delta_vjp_jax :529-588): same inputs as the
+ * residual (q, k, v, beta, s0), same grads (go, gs), same five fp32 outputs
+ * in the order (gq, gk, gv, gbeta, gs0).
+ *   go (B, T, H, D) fp32 or NULL (zeros); gs (B, H, D, D) fp32 or NULL (zeros);
+ *   s0 NULL means a zero initial state;
+ *   gq, gk, gv (B, T, H, D), gbeta (B, T, H), gs0 (B, H, D, D): fp32 outputs.
+ * q, k, v are fp32 or bf16 (in_dtype); 1 <= D <= 128.
+ * workspace: device memory of at least pm_delta_bwd_workspace_bytes(B, T,
+ * H, D) bytes, 4-byte aligned, contents undefined on entry and exit
+ * (per-token u = v - S^T k and the state every 8 tokens: 4 * B * H *
+ * (T * D + ceil(T / 8) * D * D) bytes).
+ * T == 0 gives gs0 = gs (or zeros).
+ */
+int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
+                 const float* s0, const float* go, const float* gs, float* gq, float* gk,
+                 float* gv, float* gbeta, float* gs0, int B, int T, int H, int D, int in_dtype,
+                 void* workspace, size_t ws_bytes, void* stream);
+
+/* Workspace bytes pm_delta_bwd needs (0 for invalid shapes or D > 128). */
+size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D);
 
 /* Thread-local message for the last nonzero return on this thread. */
 const char* pm_last_error(void);

@@ -22,6 +22,7 @@ ABI_VERSION = 1
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256
+MAX_D_BWD = 128
 
 E_NULL, E_SHAPE, E_DTYPE, E_ALIGN, E_WORKSPACE, E_UNSUPPORTED = -1, -2, -3, -4, -5, -6
 
@@ -31,6 +32,8 @@ EXPORTS = (
     "pm_delta_fwd_varlen",
     "pm_delta_step",
     "pm_delta_workspace_bytes",
+    "pm_delta_bwd",
+    "pm_delta_bwd_workspace_bytes",
     "pm_last_error",
     "pm_abi_version",
     "pm_delta_set_path",
@@ -73,6 +76,10 @@ def lib() -> ctypes.CDLL:
         L.pm_delta_step.restype = i
         L.pm_delta_workspace_bytes.argtypes = [i, i, i, i, i]
         L.pm_delta_workspace_bytes.restype = sz
+        L.pm_delta_bwd.argtypes = [vp] * 12 + [i] * 5 + [vp, sz, vp]
+        L.pm_delta_bwd.restype = i
+        L.pm_delta_bwd_workspace_bytes.argtypes = [i, i, i, i]
+        L.pm_delta_bwd_workspace_bytes.restype = sz
         L.pm_last_error.argtypes = []
         L.pm_last_error.restype = ctypes.c_char_p
         L.pm_abi_version.argtypes = []

@@ -5,6 +5,7 @@
 //   K1/K2 delta_chunked.hip    chunked WY/UT forward on bf16 MFMA
 //   K3    delta_step.hip       decode step, HBM-streaming
 //   K4    delta_recurrent.hip  per-token fp32 recurrence (generic shapes)
+//   K5    delta_bwd.hip        reverse mode, fp32, checkpointed
 // Mirrors the checks of kernels/__init__.py:308-338 (shapes), :613-614 and
 // :676-677 (chunk >= 1); shapes arrive as integers, so the Python layer
 // (prometheus_amd/kernels) raises KernelError for the tensor-level checks
@@ -142,6 +143,43 @@ int pm_abi_version(void) { return PM_DELTA_ABI_VERSION; }
 const char* pm_last_error(void) { return g_err; }
 
 size_t pm_delta_workspace_bytes(int, int, int, int, int) { return 0; }
+
+size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D) {
+    if (B < 0 || T < 0 || H < 0 || D < 1 || D > pm::kBwdMaxD) return 0;
+    return sizeof(float) * pm::bwd_workspace_floats(static_cast<long>(B) * H, T, D);
+}
+
+int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
+                 const float* s0, const float* go, const float* gs, float* gq, float* gk,
+                 float* gv, float* gbeta, float* gs0, int B, int T, int H, int D, int in_dtype,
+                 void* workspace, size_t ws_bytes, void* stream) {
+    g_err[0] = '\0';
+    if (B < 0 || T < 0 || H < 0)
+        return fail(PM_E_SHAPE, "B, T, H must be >= 0 (got %d, %d, %d)", B, T, H);
+    if (D < 1 || D > pm::kBwdMaxD)
+        return fail(PM_E_SHAPE, "backward D must be in [1, %d] (got %d)", pm::kBwdMaxD, D);
+    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16)
+        return fail(PM_E_DTYPE, "in_dtype %d is not PM_DTYPE_F32 or PM_DTYPE_BF16", in_dtype);
+    const long n_pairs = static_cast<long>(B) * H;
+    const long n_tok = static_cast<long>(B) * T;
+    if (n_pairs == 0) return 0;
+    if (n_pairs > (1L << 30) || n_tok > (1L << 40)) return fail(PM_E_SHAPE, "problem too large");
+    if (!gs0) return fail(PM_E_NULL, "gs0 is NULL");
+    if (n_tok > 0 && (!q || !k || !v || !beta || !gq || !gk || !gv || !gbeta))
+        return fail(PM_E_NULL, "q, k, v, beta, gq, gk, gv and gbeta must be non-NULL");
+    const void* f32s[] = {beta, s0, go, gs, gq, gk, gv, gbeta, gs0, workspace};
+    for (const void* p : f32s)
+        if (p && !aligned(p, 4)) return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
+    const size_t need = sizeof(float) * pm::bwd_workspace_floats(n_pairs, T, D);
+    if (need > 0 && (!workspace || ws_bytes < need))
+        return fail(PM_E_WORKSPACE, "workspace of %zu bytes needed (got %zu)", need,
+                    workspace ? ws_bytes : static_cast<size_t>(0));
+    pm::BwdArgs a{q, k, v, beta, s0, go, gs, gq, gk, gv, gbeta, gs0,
+                  static_cast<float*>(workspace), static_cast<int>(n_pairs), T, H, D,
+                  in_dtype == PM_DTYPE_BF16};
+    hipError_t e = pm::launch_bwd(a, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? 0 : hip_fail(e, "backward launch");
+}
 
 int pm_delta_set_path(int path) {
     if (path < 0 || path > 2) return fail(PM_E_UNSUPPORTED, "path %d not in {0, 1, 2}", path);

@@ -57,6 +57,30 @@ struct ChunkedArgs {
 bool chunked_supported(int D, int H);  // D in {64, 128}, H*D <= 2^24
 hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st);
 
+// Reverse mode (K5, fp32): fixed-length batch of n_pairs = B*H sequences of
+// T tokens, D <= 128.  workspace holds bwd_workspace_floats(n_pairs, T, D)
+// floats: u (n_pairs x T x D) then the checkpoints (n_pairs x ceil(T/8) x D x D).
+struct BwdArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* beta;
+    const float* s0;  // nullable
+    const float* go;  // nullable (zeros)
+    const float* gs;  // nullable (zeros)
+    float* gq;
+    float* gk;
+    float* gv;
+    float* gbeta;
+    float* gs0;
+    float* workspace;
+    int n_pairs, T, H, D;
+    bool in_bf16;
+};
+constexpr int kBwdMaxD = 128;
+size_t bwd_workspace_floats(long n_pairs, int T, int D);
+hipError_t launch_bwd(const BwdArgs& a, hipStream_t st);
+
 // Zero fill (used instead of hipMemsetAsync so callers may graph-capture).
 hipError_t launch_fill_zero(float* p, size_t n, hipStream_t st);
 hipError_t launch_copy_f32(float* dst, const float* src, size_t n, hipStream_t st);

@@ -255,12 +255,46 @@ def chunked_delta_rule_fwd(q, k, v, beta, state, config, *, out_dtype=None):
 
 
 def chunked_delta_rule_bwd(residual: _DeltaResidual, grads):
-    """Backward of the VJP pair (``kernels/__init__.py:692-719``): not built yet.
+    """Backward of the VJP pair (``kernels/__init__.py:692-719``).
 
-    The MI355X build covers the forward and the decode step; the chunked
-    recompute backward is the next item of the roadmap.
+    ``grads = (go, gs)``: dL/dO (B, T, H, D) and dL/dS_T (B, H, D, D), either
+    may be None (zeros, as the custom-VJP rule treats missing cotangents,
+    ``:638-653``). Returns ``(gq, gk, gv, gbeta, gstate)``, all fp32, shaped
+    like ``q, k, v, beta, state0``: the gradients of the reference's
+    ``_delta_vjp_np`` / ``_delta_vjp_jax`` (``:460-588``), computed by the
+    checkpointed reverse-mode kernel (no per-token state history). Head
+    dimension up to 128.
     """
-    raise NotImplementedError("chunked_delta_rule_bwd: the MI355X backward is not built yet")
+    go, gs = grads
+    q, k, v, beta, s0 = residual.q, residual.k, residual.v, residual.beta, residual.state0
+    batch, seq, heads, dim = _validate(q, k, v, beta, s0)
+    if dim > _native.MAX_D_BWD:
+        raise KernelError(f"backward head dimension {dim} exceeds {_native.MAX_D_BWD}")
+    if go is not None and _shape(go) != (batch, seq, heads, dim):
+        raise KernelError(f"grad of output shape {_shape(go)} != {(batch, seq, heads, dim)}")
+    if gs is not None and _shape(gs) != (batch, heads, dim, dim):
+        raise KernelError(f"grad of state shape {_shape(gs)} != {(batch, heads, dim, dim)}")
+    call = _Call(q, k, v, beta, s0, go, gs)
+    cdt = _qkv_dtype(q, k, v)
+    f32 = torch.float32
+    with torch.cuda.device(call.device):
+        qd, kd, vd = call.dev(q, cdt), call.dev(k, cdt), call.dev(v, cdt)
+        bd, sd = call.dev(beta, f32), call.dev(s0, f32)
+        god, gsd = call.dev(go, f32), call.dev(gs, f32)
+        gq = torch.empty((batch, seq, heads, dim), dtype=f32, device=call.device)
+        gk, gv = torch.empty_like(gq), torch.empty_like(gq)
+        gb = torch.empty((batch, seq, heads), dtype=f32, device=call.device)
+        gs0 = torch.empty((batch, heads, dim, dim), dtype=f32, device=call.device)
+        L = _native.lib()
+        nbytes = L.pm_delta_bwd_workspace_bytes(batch, seq, heads, dim)
+        ws = torch.empty(((nbytes + 3) // 4,), dtype=f32, device=call.device) if nbytes else None
+        rc = L.pm_delta_bwd(
+            _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(sd), _ptr(god), _ptr(gsd),
+            _ptr(gq), _ptr(gk), _ptr(gv), _ptr(gb), _ptr(gs0),
+            batch, seq, heads, dim, _code(cdt), _ptr(ws), nbytes, _stream(call.device),
+        )
+        _native.check(rc)
+    return tuple(call.out(x) for x in (gq, gk, gv, gb, gs0))
 
 
 # ---------------------------------------------------------------------------

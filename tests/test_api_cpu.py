@@ -88,9 +88,55 @@ def test_head_dim_limit_raises_kernel_error():
         kernels.chunked_delta_rule(z, z, z, np.zeros((1, 1, 1), np.float32))
 
 
-def test_bwd_is_not_built_yet():
-    with pytest.raises(NotImplementedError):
-        kernels.chunked_delta_rule_bwd(None, (None, None))
+def _residual(b=1, t=3, h=2, d=4, state=True):
+    z = np.zeros((b, t, h, d), np.float32)
+    s0 = np.zeros((b, h, d, d), np.float32)
+    return kernels._DeltaResidual(q=z, k=z, v=z, beta=np.zeros((b, t, h), np.float32),
+                                  state0=s0 if state else None, chunk=64)
+
+
+def test_bwd_shape_checks_raise_before_any_device_work():
+    r = _residual()
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule_bwd(r, (np.zeros((1, 3, 2, 5), np.float32), None))
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule_bwd(r, (None, np.zeros((1, 2, 4, 3), np.float32)))
+    big = _residual(d=129)
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_delta_rule_bwd(big, (None, None))
+
+
+def test_bwd_workspace_bytes():
+    lib = _native.lib()
+    for b, t, h, d in [(1, 1, 1, 3), (2, 130, 3, 64), (4, 4096, 16, 128), (1, 0, 2, 8)]:
+        n_ck = -(-t // 8)
+        assert lib.pm_delta_bwd_workspace_bytes(b, t, h, d) == 4 * b * h * (t * d + n_ck * d * d)
+    assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 129) == 0
+    assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 0) == 0
+
+
+def test_bwd_abi_argument_validation_without_gpu():
+    lib = _native.lib()
+    f = lib.pm_delta_bwd
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+
+    def call(b, t, h, d, dt, ws, nbytes, *, ptrs=None, gs0=p):
+        q = ptrs if ptrs is not None else [p, p, p, p, None, None, None, p, p, p, p]
+        return f(*q, gs0, b, t, h, d, dt, ws, nbytes, None)
+
+    assert call(1, 4, 1, 0, 0, p, 1 << 20) == _native.E_SHAPE
+    assert call(1, 4, 1, 129, 0, p, 1 << 20) == _native.E_SHAPE
+    assert b"backward D" in lib.pm_last_error()
+    assert call(-1, 4, 1, 8, 0, p, 1 << 20) == _native.E_SHAPE
+    assert call(1, 4, 1, 8, 3, p, 1 << 20) == _native.E_DTYPE
+    assert call(1, 4, 1, 8, 0, p, 1 << 20, gs0=None) == _native.E_NULL
+    assert call(1, 4, 1, 8, 0, p, 1 << 20, ptrs=[None] + [p] * 3 + [None] * 3 + [p] * 4) == _native.E_NULL
+    need = lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 8)
+    assert call(1, 4, 1, 8, 0, p, need - 4) == _native.E_WORKSPACE
+    assert call(1, 4, 1, 8, 0, None, need) == _native.E_WORKSPACE
+    assert call(1, 4, 1, 8, 0, ctypes.c_void_p(18), need) == _native.E_ALIGN
+    # nothing to do: B*H == 0
+    assert call(0, 4, 1, 8, 0, None, 0) == 0
 
 
 def test_varlen_checks():

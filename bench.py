@@ -14,7 +14,8 @@ forward kernel (HBM-bound at this shape: 340.8 MB vs 47.6 GFLOP) and
 ``cpu_baseline`` (the C restatement of the reference's per-token CPU
 algorithm, OpenMP over the 64 (b, h) sequences, on this host). The decode
 step (cfg4: B=256 H=32 D=128, fp32 state updated in place) is measured in
-the same run and reported under ``decode``.
+the same run and reported under ``decode``, and the backward at cfg1 under
+``backward``.
 """
 
 from __future__ import annotations
@@ -50,6 +51,13 @@ def fwd_bytes(B, T, H, D, s_in=2, s_out=4, s0=False) -> float:
     E = B * T * H * D
     S = 4 * B * H * D * D
     return 3 * E * s_in + 4 * B * T * H + E * s_out + S + (S if s0 else 0)
+
+
+def bwd_bytes(B, T, H, D, s_in=2) -> float:
+    """Backward: q, k, v, beta, S0, go, gS in; gq, gk, gv, gbeta, gS0 out (fp32 grads)."""
+    E = B * T * H * D
+    S = 4 * B * H * D * D
+    return 3 * E * s_in + 4 * E + 3 * 4 * E + 2 * 4 * B * T * H + 3 * S
 
 
 def step_bytes(B, H, D, s_in=2) -> float:
@@ -95,6 +103,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--decode-steps", type=int, default=64)
+    ap.add_argument("--bwd-steps", type=int, default=3,
+                    help="timed calls of the backward at cfg1 (0 skips it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_cfg1.json"),
                     help="JSON with measured HBM bytes per launch (from rocprofv3 --pmc)")
@@ -240,6 +250,49 @@ def main():
                      "frac": dbytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
     }
 
+    # backward at cfg1 (chunked_delta_rule_bwd through the C ABI): bf16 q/k/v, zero S0,
+    # random go and gS, fp32 gradients
+    backward = None
+    if args.bwd_steps > 0:
+        q, k, v, beta = sets[last]
+        g.manual_seed(5)
+        go = torch.randn((B, T, H, D), generator=g, device=dev)
+        gs = torch.randn((B, H, D, D), generator=g, device=dev) * 0.05
+        gq, gk, gv = (torch.empty((B, T, H, D), device=dev) for _ in range(3))
+        gb = torch.empty((B, T, H), device=dev)
+        gs0 = torch.empty((B, H, D, D), device=dev)
+        nbytes = lib.pm_delta_bwd_workspace_bytes(B, T, H, D)
+        ws = torch.empty(((nbytes + 3) // 4,), device=dev)
+
+        def bwd():
+            rc = lib.pm_delta_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), None,
+                                  go.data_ptr(), gs.data_ptr(), gq.data_ptr(), gk.data_ptr(),
+                                  gv.data_ptr(), gb.data_ptr(), gs0.data_ptr(), B, T, H, D,
+                                  _native.DTYPE_BF16, ws.data_ptr(), nbytes, stream.cuda_stream)
+            _native.check(rc)
+
+        bwd()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.bwd_steps):
+            bwd()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        bwd_ms = e0.elapsed_time(e1) / args.bwd_steps
+        bb = bwd_bytes(B, T, H, D)
+        backward = {
+            "workload": "cfg1 backward (chunked_delta_rule_bwd), bf16 q/k/v, fp32 grads",
+            "calls": args.bwd_steps,
+            "ms_per_call": bwd_ms,
+            "tokens_per_s": tokens / (bwd_ms * 1e-3),
+            "workspace_bytes": nbytes,
+            "roofline": {"bound": "hbm", "achieved": bb / (bwd_ms * 1e-3) / 1e9,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": bb / (bwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        }
+        del go, gs, gq, gk, gv, gb, gs0, ws
+
     if args.calib_copy:
         n = CALIB_COPY_BYTES // 4
         x = torch.randn(n, device=dev)
@@ -277,6 +330,7 @@ def main():
         "cpu_baseline": cpu,
         "parity": parity,
         "decode": decode,
+        "backward": backward,
     }
     print(json.dumps(line), flush=True)
     if parity is not None and not parity["ok"]:

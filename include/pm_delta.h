@@ -120,7 +120,9 @@ size_t pm_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype);
  * workspace: device memory of at least pm_delta_bwd_workspace_bytes(B, T,
  * H, D) bytes, 4-byte aligned, contents undefined on entry and exit
  * (per-token u = v - S^T k and the state every 8 tokens: 4 * B * H *
- * (T * D + ceil(T / 8) * D * D) bytes).
+ * (T * D + ceil(T / 8) * D * D) bytes; for D > 32 also the partial sums
+ * of gq, gk and gbeta over 32-column tiles of the state: 4 * B * H * T *
+ * ceil(D / 32) * (2 * D + 1) bytes more).
  * T == 0 gives gs0 = gs (or zeros).
  */
 int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,

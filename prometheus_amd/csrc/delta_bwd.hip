@@ -20,13 +20,21 @@
 // kept short: kCk = 8 holds the reference's own growing test case
 // (tests/test_kernels.py:1537-1548) at 1e-6, where 16 reaches 3e-5.
 //
-// K5a (checkpoint pass) is the forward recurrence in the per-token layout of
-// K4, writing u and the block-end states.  K5b (reverse pass) holds three
-// D x D fp32 matrices on chip: G by columns (thread (e, r): rows r*RPT.. of
-// column e, for w = G^T k), G by rows and S by rows (thread (d, r): columns
-// r*RPT.. of row d, for x = G u, S go and S w); every product is a
-// per-thread partial sum reduced over RS adjacent lanes.  w moves from the
-// column to the row layout through LDS: one barrier per token.
+// The recurrence is separable along the columns of S and G (d_v): a
+// workgroup owns a tile of NC = min(D, 32) columns of one (b, h), so B*H*
+// ceil(D/NC) workgroups run (256 at cfg1 instead of 64).  gv and gS0 are
+// per column; gq, gk and gbeta sum over all columns (x, y and S go are row
+// sums), so with several tiles each writes its partial sums and a final
+// pass adds them (in a fixed order: results do not depend on scheduling).
+//
+// K5a (checkpoint pass) runs the forward recurrence for its columns, one
+// thread per (column, slice of RPT rows), writing u and the block-end
+// states.  K5b (reverse pass) holds three fp32 matrices of the tile on chip:
+// G by columns (thread (e, rc): rows rc*RPT.. of column e, for w = G^T k),
+// G by rows and S by rows (thread (d, rr): tile columns rr*RPT.. of row d,
+// for x = G u, S go and S w); every product is a per-thread partial sum
+// reduced over adjacent lanes.  w moves from the column to the row layout
+// through LDS: one barrier per token.
 
 #include "pm_common.h"
 #include "pm_internal.h"
@@ -35,73 +43,96 @@ namespace pm {
 
 constexpr int kBwdSteps = 8;  // tokens staged in LDS at a time
 constexpr int kCk = 8;        // tokens between state checkpoints (multiple of kBwdSteps)
+constexpr int kRpt = 16;      // elements of a row or column slice per thread
+constexpr int kTileCols = 32; // columns per workgroup when D > 32
 static_assert(kCk % kBwdSteps == 0, "checkpoint interval");
 
+struct BwdGeo {
+    int nc, n_tiles;  // tile columns, tiles per (b, h)
+    int rsc, rsr;     // row slices per column (column layout), column slices per row (row layout)
+    int threads;
+};
+static int pow2_at_least(int x) {
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+static BwdGeo bwd_geo(int D) {
+    BwdGeo g;
+    g.nc = D <= kTileCols ? D : kTileCols;
+    g.n_tiles = (D + g.nc - 1) / g.nc;
+    g.rsc = pow2_at_least((D + kRpt - 1) / kRpt);
+    g.rsr = pow2_at_least((g.nc + kRpt - 1) / kRpt);
+    const int t = max(g.nc * g.rsc, D * g.rsr);
+    g.threads = ((t + 63) / 64) * 64;
+    return g;
+}
+
 // ---------------- K5a: forward pass writing u and block-end states ----------------
-template <int RPT, typename InT>
+template <typename InT>
 __global__ __launch_bounds__(512) void delta_bwd_ckpt_kernel(
     const InT* __restrict__ k, const InT* __restrict__ v, const float* __restrict__ beta,
     const float* __restrict__ s0, float* __restrict__ u_ws, float* __restrict__ ck_ws, int T,
-    int H, int D, int RS) {
+    int H, int D, int NC, int n_tiles, int RS) {
     extern __shared__ float lds[];
-    const int DP = RS * RPT;
+    const int DP = RS * kRpt;
     float* sk = lds;                  // [kBwdSteps][DP]
-    float* sv = sk + kBwdSteps * DP;  // [kBwdSteps][DP]
-    float* sb = sv + kBwdSteps * DP;  // [kBwdSteps]
+    float* sv = sk + kBwdSteps * DP;  // [kBwdSteps][NC]
+    float* sb = sv + kBwdSteps * NC;  // [kBwdSteps]
 
-    const int pair = blockIdx.x;
+    const int pair = blockIdx.x / n_tiles, col0 = (blockIdx.x % n_tiles) * NC;
     const int seq = pair / H, h = pair % H;
     const long tok0 = static_cast<long>(seq) * T;
     const int tid = threadIdx.x;
-    const int e = tid / RS, r = tid % RS;
-    const bool ok = e < D;
+    const int e = tid / RS, r = tid % RS;  // tile column e, rows r*kRpt..
+    const int col = col0 + e;
+    const bool ok = e < NC && col < D;
     const size_t sbase = static_cast<size_t>(pair) * D * D;
     const int n_ck = (T + kCk - 1) / kCk;
     float* u_p = u_ws + static_cast<size_t>(pair) * T * D;
     float* ck_p = ck_ws + static_cast<size_t>(pair) * n_ck * D * D;
 
-    float S[RPT];  // S[r*RPT + i][e]
+    float S[kRpt];  // S[r*kRpt + i][col]
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-        const int d = r * RPT + i;
-        S[i] = (s0 && ok && d < D) ? s0[sbase + static_cast<size_t>(d) * D + e] : 0.f;
+    for (int i = 0; i < kRpt; ++i) {
+        const int d = r * kRpt + i;
+        S[i] = (s0 && ok && d < D) ? s0[sbase + static_cast<size_t>(d) * D + col] : 0.f;
     }
     for (int t0 = 0; t0 < T; t0 += kBwdSteps) {
         const int nst = min(kBwdSteps, T - t0);
         __syncthreads();
         for (int idx = tid; idx < kBwdSteps * DP; idx += blockDim.x) {
             const int j = idx / DP, d = idx % DP;
-            float kv = 0.f, vv = 0.f;
-            if (j < nst && d < D) {
-                const size_t a = (static_cast<size_t>(tok0 + t0 + j) * H + h) * D + d;
-                kv = to_f32(k[a]);
-                vv = to_f32(v[a]);
-            }
-            sk[idx] = kv;
-            sv[idx] = vv;
+            sk[idx] = (j < nst && d < D)
+                          ? to_f32(k[(static_cast<size_t>(tok0 + t0 + j) * H + h) * D + d]) : 0.f;
+        }
+        for (int idx = tid; idx < kBwdSteps * NC; idx += blockDim.x) {
+            const int j = idx / NC, c = idx % NC;
+            sv[idx] = (j < nst && col0 + c < D)
+                          ? to_f32(v[(static_cast<size_t>(tok0 + t0 + j) * H + h) * D + col0 + c]) : 0.f;
         }
         for (int j = tid; j < kBwdSteps; j += blockDim.x)
             sb[j] = (j < nst) ? beta[static_cast<size_t>(tok0 + t0 + j) * H + h] : 0.f;
         __syncthreads();
         for (int j = 0; j < nst; ++j) {
-            const float* kr = sk + j * DP + r * RPT;
+            const float* kr = sk + j * DP + r * kRpt;
             float ks = 0.f;
 #pragma unroll
-            for (int i = 0; i < RPT; ++i) ks = fmaf(kr[i], S[i], ks);
+            for (int i = 0; i < kRpt; ++i) ks = fmaf(kr[i], S[i], ks);
             for (int m = 1; m < RS; m <<= 1) ks += __shfl_xor(ks, m);
             const int t = t0 + j;
-            const float u = (ok ? sv[j * DP + e] : 0.f) - ks;
-            if (r == 0 && ok) u_p[static_cast<size_t>(t) * D + e] = u;
+            const float u = (ok ? sv[j * NC + e] : 0.f) - ks;
+            if (r == 0 && ok) u_p[static_cast<size_t>(t) * D + col] = u;
             const float bu = sb[j] * u;
 #pragma unroll
-            for (int i = 0; i < RPT; ++i) S[i] = fmaf(kr[i], bu, S[i]);
+            for (int i = 0; i < kRpt; ++i) S[i] = fmaf(kr[i], bu, S[i]);
             if ((t + 1) % kCk == 0 || t + 1 == T) {
                 float* c = ck_p + static_cast<size_t>(t / kCk) * D * D;
                 if (ok) {
 #pragma unroll
-                    for (int i = 0; i < RPT; ++i) {
-                        const int d = r * RPT + i;
-                        if (d < D) c[static_cast<size_t>(d) * D + e] = S[i];
+                    for (int i = 0; i < kRpt; ++i) {
+                        const int d = r * kRpt + i;
+                        if (d < D) c[static_cast<size_t>(d) * D + col] = S[i];
                     }
                 }
             }
@@ -109,74 +140,90 @@ __global__ __launch_bounds__(512) void delta_bwd_ckpt_kernel(
     }
 }
 
-// ---------------- K5b: reverse pass ----------------
-template <int RPT, typename InT>
+// ---------------- K5b: reverse pass over one column tile ----------------
+// gq/gk/gb receive this tile's sums over its columns: the outputs themselves
+// when n_tiles == 1, else this tile's slot of the partial-sum buffers.
+template <typename InT>
 __global__ __launch_bounds__(512) void delta_bwd_kernel(
     const InT* __restrict__ q, const InT* __restrict__ k, const float* __restrict__ beta,
     const float* __restrict__ go, const float* __restrict__ gs, const float* __restrict__ u_ws,
     const float* __restrict__ ck_ws, float* __restrict__ gq, float* __restrict__ gk,
-    float* __restrict__ gv, float* __restrict__ gbeta, float* __restrict__ gs0, int T, int H,
-    int D, int RS) {
+    float* __restrict__ gv, float* __restrict__ gb, float* __restrict__ gs0, int T, int H, int D,
+    int NC, int n_tiles, int RSC, int RSR, size_t part_stride_e, size_t part_stride_b) {
     extern __shared__ float lds[];
-    const int DP = RS * RPT;
+    const int DP = RSC * kRpt;   // padded rows (column layout)
+    const int CP = RSR * kRpt;   // padded tile columns (row layout)
     const int NWV = blockDim.x / 64;
-    float* sk = lds;                   // [kBwdSteps][DP]
-    float* sq = sk + kBwdSteps * DP;   // [kBwdSteps][DP]
-    float* sg = sq + kBwdSteps * DP;   // [kBwdSteps][DP]  go
-    float* su = sg + kBwdSteps * DP;   // [kBwdSteps][DP]  u
-    float* sw = su + kBwdSteps * DP;   // [2][DP]          w, by token parity
-    float* sb = sw + 2 * DP;           // [kBwdSteps]
-    float* sgb = sb + kBwdSteps;       // [kBwdSteps][NWV] gbeta partial sums
+    float* sk = lds;                    // [kBwdSteps][DP]  k
+    float* sq = sk + kBwdSteps * DP;    // [kBwdSteps][DP]  q
+    float* sg = sq + kBwdSteps * DP;    // [kBwdSteps][CP]  go (tile columns)
+    float* su = sg + kBwdSteps * CP;    // [kBwdSteps][CP]  u (tile columns)
+    float* sw = su + kBwdSteps * CP;    // [2][CP]          w, by token parity
+    float* sb = sw + 2 * CP;            // [kBwdSteps]
+    float* sgb = sb + kBwdSteps;        // [kBwdSteps][NWV] gbeta partial sums
 
-    const int pair = blockIdx.x;
+    const int tile = blockIdx.x % n_tiles, pair = blockIdx.x / n_tiles, col0 = tile * NC;
     const int seq = pair / H, h = pair % H;
     const long tok0 = static_cast<long>(seq) * T;
     const int tid = threadIdx.x;
-    const int a = tid / RS, r = tid % RS;  // column a (column layout) / row a (row layout)
-    const bool ok = a < D;
     const int lane = tid & 63, wave = tid >> 6;
+    // column layout: tile column e, rows rc*kRpt..; row layout: row d, tile columns rr*kRpt..
+    const int e = tid / RSC, rc = tid % RSC;
+    const int d = tid / RSR, rr = tid % RSR;
+    const bool ok_c = e < NC && col0 + e < D;
+    const bool ok_r = d < D;
     const size_t sbase = static_cast<size_t>(pair) * D * D;
     const int n_ck = (T + kCk - 1) / kCk;
     const float* u_p = u_ws + static_cast<size_t>(pair) * T * D;
     const float* ck_p = ck_ws + static_cast<size_t>(pair) * n_ck * D * D;
+    float* gq_t = gq + tile * part_stride_e;
+    float* gk_t = gk + tile * part_stride_e;
+    float* gb_t = gb + tile * part_stride_b;
 
-    // w's padding entries (rows >= D) are read as zeros, never written
-    for (int x = tid; x < 2 * DP; x += blockDim.x) sw[x] = 0.f;
+    // w's padding entries (tile columns past NC or D) are read as zeros, never written
+    for (int x = tid; x < 2 * CP; x += blockDim.x) sw[x] = 0.f;
 
-    float Gc[RPT], Gr[RPT], Sr[RPT];  // G[r*RPT+i][a], G[a][r*RPT+i], S[a][r*RPT+i]
+    float Gc[kRpt], Gr[kRpt], Sr[kRpt];  // G[rc*R+i][col0+e], G[d][col0+rr*R+i], S[d][col0+rr*R+i]
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-        const int x = r * RPT + i;
-        const bool in = gs && ok && x < D;
-        Gc[i] = in ? gs[sbase + static_cast<size_t>(x) * D + a] : 0.f;
-        Gr[i] = in ? gs[sbase + static_cast<size_t>(a) * D + x] : 0.f;
+    for (int i = 0; i < kRpt; ++i) {
+        const int row = rc * kRpt + i, c = rr * kRpt + i;
+        Gc[i] = (gs && ok_c && row < D) ? gs[sbase + static_cast<size_t>(row) * D + col0 + e] : 0.f;
+        Gr[i] = (gs && ok_r && c < NC && col0 + c < D)
+                    ? gs[sbase + static_cast<size_t>(d) * D + col0 + c] : 0.f;
     }
 
     for (int blk = n_ck - 1; blk >= 0; --blk) {
         const int t_lo = blk * kCk, t_hi = min(T, t_lo + kCk);
         {
-            const float* c = ck_p + static_cast<size_t>(blk) * D * D;
+            const float* cp = ck_p + static_cast<size_t>(blk) * D * D;
 #pragma unroll
-            for (int i = 0; i < RPT; ++i) {
-                const int x = r * RPT + i;
-                Sr[i] = (ok && x < D) ? c[static_cast<size_t>(a) * D + x] : 0.f;
+            for (int i = 0; i < kRpt; ++i) {
+                const int c = rr * kRpt + i;
+                Sr[i] = (ok_r && c < NC && col0 + c < D) ? cp[static_cast<size_t>(d) * D + col0 + c] : 0.f;
             }
         }
         for (int hi = t_hi; hi > t_lo; hi -= kBwdSteps) {
             const int lo = max(t_lo, hi - kBwdSteps), nst = hi - lo;
             __syncthreads();
             for (int idx = tid; idx < kBwdSteps * DP; idx += blockDim.x) {
-                const int j = idx / DP, d = idx % DP;
-                float kv = 0.f, qv = 0.f, gv_ = 0.f, uv = 0.f;
-                if (j < nst && d < D) {
-                    const size_t x = (static_cast<size_t>(tok0 + lo + j) * H + h) * D + d;
-                    kv = to_f32(k[x]);
-                    qv = to_f32(q[x]);
-                    gv_ = go ? go[x] : 0.f;
-                    uv = u_p[static_cast<size_t>(lo + j) * D + d];
+                const int j = idx / DP, x = idx % DP;
+                float kv = 0.f, qv = 0.f;
+                if (j < nst && x < D) {
+                    const size_t a = (static_cast<size_t>(tok0 + lo + j) * H + h) * D + x;
+                    kv = to_f32(k[a]);
+                    qv = to_f32(q[a]);
                 }
                 sk[idx] = kv;
                 sq[idx] = qv;
+            }
+            for (int idx = tid; idx < kBwdSteps * CP; idx += blockDim.x) {
+                const int j = idx / CP, c = idx % CP;
+                float gv_ = 0.f, uv = 0.f;
+                if (j < nst && c < NC && col0 + c < D) {
+                    const size_t a = (static_cast<size_t>(tok0 + lo + j) * H + h) * D + col0 + c;
+                    gv_ = go ? go[a] : 0.f;
+                    uv = u_p[static_cast<size_t>(lo + j) * D + col0 + c];
+                }
                 sg[idx] = gv_;
                 su[idx] = uv;
             }
@@ -187,121 +234,146 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
             for (int j = nst - 1; j >= 0; --j) {
                 const int t = lo + j;
                 const float b = sb[j];
-                const float* kc = sk + j * DP + r * RPT;  // k[r*RPT + i]
-                const float* qc = sq + j * DP + r * RPT;
-                const float* gc = sg + j * DP + r * RPT;  // go[r*RPT + i]
-                const float* uc = su + j * DP + r * RPT;  // u[r*RPT + i]
-                const float ka = ok ? sk[j * DP + a] : 0.f;
-                const float qa = ok ? sq[j * DP + a] : 0.f;
-                const float ga = ok ? sg[j * DP + a] : 0.f;
-                // G += q go^T (both layouts); gq = S_t go (row layout)
+                const float* kc = sk + j * DP + rc * kRpt;  // k[rc*R + i]      (column layout)
+                const float* qc = sq + j * DP + rc * kRpt;  // q[rc*R + i]
+                const float* gr = sg + j * CP + rr * kRpt;  // go[col0 + rr*R + i] (row layout)
+                const float* ur = su + j * CP + rr * kRpt;  // u[col0 + rr*R + i]
+                const float ge = ok_c ? sg[j * CP + e] : 0.f;  // go[col0 + e]
+                const float kd = ok_r ? sk[j * DP + d] : 0.f;  // k[d]
+                const float qd = ok_r ? sq[j * DP + d] : 0.f;  // q[d]
+                // G += q go^T (both layouts); S_t go over the tile's columns (row layout)
                 float gqp = 0.f;
 #pragma unroll
-                for (int i = 0; i < RPT; ++i) {
-                    Gc[i] = fmaf(qc[i], ga, Gc[i]);
-                    Gr[i] = fmaf(qa, gc[i], Gr[i]);
-                    gqp = fmaf(Sr[i], gc[i], gqp);
+                for (int i = 0; i < kRpt; ++i) {
+                    Gc[i] = fmaf(qc[i], ge, Gc[i]);
+                    Gr[i] = fmaf(qd, gr[i], Gr[i]);
+                    gqp = fmaf(Sr[i], gr[i], gqp);
                 }
-                // w = G^T k (column layout), x = G u (row layout)
+                // w = G^T k (column layout), x = G u over the tile's columns (row layout)
                 float wp = 0.f, xp = 0.f;
 #pragma unroll
-                for (int i = 0; i < RPT; ++i) {
+                for (int i = 0; i < kRpt; ++i) {
                     wp = fmaf(Gc[i], kc[i], wp);
-                    xp = fmaf(Gr[i], uc[i], xp);
+                    xp = fmaf(Gr[i], ur[i], xp);
                 }
-                for (int m = 1; m < RS; m <<= 1) {
+                for (int m = 1; m < RSC; m <<= 1) wp += __shfl_xor(wp, m);
+                for (int m = 1; m < RSR; m <<= 1) {
                     gqp += __shfl_xor(gqp, m);
-                    wp += __shfl_xor(wp, m);
                     xp += __shfl_xor(xp, m);
                 }
-                float* swp = sw + (t & 1) * DP;
-                if (r == 0 && ok) {
-                    swp[a] = wp;
-                    const size_t o = (static_cast<size_t>(tok0 + t) * H + h) * D + a;
-                    gq[o] = gqp;
-                    gv[o] = b * wp;
+                float* swp = sw + (t & 1) * CP;
+                const size_t orow = (static_cast<size_t>(tok0 + t) * H + h) * D;
+                if (rc == 0 && ok_c) {
+                    swp[e] = wp;
+                    gv[orow + col0 + e] = b * wp;
                 }
+                if (rr == 0 && ok_r) gq_t[orow + d] = gqp;
                 // S_{t-1} = S_t - b k u^T (row layout)
-                const float bka = b * ka;
+                const float bkd = b * kd;
 #pragma unroll
-                for (int i = 0; i < RPT; ++i) Sr[i] = fmaf(-bka, uc[i], Sr[i]);
+                for (int i = 0; i < kRpt; ++i) Sr[i] = fmaf(-bkd, ur[i], Sr[i]);
                 __syncthreads();  // w visible to the row layout
-                const float* wc = swp + r * RPT;  // w[r*RPT + i]
+                const float* wr = swp + rr * kRpt;  // w[col0 + rr*R + i]
                 float yp = 0.f;
 #pragma unroll
-                for (int i = 0; i < RPT; ++i) yp = fmaf(Sr[i], wc[i], yp);
-                for (int m = 1; m < RS; m <<= 1) yp += __shfl_xor(yp, m);
-                if (r == 0 && ok) gk[(static_cast<size_t>(tok0 + t) * H + h) * D + a] = b * (xp - yp);
+                for (int i = 0; i < kRpt; ++i) yp = fmaf(Sr[i], wr[i], yp);
+                for (int m = 1; m < RSR; m <<= 1) yp += __shfl_xor(yp, m);
+                if (rr == 0 && ok_r) gk_t[orow + d] = b * (xp - yp);
                 // gbeta = k . x, reduced over the rows held by this wave, then over waves
-                float gbp = (r == 0 && ok) ? ka * xp : 0.f;
+                float gbp = (rr == 0 && ok_r) ? kd * xp : 0.f;
                 for (int m = 1; m < 64; m <<= 1) gbp += __shfl_xor(gbp, m);
                 if (lane == 0) sgb[j * NWV + wave] = gbp;
                 // G -= b k w^T (both layouts)
 #pragma unroll
-                for (int i = 0; i < RPT; ++i) {
+                for (int i = 0; i < kRpt; ++i) {
                     Gc[i] = fmaf(-b * kc[i], wp, Gc[i]);
-                    Gr[i] = fmaf(-bka, wc[i], Gr[i]);
+                    Gr[i] = fmaf(-bkd, wr[i], Gr[i]);
                 }
             }
             __syncthreads();
             for (int j = tid; j < nst; j += blockDim.x) {
-                float s = 0.f;
-                for (int x = 0; x < NWV; ++x) s += sgb[j * NWV + x];
-                gbeta[static_cast<size_t>(tok0 + lo + j) * H + h] = s;
+                float sum = 0.f;
+                for (int x = 0; x < NWV; ++x) sum += sgb[j * NWV + x];
+                gb_t[static_cast<size_t>(tok0 + lo + j) * H + h] = sum;
             }
         }
     }
-    if (ok) {
+    if (ok_c) {
 #pragma unroll
-        for (int i = 0; i < RPT; ++i) {
-            const int x = r * RPT + i;
-            if (x < D) gs0[sbase + static_cast<size_t>(x) * D + a] = Gc[i];
+        for (int i = 0; i < kRpt; ++i) {
+            const int row = rc * kRpt + i;
+            if (row < D) gs0[sbase + static_cast<size_t>(row) * D + col0 + e] = Gc[i];
         }
     }
 }
 
-// rows-per-thread and row slices for head dimension D <= 128 (as K4)
-static void bwd_geometry(int D, int* rpt, int* rs) {
-    int r = (D <= 8) ? 8 : (D <= 16) ? 16 : 32;
-    int s = 1;
-    while (r * s < D) s <<= 1;
-    *rpt = r;
-    *rs = s;
+// out[i] = sum over tiles of part[tile * stride + i], tiles in order
+__global__ void bwd_reduce_kernel(float* __restrict__ out, const float* __restrict__ part,
+                                  size_t n, size_t stride, int n_tiles) {
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t step = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (; i < n; i += step) {
+        float s = part[i];
+        for (int t = 1; t < n_tiles; ++t) s += part[t * stride + i];
+        out[i] = s;
+    }
+}
+
+static hipError_t launch_reduce(float* out, const float* part, size_t n, size_t stride, int n_tiles,
+                                hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    size_t g = (n + 255) / 256;
+    if (g > 65536) g = 65536;
+    hipLaunchKernelGGL(bwd_reduce_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, st, out,
+                       part, n, stride, n_tiles);
+    return hipGetLastError();
 }
 
 size_t bwd_workspace_floats(long n_pairs, int T, int D) {
+    const BwdGeo g = bwd_geo(D);
     const long n_ck = (T + kCk - 1) / kCk;
-    return static_cast<size_t>(n_pairs) * (static_cast<size_t>(T) * D + static_cast<size_t>(n_ck) * D * D);
-}
-
-template <int RPT, typename InT>
-static hipError_t launch_bwd_t(const BwdArgs& a, int rs, hipStream_t st) {
-    const int threads = ((a.D * rs + 63) / 64) * 64;
-    const int dp = rs * RPT;
-    float* u_ws = a.workspace;
-    float* ck_ws = a.workspace + static_cast<size_t>(a.n_pairs) * a.T * a.D;
-    const size_t lds_a = sizeof(float) * (2 * kBwdSteps * dp + kBwdSteps);
-    hipLaunchKernelGGL((delta_bwd_ckpt_kernel<RPT, InT>), dim3(a.n_pairs), dim3(threads), lds_a, st,
-                       static_cast<const InT*>(a.k), static_cast<const InT*>(a.v), a.beta, a.s0,
-                       u_ws, ck_ws, a.T, a.H, a.D, rs);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const size_t lds_b = sizeof(float) * (4 * kBwdSteps * dp + 2 * dp + kBwdSteps + kBwdSteps * (threads / 64));
-    hipLaunchKernelGGL((delta_bwd_kernel<RPT, InT>), dim3(a.n_pairs), dim3(threads), lds_b, st,
-                       static_cast<const InT*>(a.q), static_cast<const InT*>(a.k), a.beta, a.go,
-                       a.gs, u_ws, ck_ws, a.gq, a.gk, a.gv, a.gbeta, a.gs0, a.T, a.H, a.D, rs);
-    return hipGetLastError();
+    const size_t e = static_cast<size_t>(n_pairs) * T * D, bt = static_cast<size_t>(n_pairs) * T;
+    size_t f = e + static_cast<size_t>(n_pairs) * n_ck * D * D;
+    if (g.n_tiles > 1) f += static_cast<size_t>(g.n_tiles) * (2 * e + bt);
+    return f;
 }
 
 template <typename InT>
 static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
-    int rpt, rs;
-    bwd_geometry(a.D, &rpt, &rs);
-    switch (rpt) {
-        case 8: return launch_bwd_t<8, InT>(a, rs, st);
-        case 16: return launch_bwd_t<16, InT>(a, rs, st);
-        default: return launch_bwd_t<32, InT>(a, rs, st);
-    }
+    const BwdGeo g = bwd_geo(a.D);
+    const size_t e = static_cast<size_t>(a.n_pairs) * a.T * a.D;
+    const size_t bt = static_cast<size_t>(a.n_pairs) * a.T;
+    const long n_ck = (a.T + kCk - 1) / kCk;
+    float* u_ws = a.workspace;
+    float* ck_ws = u_ws + e;
+    float* part = ck_ws + static_cast<size_t>(a.n_pairs) * n_ck * a.D * a.D;
+    const unsigned grid = static_cast<unsigned>(a.n_pairs) * g.n_tiles;
+
+    // K5a: one thread per (tile column, slice of kRpt rows)
+    const int threads_a = ((g.nc * g.rsc + 63) / 64) * 64;
+    const size_t lds_a = sizeof(float) * (kBwdSteps * g.rsc * kRpt + kBwdSteps * g.nc + kBwdSteps);
+    hipLaunchKernelGGL((delta_bwd_ckpt_kernel<InT>), dim3(grid), dim3(threads_a), lds_a, st,
+                       static_cast<const InT*>(a.k), static_cast<const InT*>(a.v), a.beta, a.s0,
+                       u_ws, ck_ws, a.T, a.H, a.D, g.nc, g.n_tiles, g.rsc);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+
+    const bool split = g.n_tiles > 1;
+    float* gq = split ? part : a.gq;
+    float* gk = split ? part + static_cast<size_t>(g.n_tiles) * e : a.gk;
+    float* gb = split ? part + static_cast<size_t>(2 * g.n_tiles) * e : a.gbeta;
+    const int dp = g.rsc * kRpt, cp = g.rsr * kRpt;
+    const size_t lds_b = sizeof(float) * (2 * kBwdSteps * dp + 2 * kBwdSteps * cp + 2 * cp +
+                                          kBwdSteps + kBwdSteps * (g.threads / 64));
+    hipLaunchKernelGGL((delta_bwd_kernel<InT>), dim3(grid), dim3(g.threads), lds_b, st,
+                       static_cast<const InT*>(a.q), static_cast<const InT*>(a.k), a.beta, a.go,
+                       a.gs, u_ws, ck_ws, gq, gk, a.gv, gb, a.gs0, a.T, a.H, a.D, g.nc, g.n_tiles,
+                       g.rsc, g.rsr, split ? e : 0, split ? bt : 0);
+    err = hipGetLastError();
+    if (err != hipSuccess || !split) return err;
+    if ((err = launch_reduce(a.gq, gq, e, e, g.n_tiles, st)) != hipSuccess) return err;
+    if ((err = launch_reduce(a.gk, gk, e, e, g.n_tiles, st)) != hipSuccess) return err;
+    return launch_reduce(a.gbeta, gb, bt, bt, g.n_tiles, st);
 }
 
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t st) {

@@ -59,7 +59,9 @@ hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st);
 
 // Reverse mode (K5, fp32): fixed-length batch of n_pairs = B*H sequences of
 // T tokens, D <= 128.  workspace holds bwd_workspace_floats(n_pairs, T, D)
-// floats: u (n_pairs x T x D) then the checkpoints (n_pairs x ceil(T/8) x D x D).
+// floats: u (n_pairs x T x D), the checkpoints (n_pairs x ceil(T/8) x D x D),
+// then for D > 32 the per-column-tile partial sums of gq, gk (ceil(D/32) x
+// n_pairs x T x D each) and gbeta (ceil(D/32) x n_pairs x T).
 struct BwdArgs {
     const void* q;
     const void* k;

@@ -109,8 +109,9 @@ def test_bwd_shape_checks_raise_before_any_device_work():
 def test_bwd_workspace_bytes():
     lib = _native.lib()
     for b, t, h, d in [(1, 1, 1, 3), (2, 130, 3, 64), (4, 4096, 16, 128), (1, 0, 2, 8)]:
-        n_ck = -(-t // 8)
-        assert lib.pm_delta_bwd_workspace_bytes(b, t, h, d) == 4 * b * h * (t * d + n_ck * d * d)
+        n_ck, n_tiles = -(-t // 8), -(-d // 32)
+        part = n_tiles * t * (2 * d + 1) if n_tiles > 1 else 0
+        assert lib.pm_delta_bwd_workspace_bytes(b, t, h, d) == 4 * b * h * (t * d + n_ck * d * d + part)
     assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 129) == 0
     assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 0) == 0
 

@@ -6,8 +6,8 @@ Mirrors the reference's backward tests: the seeded fwd->bwd cases with
 random go / gs (tests/test_kernels_delta_fwd_jit.py:284-347, seeds 105 and
 106), the finite-difference test of the gradients (tests/test_kernels.py:
 409-432, seed 18), plus the shapes this build adds: head dimensions up to
-128 with padded row slices, sequences across several 64-token checkpoint
-blocks, bf16 q/k/v, missing cotangents, T = 0 and repeatability.
+128 with padded row slices and ragged 32-column tiles of the state,
+sequences across several checkpoint blocks, bf16 q/k/v, missing cotangents, T = 0 and repeatability.
 
 Tolerance: fp32 (tests/parity.py), rel-L2 <= 1e-5 and max-abs <= 1e-4
 (scaled), against the fp64 oracle on the same (for bf16: bf16-rounded)
@@ -111,7 +111,7 @@ def test_finite_differences_of_the_gpu_forward():
 
 
 @pytest.mark.parametrize("shape", [(1, 1, 1, 8), (2, 63, 2, 16), (1, 65, 2, 48), (1, 200, 2, 64),
-                                   (2, 130, 1, 128)])
+                                   (2, 130, 1, 128), (1, 17, 2, 33), (1, 20, 1, 100)])
 @pytest.mark.parametrize("state", [True, False])
 def test_shapes_across_checkpoint_blocks(shape, state):
     x = synth.fwd_inputs(shape, seed=sum(shape) + state, dtype="fp32",

@@ -261,7 +261,7 @@ def main():
         gq, gk, gv = (torch.empty((B, T, H, D), device=dev) for _ in range(3))
         gb = torch.empty((B, T, H), device=dev)
         gs0 = torch.empty((B, H, D, D), device=dev)
-        nbytes = lib.pm_delta_bwd_workspace_bytes(B, T, H, D)
+        nbytes = lib.pm_delta_bwd_workspace_bytes(B, T, H, D, _native.DTYPE_BF16)
         ws = torch.empty(((nbytes + 3) // 4,), device=dev)
 
         def bwd():

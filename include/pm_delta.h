@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 1
+#define PM_DELTA_ABI_VERSION 2
 
 /* element types */
 #define PM_DTYPE_F32 0
@@ -117,12 +117,21 @@ size_t pm_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype);
  *   s0 NULL means a zero initial state;
  *   gq, gk, gv (B, T, H, D), gbeta (B, T, H), gs0 (B, H, D, D): fp32 outputs.
  * q, k, v are fp32 or bf16 (in_dtype); 1 <= D <= 128.
+ * Two kernels, chosen as the forward's are (pm_delta_set_path):
+ *   - bf16 q/k/v with D in {64, 128}: the chunked backward on bf16 MFMA
+ *     (the forward's chunked kernel in reverse; bf16 parity, rel-L2 <= 2e-2
+ *     against the fp32 reference).  q, k, v, go and workspace 16-byte
+ *     aligned.  Workspace, per (b, h) and 64-token chunk: the chunk's start
+ *     state and end state gradient and W (bf16), and three packed 64x64
+ *     operands: 2 * B * H * ceil(T / 64) * (2 * D * D + 64 * D + 9216) bytes.
+ *   - otherwise the per-token fp32 backward (fp32 parity).  Workspace:
+ *     per-token u = v - S^T k and the state every 8 tokens, 4 * B * H *
+ *     (T * D + ceil(T / 8) * D * D) bytes, and for D > 32 the partial sums
+ *     of gq, gk and gbeta over 32-column tiles of the state, 4 * B * H * T
+ *     * ceil(D / 32) * (2 * D + 1) bytes more.
  * workspace: device memory of at least pm_delta_bwd_workspace_bytes(B, T,
- * H, D) bytes, 4-byte aligned, contents undefined on entry and exit
- * (per-token u = v - S^T k and the state every 8 tokens: 4 * B * H *
- * (T * D + ceil(T / 8) * D * D) bytes; for D > 32 also the partial sums
- * of gq, gk and gbeta over 32-column tiles of the state: 4 * B * H * T *
- * ceil(D / 32) * (2 * D + 1) bytes more).
+ * H, D, in_dtype) bytes (queried under the same path setting), 4-byte
+ * aligned, contents undefined on entry and exit.
  * T == 0 gives gs0 = gs (or zeros).
  */
 int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
@@ -130,8 +139,9 @@ int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
                  float* gv, float* gbeta, float* gs0, int B, int T, int H, int D, int in_dtype,
                  void* workspace, size_t ws_bytes, void* stream);
 
-/* Workspace bytes pm_delta_bwd needs (0 for invalid shapes or D > 128). */
-size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D);
+/* Workspace bytes pm_delta_bwd needs for these shapes and in_dtype under the
+ * current path setting (0 for invalid shapes, dtypes or D > 128). */
+size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype);
 
 /* Thread-local message for the last nonzero return on this thread. */
 const char* pm_last_error(void);
@@ -140,11 +150,11 @@ const char* pm_last_error(void);
 int pm_abi_version(void);
 
 /*
- * Kernel selection for pm_delta_fwd / pm_delta_fwd_varlen, for tests and
- * benchmarks: 0 = automatic (chunked MFMA kernel where the shape and dtype
- * allow, else the per-token kernel), 1 = always the per-token kernel,
- * 2 = chunked kernel required (PM_E_UNSUPPORTED when it cannot serve the
- * call).  The previous value is returned.  Process-wide.
+ * Kernel selection for pm_delta_fwd, pm_delta_fwd_varlen and pm_delta_bwd,
+ * for tests and benchmarks: 0 = automatic (chunked MFMA kernel where the
+ * shape and dtype allow, else the per-token kernel), 1 = always the
+ * per-token kernel, 2 = chunked kernel required (PM_E_UNSUPPORTED when it
+ * cannot serve the call).  The previous value is returned.  Process-wide.
  */
 int pm_delta_set_path(int path);
 

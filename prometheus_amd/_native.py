@@ -18,7 +18,7 @@ import torch  # noqa: F401  (see module docstring: must precede CDLL)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpmdelta.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256
@@ -78,7 +78,7 @@ def lib() -> ctypes.CDLL:
         L.pm_delta_workspace_bytes.restype = sz
         L.pm_delta_bwd.argtypes = [vp] * 12 + [i] * 5 + [vp, sz, vp]
         L.pm_delta_bwd.restype = i
-        L.pm_delta_bwd_workspace_bytes.argtypes = [i, i, i, i]
+        L.pm_delta_bwd_workspace_bytes.argtypes = [i, i, i, i, i]
         L.pm_delta_bwd_workspace_bytes.restype = sz
         L.pm_last_error.argtypes = []
         L.pm_last_error.restype = ctypes.c_char_p

@@ -52,208 +52,11 @@
 // Numerics: q/k/v bf16, every product fp32-accumulated; T, P, R, U and the
 // MFMA copy of S are rounded to bf16; S itself is carried in fp32.
 
-#include "pm_common.h"
+#include "pm_cdna4.h"
 #include "pm_internal.h"
 
 namespace pm {
 namespace {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-
-constexpr int kC = 64;  // chunk length (tokens)
-// Buffer descriptor word 3 for raw (untyped, unswizzled) gfx9 buffer access.
-constexpr int kRsrcWord3 = 0x00020000;
-
-__device__ __forceinline__ f32x4_t mfma32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x4_t mfma16(u32x2_t a, u32x2_t b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, a),
-                                                     __builtin_bit_cast(bf16x4_t, b), c, 0, 0, 0);
-}
-
-// bf16 operands are assembled from 16-bit patterns packed into 32-bit
-// words and bit-cast to the MFMA vector type only at the call: element
-// access on bf16 vectors (extract or insert) is avoided on purpose, since
-// hipcc (ROCm 7.2) miscompiled an element extract feeding a 16-bit LDS store.
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-// Two floats -> packed bf16 pair (round to nearest even) in one v_cvt_pk_bf16_f32.
-__device__ __forceinline__ unsigned pack2(float a, float b) {
-    const f32x2_t v = {a, b};
-    return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2_t));
-}
-__device__ __forceinline__ unsigned pack_rne(float a, float b) {
-    return static_cast<unsigned>(f32_to_bf16(a)) | (static_cast<unsigned>(f32_to_bf16(b)) << 16);
-}
-__device__ __forceinline__ u32x2_t cvt4(f32x4_t x) {
-    const u32x2_t r = {pack2(x.x, x.y), pack2(x.z, x.w)};
-    return r;
-}
-// Two stacked accumulator tiles (rows 0-15 and 16-31 of a 32-block) as a B operand.
-__device__ __forceinline__ bf16x8_t acc_to_b(f32x4_t lo, f32x4_t hi) {
-    const u32x4_t r = {pack2(lo.x, lo.y), pack2(lo.z, lo.w), pack2(hi.x, hi.y), pack2(hi.z, hi.w)};
-    return __builtin_bit_cast(bf16x8_t, r);
-}
-__device__ __forceinline__ f32x4_t widen4(u32x2_t v) {
-    const f32x4_t r = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
-                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
-    return r;
-}
-
-// LDS layout of a token-major tile (K or Q: D bf16 per row, V: DV per row).
-// Rows have no padding; the 16-byte chunk c of row r is stored at chunk
-// c ^ f(r), with f depending on r mod 16 only.  The copies (1 KiB contiguous
-// per instruction) are conflict-free for any f.  f was chosen by measuring
-// SQ_LDS_BANK_CONFLICT on gfx950 for the two patterns that read these tiles:
-//   * 16-byte MFMA operand reads (lane (g, l16): row l16, chunk (4kb+g) ^ f);
-//   * 8-byte transpose reads of K^T (lanes 4j+cc of group g: row 4g+j,
-//     chunk (4kb+cc) ^ f).
-// D = 128 (16 chunks per row): the table below makes the operand reads
-// conflict-free (3.9 LDS cycles per instruction instead of 7.7) and costs the
-// transpose reads 5.8 cycles instead of 3.9; no f of the 4096 tried makes
-// both conflict-free, and the operand reads are twice as frequent.
-// D = 64 (8 chunks per row): f(r) = r mod 8 makes both conflict-free.
-template <int D>
-__device__ __forceinline__ int kq_f(int r) {
-    if constexpr (D == 128) return static_cast<int>((0x45AD27F936E8CB01ull >> (4 * (r & 15))) & 15);
-    else return r & 7;
-}
-template <int DV>
-__device__ __forceinline__ int v_f(int r) {
-    if constexpr (DV == 32) return 2 * ((r >> 2) & 1);  // rows r and r+4 share banks
-    else return 0;                                       // 8 rows of 32 bytes cover all banks
-}
-
-// Contraction over d.  In every product that contracts over d (X = K S,
-// Y^T = S^T Q^T, K K^T, Q K^T) lane group g's 8 slots of 32-block kb are
-// d = 32 kb + 8 g + [0, 8): one 16-byte chunk of a K/Q row.  To match,
-// accumulator tile md = 2 kb + h of S holds the rows
-//     d = 32 kb + 8 (r / 4) + 4 h + r % 4,   r = 0..15,
-// so that acc_to_b(S[2 kb], S[2 kb + 1]) puts exactly those d in the slots.
-__device__ __forceinline__ int s_row_d(int md, int r) {
-    return 32 * (md >> 1) + 8 * (r >> 2) + 4 * (md & 1) + (r & 3);
-}
-// Operand (A or B) over d from a swizzled K/Q tile: row `row`, 32-block kb, lane group g.
-template <int D>
-__device__ __forceinline__ bf16x8_t lds_op_kq(const uint16_t* m, int row, int kb, int g) {
-    return __builtin_bit_cast(bf16x8_t,
-                              *reinterpret_cast<const u32x4_t*>(m + row * D + 8 * ((4 * kb + g) ^ kq_f<D>(row))));
-}
-
-// ds_read_b64_tr_b16: within each 16-lane group, the four 4-element rows
-// addressed by lanes 4j..4j+3 (16 consecutive elements of row j) are
-// transposed: lane i receives element i of rows 0..3.
-//
-// Issued as inline asm: the compiler's intrinsic for it carries no LDS
-// memory operand, so hipcc (ROCm 7.2) puts a vmcnt(0) wait -- for every
-// pending global store -- in front of it.  The asm form is asynchronous:
-// results are valid only after lds_wait() takes them as operands.
-__device__ __forceinline__ unsigned lds_addr(const void* p) {
-    typedef __attribute__((address_space(3))) const void lds_cvoid_t;
-    return static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_cvoid_t*)(p)));
-}
-template <int OFFSET>
-__device__ __forceinline__ u32x2_t lds_tr16_issue(unsigned addr) {
-    u32x2_t r;
-    __asm__ volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFFSET) : "memory");
-    return r;
-}
-// Wait for all of this wave's LDS reads; x's registers are tied to the wait
-// so that no use of them is scheduled before it.
-__device__ __forceinline__ void lds_wait(u32x2_t& a, u32x2_t& b, u32x2_t& c, u32x2_t& d) {
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : : "memory");
-}
-__device__ __forceinline__ void lds_wait(u32x4_t& a, u32x4_t& b, u32x4_t& c, u32x4_t& d, u32x4_t& e,
-                                         u32x4_t& f, u32x4_t& g, u32x4_t& h) {
-    __asm__ volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f), "+v"(g), "+v"(h)
-                     :
-                     : "memory");
-}
-// A operand of K^T for S tile md (rows d = s_row_d(md, l16), contraction
-// over tokens K0 + {4g..4g+3, 16+4g..16+4g+3}) from the token-major K
-// tile: two transpose reads, 16 rows apart (kq_f(t + 16) == kq_f(t)); the
-// four lanes 4j + cc of a group address d = 32 kb + 8 cc + 4 h + [0, 4).
-template <int D, int K0>
-__device__ __forceinline__ u32x4_t lds_kt_issue(const uint16_t* Ks, int md, int lane) {
-    const int g = lane >> 4, j = (lane >> 2) & 3, cc = lane & 3;
-    const int t = K0 + 4 * g + j;
-    const unsigned a = lds_addr(Ks + t * D + 8 * ((4 * (md >> 1) + cc) ^ kq_f<D>(t)) + 4 * (md & 1));
-    const u32x2_t lo = lds_tr16_issue<0>(a), hi = lds_tr16_issue<16 * D * 2>(a);
-    const u32x4_t v = {lo.x, lo.y, hi.x, hi.y};
-    return v;
-}
-// V in accumulator layout: lane (g, l16) gets V[16m + 4g + i][16w + l16], i < 4
-// (bf16 pairs; widen4 after lds_wait).
-template <int DV>
-__device__ __forceinline__ u32x2_t lds_v_issue(const uint16_t* Vs, int m, int w, int lane) {
-    const int g = lane >> 4, j = (lane >> 2) & 3, cc = lane & 3;
-    const int t = 16 * m + 4 * g + j;
-    return lds_tr16_issue<0>(lds_addr(Vs + t * DV + 8 * ((2 * w + (cc >> 1)) ^ v_f<DV>(t)) + 4 * (cc & 1)));
-}
-
-// Packed operand layout of the 64x64 lower-triangular T and P: operand
-// block q holds rows 16m.. and contraction block kb (32 columns) for
-// (m, kb) in (0,0) (1,0) (2,0) (2,1) (3,0) (3,1); lane L's 8 values are
-// contiguous at q*512 + L*8 (bf16 elements).
-__device__ __forceinline__ int qblk(int m, int kb) { return m < 2 ? m : 2 * m - 2 + kb; }
-
-__device__ __forceinline__ bf16x8_t packed_a(const uint16_t* buf, int q, int lane) {
-    return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(buf + q * 512 + lane * 8));
-}
-
-// Store block (i, j) of a 64x64 matrix M into the packed operand layout,
-// given the accumulator tile of its transpose (lane (g, l16) holds
-// M[16i+l16][16j+4g+r], r<4): those are exactly this lane's operand slots
-// 4(j&1)..4(j&1)+3, so one 8-byte write per lane, contiguous across the wave.
-__device__ __forceinline__ void store_packed_t(uint16_t* buf, int i, int j, f32x4_t acc_t, int lane) {
-    *reinterpret_cast<u32x2_t*>(buf + qblk(i, j >> 1) * 512 + lane * 8 + 4 * (j & 1)) = cvt4(acc_t);
-}
-// Zero the upper 16-column half of operand block q (T/P blocks (0,1), (2,3)).
-__device__ __forceinline__ void zero_upper_half(uint16_t* buf, int q, int lane) {
-    const u32x2_t z = {0u, 0u};
-    *reinterpret_cast<u32x2_t*>(buf + q * 512 + lane * 8 + 4) = z;
-}
-
-// Wave-uniform values made visibly uniform (SGPRs), so that buffer
-// descriptors and role branches are scalar rather than per-lane.
-__device__ __forceinline__ unsigned uniform(unsigned x) { return __builtin_amdgcn_readfirstlane(x); }
-template <typename T>
-__device__ __forceinline__ T* uniform_ptr(T* p) {
-    const unsigned long long u = reinterpret_cast<unsigned long long>(p);
-    const unsigned long long lo = uniform(static_cast<unsigned>(u));
-    const unsigned long long hi = uniform(static_cast<unsigned>(u >> 32));
-    return reinterpret_cast<T*>((hi << 32) | lo);
-}
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(const_cast<void*>(base)), 0, uniform(bytes),
-                                             kRsrcWord3);
-}
-
-// Asynchronous copy of 16 (or 4) bytes per lane from a buffer to LDS:
-// lane L's bytes land at dst + L * size (dst wave-uniform).
-__device__ __forceinline__ void copy_to_lds(__amdgpu_buffer_rsrc_t rsrc, void* dst, int size,
-                                            unsigned voffset) {
-    typedef __attribute__((address_space(3))) void lds_void_t;
-    if (size == 16)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(dst), 16, voffset, 0, 0, 0);
-    else
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(dst), 4, voffset, 0, 0, 0);
-}
-
-// LDS-only workgroup barrier: waits for this wave's LDS traffic, never for
-// global loads or stores still in flight.
-__device__ __forceinline__ void lds_barrier() {
-    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-// Wait for this wave's outstanding buffer loads (and so its LDS copies).
-__device__ __forceinline__ void wait_copies() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 template <int D, int DV>
 struct Geo {
@@ -278,12 +81,17 @@ struct Geo {
     static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
-template <int D, int DV, bool OUT_BF16>
+// HIST: the backward's state recompute.  Instead of O and the final state,
+// each chain wave writes the state at the start of every chunk, rounded to
+// bf16, as rows of S^T: s_hist[(pair * n_chunks + c) * D * D + col * D + d]
+// (fixed-length batches only).
+template <int D, int DV, bool OUT_BF16, bool HIST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void delta_chunked_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ beta,
     const float* __restrict__ s0, void* __restrict__ o_out, float* __restrict__ s_out,
-    const int32_t* __restrict__ cu_seqlens, int n_pairs, int T, int H, int n_tiles) {
+    uint16_t* __restrict__ s_hist, const int32_t* __restrict__ cu_seqlens, int n_pairs, int T,
+    int H, int n_tiles) {
     using G = Geo<D, DV>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
@@ -562,6 +370,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
         const int base = c * kC;
         const int clen = min(kC, len - base);
+        if constexpr (HIST) {
+            uint16_t* hp = s_hist + (static_cast<size_t>(pair) * n_chunks + c) * D * D +
+                           static_cast<size_t>(ecol) * D;
+#pragma unroll
+            for (int md = 0; md < D / 16; ++md)
+                *reinterpret_cast<u32x2_t*>(hp + s_row_d(md, 4 * lg)) = cvt4(S[md]);
+        }
         // X = K S (token rows) and Y^T = S^T Q^T (column rows: lane holds 4 columns of a token)
         f32x4_t X[4], Y[4];
 #pragma unroll
@@ -630,7 +445,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int t = 16 * m + l16;
-            if (t < clen) {
+            if (!HIST && t < clen) {
                 const size_t a = (tok0 + base + t) * tstride + static_cast<size_t>(h) * D + ocol;
                 if constexpr (OUT_BF16) {
                     const u32x2_t ob = {pack_rne(O[m].x, O[m].y), pack_rne(O[m].z, O[m].w)};
@@ -676,7 +491,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
     }
 
-    if (chain) {
+    if (chain && !HIST) {
 #pragma unroll
         for (int md = 0; md < D / 16; ++md) {
 #pragma unroll
@@ -688,10 +503,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
-template <int D, int DV, bool OB>
-hipError_t launch_t(const ChunkedArgs& a, hipStream_t st) {
+template <int D, int DV, bool OB, bool HIST>
+hipError_t launch_t(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
     using G = Geo<D, DV>;
-    auto kern = delta_chunked_kernel<D, DV, OB>;
+    auto kern = delta_chunked_kernel<D, DV, OB, HIST>;
     // the dynamic-LDS limit is a per-device function attribute
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -708,13 +523,14 @@ hipError_t launch_t(const ChunkedArgs& a, hipStream_t st) {
     const int slots = (n_pairs + 7) / 8;
     const dim3 grid(static_cast<unsigned>(slots * 8 * n_tiles));
     hipLaunchKernelGGL(kern, grid, dim3(256), G::BYTES, st, a.q, a.k, a.v, a.beta, a.s0, a.o,
-                       a.s_out, a.cu_seqlens, n_pairs, a.T, a.H, n_tiles);
+                       a.s_out, s_hist, a.cu_seqlens, n_pairs, a.T, a.H, n_tiles);
     return hipGetLastError();
 }
 
 template <int D, int DV>
 hipError_t launch_dv(const ChunkedArgs& a, hipStream_t st) {
-    return a.out_bf16 ? launch_t<D, DV, true>(a, st) : launch_t<D, DV, false>(a, st);
+    return a.out_bf16 ? launch_t<D, DV, true, false>(a, nullptr, st)
+                      : launch_t<D, DV, false, false>(a, nullptr, st);
 }
 
 // Tile width: 32 columns (two chain waves) unless that leaves CUs idle.
@@ -738,6 +554,18 @@ hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st) {
     const int dv = pick_tile(a.D, n_pairs, a.dv_tile);
     if (a.D == 128) return dv == 16 ? launch_dv<128, 16>(a, st) : launch_dv<128, 32>(a, st);
     return dv == 16 ? launch_dv<64, 16>(a, st) : launch_dv<64, 32>(a, st);
+}
+
+hipError_t launch_chunked_states(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
+    const long n_pairs = static_cast<long>(a.n_seq) * a.H;
+    if (n_pairs == 0) return hipSuccess;
+    if (!chunked_supported(a.D, a.H) || a.cu_seqlens) return hipErrorInvalidValue;
+    const int dv = pick_tile(a.D, n_pairs, a.dv_tile);
+    if (a.D == 128)
+        return dv == 16 ? launch_t<128, 16, false, true>(a, s_hist, st)
+                        : launch_t<128, 32, false, true>(a, s_hist, st);
+    return dv == 16 ? launch_t<64, 16, false, true>(a, s_hist, st)
+                    : launch_t<64, 32, false, true>(a, s_hist, st);
 }
 
 }  // namespace pm

@@ -1,0 +1,826 @@
+// delta_chunked_bwd.hip — K6: reverse mode of the chunked forward on bf16
+// MFMA (bf16 q/k/v, D in {64, 128}).
+//
+// Gradients of the reference's backward (kernels/__init__.py:692-719 ->
+// _delta_vjp_np :460-527) restated per chunk of C = 64 tokens.  With the
+// chunk's start state S, T = (I + A)^-1, A = strict_lower(diag(beta) K K^T),
+// X = diag(beta)(V - K S), U = T X, P = lower_incl(Q K^T), the forward is
+//     O = Q S + P U,      S_next = S + K^T U.
+// Given G = dL/dS_next and dO, the reverse of one chunk is
+//     W   = T^T (K G + P^T dO)                  (= dL/dX)
+//     dS  = G + Q^T dO - K^T diag(beta) W       (G of the previous chunk)
+//     dV  = diag(beta) W
+//     dP  = lower_incl(dO U^T),   dA = -strict_lower(W U^T)
+//     dQ  = dO S^T + dP K
+//     dK  = U G^T + dP^T Q - diag(beta) W S^T + diag(beta) dA K + dA^T diag(beta) K
+//     dbeta_t = W_t . (v_t - S^T k_t) + sum_{s<t} dA_ts (k_t . k_s)
+// (dT = dU X^T and dA = -T^T dT T^T = -W U^T.)  Only the state gradient G
+// is carried from chunk to chunk; everything else is local to a chunk once
+// its start state S and end gradient G are known.  Four launches:
+//   1. the forward kernel in its state-history mode writes every chunk's S
+//      (bf16, as rows of S^T);
+//   2. bwd_prep_kernel, one wave per chunk: T (the forward's builder), and
+//      T^T and P^T, in packed MFMA operand order;
+//   3. bwd_rev_kernel walks the chunks backwards per (b, h, 64 columns of
+//      d_v) carrying G in fp32 MFMA accumulators (the columns of G are
+//      independent), writes G_c (bf16, rows of G^T), W (bf16, rows of W^T),
+//      dV and finally dS_0;
+//   4. bwd_grad_kernel, one workgroup per chunk, all chunks in parallel:
+//      dQ, dK and dbeta from S_c, G_c, W and the chunk's q/k/v/beta.
+// Numerics as in the forward: bf16 operands, fp32 accumulation; G and the
+// outputs stay fp32.
+//
+// Operand orders.  An MFMA A (B) operand gives lane (g, l16) 8 values of row
+// (column) l16 along the contraction.  Operands read from LDS use the
+// natural order (slots = 8g .. 8g+7 of a 32-block): rows read directly
+// (16 bytes, lds_op_kq) and columns read through the LDS transpose
+// (lds_col_issue).  Operands built from accumulators (acc_to_b) and the
+// packed 64x64 blocks use the order {4g..4g+3, 16+4g..16+4g+3}, and are only
+// ever paired with each other or with the forward's K^T reads (lds_kt_issue).
+
+#include "pm_cdna4.h"
+#include "pm_internal.h"
+
+namespace pm {
+namespace {
+
+constexpr int kPacked = 6 * 512;  // bf16 elements of one packed 64x64 triangular operand
+
+// Packed index of the upper-triangular operands (T^T, P^T): block (m, kb)
+// for (0,0) (0,1) (1,0) (1,1) (2,1) (3,1).
+__device__ __forceinline__ int qblk_u(int m, int kb) { return m < 2 ? 2 * m + kb : m + 2; }
+
+// Ties registers filled by asynchronous LDS reads to a wait for all of them.
+__device__ __forceinline__ void lds_wait_all() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <typename V>
+__device__ __forceinline__ void tie(V& x) {
+    __asm__ volatile("" : "+v"(x));
+}
+
+// Natural-order column operand from a swizzled tile with rows of RL
+// elements: lane (g, l16) gets M[r0 + 8g + i][c0 + l16], i < 8 (two
+// transpose reads; valid after lds_wait_all + tie).
+template <int RL>
+__device__ __forceinline__ u32x4_t lds_col_issue(const uint16_t* M, int r0, int c0, int lane) {
+    const int g = lane >> 4, j = (lane >> 2) & 3, cc = lane & 3;
+    const int col = c0 + 4 * cc;
+    const int ra = r0 + 8 * g + j, rb = ra + 4;
+    const u32x2_t lo = lds_tr16_issue<0>(lds_addr(M + ra * RL + 8 * ((col >> 3) ^ kq_f<RL>(ra)) + (col & 7)));
+    const u32x2_t hi = lds_tr16_issue<0>(lds_addr(M + rb * RL + 8 * ((col >> 3) ^ kq_f<RL>(rb)) + (col & 7)));
+    const u32x4_t v = {lo.x, lo.y, hi.x, hi.y};
+    return v;
+}
+// Accumulator-layout tile: lane (g, l16) gets M[r0 + 4g + i][c0 + l16], i < 4.
+template <int RL>
+__device__ __forceinline__ u32x2_t lds_acc_issue(const uint16_t* M, int r0, int c0, int lane) {
+    const int g = lane >> 4, j = (lane >> 2) & 3, cc = lane & 3;
+    const int col = c0 + 4 * cc, r = r0 + 4 * g + j;
+    return lds_tr16_issue<0>(lds_addr(M + r * RL + 8 * ((col >> 3) ^ kq_f<RL>(r)) + (col & 7)));
+}
+// Element offset of M[r][c .. c+3] in a swizzled tile (c a multiple of 4).
+template <int RL>
+__device__ __forceinline__ int swz(int r, int c) {
+    return r * RL + 8 * ((c >> 3) ^ kq_f<RL>(r)) + (c & 7);
+}
+__device__ __forceinline__ bf16x8_t as_b(u32x4_t x) { return __builtin_bit_cast(bf16x8_t, x); }
+
+// Copy n_instr KiB of a tile of rows of RL bf16 (rows src_row_bytes apart
+// in the buffer) into a swizzled LDS tile; instruction ii (taken by wave
+// ii % nw) fills LDS bytes [1024 ii, +1024).
+template <int RL>
+__device__ __forceinline__ void copy_rows(__amdgpu_buffer_rsrc_t rs, unsigned char* dst, int n_instr,
+                                          unsigned src_row_bytes, int w, int nw, int lane) {
+    for (int ii = w; ii < n_instr; ii += nw) {
+        const int pos = 512 * ii + 8 * lane;
+        const int r = pos / RL, p = (pos % RL) / 8;
+        copy_to_lds(rs, dst + 1024 * ii, 16, static_cast<unsigned>(r) * src_row_bytes + 16u * (p ^ kq_f<RL>(r)));
+    }
+}
+// Copy n_instr contiguous KiB (no swizzle).
+__device__ __forceinline__ void copy_flat(__amdgpu_buffer_rsrc_t rs, unsigned char* dst, int n_instr, int w,
+                                          int nw, int lane) {
+    for (int ii = w; ii < n_instr; ii += nw)
+        copy_to_lds(rs, dst + 1024 * ii, 16, static_cast<unsigned>(1024 * ii + 16 * lane));
+}
+
+// ---------------------------------------------------------------------------
+// 2. prep: packed T, T^T and P^T of one chunk (one wave)
+// ---------------------------------------------------------------------------
+template <int D>
+struct PrepGeo {
+    static constexpr int KS = 0;
+    static constexpr int QS = KS + kC * D * 2;
+    static constexpr int BS = QS + kC * D * 2;
+    static constexpr int TP = BS + kC * 4;
+    static constexpr int BYTES = TP + kPacked * 2;
+};
+
+template <int D>
+__global__ __launch_bounds__(64) void bwd_prep_kernel(const uint16_t* __restrict__ q,
+                                                      const uint16_t* __restrict__ k,
+                                                      const float* __restrict__ beta,
+                                                      uint16_t* __restrict__ tp_ws, int T, int H,
+                                                      int n_ch) {
+    using G = PrepGeo<D>;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int pair = blockIdx.x / n_ch, c = blockIdx.x % n_ch;
+    const int seq = pair / H, h = pair % H;
+    const int lane = threadIdx.x, l16 = lane & 15, lg = lane >> 4;
+    const int base = c * kC, clen = min(kC, T - base);
+    const size_t tstride = static_cast<size_t>(H) * D;
+    const size_t row0 = (static_cast<size_t>(seq) * T + base) * tstride + static_cast<size_t>(h) * D;
+    const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
+    const unsigned n_b = static_cast<unsigned>(((clen - 1) * H + 1) * 4);
+    copy_rows<D>(make_rsrc(k + row0, n_kq), smem + G::KS, kC * D * 2 / 1024,
+                 static_cast<unsigned>(tstride * 2), 0, 1, lane);
+    copy_rows<D>(make_rsrc(q + row0, n_kq), smem + G::QS, kC * D * 2 / 1024,
+                 static_cast<unsigned>(tstride * 2), 0, 1, lane);
+    copy_to_lds(make_rsrc(beta + (static_cast<size_t>(seq) * T + base) * H + h, n_b), smem + G::BS, 4,
+                static_cast<unsigned>(lane * H * 4));
+    wait_copies();
+    __syncthreads();
+
+    uint16_t* Tp = reinterpret_cast<uint16_t*>(smem + G::TP);
+    build_t_packed<D, G::KS, G::BS>(smem, Tp, lane);
+    __syncthreads();
+
+    uint16_t* out = tp_ws + (static_cast<size_t>(pair) * n_ch + c) * 3 * kPacked;
+    // packed T as built
+#pragma unroll
+    for (int x = 0; x < 6; ++x)
+        *reinterpret_cast<u32x4_t*>(out + x * 512 + lane * 8) =
+            *reinterpret_cast<const u32x4_t*>(Tp + x * 512 + lane * 8);
+    // packed T^T: lane (g, l16), slot x of block (m, kb) = T[32kb + o(g, x)][16m + l16]
+    auto t_at = [&](int i, int kk) -> uint16_t {  // T[i][kk] from the packed T (0 above the diagonal)
+        if (kk > i) return 0;
+        const int gg = (kk & 15) >> 2, x = (kk & 3) + 4 * ((kk >> 4) & 1);
+        return Tp[qblk(i >> 4, kk >> 5) * 512 + (16 * gg + (i & 15)) * 8 + x];
+    };
+    const int mk[6][2] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}, {2, 1}, {3, 1}};
+#pragma unroll
+    for (int b = 0; b < 6; ++b) {
+        const int m = mk[b][0], kb = mk[b][1];
+        const int s = 16 * m + l16;
+        unsigned wds[4];
+#pragma unroll
+        for (int x = 0; x < 8; x += 2) {
+            const int t0 = 32 * kb + (x < 4 ? 4 * lg + x : 12 + 4 * lg + x);
+            wds[x / 2] = static_cast<unsigned>(t_at(t0, s)) | (static_cast<unsigned>(t_at(t0 + 1, s)) << 16);
+        }
+        const u32x4_t v = {wds[0], wds[1], wds[2], wds[3]};
+        *reinterpret_cast<u32x4_t*>(out + kPacked + qblk_u(m, kb) * 512 + lane * 8) = v;
+    }
+    // packed P^T: the accumulator tile of Q_j K_i^T (lane: P[16j + 4g + r][16i + l16])
+    // is block (i, j) of P^T in the form the packed store takes
+    const uint16_t* Ks = reinterpret_cast<const uint16_t*>(smem + G::KS);
+    const uint16_t* Qs = reinterpret_cast<const uint16_t*>(smem + G::QS);
+    uint16_t* pt = out + 2 * kPacked;
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = i; j < 4; ++j) {
+            f32x4_t acc = zero;
+#pragma unroll
+            for (int kb = 0; kb < D / 32; ++kb)
+                acc = mfma32(lds_op_kq<D>(Qs, 16 * j + l16, kb, lg), lds_op_kq<D>(Ks, 16 * i + l16, kb, lg), acc);
+            if (i == j) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] = (4 * lg + r >= l16) ? acc[r] : 0.f;
+            }
+            *reinterpret_cast<u32x2_t*>(pt + qblk_u(i, j >> 1) * 512 + lane * 8 + 4 * (j & 1)) = cvt4(acc);
+        }
+    }
+    const u32x2_t z2 = {0u, 0u};
+    *reinterpret_cast<u32x2_t*>(pt + qblk_u(1, 0) * 512 + lane * 8) = z2;  // t < 16 <= s
+    *reinterpret_cast<u32x2_t*>(pt + qblk_u(3, 1) * 512 + lane * 8) = z2;  // t < 48 <= s
+}
+
+// ---------------------------------------------------------------------------
+// 3. reverse sweep over chunks: G, W, dV, dS_0
+// ---------------------------------------------------------------------------
+template <int D>
+struct RevGeo {
+    static constexpr int KS = 0;
+    static constexpr int QS = KS + kC * D * 2;
+    static constexpr int TT = QS + kC * D * 2;  // packed T^T, then packed P^T
+    static constexpr int PT = TT + kPacked * 2;
+    static constexpr int BS = PT + kPacked * 2;
+    static constexpr int BUF = BS + kC * 4;
+    static constexpr int BYTES = 2 * BUF;
+    static constexpr int NC = 64;  // columns per workgroup (16 per wave)
+    static_assert(BUF % 16 == 0, "layout");
+};
+
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_rev_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const float* __restrict__ beta,
+    const float* __restrict__ go, const float* __restrict__ gs, const uint16_t* __restrict__ tp_ws,
+    uint16_t* __restrict__ g_hist, uint16_t* __restrict__ w_hist, float* __restrict__ gv,
+    float* __restrict__ gs0, int n_pairs, int T, int H, int n_ch, int n_tiles) {
+    using G = RevGeo<D>;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    // the n_tiles workgroups of a pair share bid % 8 (one XCD, one L2)
+    const int bid = blockIdx.x;
+    const int xcd = bid & 7, slot = bid >> 3;
+    const int tile = slot % n_tiles;
+    const int pair = (slot / n_tiles) * 8 + xcd;
+    if (pair >= n_pairs) return;
+    const int seq = pair / H, h = pair % H;
+    const long tok0 = static_cast<long>(seq) * T;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = static_cast<int>(uniform(static_cast<unsigned>(tid >> 6)));
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int j = tile * G::NC + 16 * w + l16;  // this lane's column of G
+    const size_t tstride = static_cast<size_t>(H) * D;
+    const size_t sbase = static_cast<size_t>(pair) * D * D;
+
+    f32x4_t Gm[D / 16];
+#pragma unroll
+    for (int md = 0; md < D / 16; ++md)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            Gm[md][r] = gs ? gs[sbase + static_cast<size_t>(s_row_d(md, 4 * lg + r)) * D + j] : 0.f;
+    bf16x8_t Gb[D / 32];
+#pragma unroll
+    for (int kb = 0; kb < D / 32; ++kb) Gb[kb] = acc_to_b(Gm[2 * kb], Gm[2 * kb + 1]);
+
+    auto buf = [&](int c) { return smem + ((n_ch - 1 - c) & 1) * G::BUF; };
+    auto issue = [&](int c) {
+        const int base = c * kC, clen = min(kC, T - base);
+        const size_t row0 = (tok0 + base) * tstride + static_cast<size_t>(h) * D;
+        const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
+        unsigned char* b = uniform_ptr(buf(c));
+        copy_rows<D>(make_rsrc(k + row0, n_kq), b + G::KS, kC * D * 2 / 1024,
+                     static_cast<unsigned>(tstride * 2), w, 4, lane);
+        copy_rows<D>(make_rsrc(q + row0, n_kq), b + G::QS, kC * D * 2 / 1024,
+                     static_cast<unsigned>(tstride * 2), w, 4, lane);
+        copy_flat(make_rsrc(tp_ws + (static_cast<size_t>(pair) * n_ch + c) * 3 * kPacked + kPacked,
+                            4 * kPacked),
+                  b + G::TT, 4 * kPacked / 1024, w, 4, lane);
+        if (w == 3)
+            copy_to_lds(make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4)),
+                        b + G::BS, 4, static_cast<unsigned>(lane * H * 4));
+    };
+    // dO of chunk c as B operands over tokens 32kb + {4g..4g+3, 16+4g..16+4g+3}, column j
+    auto load_do = [&](int c, u32x4_t (&o)[2]) {
+        const int base = c * kC, clen = min(kC, T - base);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            float f[8];
+#pragma unroll
+            for (int x = 0; x < 8; ++x) {
+                const int t = 32 * kb + (x < 4 ? 4 * lg + x : 12 + 4 * lg + x);
+                f[x] = (go && t < clen) ? go[(tok0 + base + t) * tstride + static_cast<size_t>(h) * D + j] : 0.f;
+            }
+            const u32x4_t v = {pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7])};
+            o[kb] = v;
+        }
+    };
+
+    u32x4_t dcur[2], dnext[2];
+    if (n_ch > 0) {
+        issue(n_ch - 1);
+        load_do(n_ch - 1, dcur);
+        wait_copies();
+        __syncthreads();
+    }
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    for (int c = n_ch - 1; c >= 0; --c) {
+        if (c > 0) {
+            issue(c - 1);
+            load_do(c - 1, dnext);
+        }
+        unsigned char* b = buf(c);
+        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(b + G::KS);
+        const uint16_t* Qs = reinterpret_cast<const uint16_t*>(b + G::QS);
+        const uint16_t* TTp = reinterpret_cast<const uint16_t*>(b + G::TT);
+        const uint16_t* PTp = reinterpret_cast<const uint16_t*>(b + G::PT);
+        const float* Bs = reinterpret_cast<const float*>(b + G::BS);
+        const int base = c * kC, clen = min(kC, T - base);
+        // G_c: the gradient of the state at the end of chunk c, as rows of G^T
+        {
+            uint16_t* hp = g_hist + (static_cast<size_t>(pair) * n_ch + c) * D * D + static_cast<size_t>(j) * D;
+#pragma unroll
+            for (int md = 0; md < D / 16; ++md)
+                *reinterpret_cast<u32x2_t*>(hp + s_row_d(md, 4 * lg)) = cvt4(Gm[md]);
+        }
+        const bf16x8_t d0 = as_b(dcur[0]), d1 = as_b(dcur[1]);
+        // Y = K G + P^T dO
+        f32x4_t Y[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) Y[m] = zero;
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb) {
+            bf16x8_t fk[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) fk[m] = lds_op_kq<D>(Ks, 16 * m + l16, kb, lg);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) Y[m] = mfma32(fk[m], Gb[kb], Y[m]);
+        }
+        Y[0] = mfma32(packed_a(PTp, qblk_u(0, 1), lane), d1, mfma32(packed_a(PTp, qblk_u(0, 0), lane), d0, Y[0]));
+        Y[1] = mfma32(packed_a(PTp, qblk_u(1, 1), lane), d1, mfma32(packed_a(PTp, qblk_u(1, 0), lane), d0, Y[1]));
+        Y[2] = mfma32(packed_a(PTp, qblk_u(2, 1), lane), d1, Y[2]);
+        Y[3] = mfma32(packed_a(PTp, qblk_u(3, 1), lane), d1, Y[3]);
+        // W = T^T Y
+        const bf16x8_t Yb0 = acc_to_b(Y[0], Y[1]), Yb1 = acc_to_b(Y[2], Y[3]);
+        f32x4_t W[4];
+        W[0] = mfma32(packed_a(TTp, qblk_u(0, 1), lane), Yb1, mfma32(packed_a(TTp, qblk_u(0, 0), lane), Yb0, zero));
+        W[1] = mfma32(packed_a(TTp, qblk_u(1, 1), lane), Yb1, mfma32(packed_a(TTp, qblk_u(1, 0), lane), Yb0, zero));
+        W[2] = mfma32(packed_a(TTp, qblk_u(2, 1), lane), Yb1, zero);
+        W[3] = mfma32(packed_a(TTp, qblk_u(3, 1), lane), Yb1, zero);
+        // dV = beta W; W^T rows for the gradient kernel
+        f32x4_t NBW[4];
+        uint16_t* wp = w_hist + (static_cast<size_t>(pair) * n_ch + c) * D * kC + static_cast<size_t>(j) * kC;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int t0 = 16 * m + 4 * lg;
+            const f32x4_t bw = *reinterpret_cast<const f32x4_t*>(Bs + t0) * W[m];
+            NBW[m] = -bw;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (t0 + r < clen) gv[(tok0 + base + t0 + r) * tstride + static_cast<size_t>(h) * D + j] = bw[r];
+            *reinterpret_cast<u32x2_t*>(wp + t0) = cvt4(W[m]);
+        }
+        // G += Q^T dO - K^T diag(beta) W
+        const bf16x8_t nb0 = acc_to_b(NBW[0], NBW[1]), nb1 = acc_to_b(NBW[2], NBW[3]);
+#pragma unroll
+        for (int h4 = 0; h4 < D / 64; ++h4) {
+            u32x4_t a0 = lds_kt_issue<D, 0>(Ks, 4 * h4 + 0, lane), b0 = lds_kt_issue<D, 32>(Ks, 4 * h4 + 0, lane);
+            u32x4_t a1 = lds_kt_issue<D, 0>(Ks, 4 * h4 + 1, lane), b1 = lds_kt_issue<D, 32>(Ks, 4 * h4 + 1, lane);
+            u32x4_t a2 = lds_kt_issue<D, 0>(Ks, 4 * h4 + 2, lane), b2 = lds_kt_issue<D, 32>(Ks, 4 * h4 + 2, lane);
+            u32x4_t a3 = lds_kt_issue<D, 0>(Ks, 4 * h4 + 3, lane), b3 = lds_kt_issue<D, 32>(Ks, 4 * h4 + 3, lane);
+            lds_wait(a0, b0, a1, b1, a2, b2, a3, b3);
+            u32x4_t e0 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 0, lane), f0 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 0, lane);
+            u32x4_t e1 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 1, lane), f1 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 1, lane);
+            u32x4_t e2 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 2, lane), f2 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 2, lane);
+            u32x4_t e3 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 3, lane), f3 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 3, lane);
+            const u32x4_t ka[4] = {a0, a1, a2, a3}, kb_[4] = {b0, b1, b2, b3};
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                Gm[4 * h4 + x] = mfma32(as_b(ka[x]), nb0, Gm[4 * h4 + x]);
+                Gm[4 * h4 + x] = mfma32(as_b(kb_[x]), nb1, Gm[4 * h4 + x]);
+            }
+            lds_wait(e0, f0, e1, f1, e2, f2, e3, f3);
+            const u32x4_t qa[4] = {e0, e1, e2, e3}, qb[4] = {f0, f1, f2, f3};
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                Gm[4 * h4 + x] = mfma32(as_b(qa[x]), d0, Gm[4 * h4 + x]);
+                Gm[4 * h4 + x] = mfma32(as_b(qb[x]), d1, Gm[4 * h4 + x]);
+            }
+        }
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb) Gb[kb] = acc_to_b(Gm[2 * kb], Gm[2 * kb + 1]);
+        if (c > 0) {
+            wait_copies();
+            __syncthreads();
+            dcur[0] = dnext[0];
+            dcur[1] = dnext[1];
+        }
+    }
+#pragma unroll
+    for (int md = 0; md < D / 16; ++md)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            gs0[sbase + static_cast<size_t>(s_row_d(md, 4 * lg + r)) * D + j] = Gm[md][r];
+}
+
+// ---------------------------------------------------------------------------
+// 4. per-chunk gradients dQ, dK, dbeta (all chunks in parallel)
+// ---------------------------------------------------------------------------
+template <int D>
+struct GradGeo {
+    static constexpr int KS = 0;                   // K  [t][d]
+    static constexpr int QS = KS + kC * D * 2;     // Q  [t][d]
+    static constexpr int VS = QS + kC * D * 2;     // V  [t][j], later U^T [j][t]
+    static constexpr int DO = VS + kC * D * 2;     // dO [t][j] (bf16)
+    static constexpr int ST = DO + kC * D * 2;     // S^T [j][d]
+    static constexpr int GT = ST + D * D * 2;      // G^T [j][d], later dP^T, (beta dA)^T [s][t]
+    static constexpr int GT_BYTES = D * D * 2 > 4 * kC * kC ? D * D * 2 : 4 * kC * kC;
+    static constexpr int WT = GT + GT_BYTES;       // W^T [j][t]
+    static constexpr int TP = WT + D * kC * 2;     // packed T
+    static constexpr int BS = TP + kPacked * 2;    // beta
+    static constexpr int DB = BS + kC * 4;         // dbeta partial sums [2][4][kC]
+    static constexpr int BYTES = DB + 2 * 4 * kC * 4;
+    static constexpr int JW = D / 64;              // 16-column tiles per wave
+    static_assert(BYTES <= 160 * 1024, "LDS budget");
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void bwd_grad_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const float* __restrict__ beta, const float* __restrict__ go, const uint16_t* __restrict__ s_hist,
+    const uint16_t* __restrict__ g_hist, const uint16_t* __restrict__ w_hist,
+    const uint16_t* __restrict__ tp_ws, float* __restrict__ gq, float* __restrict__ gk,
+    float* __restrict__ gbeta, int T, int H, int n_ch) {
+    using G = GradGeo<D>;
+    constexpr int JW = G::JW;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int pair = blockIdx.x / n_ch, c = blockIdx.x % n_ch;
+    const int seq = pair / H, h = pair % H;
+    const long tok0 = static_cast<long>(seq) * T;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = static_cast<int>(uniform(static_cast<unsigned>(tid >> 6)));
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int base = c * kC, clen = min(kC, T - base);
+    const size_t tstride = static_cast<size_t>(H) * D;
+    const size_t row0 = (tok0 + base) * tstride + static_cast<size_t>(h) * D;
+    const size_t cidx = static_cast<size_t>(pair) * n_ch + c;
+
+    uint16_t* Ks = reinterpret_cast<uint16_t*>(smem + G::KS);
+    uint16_t* Qs = reinterpret_cast<uint16_t*>(smem + G::QS);
+    uint16_t* Vs = reinterpret_cast<uint16_t*>(smem + G::VS);
+    uint16_t* Ut = Vs;
+    uint16_t* DOs = reinterpret_cast<uint16_t*>(smem + G::DO);
+    uint16_t* St = reinterpret_cast<uint16_t*>(smem + G::ST);
+    uint16_t* Gt = reinterpret_cast<uint16_t*>(smem + G::GT);
+    uint16_t* dPt = Gt;
+    uint16_t* dAt = Gt + kC * kC;
+    uint16_t* Wt = reinterpret_cast<uint16_t*>(smem + G::WT);
+    const uint16_t* Tp = reinterpret_cast<const uint16_t*>(smem + G::TP);
+    const float* Bs = reinterpret_cast<const float*>(smem + G::BS);
+    float* db1 = reinterpret_cast<float*>(smem + G::DB);  // [wave][t]: W . (V - K S)
+    float* db2 = db1 + 4 * kC;                             // [wave][t]: sum_s dA (k_t . k_s)
+
+    {
+        const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
+        const unsigned rb = static_cast<unsigned>(tstride * 2);
+        copy_rows<D>(make_rsrc(k + row0, n_kq), smem + G::KS, kC * D * 2 / 1024, rb, w, 4, lane);
+        copy_rows<D>(make_rsrc(q + row0, n_kq), smem + G::QS, kC * D * 2 / 1024, rb, w, 4, lane);
+        copy_rows<D>(make_rsrc(v + row0, n_kq), smem + G::VS, kC * D * 2 / 1024, rb, w, 4, lane);
+        copy_rows<D>(make_rsrc(s_hist + cidx * D * D, D * D * 2), smem + G::ST, D * D * 2 / 1024, D * 2, w, 4, lane);
+        copy_rows<D>(make_rsrc(g_hist + cidx * D * D, D * D * 2), smem + G::GT, D * D * 2 / 1024, D * 2, w, 4, lane);
+        copy_rows<kC>(make_rsrc(w_hist + cidx * D * kC, D * kC * 2), smem + G::WT, D * kC * 2 / 1024, kC * 2, w, 4, lane);
+        copy_flat(make_rsrc(tp_ws + cidx * 3 * kPacked, kPacked * 2), smem + G::TP, kPacked * 2 / 1024, w, 4, lane);
+        if (w == 3)
+            copy_to_lds(make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4)),
+                        smem + G::BS, 4, static_cast<unsigned>(lane * H * 4));
+        // dO (fp32) -> bf16 token rows
+        for (int e = tid; e < kC * D / 4; e += 256) {
+            const int t = e / (D / 4), d = 4 * (e % (D / 4));
+            f32x4_t x = {0.f, 0.f, 0.f, 0.f};
+            if (go && t < clen) x = *reinterpret_cast<const f32x4_t*>(go + row0 + t * tstride + d);
+            *reinterpret_cast<u32x2_t*>(DOs + swz<D>(t, d)) = cvt4(x);
+        }
+        wait_copies();
+        __syncthreads();
+    }
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+
+    // ---- phase 1: R' = V - K S and U = T diag(beta) R' for this wave's columns ----
+    f32x4_t U[4][JW];
+    {
+        f32x4_t X[4][JW];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int jj = 0; jj < JW; ++jj) X[m][jj] = zero;
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb) {
+            bf16x8_t fk[4], fs[JW];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) fk[m] = lds_op_kq<D>(Ks, 16 * m + l16, kb, lg);
+#pragma unroll
+            for (int jj = 0; jj < JW; ++jj) fs[jj] = lds_op_kq<D>(St, 16 * (JW * w + jj) + l16, kb, lg);
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int jj = 0; jj < JW; ++jj) X[m][jj] = mfma32(fk[m], fs[jj], X[m][jj]);
+        }
+        f32x4_t dbp[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) dbp[m] = zero;
+#pragma unroll
+        for (int jj = 0; jj < JW; ++jj) {
+            const int jt = JW * w + jj, jcol = 16 * jt + l16;
+            u32x2_t vv0 = lds_acc_issue<D>(Vs, 0, 16 * jt, lane), vv1 = lds_acc_issue<D>(Vs, 16, 16 * jt, lane);
+            u32x2_t vv2 = lds_acc_issue<D>(Vs, 32, 16 * jt, lane), vv3 = lds_acc_issue<D>(Vs, 48, 16 * jt, lane);
+            lds_wait(vv0, vv1, vv2, vv3);
+            const u32x2_t vv[4] = {vv0, vv1, vv2, vv3};
+            f32x4_t R[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const int t0 = 16 * m + 4 * lg;
+                const f32x4_t rp = widen4(vv[m]) - X[m][jj];  // V - K S
+                const f32x4_t wv = widen4(*reinterpret_cast<const u32x2_t*>(Wt + swz<kC>(jcol, t0)));
+                dbp[m] += wv * rp;
+                R[m] = *reinterpret_cast<const f32x4_t*>(Bs + t0) * rp;
+            }
+            const bf16x8_t Rb0 = acc_to_b(R[0], R[1]), Rb1 = acc_to_b(R[2], R[3]);
+            U[0][jj] = mfma32(packed_a(Tp, 0, lane), Rb0, zero);
+            U[1][jj] = mfma32(packed_a(Tp, 1, lane), Rb0, zero);
+            U[2][jj] = mfma32(packed_a(Tp, 3, lane), Rb1, mfma32(packed_a(Tp, 2, lane), Rb0, zero));
+            U[3][jj] = mfma32(packed_a(Tp, 5, lane), Rb1, mfma32(packed_a(Tp, 4, lane), Rb0, zero));
+        }
+        // dbeta, first term: sum over this wave's columns (lanes l16, then its tiles)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float x = dbp[m][r];
+                x += __shfl_xor(x, 1);
+                x += __shfl_xor(x, 2);
+                x += __shfl_xor(x, 4);
+                x += __shfl_xor(x, 8);
+                dbp[m][r] = x;
+            }
+            if (l16 == 0) *reinterpret_cast<f32x4_t*>(db1 + w * kC + 16 * m + 4 * lg) = dbp[m];
+        }
+    }
+    __syncthreads();  // V is dead: its space takes U^T
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int jj = 0; jj < JW; ++jj)
+            *reinterpret_cast<u32x2_t*>(Ut + swz<kC>(16 * (JW * w + jj) + l16, 16 * m + 4 * lg)) = cvt4(U[m][jj]);
+    __syncthreads();
+
+    // ---- phase 2: products contracting over the d_v index j ----
+    // dQ1 = dO S^T, dKa = U G^T, dKb = W S^T for this wave's d tiles; the lower
+    // 16x16 tiles (m, st), m >= st, numbered 0..9 row by row, go to waves by number mod 4:
+    // dP = dO U^T, dA = -W U^T, KK = K K^T.
+    f32x4_t dQ[4][JW], dKa[4][JW], dKb[4][JW];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int dd = 0; dd < JW; ++dd) {
+            dQ[m][dd] = zero;
+            dKa[m][dd] = zero;
+            dKb[m][dd] = zero;
+        }
+    constexpr int kTiles = 3;  // wave w takes lower tiles w, w + 4, w + 8
+    auto tile_m = [](int idx) { return idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0; };
+    auto tile_s = [&](int idx) { const int m = tile_m(idx); return idx - m * (m + 1) / 2; };
+    const int nt = w < 2 ? 3 : 2;
+    int tm[kTiles], ts[kTiles];
+#pragma unroll
+    for (int x = 0; x < kTiles; ++x) {
+        const int idx = min(w + 4 * x, 9);
+        tm[x] = tile_m(idx);
+        ts[x] = tile_s(idx);
+    }
+    f32x4_t dP[kTiles], dA[kTiles], KK[kTiles];
+#pragma unroll
+    for (int x = 0; x < kTiles; ++x) dP[x] = dA[x] = KK[x] = zero;
+#pragma unroll
+    for (int kb = 0; kb < D / 32; ++kb) {
+        u32x4_t fu[4], fw[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            fu[m] = lds_col_issue<kC>(Ut, 32 * kb, 16 * m, lane);
+            fw[m] = lds_col_issue<kC>(Wt, 32 * kb, 16 * m, lane);
+        }
+        u32x4_t fst[JW], fgt[JW];
+#pragma unroll
+        for (int dd = 0; dd < JW; ++dd) {
+            fst[dd] = lds_col_issue<D>(St, 32 * kb, 16 * (JW * w + dd), lane);
+            fgt[dd] = lds_col_issue<D>(Gt, 32 * kb, 16 * (JW * w + dd), lane);
+        }
+        bf16x8_t fdo[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) fdo[m] = lds_op_kq<D>(DOs, 16 * m + l16, kb, lg);
+        lds_wait_all();
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            tie(fu[m]);
+            tie(fw[m]);
+        }
+#pragma unroll
+        for (int dd = 0; dd < JW; ++dd) {
+            tie(fst[dd]);
+            tie(fgt[dd]);
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int dd = 0; dd < JW; ++dd) {
+                dQ[m][dd] = mfma32(fdo[m], as_b(fst[dd]), dQ[m][dd]);
+                dKa[m][dd] = mfma32(as_b(fu[m]), as_b(fgt[dd]), dKa[m][dd]);
+                dKb[m][dd] = mfma32(as_b(fw[m]), as_b(fst[dd]), dKb[m][dd]);
+            }
+#pragma unroll
+        for (int x = 0; x < kTiles; ++x) {
+            if (x < nt) {
+                // select row block tm[x] and column block ts[x] without dynamic register indexing
+                bf16x8_t ado = fdo[0];
+                u32x4_t aw = fw[0], bu = fu[0];
+#pragma unroll
+                for (int m = 1; m < 4; ++m) {
+                    if (tm[x] == m) {
+                        ado = fdo[m];
+                        aw = fw[m];
+                    }
+                    if (ts[x] == m) bu = fu[m];
+                }
+                dP[x] = mfma32(ado, as_b(bu), dP[x]);
+                dA[x] = mfma32(as_b(aw), as_b(bu), dA[x]);
+            }
+        }
+    }
+#pragma unroll
+    for (int x = 0; x < kTiles; ++x) {
+        if (x < nt) {
+#pragma unroll
+            for (int kb = 0; kb < D / 32; ++kb)
+                KK[x] = mfma32(lds_op_kq<D>(Ks, 16 * tm[x] + l16, kb, lg), lds_op_kq<D>(Ks, 16 * ts[x] + l16, kb, lg), KK[x]);
+        }
+    }
+    // masks, dbeta second term, beta dA
+    f32x4_t db2p[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) db2p[m] = zero;
+#pragma unroll
+    for (int x = 0; x < kTiles; ++x) {
+        if (x < nt) {
+            const int m = tm[x], st = ts[x];
+            const int t0 = 16 * m + 4 * lg, s = 16 * st + l16;
+            const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + t0);
+            f32x4_t e = zero;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (t0 + r < s) dP[x][r] = 0.f;
+                const float a = (t0 + r > s) ? -dA[x][r] : 0.f;
+                e[r] = a * KK[x][r];
+                dA[x][r] = bs[r] * a;
+            }
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm)
+                if (mm == m) db2p[mm] += e;
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float x = db2p[m][r];
+            x += __shfl_xor(x, 1);
+            x += __shfl_xor(x, 2);
+            x += __shfl_xor(x, 4);
+            x += __shfl_xor(x, 8);
+            db2p[m][r] = x;
+        }
+        if (l16 == 0) *reinterpret_cast<f32x4_t*>(db2 + w * kC + 16 * m + 4 * lg) = db2p[m];
+    }
+    __syncthreads();  // G^T is dead: its space takes dP^T and (beta dA)^T
+#pragma unroll
+    for (int x = 0; x < kTiles; ++x) {
+        if (x < nt) {
+            const int o = swz<kC>(16 * ts[x] + l16, 16 * tm[x] + 4 * lg);
+            *reinterpret_cast<u32x2_t*>(dPt + o) = cvt4(dP[x]);
+            *reinterpret_cast<u32x2_t*>(dAt + o) = cvt4(dA[x]);
+        }
+    }
+    {
+        // the upper tiles (m < st) are zero; 6 of them, numbered row by row, by number mod 4
+        int idx = 0;
+        const u32x2_t z2 = {0u, 0u};
+        for (int m = 0; m < 4; ++m)
+            for (int st = m + 1; st < 4; ++st, ++idx)
+                if ((idx & 3) == w) {
+                    const int o = swz<kC>(16 * st + l16, 16 * m + 4 * lg);
+                    *reinterpret_cast<u32x2_t*>(dPt + o) = z2;
+                    *reinterpret_cast<u32x2_t*>(dAt + o) = z2;
+                }
+    }
+    __syncthreads();
+
+    // ---- phase 3: products contracting over tokens ----
+    // dQ += dP K;  dKc = dP^T Q + (beta dA)^T K + (beta dA) K
+    f32x4_t dKc[4][JW];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int dd = 0; dd < JW; ++dd) dKc[m][dd] = zero;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        u32x4_t fkc[JW], fqc[JW], fpc[4], fac[4];
+#pragma unroll
+        for (int dd = 0; dd < JW; ++dd) {
+            fkc[dd] = lds_col_issue<D>(Ks, 32 * kb, 16 * (JW * w + dd), lane);
+            fqc[dd] = lds_col_issue<D>(Qs, 32 * kb, 16 * (JW * w + dd), lane);
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            fpc[m] = lds_col_issue<kC>(dPt, 32 * kb, 16 * m, lane);
+            fac[m] = lds_col_issue<kC>(dAt, 32 * kb, 16 * m, lane);
+        }
+        bf16x8_t fpr[4], far[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            fpr[m] = lds_op_kq<kC>(dPt, 16 * m + l16, kb, lg);
+            far[m] = lds_op_kq<kC>(dAt, 16 * m + l16, kb, lg);
+        }
+        lds_wait_all();
+#pragma unroll
+        for (int dd = 0; dd < JW; ++dd) {
+            tie(fkc[dd]);
+            tie(fqc[dd]);
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            tie(fpc[m]);
+            tie(fac[m]);
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int dd = 0; dd < JW; ++dd) {
+                dQ[m][dd] = mfma32(as_b(fpc[m]), as_b(fkc[dd]), dQ[m][dd]);
+                dKc[m][dd] = mfma32(fpr[m], as_b(fqc[dd]), dKc[m][dd]);
+                dKc[m][dd] = mfma32(far[m], as_b(fkc[dd]), dKc[m][dd]);
+                dKc[m][dd] = mfma32(as_b(fac[m]), as_b(fkc[dd]), dKc[m][dd]);
+            }
+    }
+    // outputs
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int t0 = 16 * m + 4 * lg;
+        const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + t0);
+#pragma unroll
+        for (int dd = 0; dd < JW; ++dd) {
+            const int d = 16 * (JW * w + dd) + l16;
+            const f32x4_t kk = dKa[m][dd] - bs * dKb[m][dd] + dKc[m][dd];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (t0 + r < clen) {
+                    const size_t a = row0 + (t0 + r) * tstride + d;
+                    gq[a] = dQ[m][dd][r];
+                    gk[a] = kk[r];
+                }
+            }
+        }
+    }
+    if (tid < clen) {
+        float s = 0.f;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) s += db1[x * kC + tid];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) s += db2[x * kC + tid];
+        gbeta[(tok0 + base + tid) * H + h] = s;
+    }
+}
+
+template <typename Kern>
+hipError_t set_lds(Kern kern, int bytes) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               bytes);
+}
+
+template <int D>
+hipError_t launch_d(const BwdArgs& a, hipStream_t st) {
+    const int n_ch = (a.T + kC - 1) / kC;
+    const ChunkedBwdWs ws = chunked_bwd_ws(a.n_pairs, a.T, D);
+    unsigned char* base = reinterpret_cast<unsigned char*>(a.workspace);
+    uint16_t* s_hist = reinterpret_cast<uint16_t*>(base + ws.s_hist);
+    uint16_t* g_hist = reinterpret_cast<uint16_t*>(base + ws.g_hist);
+    uint16_t* w_hist = reinterpret_cast<uint16_t*>(base + ws.w_hist);
+    uint16_t* tp = reinterpret_cast<uint16_t*>(base + ws.tp);
+    const uint16_t* q = static_cast<const uint16_t*>(a.q);
+    const uint16_t* k = static_cast<const uint16_t*>(a.k);
+    const uint16_t* v = static_cast<const uint16_t*>(a.v);
+    hipError_t e;
+    if (n_ch > 0) {
+        ChunkedArgs f{q, k, v, a.beta, a.s0, nullptr, nullptr, nullptr, a.n_pairs / a.H, a.T, a.H, D, false, 0};
+        if ((e = launch_chunked_states(f, s_hist, st)) != hipSuccess) return e;
+        if ((e = set_lds(bwd_prep_kernel<D>, PrepGeo<D>::BYTES)) != hipSuccess) return e;
+        hipLaunchKernelGGL(bwd_prep_kernel<D>, dim3(static_cast<unsigned>(a.n_pairs) * n_ch), dim3(64),
+                           PrepGeo<D>::BYTES, st, q, k, a.beta, tp, a.T, a.H, n_ch);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    const int n_tiles = D / RevGeo<D>::NC;
+    const int slots = (a.n_pairs + 7) / 8;
+    if ((e = set_lds(bwd_rev_kernel<D>, RevGeo<D>::BYTES)) != hipSuccess) return e;
+    hipLaunchKernelGGL(bwd_rev_kernel<D>, dim3(static_cast<unsigned>(slots * 8 * n_tiles)), dim3(256),
+                       RevGeo<D>::BYTES, st, q, k, a.beta, a.go, a.gs, tp, g_hist, w_hist, a.gv, a.gs0,
+                       a.n_pairs, a.T, a.H, n_ch, n_tiles);
+    if ((e = hipGetLastError()) != hipSuccess || n_ch == 0) return e;
+    if ((e = set_lds(bwd_grad_kernel<D>, GradGeo<D>::BYTES)) != hipSuccess) return e;
+    hipLaunchKernelGGL(bwd_grad_kernel<D>, dim3(static_cast<unsigned>(a.n_pairs) * n_ch), dim3(256),
+                       GradGeo<D>::BYTES, st, q, k, v, a.beta, a.go, s_hist, g_hist, w_hist, tp, a.gq, a.gk,
+                       a.gbeta, a.T, a.H, n_ch);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+ChunkedBwdWs chunked_bwd_ws(long n_pairs, int T, int D) {
+    const size_t n = static_cast<size_t>(n_pairs) * ((T + kC - 1) / kC);
+    ChunkedBwdWs w;
+    w.s_hist = 0;
+    w.g_hist = w.s_hist + n * D * D * 2;
+    w.w_hist = w.g_hist + n * D * D * 2;
+    w.tp = w.w_hist + n * D * kC * 2;
+    w.bytes = w.tp + n * 3 * kPacked * 2;
+    return w;
+}
+
+hipError_t launch_bwd_chunked(const BwdArgs& a, hipStream_t st) {
+    if (a.n_pairs == 0) return hipSuccess;
+    if (!a.in_bf16 || !chunked_supported(a.D, a.H)) return hipErrorInvalidValue;
+    return a.D == 128 ? launch_d<128>(a, st) : launch_d<64>(a, st);
+}
+
+}  // namespace pm

@@ -144,9 +144,22 @@ const char* pm_last_error(void) { return g_err; }
 
 size_t pm_delta_workspace_bytes(int, int, int, int, int) { return 0; }
 
-size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D) {
+// Which backward serves (B, T, H, D, in_dtype) under the current path setting:
+// the chunked kernel for bf16 inputs with D in {64, 128}, else the per-token one.
+bool bwd_chunked(int H, int D, int in_dtype) {
+    return g_path.load() != 1 && in_dtype == PM_DTYPE_BF16 && pm::chunked_supported(D, H);
+}
+
+size_t bwd_ws_bytes(int B, int T, int H, int D, int in_dtype) {
+    const long n_pairs = static_cast<long>(B) * H;
+    if (bwd_chunked(H, D, in_dtype)) return pm::chunked_bwd_ws(n_pairs, T, D).bytes;
+    return sizeof(float) * pm::bwd_workspace_floats(n_pairs, T, D);
+}
+
+size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype) {
     if (B < 0 || T < 0 || H < 0 || D < 1 || D > pm::kBwdMaxD) return 0;
-    return sizeof(float) * pm::bwd_workspace_floats(static_cast<long>(B) * H, T, D);
+    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16) return 0;
+    return bwd_ws_bytes(B, T, H, D, in_dtype);
 }
 
 int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
@@ -170,14 +183,26 @@ int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
     const void* f32s[] = {beta, s0, go, gs, gq, gk, gv, gbeta, gs0, workspace};
     for (const void* p : f32s)
         if (p && !aligned(p, 4)) return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
-    const size_t need = sizeof(float) * pm::bwd_workspace_floats(n_pairs, T, D);
+    const bool chunked = bwd_chunked(H, D, in_dtype);
+    if (g_path.load() == 2 && !chunked)
+        return fail(PM_E_UNSUPPORTED,
+                    "chunked backward needs bf16 inputs and D in {64, 128} (got in_dtype %d, D %d)",
+                    in_dtype, D);
+    if (chunked && n_tok > 0) {
+        const void* v16[] = {q, k, v, go, workspace};
+        for (const void* p : v16)
+            if (p && !aligned(p, 16))
+                return fail(PM_E_ALIGN, "chunked backward: q, k, v, go and workspace must be 16-byte aligned");
+    }
+    const size_t need = bwd_ws_bytes(B, T, H, D, in_dtype);
     if (need > 0 && (!workspace || ws_bytes < need))
         return fail(PM_E_WORKSPACE, "workspace of %zu bytes needed (got %zu)", need,
                     workspace ? ws_bytes : static_cast<size_t>(0));
     pm::BwdArgs a{q, k, v, beta, s0, go, gs, gq, gk, gv, gbeta, gs0,
                   static_cast<float*>(workspace), static_cast<int>(n_pairs), T, H, D,
                   in_dtype == PM_DTYPE_BF16};
-    hipError_t e = pm::launch_bwd(a, static_cast<hipStream_t>(stream));
+    hipError_t e = chunked ? pm::launch_bwd_chunked(a, static_cast<hipStream_t>(stream))
+                           : pm::launch_bwd(a, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? 0 : hip_fail(e, "backward launch");
 }
 

@@ -56,6 +56,10 @@ struct ChunkedArgs {
 };
 bool chunked_supported(int D, int H);  // D in {64, 128}, H*D <= 2^24
 hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st);
+// The same kernel writing, instead of O and the final state, the state at
+// the start of every chunk as bf16 rows of S^T (fixed-length batches only):
+// s_hist holds n_seq*H x ceil(T/64) x D x D values.
+hipError_t launch_chunked_states(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st);
 
 // Reverse mode (K5, fp32): fixed-length batch of n_pairs = B*H sequences of
 // T tokens, D <= 128.  workspace holds bwd_workspace_floats(n_pairs, T, D)
@@ -82,6 +86,17 @@ struct BwdArgs {
 constexpr int kBwdMaxD = 128;
 size_t bwd_workspace_floats(long n_pairs, int T, int D);
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t st);
+
+// Chunked reverse mode (K6, bf16 MFMA): bf16 q/k/v and chunked_supported(D,
+// H).  a.workspace is a byte buffer of chunked_bwd_ws(...).bytes bytes (16-byte
+// aligned) holding, per chunk of every (b, h), the start state and the end
+// gradient of the state (bf16 rows of S^T and G^T), W (bf16 rows of W^T) and
+// the packed T, T^T, P^T.
+struct ChunkedBwdWs {
+    size_t s_hist, g_hist, w_hist, tp, bytes;
+};
+ChunkedBwdWs chunked_bwd_ws(long n_pairs, int T, int D);
+hipError_t launch_bwd_chunked(const BwdArgs& a, hipStream_t st);
 
 // Zero fill (used instead of hipMemsetAsync so callers may graph-capture).
 hipError_t launch_fill_zero(float* p, size_t n, hipStream_t st);

@@ -261,9 +261,11 @@ def chunked_delta_rule_bwd(residual: _DeltaResidual, grads):
     may be None (zeros, as the custom-VJP rule treats missing cotangents,
     ``:638-653``). Returns ``(gq, gk, gv, gbeta, gstate)``, all fp32, shaped
     like ``q, k, v, beta, state0``: the gradients of the reference's
-    ``_delta_vjp_np`` / ``_delta_vjp_jax`` (``:460-588``), computed by the
-    checkpointed reverse-mode kernel (no per-token state history). Head
-    dimension up to 128.
+    ``_delta_vjp_np`` / ``_delta_vjp_jax`` (``:460-588``). Head dimension up
+    to 128. As in the forward, bf16 q/k/v with head dimension 64 or 128 run
+    the chunked backward on bf16 MFMA (bf16 parity); everything else runs the
+    fp32 per-token reverse-mode kernel with state checkpoints (fp32 parity).
+    Neither keeps the reference's per-token state history.
     """
     go, gs = grads
     q, k, v, beta, s0 = residual.q, residual.k, residual.v, residual.beta, residual.state0
@@ -286,7 +288,7 @@ def chunked_delta_rule_bwd(residual: _DeltaResidual, grads):
         gb = torch.empty((batch, seq, heads), dtype=f32, device=call.device)
         gs0 = torch.empty((batch, heads, dim, dim), dtype=f32, device=call.device)
         L = _native.lib()
-        nbytes = L.pm_delta_bwd_workspace_bytes(batch, seq, heads, dim)
+        nbytes = L.pm_delta_bwd_workspace_bytes(batch, seq, heads, dim, _code(cdt))
         ws = torch.empty(((nbytes + 3) // 4,), dtype=f32, device=call.device) if nbytes else None
         rc = L.pm_delta_bwd(
             _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(sd), _ptr(god), _ptr(gsd),

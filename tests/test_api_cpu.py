@@ -106,14 +106,32 @@ def test_bwd_shape_checks_raise_before_any_device_work():
         kernels.chunked_delta_rule_bwd(big, (None, None))
 
 
+def _per_token_ws(b, t, h, d):
+    n_ck, n_tiles = -(-t // 8), -(-d // 32)
+    part = n_tiles * t * (2 * d + 1) if n_tiles > 1 else 0
+    return 4 * b * h * (t * d + n_ck * d * d + part)
+
+
+def _chunked_ws(b, t, h, d):
+    return 2 * b * h * (-(-t // 64)) * (2 * d * d + 64 * d + 9216)
+
+
 def test_bwd_workspace_bytes():
     lib = _native.lib()
-    for b, t, h, d in [(1, 1, 1, 3), (2, 130, 3, 64), (4, 4096, 16, 128), (1, 0, 2, 8)]:
-        n_ck, n_tiles = -(-t // 8), -(-d // 32)
-        part = n_tiles * t * (2 * d + 1) if n_tiles > 1 else 0
-        assert lib.pm_delta_bwd_workspace_bytes(b, t, h, d) == 4 * b * h * (t * d + n_ck * d * d + part)
-    assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 129) == 0
-    assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 0) == 0
+    f32, bf16 = _native.DTYPE_F32, _native.DTYPE_BF16
+    for b, t, h, d in [(1, 1, 1, 3), (2, 130, 3, 64), (4, 4096, 16, 128), (1, 0, 2, 8), (1, 70, 2, 48)]:
+        assert lib.pm_delta_bwd_workspace_bytes(b, t, h, d, f32) == _per_token_ws(b, t, h, d)
+        want = _chunked_ws(b, t, h, d) if d in (64, 128) else _per_token_ws(b, t, h, d)
+        assert lib.pm_delta_bwd_workspace_bytes(b, t, h, d, bf16) == want
+    # path 1 (per-token kernel) applies to the backward as well
+    old = _native.set_path(1)
+    try:
+        assert lib.pm_delta_bwd_workspace_bytes(2, 130, 3, 64, bf16) == _per_token_ws(2, 130, 3, 64)
+    finally:
+        _native.set_path(old)
+    assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 129, f32) == 0
+    assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 0, f32) == 0
+    assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 8, 3) == 0
 
 
 def test_bwd_abi_argument_validation_without_gpu():
@@ -132,10 +150,22 @@ def test_bwd_abi_argument_validation_without_gpu():
     assert call(1, 4, 1, 8, 3, p, 1 << 20) == _native.E_DTYPE
     assert call(1, 4, 1, 8, 0, p, 1 << 20, gs0=None) == _native.E_NULL
     assert call(1, 4, 1, 8, 0, p, 1 << 20, ptrs=[None] + [p] * 3 + [None] * 3 + [p] * 4) == _native.E_NULL
-    need = lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 8)
+    need = lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 8, 0)
     assert call(1, 4, 1, 8, 0, p, need - 4) == _native.E_WORKSPACE
     assert call(1, 4, 1, 8, 0, None, need) == _native.E_WORKSPACE
     assert call(1, 4, 1, 8, 0, ctypes.c_void_p(18), need) == _native.E_ALIGN
+    # chunked backward (bf16, D = 64): 16-byte alignment of q, k, v, go, workspace
+    need = lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 64, 1)
+    odd = ctypes.c_void_p(24)
+    assert call(1, 4, 1, 64, 1, p, need, ptrs=[odd, p, p, p, None, None, None, p, p, p, p]) == _native.E_ALIGN
+    assert call(1, 4, 1, 64, 1, odd, need) == _native.E_ALIGN
+    # path 2 (chunked required) refuses what only the per-token kernel serves
+    old = _native.set_path(2)
+    try:
+        assert call(1, 4, 1, 8, 0, p, 1 << 20) == _native.E_UNSUPPORTED
+        assert call(1, 4, 1, 48, 1, p, 1 << 20) == _native.E_UNSUPPORTED
+    finally:
+        _native.set_path(old)
     # nothing to do: B*H == 0
     assert call(0, 4, 1, 8, 0, None, 0) == 0
 

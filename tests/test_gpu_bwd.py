@@ -21,7 +21,7 @@ import pytest
 import torch
 
 from oracle import delta_oracle as ref
-from prometheus_amd import kernels, synth
+from prometheus_amd import _native, kernels, synth
 from tests.golden.make_golden import reference_cases
 from tests.parity import assert_f32_parity
 
@@ -126,6 +126,9 @@ def test_shapes_across_checkpoint_blocks(shape, state):
 
 
 def test_bf16_inputs_against_rounded_values():
+    """The per-token kernel (path 1) reading bf16 q/k/v: fp32 parity on the
+    rounded values. (The automatic choice for bf16 and D = 64 is the chunked
+    kernel, tests/test_gpu_bwd_chunked.py.)"""
     x = synth.fwd_inputs((2, 100, 2, 64), seed=9, dtype="bf16", s0_std=0.02)
     rng = np.random.default_rng(9)
     go = rng.standard_normal(x.q.shape).astype(np.float32)
@@ -136,7 +139,11 @@ def test_bf16_inputs_against_rounded_values():
 
     res = kernels._DeltaResidual(q=bf(x.q_bits), k=bf(x.k_bits), v=bf(x.v_bits), beta=_dev(x.beta),
                                  state0=_dev(x.s0), chunk=64)
-    got = kernels.chunked_delta_rule_bwd(res, (_dev(go), _dev(gs)))
+    old = _native.set_path(1)
+    try:
+        got = kernels.chunked_delta_rule_bwd(res, (_dev(go), _dev(gs)))
+    finally:
+        _native.set_path(old)
     # x.q, x.k, x.v are the bf16-rounded values in fp32
     _check(got, ref.delta_vjp(x.q, x.k, x.v, x.beta, go, gs, x.s0), "bf16")
 

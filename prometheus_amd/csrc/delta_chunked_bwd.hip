@@ -205,12 +205,16 @@ struct RevGeo {
     static constexpr int QS = KS + kC * D * 2;
     static constexpr int TT = QS + kC * D * 2;  // packed T^T, then packed P^T
     static constexpr int PT = TT + kPacked * 2;
-    static constexpr int BS = PT + kPacked * 2;
+    static constexpr int NC = 64;                // columns per workgroup (16 per wave)
+    static constexpr int DO = PT + kPacked * 2;  // dO tile, fp32 [t][NC], 16-byte chunks swizzled
+    static constexpr int BS = DO + kC * NC * 4;
     static constexpr int BUF = BS + kC * 4;
     static constexpr int BYTES = 2 * BUF;
-    static constexpr int NC = 64;  // columns per workgroup (16 per wave)
     static_assert(BUF % 16 == 0, "layout");
 };
+// dO tile: 16-byte chunk p of token row t sits at chunk p ^ fdo(t); the operand reads
+// (rows 4g + i, 16 consecutive columns per lane group g) then hit 64 distinct banks.
+__device__ __forceinline__ int fdo(int t) { return 4 * ((t >> 2) & 3); }
 
 template <int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_rev_kernel(
@@ -245,6 +249,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int kb = 0; kb < D / 32; ++kb) Gb[kb] = acc_to_b(Gm[2 * kb], Gm[2 * kb + 1]);
 
+    const int col0 = tile * G::NC;
     auto buf = [&](int c) { return smem + ((n_ch - 1 - c) & 1) * G::BUF; };
     auto issue = [&](int c) {
         const int base = c * kC, clen = min(kC, T - base);
@@ -258,54 +263,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         copy_flat(make_rsrc(tp_ws + (static_cast<size_t>(pair) * n_ch + c) * 3 * kPacked + kPacked,
                             4 * kPacked),
                   b + G::TT, 4 * kPacked / 1024, w, 4, lane);
+        // dO (fp32): rows of NC values from column col0; a NULL go reads as zeros
+        const unsigned n_do = go ? static_cast<unsigned>(((clen - 1) * tstride + G::NC) * 4) : 0u;
+        const __amdgpu_buffer_rsrc_t rd = make_rsrc(go ? go + row0 + col0 : go, n_do);
+        for (int ii = w; ii < kC * G::NC * 4 / 1024; ii += 4) {
+            const int pos = 1024 * ii + 16 * lane;  // byte in the LDS tile
+            const int r = pos / (G::NC * 4), p = (pos % (G::NC * 4)) / 16;
+            copy_to_lds(rd, b + G::DO + 1024 * ii, 16,
+                        static_cast<unsigned>(r * tstride * 4) + 16u * static_cast<unsigned>(p ^ fdo(r)));
+        }
         if (w == 3)
             copy_to_lds(make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4)),
                         b + G::BS, 4, static_cast<unsigned>(lane * H * 4));
     };
-    // dO of chunk c as B operands over tokens 32kb + {4g..4g+3, 16+4g..16+4g+3}, column j
-    auto load_do = [&](int c, u32x4_t (&o)[2]) {
-        const int base = c * kC, clen = min(kC, T - base);
+    // dO as a B operand over tokens 32kb + {4g..4g+3, 16+4g..16+4g+3}, column j
+    const int jl = 16 * w + l16;  // column within the tile
+    auto do_op = [&](const float* Ds, int kb) {
+        float f[8];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            float f[8];
-#pragma unroll
-            for (int x = 0; x < 8; ++x) {
-                const int t = 32 * kb + (x < 4 ? 4 * lg + x : 12 + 4 * lg + x);
-                f[x] = (go && t < clen) ? go[(tok0 + base + t) * tstride + static_cast<size_t>(h) * D + j] : 0.f;
-            }
-            const u32x4_t v = {pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7])};
-            o[kb] = v;
+        for (int y = 0; y < 8; ++y) {
+            const int t = 32 * kb + (y < 4 ? 4 * lg + y : 12 + 4 * lg + y);
+            f[y] = Ds[t * G::NC + 4 * ((jl >> 2) ^ fdo(t)) + (jl & 3)];
         }
+        const u32x4_t v = {pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7])};
+        return as_b(v);
     };
 
-    u32x4_t dcur[2], dnext[2];
     if (n_ch > 0) {
         issue(n_ch - 1);
-        load_do(n_ch - 1, dcur);
         wait_copies();
         __syncthreads();
     }
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
     for (int c = n_ch - 1; c >= 0; --c) {
-        if (c > 0) {
-            issue(c - 1);
-            load_do(c - 1, dnext);
-        }
+        if (c > 0) issue(c - 1);
         unsigned char* b = buf(c);
         const uint16_t* Ks = reinterpret_cast<const uint16_t*>(b + G::KS);
         const uint16_t* Qs = reinterpret_cast<const uint16_t*>(b + G::QS);
         const uint16_t* TTp = reinterpret_cast<const uint16_t*>(b + G::TT);
         const uint16_t* PTp = reinterpret_cast<const uint16_t*>(b + G::PT);
         const float* Bs = reinterpret_cast<const float*>(b + G::BS);
+        const float* Ds = reinterpret_cast<const float*>(b + G::DO);
         const int base = c * kC, clen = min(kC, T - base);
-        // G_c: the gradient of the state at the end of chunk c, as rows of G^T
+        // G_c: the gradient of the state at the end of chunk c, as rows of G^T (Gb[kb] holds
+        // G[32kb + 8g .. +8][j])
         {
             uint16_t* hp = g_hist + (static_cast<size_t>(pair) * n_ch + c) * D * D + static_cast<size_t>(j) * D;
 #pragma unroll
-            for (int md = 0; md < D / 16; ++md)
-                *reinterpret_cast<u32x2_t*>(hp + s_row_d(md, 4 * lg)) = cvt4(Gm[md]);
+            for (int kb = 0; kb < D / 32; ++kb)
+                *reinterpret_cast<bf16x8_t*>(hp + 32 * kb + 8 * lg) = Gb[kb];
         }
-        const bf16x8_t d0 = as_b(dcur[0]), d1 = as_b(dcur[1]);
+        const bf16x8_t d0 = do_op(Ds, 0), d1 = do_op(Ds, 1);
         // Y = K G + P^T dO
         f32x4_t Y[4];
 #pragma unroll
@@ -374,8 +382,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         if (c > 0) {
             wait_copies();
             __syncthreads();
-            dcur[0] = dnext[0];
-            dcur[1] = dnext[1];
         }
     }
 #pragma unroll
@@ -817,9 +823,14 @@ ChunkedBwdWs chunked_bwd_ws(long n_pairs, int T, int D) {
     return w;
 }
 
+// 32-bit buffer offsets: a chunk of fp32 dO spans 64 token rows of H*D values.
+bool chunked_bwd_supported(int D, int H) {
+    return chunked_supported(D, H) && static_cast<long>(H) * D <= (1L << 23);
+}
+
 hipError_t launch_bwd_chunked(const BwdArgs& a, hipStream_t st) {
     if (a.n_pairs == 0) return hipSuccess;
-    if (!a.in_bf16 || !chunked_supported(a.D, a.H)) return hipErrorInvalidValue;
+    if (!a.in_bf16 || !chunked_bwd_supported(a.D, a.H)) return hipErrorInvalidValue;
     return a.D == 128 ? launch_d<128>(a, st) : launch_d<64>(a, st);
 }
 

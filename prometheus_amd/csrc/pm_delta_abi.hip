@@ -147,7 +147,7 @@ size_t pm_delta_workspace_bytes(int, int, int, int, int) { return 0; }
 // Which backward serves (B, T, H, D, in_dtype) under the current path setting:
 // the chunked kernel for bf16 inputs with D in {64, 128}, else the per-token one.
 bool bwd_chunked(int H, int D, int in_dtype) {
-    return g_path.load() != 1 && in_dtype == PM_DTYPE_BF16 && pm::chunked_supported(D, H);
+    return g_path.load() != 1 && in_dtype == PM_DTYPE_BF16 && pm::chunked_bwd_supported(D, H);
 }
 
 size_t bwd_ws_bytes(int B, int T, int H, int D, int in_dtype) {

@@ -96,6 +96,7 @@ struct ChunkedBwdWs {
     size_t s_hist, g_hist, w_hist, tp, bytes;
 };
 ChunkedBwdWs chunked_bwd_ws(long n_pairs, int T, int D);
+bool chunked_bwd_supported(int D, int H);  // chunked_supported and H*D <= 2^23 (fp32 dO rows)
 hipError_t launch_bwd_chunked(const BwdArgs& a, hipStream_t st);
 
 // Zero fill (used instead of hipMemsetAsync so callers may graph-capture).

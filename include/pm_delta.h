@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 2
+#define PM_DELTA_ABI_VERSION 3
 
 /* element types */
 #define PM_DTYPE_F32 0
@@ -102,6 +102,20 @@ int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float
 int pm_delta_step(float* s_inout, const void* q, const void* k, const void* v,
                   const float* beta, float* o, int B, int H, int D, int in_dtype,
                   void* stream);
+
+/*
+ * The model's linear attention (Gated DeltaNet / KDA family, beta = 1).
+ * Replaces the recurrence of model.linear_attention (model/__init__.py:
+ * 393-432, called by model._linear_attn :726-734): per (b, h) and token,
+ *   q^ = q / max(||q||, 1e-6),  k^ = k / max(||k||, 1e-6)   (:203-205)
+ *   S_t = (I - k^ k^^T) S_{t-1} + k^ v^T,   o_t = q^ S_t
+ * with the normalisation done by the kernel as it loads q and k (no
+ * normalised copies in memory).  Shapes, dtypes and state handling as
+ * pm_delta_fwd without beta; fp32 recurrence (the per-token kernel).
+ */
+int pm_linear_attention(const void* q, const void* k, const void* v, const float* s0, void* o,
+                        float* s_out, int B, int T, int H, int D, int in_dtype, int out_dtype,
+                        void* stream);
 
 /* Workspace bytes pm_delta_fwd would need (0 in this build). */
 size_t pm_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype);

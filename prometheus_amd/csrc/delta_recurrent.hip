@@ -14,6 +14,10 @@
 // staged into LDS STEPS at a time so the inner loop has no barriers.
 // S is read once at the start and written once at the end, so s0 may alias
 // s_out (the decode step runs in place).
+//
+// The model's linear attention (model/__init__.py:393-432) runs here too:
+// with l2norm, each staged q and k row is divided by max(||row||_2, 1e-6)
+// (its _l2_normalize, :203-205) before use, and a NULL beta means beta = 1.
 
 #include "pm_common.h"
 #include "pm_internal.h"
@@ -29,7 +33,7 @@ template <int RPT, typename InT, typename OutT>
 __global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel(
     const InT* __restrict__ q, const InT* __restrict__ k, const InT* __restrict__ v,
     const float* __restrict__ beta, const float* s0, OutT* __restrict__ o, float* s_out,
-    const int32_t* __restrict__ cu_seqlens, int T, int H, int D, int RS) {
+    const int32_t* __restrict__ cu_seqlens, int T, int H, int D, int RS, int l2norm) {
     extern __shared__ float lds[];
     const int DP = RS * RPT;  // padded row count per column
     float* sk = lds;                          // [kRecSteps][DP]
@@ -82,8 +86,21 @@ __global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel
             sv[idx] = vv;
         }
         for (int j = tid; j < kRecSteps; j += blockDim.x)
-            sb[j] = (j < nst) ? beta[static_cast<size_t>(tok0 + t0 + j) * H + h] : 0.f;
+            sb[j] = (j >= nst) ? 0.f : beta ? beta[static_cast<size_t>(tok0 + t0 + j) * H + h] : 1.f;
         __syncthreads();
+        if (l2norm) {
+            // one wave per staged row (k rows, then q rows): x / max(||x||, 1e-6)
+            const int lane = tid & 63, nw = blockDim.x >> 6;
+            for (int row = tid >> 6; row < 2 * nst; row += nw) {
+                float* x = (row < nst ? sk : sq) + (row % nst) * DP;
+                float ss = 0.f;
+                for (int d = lane; d < D; d += 64) ss = fmaf(x[d], x[d], ss);
+                for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+                const float den = fmaxf(sqrtf(ss), 1e-6f);
+                for (int d = lane; d < D; d += 64) x[d] = x[d] / den;
+            }
+            __syncthreads();
+        }
 
         for (int j = 0; j < nst; ++j) {
             const float* kr = sk + j * DP + r * RPT;
@@ -129,7 +146,7 @@ static hipError_t launch_rec_t(const RecurrentArgs& a, int rs, hipStream_t st) {
     hipLaunchKernelGGL((delta_recurrent_kernel<RPT, InT, OutT>), dim3(a.n_pairs), dim3(threads),
                        lds, st, static_cast<const InT*>(a.q), static_cast<const InT*>(a.k),
                        static_cast<const InT*>(a.v), a.beta, a.s0, static_cast<OutT*>(a.o),
-                       a.s_out, a.cu_seqlens, a.T, a.H, a.D, rs);
+                       a.s_out, a.cu_seqlens, a.T, a.H, a.D, rs, a.l2norm ? 1 : 0);
     return hipGetLastError();
 }
 

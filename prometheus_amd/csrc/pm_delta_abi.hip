@@ -255,6 +255,37 @@ int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float
                    out_dtype, chunk, static_cast<hipStream_t>(stream));
 }
 
+int pm_linear_attention(const void* q, const void* k, const void* v, const float* s0, void* o,
+                        float* s_out, int B, int T, int H, int D, int in_dtype, int out_dtype,
+                        void* stream) {
+    g_err[0] = '\0';
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (B < 0 || T < 0 || H < 0)
+        return fail(PM_E_SHAPE, "B, T, H must be >= 0 (got %d, %d, %d)", B, T, H);
+    if (D < 1 || D > PM_DELTA_MAX_D)
+        return fail(PM_E_SHAPE, "D must be in [1, %d] (got %d)", PM_DELTA_MAX_D, D);
+    if (int rc = check_dtypes(in_dtype, out_dtype)) return rc;
+    const long n_pairs = static_cast<long>(B) * H;
+    const long n_tok = static_cast<long>(B) * T;
+    if (n_pairs == 0) return 0;
+    if (n_pairs > (1L << 30) || n_tok > (1L << 40)) return fail(PM_E_SHAPE, "problem too large");
+    if (!s_out) return fail(PM_E_NULL, "s_out is NULL");
+    if (n_tok > 0 && (!q || !k || !v || !o))
+        return fail(PM_E_NULL, "q, k, v and o must be non-NULL");
+    if (!aligned(s_out, 4) || (s0 && !aligned(s0, 4)))
+        return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
+    if (n_tok == 0) {
+        const size_t s_elems = static_cast<size_t>(n_pairs) * D * D;
+        hipError_t e = s0 ? pm::launch_copy_f32(s_out, s0, s_elems, st)
+                          : pm::launch_fill_zero(s_out, s_elems, st);
+        return e == hipSuccess ? 0 : hip_fail(e, "state copy");
+    }
+    pm::RecurrentArgs a{q, k, v, nullptr, s0, o, s_out, nullptr, static_cast<int>(n_pairs), T, H, D,
+                        in_dtype == PM_DTYPE_BF16, out_dtype == PM_DTYPE_BF16, true};
+    hipError_t e = pm::launch_recurrent(a, st);
+    return e == hipSuccess ? 0 : hip_fail(e, "linear attention launch");
+}
+
 int pm_delta_step(float* s_inout, const void* q, const void* k, const void* v,
                   const float* beta, float* o, int B, int H, int D, int in_dtype, void* stream) {
     g_err[0] = '\0';

@@ -14,14 +14,15 @@ struct RecurrentArgs {
     const void* q;
     const void* k;
     const void* v;
-    const float* beta;
-    const float* s0;  // nullable; may alias s_out
+    const float* beta;  // nullable: beta = 1
+    const float* s0;    // nullable; may alias s_out
     void* o;
     float* s_out;
     const int32_t* cu_seqlens;  // nullable
     int n_pairs;
     int T, H, D;
     bool in_bf16, out_bf16;
+    bool l2norm = false;  // q and k divided by max(||.||_2, 1e-6) per token on load
 };
 hipError_t launch_recurrent(const RecurrentArgs& a, hipStream_t st);
 

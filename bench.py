@@ -261,14 +261,14 @@ def main():
         gq, gk, gv = (torch.empty((B, T, H, D), device=dev) for _ in range(3))
         gb = torch.empty((B, T, H), device=dev)
         gs0 = torch.empty((B, H, D, D), device=dev)
-        nbytes = lib.pm_delta_bwd_workspace_bytes(B, T, H, D, _native.DTYPE_BF16)
-        ws = torch.empty(((nbytes + 3) // 4,), device=dev)
+        ws_bytes = lib.pm_delta_bwd_workspace_bytes(B, T, H, D, _native.DTYPE_BF16)
+        ws = torch.empty(((ws_bytes + 3) // 4,), device=dev)
 
         def bwd():
             rc = lib.pm_delta_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), None,
                                   go.data_ptr(), gs.data_ptr(), gq.data_ptr(), gk.data_ptr(),
                                   gv.data_ptr(), gb.data_ptr(), gs0.data_ptr(), B, T, H, D,
-                                  _native.DTYPE_BF16, ws.data_ptr(), nbytes, stream.cuda_stream)
+                                  _native.DTYPE_BF16, ws.data_ptr(), ws_bytes, stream.cuda_stream)
             _native.check(rc)
 
         bwd()
@@ -286,7 +286,7 @@ def main():
             "calls": args.bwd_steps,
             "ms_per_call": bwd_ms,
             "tokens_per_s": tokens / (bwd_ms * 1e-3),
-            "workspace_bytes": nbytes,
+            "workspace_bytes": ws_bytes,
             "roofline": {"bound": "hbm", "achieved": bb / (bwd_ms * 1e-3) / 1e9,
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": bb / (bwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},

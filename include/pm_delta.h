@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 3
+#define PM_DELTA_ABI_VERSION 4
 
 /* element types */
 #define PM_DTYPE_F32 0
@@ -102,6 +102,24 @@ int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float
 int pm_delta_step(float* s_inout, const void* q, const void* k, const void* v,
                   const float* beta, float* o, int B, int H, int D, int in_dtype,
                   void* stream);
+
+/*
+ * Decode step over a serving-side state cache (no reference counterpart in
+ * code: the consumer the reference's serving spec names, spec/13-serving.md
+ * item 4 and sglang-fork/sglang_fork/model_def.py, whose linear layers keep
+ * a fixed-size state per request).  The step of pm_delta_step
+ * (kernels/__init__.py:357-376) for B requests, request b updating the
+ * state pool[slots[b]] in place:
+ *   pool  (n_slots, H, D, D) fp32, 16-byte aligned;  slots (B,) int32;
+ *   q, k, v (B, H, D) fp32 or bf16 (in_dtype);  beta (B, H) fp32;
+ *   o (B, H, D) fp32, 16-byte aligned.
+ * A slot outside [0, n_slots) is skipped: the pool is not touched and the
+ * request's output row is zero (padding in fixed-size, graph-captured
+ * batches).  Two requests naming the same slot race.  D in {32, 64, 128}.
+ */
+int pm_delta_step_slots(float* pool, const int32_t* slots, int n_slots, const void* q,
+                        const void* k, const void* v, const float* beta, float* o, int B, int H,
+                        int D, int in_dtype, void* stream);
 
 /*
  * The model's linear attention (Gated DeltaNet / KDA family, beta = 1).

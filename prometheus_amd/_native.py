@@ -18,7 +18,7 @@ import torch  # noqa: F401  (see module docstring: must precede CDLL)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpmdelta.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256
@@ -31,6 +31,7 @@ EXPORTS = (
     "pm_delta_fwd",
     "pm_delta_fwd_varlen",
     "pm_delta_step",
+    "pm_delta_step_slots",
     "pm_linear_attention",
     "pm_delta_workspace_bytes",
     "pm_delta_bwd",
@@ -75,6 +76,8 @@ def lib() -> ctypes.CDLL:
         L.pm_delta_fwd_varlen.restype = i
         L.pm_delta_step.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, vp]
         L.pm_delta_step.restype = i
+        L.pm_delta_step_slots.argtypes = [vp, vp, i, vp, vp, vp, vp, vp, i, i, i, i, vp]
+        L.pm_delta_step_slots.restype = i
         L.pm_linear_attention.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, i, i, vp]
         L.pm_linear_attention.restype = i
         L.pm_delta_workspace_bytes.argtypes = [i, i, i, i, i]

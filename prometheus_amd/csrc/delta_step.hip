@@ -11,6 +11,12 @@
 // instruction reads or writes two whole 512-byte rows (1 KiB contiguous).
 // Column partial sums are reduced across the row groups of a wave with
 // cross-lane shuffles, then across the 4 waves through LDS.
+//
+// State-cache mode (slots != NULL): the serving side keeps every request's
+// fixed-size state in a pool of n_slots x H x D x D and decodes a batch
+// through a slot table; request b updates pool[slots[b]].  A slot outside
+// [0, n_slots) (padding in a fixed-size, graph-captured batch) is skipped:
+// no state is read or written and the output row is zero.
 
 #include "pm_common.h"
 #include "pm_internal.h"
@@ -25,7 +31,9 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
                                                          const InT* __restrict__ k,
                                                          const InT* __restrict__ v,
                                                          const float* __restrict__ beta,
-                                                         float* __restrict__ o) {
+                                                         float* __restrict__ o,
+                                                         const int32_t* __restrict__ slots,
+                                                         int H, int n_slots) {
     constexpr int NT = 256;
     constexpr int CG = D / 4;      // column groups of 4
     constexpr int RG = NT / CG;    // row groups
@@ -41,7 +49,19 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
     const int cg = t % CG, rg = t / CG;
     const int lane = t & 63, w = t >> 6;
 
-    f32x4* sp = reinterpret_cast<f32x4*>(s + static_cast<size_t>(pair) * D * D);
+    size_t state = pair;
+    if (slots) {
+        const int slot = slots[pair / H];
+        if (slot < 0 || slot >= n_slots) {
+            if (t < CG) {
+                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                reinterpret_cast<f32x4*>(o + static_cast<size_t>(pair) * D)[cg] = z;
+            }
+            return;
+        }
+        state = static_cast<size_t>(slot) * H + pair % H;
+    }
+    f32x4* sp = reinterpret_cast<f32x4*>(s + state * D * D);
     f32x4 S[RPT];
 #pragma unroll
     for (int i = 0; i < RPT; ++i)
@@ -106,11 +126,11 @@ static hipError_t launch_step_d(const StepArgs& a, hipStream_t st) {
     if (a.in_bf16) {
         hipLaunchKernelGGL((delta_step_kernel<D, uint16_t>), dim3(a.n_pairs), dim3(256), 0, st,
                            a.s, static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.k),
-                           static_cast<const uint16_t*>(a.v), a.beta, a.o);
+                           static_cast<const uint16_t*>(a.v), a.beta, a.o, a.slots, a.H, a.n_slots);
     } else {
         hipLaunchKernelGGL((delta_step_kernel<D, float>), dim3(a.n_pairs), dim3(256), 0, st, a.s,
                            static_cast<const float*>(a.q), static_cast<const float*>(a.k),
-                           static_cast<const float*>(a.v), a.beta, a.o);
+                           static_cast<const float*>(a.v), a.beta, a.o, a.slots, a.H, a.n_slots);
     }
     return hipGetLastError();
 }

@@ -255,6 +255,30 @@ int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float
                    out_dtype, chunk, static_cast<hipStream_t>(stream));
 }
 
+int pm_delta_step_slots(float* pool, const int32_t* slots, int n_slots, const void* q,
+                        const void* k, const void* v, const float* beta, float* o, int B, int H,
+                        int D, int in_dtype, void* stream) {
+    g_err[0] = '\0';
+    if (B < 0 || H < 0 || n_slots < 0)
+        return fail(PM_E_SHAPE, "B, H, n_slots must be >= 0 (got %d, %d, %d)", B, H, n_slots);
+    if (!pm::step_supported(D))
+        return fail(PM_E_UNSUPPORTED, "slot-indexed decode step needs D in {32, 64, 128} (got %d)", D);
+    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16)
+        return fail(PM_E_DTYPE, "in_dtype %d is not PM_DTYPE_F32 or PM_DTYPE_BF16", in_dtype);
+    const long n_pairs = static_cast<long>(B) * H;
+    if (n_pairs == 0) return 0;
+    if (n_pairs > (1L << 30) || static_cast<long>(n_slots) * H > (1L << 30))
+        return fail(PM_E_SHAPE, "problem too large");
+    if (!slots || !q || !k || !v || !beta || !o || (n_slots > 0 && !pool))
+        return fail(PM_E_NULL, "slots, q, k, v, beta, o (and pool when n_slots > 0) must be non-NULL");
+    if ((pool && !aligned(pool, 16)) || !aligned(o, 16) || !aligned(slots, 4) || !aligned(beta, 4))
+        return fail(PM_E_ALIGN, "pool and o must be 16-byte aligned, slots and beta 4-byte aligned");
+    pm::StepArgs a{pool, q, k, v, beta, o, static_cast<int>(n_pairs), D, in_dtype == PM_DTYPE_BF16,
+                   slots, H, n_slots};
+    hipError_t e = pm::launch_step(a, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? 0 : hip_fail(e, "slot decode step launch");
+}
+
 int pm_linear_attention(const void* q, const void* k, const void* v, const float* s0, void* o,
                         float* s_out, int B, int T, int H, int D, int in_dtype, int out_dtype,
                         void* stream) {

@@ -36,6 +36,11 @@ struct StepArgs {
     float* o;
     int n_pairs, D;
     bool in_bf16;
+    // State-cache mode (nullable): request b = pair / H updates the state of slot
+    // slots[b] in a pool of n_slots x H states; a slot outside [0, n_slots)
+    // leaves the pool untouched and gets a zero output row.
+    const int32_t* slots = nullptr;
+    int H = 1, n_slots = 0;
 };
 bool step_supported(int D);
 hipError_t launch_step(const StepArgs& a, hipStream_t st);

@@ -288,3 +288,40 @@ def test_synth_configs_and_lengths():
     np.testing.assert_allclose(np.linalg.norm(x.q, axis=-1), 1.0, atol=1e-2)
     assert x.q_bits.dtype == np.uint16 and x.s0.shape == (1, 2, 16, 16)
     assert np.all((x.beta > 0) & (x.beta < 1))
+
+
+def test_state_cache_bookkeeping_without_gpu():
+    from prometheus_amd import serving
+
+    cache = serving.LinearStateCache(2, 4, 1, 8, device="cpu")
+    a = cache.alloc(3)
+    assert a == [0, 1, 2] and cache.n_free == 1
+    cache.pool[:, a] = 1.0
+    cache.free([1])
+    assert cache.alloc(1) == [1]  # freed slots come back zeroed
+    assert float(cache.pool[:, 1].abs().sum()) == 0.0
+    with pytest.raises(RuntimeError):
+        cache.alloc(2)
+    with pytest.raises(ValueError):
+        cache.free([3])  # never allocated
+    with pytest.raises(ValueError):
+        cache.reset([4])  # outside the pool
+    with pytest.raises(RuntimeError):  # computing needs the GPU: no host fallback
+        cache.decode(0, None, None, None, None, None)
+
+
+def test_slot_decode_abi_validation_without_gpu():
+    lib = _native.lib()
+    p = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+
+    def call(n_slots, b, h, d, dt=1, pool=p, slots=p, o=p):
+        return lib.pm_delta_step_slots(pool, slots, n_slots, p, p, p, p, o, b, h, d, dt, None)
+
+    assert call(4, 2, 2, 48) == _native.E_UNSUPPORTED
+    assert call(4, 2, 2, 64, dt=5) == _native.E_DTYPE
+    assert call(-1, 2, 2, 64) == _native.E_SHAPE
+    assert call(4, 2, 2, 64, slots=None) == _native.E_NULL
+    assert call(4, 2, 2, 64, pool=None) == _native.E_NULL
+    assert call(4, 2, 2, 64, pool=ctypes.c_void_p(8)) == _native.E_ALIGN
+    assert call(4, 2, 2, 64, o=ctypes.c_void_p(8)) == _native.E_ALIGN
+    assert call(4, 0, 2, 64) == 0  # nothing to do

@@ -14,8 +14,10 @@ forward kernel (HBM-bound at this shape: 340.8 MB vs 47.6 GFLOP) and
 ``cpu_baseline`` (the C restatement of the reference's per-token CPU
 algorithm, OpenMP over the 64 (b, h) sequences, on this host). The decode
 step (cfg4: B=256 H=32 D=128, fp32 state updated in place) is measured in
-the same run and reported under ``decode``, and the backward at cfg1 under
-``backward``.
+the same run and reported under ``decode`` (with the same batch through a
+serving state cache under ``decode.state_cache``), the backward at cfg1
+under ``backward``, and the model's linear attention at the cfg1 shape
+under ``model_linear_attention``.
 """
 
 from __future__ import annotations
@@ -103,6 +105,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--decode-steps", type=int, default=64)
+    ap.add_argument("--model-calls", type=int, default=2,
+                    help="timed pm_linear_attention calls at the cfg1 shape (0 skips)")
     ap.add_argument("--bwd-steps", type=int, default=3,
                     help="timed calls of the backward at cfg1 (0 skips it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -250,6 +254,75 @@ def main():
                      "frac": dbytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
     }
 
+    # the same decode through a serving state cache: a pool of 2*B slots, the batch's
+    # requests on a random half of them (pm_delta_step_slots)
+    pool = (torch.randn((2 * Bd, Hd, D, D), generator=g, device=dev) * 0.02).contiguous()
+    perm = torch.randperm(2 * Bd, generator=torch.Generator().manual_seed(6))[:Bd]
+    slots = perm.to(torch.int32).to(dev)
+
+    def step_slots(i):
+        qd, kd, vd, bd = toks[i % 2]
+        rc = lib.pm_delta_step_slots(pool.data_ptr(), slots.data_ptr(), 2 * Bd, qd.data_ptr(),
+                                     kd.data_ptr(), vd.data_ptr(), bd.data_ptr(), od.data_ptr(),
+                                     Bd, Hd, D, _native.DTYPE_BF16, stream.cuda_stream)
+        _native.check(rc)
+
+    for i in range(4):
+        step_slots(i)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.decode_steps)]
+    for i in range(args.decode_steps):
+        ev[i][0].record(stream)
+        step_slots(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    slot_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    decode["state_cache"] = {
+        "workload": "cfg4 decode through a 512-slot state cache (pm_delta_step_slots)",
+        "us_per_step": slot_ms * 1e3,
+        "roofline": {"bound": "hbm", "achieved": dbytes / (slot_ms * 1e-3) / 1e9,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dbytes / (slot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+    }
+    del pool, state
+
+    # the model's linear attention (pm_linear_attention: q/k L2-normalised in the
+    # kernel, beta = 1) at the cfg1 shape, fp32 inputs as the reference's model uses
+    model_la = None
+    if args.model_calls > 0:
+        g.manual_seed(7)
+        qm, km, vm = (torch.randn((B, T, H, D), generator=g, device=dev) for _ in range(3))
+        om = torch.empty((B, T, H, D), device=dev)
+        sm = torch.empty((B, H, D, D), device=dev)
+
+        def la():
+            rc = lib.pm_linear_attention(qm.data_ptr(), km.data_ptr(), vm.data_ptr(), None,
+                                         om.data_ptr(), sm.data_ptr(), B, T, H, D,
+                                         _native.DTYPE_F32, _native.DTYPE_F32, stream.cuda_stream)
+            _native.check(rc)
+
+        la()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.model_calls):
+            la()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        la_ms = e0.elapsed_time(e1) / args.model_calls
+        lb = fwd_bytes(B, T, H, D, s_in=4, s_out=4) - 4 * B * T * H  # no beta array
+        model_la = {
+            "workload": "cfg1 shape, model.linear_attention (beta 1, L2-normalised q/k), fp32 in/out",
+            "calls": args.model_calls,
+            "ms_per_call": la_ms,
+            "tokens_per_s": tokens / (la_ms * 1e-3),
+            "roofline": {"bound": "hbm", "achieved": lb / (la_ms * 1e-3) / 1e9,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": lb / (la_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        }
+        del qm, km, vm, om, sm
+
     # backward at cfg1 (chunked_delta_rule_bwd through the C ABI): bf16 q/k/v, zero S0,
     # random go and gS, fp32 gradients
     backward = None
@@ -330,6 +403,7 @@ def main():
         "cpu_baseline": cpu,
         "parity": parity,
         "decode": decode,
+        "model_linear_attention": model_la,
         "backward": backward,
     }
     print(json.dumps(line), flush=True)

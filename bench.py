@@ -287,41 +287,47 @@ def main():
     }
     del pool, state
 
-    # the model's linear attention (pm_linear_attention: q/k L2-normalised in the
-    # kernel, beta = 1) at the cfg1 shape, fp32 inputs as the reference's model uses
+    # the model's linear attention (pm_linear_attention: q/k L2-normalised inside the
+    # kernel, beta = 1) at the cfg1 shape: bf16 q/k/v on the chunked kernel, and fp32
+    # (the reference model's dtype) on the per-token kernel
     model_la = None
     if args.model_calls > 0:
+        model_la = {"workload": "cfg1 shape, model.linear_attention (beta 1, L2-normalised q/k)"}
         g.manual_seed(7)
-        qm, km, vm = (torch.randn((B, T, H, D), generator=g, device=dev) for _ in range(3))
         om = torch.empty((B, T, H, D), device=dev)
         sm = torch.empty((B, H, D, D), device=dev)
+        for name, dt, code, s_in in (("bf16", torch.bfloat16, _native.DTYPE_BF16, 2),
+                                     ("fp32", torch.float32, _native.DTYPE_F32, 4)):
+            qm, km, vm = (torch.randn((B, T, H, D), generator=g, device=dev).to(dt) for _ in range(3))
 
-        def la():
-            rc = lib.pm_linear_attention(qm.data_ptr(), km.data_ptr(), vm.data_ptr(), None,
-                                         om.data_ptr(), sm.data_ptr(), B, T, H, D,
-                                         _native.DTYPE_F32, _native.DTYPE_F32, stream.cuda_stream)
-            _native.check(rc)
+            def la():
+                rc = lib.pm_linear_attention(qm.data_ptr(), km.data_ptr(), vm.data_ptr(), None,
+                                             om.data_ptr(), sm.data_ptr(), B, T, H, D, code,
+                                             _native.DTYPE_F32, stream.cuda_stream)
+                _native.check(rc)
 
-        la()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(args.model_calls):
             la()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        la_ms = e0.elapsed_time(e1) / args.model_calls
-        lb = fwd_bytes(B, T, H, D, s_in=4, s_out=4) - 4 * B * T * H  # no beta array
-        model_la = {
-            "workload": "cfg1 shape, model.linear_attention (beta 1, L2-normalised q/k), fp32 in/out",
-            "calls": args.model_calls,
-            "ms_per_call": la_ms,
-            "tokens_per_s": tokens / (la_ms * 1e-3),
-            "roofline": {"bound": "hbm", "achieved": lb / (la_ms * 1e-3) / 1e9,
-                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": lb / (la_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
-        }
-        del qm, km, vm, om, sm
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            calls = args.model_calls * (10 if name == "bf16" else 1)
+            e0.record(stream)
+            for _ in range(calls):
+                la()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            la_ms = e0.elapsed_time(e1) / calls
+            lb = fwd_bytes(B, T, H, D, s_in=s_in, s_out=4) - 4 * B * T * H  # no beta array
+            model_la[name] = {
+                "kernel": "chunked MFMA, norms folded in" if name == "bf16" else "per-token fp32",
+                "calls": calls,
+                "ms_per_call": la_ms,
+                "tokens_per_s": tokens / (la_ms * 1e-3),
+                "roofline": {"bound": "hbm", "achieved": lb / (la_ms * 1e-3) / 1e9,
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": lb / (la_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+            }
+            del qm, km, vm
+        del om, sm
 
     # backward at cfg1 (chunked_delta_rule_bwd through the C ABI): bf16 q/k/v, zero S0,
     # random go and gS, fp32 gradients

@@ -127,9 +127,12 @@ int pm_delta_step_slots(float* pool, const int32_t* slots, int n_slots, const vo
  * 393-432, called by model._linear_attn :726-734): per (b, h) and token,
  *   q^ = q / max(||q||, 1e-6),  k^ = k / max(||k||, 1e-6)   (:203-205)
  *   S_t = (I - k^ k^^T) S_{t-1} + k^ v^T,   o_t = q^ S_t
- * with the normalisation done by the kernel as it loads q and k (no
- * normalised copies in memory).  Shapes, dtypes and state handling as
- * pm_delta_fwd without beta; fp32 recurrence (the per-token kernel).
+ * with the normalisation done inside the kernel (no normalised copies in
+ * memory).  Shapes, dtypes and state handling as pm_delta_fwd without beta.
+ * Kernels as pm_delta_fwd chooses them (pm_delta_set_path): bf16 q/k/v with
+ * D in {64, 128} run the chunked MFMA kernel, which folds the norms into its
+ * Gram tiles and row scalings (bf16 parity); everything else runs the fp32
+ * per-token kernel, which normalises the rows as it stages them (fp32 parity).
  */
 int pm_linear_attention(const void* q, const void* k, const void* v, const float* s0, void* o,
                         float* s_out, int B, int T, int H, int D, int in_dtype, int out_dtype,

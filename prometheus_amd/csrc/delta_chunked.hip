@@ -75,6 +75,9 @@ struct Geo {
     // one TP buffer: T and P, 6 operand blocks of 1 KiB each
     static constexpr int TP = 2 * 6 * 1024;
     static constexpr int BYTES = NRAW * RAW + 2 * TP;
+    // NORM mode: per chunk parity, 1/||k_t|| then 1/||q_t|| (64 floats each) after the TP buffers
+    static constexpr int RN = BYTES;
+    static constexpr int BYTES_NORM = BYTES + 2 * 512;
     static_assert(D == 64 || D == 128, "D");
     static_assert(DV == 16 || DV == 32, "DV");
     static_assert(NI_V >= 1 && RAW % 16 == 0, "RAW layout");
@@ -85,7 +88,18 @@ struct Geo {
 // each chain wave writes the state at the start of every chunk, rounded to
 // bf16, as rows of S^T: s_hist[(pair * n_chunks + c) * D * D + col * D + d]
 // (fixed-length batches only).
-template <int D, int DV, bool OUT_BF16, bool HIST>
+//
+// NORM: the model's linear attention (model/__init__.py:393-432): beta = 1
+// and q, k divided by max(||.||, 1e-6) per token, without rewriting them.
+// With r_t = 1 / max(||k_t||, 1e-6) and rq_t likewise for q, the chunk
+// algebra on the raw rows is
+//   A = strict_lower(diag(r) K K^T diag(r)),   U = T (V - diag(r) K S),
+//   S += K^T diag(r) U,   O = diag(rq) (Q S + lower_incl(Q K^T) diag(r) U).
+// The T producer reads ||k_t||^2 off the diagonal of its K K^T tiles and
+// scales the Gram entries; the P producer forms the four diagonal tiles of
+// Q Q^T alongside Q K^T for ||q_t||^2 and scales P's rows; both hand r and rq
+// to the chain through LDS with T and P.
+template <int D, int DV, bool OUT_BF16, bool HIST, bool NORM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void delta_chunked_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ beta,
@@ -129,6 +143,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     auto tpb = [&](int c) {
         return reinterpret_cast<uint16_t*>(smem + G::NRAW * G::RAW + (c & 1) * G::TP);
     };
+    auto rnb = [&](int c) { return reinterpret_cast<float*>(smem + G::RN + (c & 1) * 512); };
 
     // ---------------- loader: chunk c's K, Q, V tile and beta, HBM -> LDS ----------------
     // Copy instruction i, lane L fills LDS bytes [1024 i + 16 L, +16) of the tile: row r,
@@ -144,7 +159,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const __amdgpu_buffer_rsrc_t rk = make_rsrc(k + row0, n_kq);
         const __amdgpu_buffer_rsrc_t rq = make_rsrc(q + row0, n_kq);
         const __amdgpu_buffer_rsrc_t rv = make_rsrc(v + row0 + col0, n_v);
-        const __amdgpu_buffer_rsrc_t rb = make_rsrc(beta + (tok0 + base) * H + h, n_b);
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(NORM ? beta : beta + (tok0 + base) * H + h, NORM ? 0u : n_b);
         unsigned char* rbuf = uniform_ptr(raw(c));
 #pragma unroll
         for (int i = 0; i < G::NI_KQ; ++i) {
@@ -161,7 +176,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const unsigned vo = static_cast<unsigned>(r * tstride * 2) + 16u * (p ^ v_f<DV>(r));
             copy_to_lds(rv, rbuf + G::R_VS + 1024 * i, 16, vo);
         }
-        copy_to_lds(rb, rbuf + G::R_BS, 4, static_cast<unsigned>(lane * H * 4));
+        if constexpr (!NORM) copy_to_lds(rb, rbuf + G::R_BS, 4, static_cast<unsigned>(lane * H * 4));
     };
 
     // ---------------- producer 0: T = (I + A)^-1 in packed operand order ----------------
@@ -191,13 +206,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             gu[4] = mfma32(f[1], f[3], gu[4]);  // (1,3)
             gu[5] = mfma32(f[2], f[3], gu[5]);  // (2,3)
         }
-        // beta of the rows this lane holds in accumulator form (br4) and in A-operand form (bc)
-        f32x4_t br4[4];
-        float bc[4];
+        // beta of the rows this lane holds in accumulator form (br4) and in A-operand form (bc);
+        // NORM: beta = 1, and r_t = 1 / max(||k_t||, 1e-6) on both sides of every Gram entry
+        f32x4_t br4[4], rr4[4];
+        float bc[4], rc[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            br4[b] = *reinterpret_cast<const f32x4_t*>(Bs + 16 * b + 4 * lg);
-            bc[b] = Bs[16 * b + l16];
+            if constexpr (NORM) {
+                // ||k_t||^2, t = 16b + l16, is entry (l16, l16) of the diagonal tile: lane
+                // (l16 / 4, l16), component l16 % 4
+                const int c4 = l16 & 3;
+                const float dg = c4 == 0 ? gd[b].x : c4 == 1 ? gd[b].y : c4 == 2 ? gd[b].z : gd[b].w;
+                rc[b] = 1.f / fmaxf(sqrtf(__shfl(dg, 16 * (l16 >> 2) + l16)), 1e-6f);  // row 16b + l16
+#pragma unroll
+                for (int r = 0; r < 4; ++r) rr4[b][r] = __shfl(rc[b], 20 * lg + r);  // row 16b + 4lg + r
+                br4[b] = rr4[b] * rc[b];  // N[row][l16] and N[l16][row] carry r_row r_l16
+                bc[b] = 1.f;
+            } else {
+                br4[b] = *reinterpret_cast<const f32x4_t*>(Bs + 16 * b + 4 * lg);
+                bc[b] = Bs[16 * b + l16];
+            }
+        }
+        if constexpr (NORM) {
+            float* rn = rnb(c);
+            if (lg == 0) {
+#pragma unroll
+                for (int b = 0; b < 4; ++b) rn[16 * b + l16] = rc[b];
+            }
         }
         f32x4_t eye;
 #pragma unroll
@@ -212,7 +247,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int r = 0; r < 4; ++r) {
                 const int row = 4 * lg + r;
                 n[r] = (row > l16) ? -br4[b][r] * gd[b][r] : 0.f;   // N[row][l16]
-                nt[r] = (l16 > row) ? -bc[b] * gd[b][r] : 0.f;      // N[l16][row]
+                nt[r] = (l16 > row) ? -(NORM ? br4[b][r] : bc[b]) * gd[b][r] : 0.f;  // N[l16][row]
             }
             cn[b] = cvt4(n);
             cnt[b] = cvt4(nt);
@@ -236,7 +271,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             // cet = (I + N)^T as an accumulator, rebuilt from cnt's source values
             f32x4_t nt;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) nt[r] = (l16 > 4 * lg + r) ? -bc[b] * gd[b][r] : 0.f;
+            for (int r = 0; r < 4; ++r)
+                nt[r] = (l16 > 4 * lg + r) ? -(NORM ? br4[b][r] : bc[b]) * gd[b][r] : 0.f;
             cet[b] = cvt4(nt + eye);
             n4[b] = mfma16(cn2t[b], cn2[b], zero);
             n4t[b] = mfma16(cn2[b], cn2t[b], zero);
@@ -264,11 +300,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             ddt[b] = mfma16(ci8, cf2t, zero);
         }
         // A_ik as an A operand: upper tile (k, i) of K K^T, rows scaled by beta_{16i+l16}
-        auto a_op = [&](int x, int i) { return cvt4(bc[i] * gu[x]); };
+        // (NORM: by r_{16i+l16}, and its columns 16k + 4g + r by r_{16k+4g+r})
+        auto a_op = [&](int x, int i, int k) {
+            if constexpr (NORM) return cvt4(rc[i] * (rr4[k] * gu[x]));
+            else return cvt4(bc[i] * gu[x]);
+        };
         const u32x2_t cd0 = cvt4(dd[0]), cd1 = cvt4(dd[1]), cd2 = cvt4(dd[2]);
         const u32x2_t cdt1 = cvt4(ddt[1]), cdt2 = cvt4(ddt[2]), cdt3 = cvt4(ddt[3]);
-        const u32x2_t a10 = a_op(0, 1), a20 = a_op(1, 2), a21 = a_op(2, 2);
-        const u32x2_t a30 = a_op(3, 3), a31 = a_op(4, 3), a32 = a_op(5, 3);
+        const u32x2_t a10 = a_op(0, 1, 0), a20 = a_op(1, 2, 0), a21 = a_op(2, 2, 1);
+        const u32x2_t a30 = a_op(3, 3, 0), a31 = a_op(4, 3, 1), a32 = a_op(5, 3, 2);
         // T_ij = -D_i Z_ij with Z_ij = sum_k A_ik T_kj; cdt_i is D_i as an A operand and
         // D_i^T as a B operand, so -mfma(Z, cdt_i) is T_ij^T (what the packed store takes)
         // level 1
@@ -313,6 +353,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         f32x4_t p[10];
 #pragma unroll
         for (int x = 0; x < 10; ++x) p[x] = zero;
+        f32x4_t qd[4] = {zero, zero, zero, zero};  // NORM: diagonal tiles of Q Q^T
 #pragma unroll
         for (int kb = 0; kb < D / 32; ++kb) {
             bf16x8_t fk[4], fq[4];
@@ -321,6 +362,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 fk[r] = lds_op_kq<D>(Ks, 16 * r + l16, kb, lg);
                 fq[r] = lds_op_kq<D>(Qs, 16 * r + l16, kb, lg);
             }
+            if constexpr (NORM) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) qd[r] = mfma32(fq[r], fq[r], qd[r]);
+            }
             // accumulator of (P_ij)^T = K_j Q_i^T: lane holds P[16i+l16][16j+4g+r]
             int x = 0;
 #pragma unroll
@@ -328,12 +373,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
                 for (int j = 0; j <= i; ++j, ++x) p[x] = mfma32(fk[j], fq[i], p[x]);
         }
+        float rq[4];  // NORM: 1 / max(||q_{16i + l16}||, 1e-6), P's rows scale
+        if constexpr (NORM) {
+            float* rn = rnb(c) + kC;
+            const int c4 = l16 & 3;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // ||q_t||^2, t = 16i + l16: lane (l16 / 4, l16), component l16 % 4 of tile i
+                const float dg = c4 == 0 ? qd[i].x : c4 == 1 ? qd[i].y : c4 == 2 ? qd[i].z : qd[i].w;
+                rq[i] = 1.f / fmaxf(sqrtf(__shfl(dg, 16 * (l16 >> 2) + l16)), 1e-6f);
+                if (lg == 0) rn[16 * i + l16] = rq[i];
+            }
+        }
         int x = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j <= i; ++j, ++x) {
                 f32x4_t t = p[x];
+                if constexpr (NORM) t = t * rq[i];
                 if (i == j) {  // keep t >= s: row l16, column 4g+r
 #pragma unroll
                     for (int r = 0; r < 4; ++r) t[r] = (l16 >= 4 * lg + r) ? t[r] : 0.f;
@@ -403,11 +461,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         u32x2_t vv2 = lds_v_issue<DV>(Vs, 2, w, lane), vv3 = lds_v_issue<DV>(Vs, 3, w, lane);
         lds_wait(vv0, vv1, vv2, vv3);
         const u32x2_t vv[4] = {vv0, vv1, vv2, vv3};
-        f32x4_t R[4];
+        f32x4_t R[4], rk4[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + 16 * m + 4 * lg);
-            R[m] = bs * (widen4(vv[m]) - X[m]);
+            if constexpr (NORM) {
+                rk4[m] = *reinterpret_cast<const f32x4_t*>(rnb(c) + 16 * m + 4 * lg);
+                R[m] = widen4(vv[m]) - rk4[m] * X[m];
+            } else {
+                const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + 16 * m + 4 * lg);
+                R[m] = bs * (widen4(vv[m]) - X[m]);
+            }
         }
         const bf16x8_t Rb0 = acc_to_b(R[0], R[1]), Rb1 = acc_to_b(R[2], R[3]);
         // U = T R
@@ -416,6 +479,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         U[1] = mfma32(packed_a(Tp, 1, lane), Rb0, zero);
         U[2] = mfma32(packed_a(Tp, 3, lane), Rb1, mfma32(packed_a(Tp, 2, lane), Rb0, zero));
         U[3] = mfma32(packed_a(Tp, 5, lane), Rb1, mfma32(packed_a(Tp, 4, lane), Rb0, zero));
+        if constexpr (NORM) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) U[m] = rk4[m] * U[m];  // diag(r) U
+        }
         const bf16x8_t Ub0 = acc_to_b(U[0], U[1]), Ub1 = acc_to_b(U[2], U[3]);
         // S += K^T U (K^T operands by transpose reads of the token rows)
 #pragma unroll
@@ -434,6 +501,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
         // O^T = Y^T + U^T P^T (U tiles as the A operand give U^T; the packed P rows are the
         // B operand P^T); lane (g, l16) holds O[16m+l16][4g..4g+3] of its 16 columns
+        if constexpr (NORM) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) Y[m] = Y[m] * rnb(c)[kC + 16 * m + l16];  // diag(rq) Q S
+        }
         f32x4_t O[4];
         O[0] = mfma32(Ub0, packed_a(Pp, 0, lane), Y[0]);
         O[1] = mfma32(Ub0, packed_a(Pp, 1, lane), Y[1]);
@@ -503,10 +574,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
-template <int D, int DV, bool OB, bool HIST>
+template <int D, int DV, bool OB, bool HIST, bool NORM = false>
 hipError_t launch_t(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
     using G = Geo<D, DV>;
-    auto kern = delta_chunked_kernel<D, DV, OB, HIST>;
+    constexpr int kBytes = NORM ? G::BYTES_NORM : G::BYTES;
+    auto kern = delta_chunked_kernel<D, DV, OB, HIST, NORM>;
     // the dynamic-LDS limit is a per-device function attribute
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -514,7 +586,7 @@ hipError_t launch_t(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
     static bool attr_set[64] = {};
     if (dev < 0 || dev >= 64 || !attr_set[dev]) {
         e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, G::BYTES);
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kBytes);
         if (e != hipSuccess) return e;
         if (dev >= 0 && dev < 64) attr_set[dev] = true;
     }
@@ -522,13 +594,16 @@ hipError_t launch_t(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
     const int n_tiles = D / DV;
     const int slots = (n_pairs + 7) / 8;
     const dim3 grid(static_cast<unsigned>(slots * 8 * n_tiles));
-    hipLaunchKernelGGL(kern, grid, dim3(256), G::BYTES, st, a.q, a.k, a.v, a.beta, a.s0, a.o,
+    hipLaunchKernelGGL(kern, grid, dim3(256), kBytes, st, a.q, a.k, a.v, a.beta, a.s0, a.o,
                        a.s_out, s_hist, a.cu_seqlens, n_pairs, a.T, a.H, n_tiles);
     return hipGetLastError();
 }
 
 template <int D, int DV>
 hipError_t launch_dv(const ChunkedArgs& a, hipStream_t st) {
+    if (a.norm)
+        return a.out_bf16 ? launch_t<D, DV, true, false, true>(a, nullptr, st)
+                          : launch_t<D, DV, false, false, true>(a, nullptr, st);
     return a.out_bf16 ? launch_t<D, DV, true, false>(a, nullptr, st)
                       : launch_t<D, DV, false, false>(a, nullptr, st);
 }

@@ -304,6 +304,22 @@ int pm_linear_attention(const void* q, const void* k, const void* v, const float
                           : pm::launch_fill_zero(s_out, s_elems, st);
         return e == hipSuccess ? 0 : hip_fail(e, "state copy");
     }
+    const int path = g_path.load();
+    const bool can_chunked = in_dtype == PM_DTYPE_BF16 && pm::chunked_supported(D, H) &&
+                             aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
+                             (out_dtype == PM_DTYPE_F32 ? aligned(o, 16) : aligned(o, 8));
+    if (path == 2 && !can_chunked)
+        return fail(PM_E_UNSUPPORTED,
+                    "chunked kernel needs bf16 inputs, D in {64, 128} and 16-byte aligned "
+                    "q/k/v/o (got in_dtype %d, D %d)",
+                    in_dtype, D);
+    if (path != 1 && can_chunked) {
+        pm::ChunkedArgs a{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                          static_cast<const uint16_t*>(v), nullptr, s0, o, s_out, nullptr, B, T, H, D,
+                          out_dtype == PM_DTYPE_BF16, g_tile.load(), true};
+        hipError_t e = pm::launch_chunked(a, st);
+        return e == hipSuccess ? 0 : hip_fail(e, "chunked linear attention launch");
+    }
     pm::RecurrentArgs a{q, k, v, nullptr, s0, o, s_out, nullptr, static_cast<int>(n_pairs), T, H, D,
                         in_dtype == PM_DTYPE_BF16, out_dtype == PM_DTYPE_BF16, true};
     hipError_t e = pm::launch_recurrent(a, st);

@@ -59,6 +59,9 @@ struct ChunkedArgs {
     int T, H, D;                // varlen: T = packed token count
     bool out_bf16;
     int dv_tile;  // 0 = automatic
+    // The model's linear attention: beta = 1 (beta unused) and q, k divided by
+    // max(||.||, 1e-6) per token inside the kernel.
+    bool norm = false;
 };
 bool chunked_supported(int D, int H);  // D in {64, 128}, H*D <= 2^24
 hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st);

@@ -2,9 +2,10 @@
 the pinned oracle (oracle/model_oracle.py), following the reference's own
 tests of model.linear_attention (tests/test_model.py:353-406, seeds 7-10,
 rtol = atol = 1e-5 there) and adding: head dimensions up to 128 over
-several hundred tokens, bf16 inputs, zero and tiny vectors (the eps guard),
-a 3-D state, torch tensors in place, and the projection layer _linear_attn
-(model/__init__.py:726-734).
+several hundred tokens, zero and tiny vectors (the eps guard), a 3-D state,
+torch tensors in place, the projection layer _linear_attn
+(model/__init__.py:726-734), and bf16 inputs on the chunked MFMA kernel with
+the norms folded in (rel-L2 <= 2e-2, the bf16 bound).
 """
 
 from __future__ import annotations
@@ -14,8 +15,8 @@ import pytest
 import torch
 
 from oracle import model_oracle as mref
-from prometheus_amd import model
-from tests.parity import assert_f32_parity
+from prometheus_amd import _native, model
+from tests.parity import assert_bf16_parity, assert_f32_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -99,16 +100,63 @@ def test_zero_and_tiny_vectors():
     np.testing.assert_allclose(st, st_r, **TOL)
 
 
+def _bf16(rng, shape):
+    x = torch.from_numpy(_rand(rng, shape)).to(torch.bfloat16).cuda()
+    return x, x.float().cpu().numpy()
+
+
 def test_bf16_and_torch_tensors_in_place():
+    """bf16 tensors, used in place: the chunked kernel (bf16 parity) by default,
+    the per-token kernel (fp32 parity on the rounded values) under path 1."""
     rng = np.random.default_rng(12)
-    q, k, v = (_rand(rng, (2, 50, 2, 64)) for _ in range(3))
-    qb, kb, vb = (torch.from_numpy(x).to(torch.bfloat16).cuda() for x in (q, k, v))
+    (qb, q), (kb, k), (vb, v) = (_bf16(rng, (2, 50, 2, 64)) for _ in range(3))
+    out_r, st_r = mref.linear_attention(q, k, v, dtype=np.float64)
     out, st = model.linear_attention(qb, kb, vb)
     assert isinstance(out, torch.Tensor) and out.is_cuda and out.dtype == torch.float32
-    rounded = [x.float().cpu().numpy() for x in (qb, kb, vb)]
-    out_r, st_r = mref.linear_attention(*rounded, dtype=np.float64)
-    assert_f32_parity(out.cpu().numpy(), out_r, "bf16 out")
-    assert_f32_parity(st.cpu().numpy(), st_r, "bf16 state")
+    assert_bf16_parity(out.cpu().numpy(), out_r, "chunked out")
+    assert_bf16_parity(st.cpu().numpy(), st_r, "chunked state")
+    old = _native.set_path(1)
+    try:
+        out1, st1 = model.linear_attention(qb, kb, vb)
+    finally:
+        _native.set_path(old)
+    assert_f32_parity(out1.cpu().numpy(), out_r, "per-token out")
+    assert_f32_parity(st1.cpu().numpy(), st_r, "per-token state")
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1, 64), (2, 77, 3, 64), (1, 200, 2, 128), (2, 64, 1, 128)])
+@pytest.mark.parametrize("state", [False, True])
+def test_chunked_kernel_against_oracle(shape, state):
+    """bf16 q/k/v, D in {64, 128}: the chunked kernel folding the norms into its tiles."""
+    rng = np.random.default_rng(sum(shape) + state)
+    (qb, q), (kb, k), (vb, v) = (_bf16(rng, shape) for _ in range(3))
+    s0 = (_rand(rng, (shape[0], shape[2], shape[3], shape[3])) * 0.05) if state else None
+    out, st = model.linear_attention(qb, kb, vb, state=None if s0 is None else torch.from_numpy(s0).cuda())
+    out_r, st_r = mref.linear_attention(q, k, v, s0, dtype=np.float64)
+    assert_bf16_parity(out.cpu().numpy(), out_r, f"{shape} out")
+    assert_bf16_parity(st.cpu().numpy(), st_r, f"{shape} state")
+
+
+def test_chunked_kernel_large_zero_rows_and_repeatable():
+    """(2, 1000, 4, 128) against the per-token kernel on the same bf16 inputs, with
+    zero and tiny q/k rows (the eps guard), and bitwise repeatable."""
+    rng = np.random.default_rng(13)
+    shape = (2, 1000, 4, 128)
+    (qb, _), (kb, _), (vb, _) = (_bf16(rng, shape) for _ in range(3))
+    qb[0, 10, 1] = 0
+    kb[1, 500, 2] = 0
+    kb[0, 65, 0] = 1e-9
+    a = model.linear_attention(qb, kb, vb)
+    old = _native.set_path(1)
+    try:
+        exact = model.linear_attention(qb, kb, vb)
+    finally:
+        _native.set_path(old)
+    for x, e, n in zip(a, exact, ("out", "state")):
+        assert_bf16_parity(x.cpu().numpy(), e.cpu().numpy(), n)
+    assert torch.all(a[0][0, 10, 1] == 0)
+    b = model.linear_attention(qb, kb, vb)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
 def test_empty_sequence_passes_state_through():

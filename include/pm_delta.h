@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 4
+#define PM_DELTA_ABI_VERSION 5
 
 /* element types */
 #define PM_DTYPE_F32 0
@@ -102,6 +102,29 @@ int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float
 int pm_delta_step(float* s_inout, const void* q, const void* k, const void* v,
                   const float* beta, float* o, int B, int H, int D, int in_dtype,
                   void* stream);
+
+/*
+ * The gated delta rule (Gated DeltaNet; the reference names it as its
+ * model's intent, spec/03-model.md:12, and has no code for it:
+ * PROGRESS.md:109).  No reference counterpart: the recurrence of
+ * pm_delta_fwd with a per-(token, head) log-gate g, alpha = exp(g):
+ *   S_t = alpha_t (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T,  o_t = q_t S_t
+ * g (B, T, H) fp32, NULL only when B*T*H == 0; everything else as
+ * pm_delta_fwd (chunk 64).  bf16 q/k/v with D in {64, 128} run the chunked
+ * MFMA kernel (in-chunk decays exp(G_t - G_s), at most 1 when g <= 0);
+ * other inputs run the fp32 per-token kernel.
+ */
+int pm_gated_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
+                       const float* g, const float* s0, void* o, float* s_out, int B, int T, int H,
+                       int D, int in_dtype, int out_dtype, void* stream);
+
+/*
+ * One gated step: S' = alpha (S - beta k (k^T S)) + beta k v^T, o = q S',
+ * alpha = exp(g), g (B, H) fp32; otherwise as pm_delta_step.
+ */
+int pm_gated_delta_step(float* s_inout, const void* q, const void* k, const void* v,
+                        const float* beta, const float* g, float* o, int B, int H, int D,
+                        int in_dtype, void* stream);
 
 /*
  * Decode step over a serving-side state cache (no reference counterpart in

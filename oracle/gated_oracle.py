@@ -1,0 +1,85 @@
+"""NumPy restatement of the gated delta rule (test infrastructure).
+
+Not the product: only ``tests/`` uses this module, as the checker.
+
+The reference names the gated variant as its model's intent (Gated
+DeltaNet / KDA, ``spec/03-model.md:12``) and as known missing
+(``PROGRESS.md:109``); it has no code or oracle for it. This restates the
+published recurrence (Yang, Kautz, Hatamizadeh, "Gated Delta Networks:
+Improving Mamba2 with Delta Rule", ICLR 2025) in this build's state
+convention ([d_k][d_v], ``o_t = q_t S_t``) with a scalar log-gate per
+(token, head), ``alpha_t = exp(g_t)``:
+
+    S_t = alpha_t (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T
+    o_t = q_t S_t
+
+With ``g = 0`` it is the delta rule of ``delta_oracle.gated_delta_rule``.
+
+Pinned (tests/test_oracle_gated.py) by: reduction to the pinned delta-rule
+oracle at g = 0; the closed forms at beta = 0 (pure decay: S_T = prod(alpha)
+S_0) and for one token; linearity in (v, S_0); agreement of the per-token
+form with the independent chunked (WY) restatement below at several chunk
+sizes; and planted mistakes (gate applied after the update, gate on the
+rank-1 term only, exp of the wrong sign) that these checks catch.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def gated_delta_rule(q, k, v, beta, g, state=None, dtype=np.float64):
+    """Per-token recurrence; q, k, v (B, T, H, D), beta and g (B, T, H), state (B, H, D, D)."""
+    q, k, v, beta, g = (np.asarray(x, dtype=dtype) for x in (q, k, v, beta, g))
+    b, t, h, d = q.shape
+    s = np.zeros((b, h, d, d), dtype=dtype) if state is None else np.array(state, dtype=dtype)
+    out = np.zeros((b, t, h, d), dtype=dtype)
+    for i in range(t):
+        kt, vt, qt = k[:, i], v[:, i], q[:, i]
+        bt = beta[:, i][..., None, None]
+        at = np.exp(g[:, i])[..., None, None]
+        ks = np.einsum("bhd,bhde->bhe", kt, s)
+        s = at * (s - bt * np.einsum("bhd,bhe->bhde", kt, ks)) + bt * np.einsum("bhd,bhe->bhde", kt, vt)
+        out[:, i] = np.einsum("bhd,bhde->bhe", qt, s)
+    return out, s
+
+
+def gated_wy_chunked(q, k, v, beta, g, state=None, chunk=64, dtype=np.float64):
+    """The chunked (WY/UT) form with in-chunk decays, independent of the loop above.
+
+    Per chunk, with G the cumulative log-gate inside the chunk and
+    Gam[t, s] = exp(G_t - G_s) (t >= s; every factor <= 1 when g <= 0):
+        A = strict_lower(diag(beta) (Gam * K K^T)),  T = (I + A)^-1
+        U = T diag(beta) (V - diag(exp G) K S)
+        O = diag(exp G) Q S + (Gam * lower_incl(Q K^T)) U
+        S <- exp(G_C) S + K^T diag(exp(G_C - G)) U
+    """
+    q, k, v, beta, g = (np.asarray(x, dtype=dtype) for x in (q, k, v, beta, g))
+    b, t, h, d = q.shape
+    s_all = np.zeros((b, h, d, d), dtype=dtype) if state is None else np.array(state, dtype=dtype)
+    out = np.zeros((b, t, h, d), dtype=dtype)
+    for bi in range(b):
+        for hi in range(h):
+            s = s_all[bi, hi]
+            for c0 in range(0, t, chunk):
+                sl = slice(c0, min(t, c0 + chunk))
+                K, Q, V = k[bi, sl, hi], q[bi, sl, hi], v[bi, sl, hi]
+                be, G = beta[bi, sl, hi], np.cumsum(g[bi, sl, hi])
+                n = K.shape[0]
+                # exponents above the diagonal are positive (and can overflow): mask them first
+                low = np.tril(np.ones((n, n), dtype=bool))
+                gam = np.exp(np.where(low, G[:, None] - G[None, :], -np.inf))
+                A = np.tril(be[:, None] * gam * (K @ K.T), -1)
+                T = np.linalg.inv(np.eye(n) + A)
+                U = T @ (be[:, None] * (V - np.exp(G)[:, None] * (K @ s)))
+                out[bi, sl, hi] = np.exp(G)[:, None] * (Q @ s) + (gam * (Q @ K.T)) @ U
+                s = np.exp(G[-1]) * s + K.T @ (np.exp(G[-1] - G)[:, None] * U)
+            s_all[bi, hi] = s
+    return out, s_all
+
+
+def gated_step(s, q, k, v, beta, g):
+    """One token for (B, H, D) inputs, beta and g (B, H); returns (o, new state)."""
+    o, s1 = gated_delta_rule(np.asarray(q)[:, None], np.asarray(k)[:, None], np.asarray(v)[:, None],
+                             np.asarray(beta)[:, None], np.asarray(g)[:, None], s)
+    return o[:, 0], s1

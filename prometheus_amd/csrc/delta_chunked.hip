@@ -58,7 +58,7 @@
 namespace pm {
 namespace {
 
-template <int D, int DV>
+template <int D, int DV, bool GATED = false>
 struct Geo {
     static constexpr int NCW = DV / 16;        // chain waves
     static constexpr int NPW = 4 - NCW;        // producer waves
@@ -70,12 +70,14 @@ struct Geo {
     static constexpr int R_QS = R_KS + kC * D * 2;
     static constexpr int R_VS = R_QS + kC * D * 2;
     static constexpr int R_BS = R_VS + kC * DV * 2;
-    static constexpr int RAW = R_BS + kC * 4;
+    static constexpr int R_GS = R_BS + kC * 4;  // GATED: the chunk's log-gates (fp32)
+    static constexpr int RAW = R_GS + (GATED ? kC * 4 : 0);
     static constexpr int NRAW = 3;
     // one TP buffer: T and P, 6 operand blocks of 1 KiB each
     static constexpr int TP = 2 * 6 * 1024;
     static constexpr int BYTES = NRAW * RAW + 2 * TP;
-    // NORM mode: per chunk parity, 1/||k_t|| then 1/||q_t|| (64 floats each) after the TP buffers
+    // NORM / GATED modes: per chunk parity, 128 floats handed from the producers to the
+    // chain after the TP buffers (NORM: 1/||k_t||, 1/||q_t||; GATED: the cumulative gates)
     static constexpr int RN = BYTES;
     static constexpr int BYTES_NORM = BYTES + 2 * 512;
     static_assert(D == 64 || D == 128, "D");
@@ -99,14 +101,27 @@ struct Geo {
 // scales the Gram entries; the P producer forms the four diagonal tiles of
 // Q Q^T alongside Q K^T for ||q_t||^2 and scales P's rows; both hand r and rq
 // to the chain through LDS with T and P.
-template <int D, int DV, bool OUT_BF16, bool HIST, bool NORM>
+//
+// GATED: the gated delta rule, S_t = alpha_t (I - beta_t k_t k_t^T) S_{t-1} +
+// beta_t k_t v_t^T with alpha = exp(g) per token and head (Gated DeltaNet).
+// With G_t the cumulative log-gate inside the chunk and
+// Gam_ts = exp(G_t - G_s) for t >= s (at most 1 when g <= 0):
+//   A = strict_lower(diag(beta) (Gam * K K^T)),  U = T diag(beta)(V - diag(e^G) K S),
+//   O = diag(e^G) Q S + (Gam * lower_incl(Q K^T)) U,
+//   S <- e^(G_C) S + K^T diag(e^(G_C - G)) U.
+// Each producer scans the chunk's gates itself (one wave, shuffles); the T
+// producer hands G to the chain.  Entries above the diagonal are selected
+// away, never multiplied, so their (possibly overflowing) exponents are
+// harmless; any g works, and g <= 0 keeps every factor at most 1.
+template <int D, int DV, bool OUT_BF16, bool HIST, bool NORM, bool GATED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void delta_chunked_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ beta,
     const float* __restrict__ s0, void* __restrict__ o_out, float* __restrict__ s_out,
     uint16_t* __restrict__ s_hist, const int32_t* __restrict__ cu_seqlens, int n_pairs, int T,
-    int H, int n_tiles) {
-    using G = Geo<D, DV>;
+    int H, int n_tiles, const float* __restrict__ gate) {
+    static_assert(!(GATED && (HIST || NORM)), "gated forward only");
+    using G = Geo<D, DV, GATED>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
     // XCD-aware placement: the n_tiles workgroups of a pair share bid % 8.
@@ -177,6 +192,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             copy_to_lds(rv, rbuf + G::R_VS + 1024 * i, 16, vo);
         }
         if constexpr (!NORM) copy_to_lds(rb, rbuf + G::R_BS, 4, static_cast<unsigned>(lane * H * 4));
+        if constexpr (GATED)
+            copy_to_lds(make_rsrc(gate + (tok0 + base) * H + h, n_b), rbuf + G::R_GS, 4,
+                        static_cast<unsigned>(lane * H * 4));
+    };
+    // GATED: inclusive scan of the chunk's log-gates (rows past the end read 0): lane t gets G_t
+    auto gate_scan = [&](const unsigned char* rb) {
+        float x = reinterpret_cast<const float*>(rb + G::R_GS)[lane];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_up(x, off);
+            if (lane >= off) x += y;
+        }
+        return x;
     };
 
     // ---------------- producer 0: T = (I + A)^-1 in packed operand order ----------------
@@ -234,6 +262,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 for (int b = 0; b < 4; ++b) rn[16 * b + l16] = rc[b];
             }
         }
+        // GATED: G of the rows this lane holds in A-operand form (gcol, 16b + l16) and in
+        // accumulator form (grow, 16b + 4lg + r); the chain gets G through LDS
+        float gcol[4];
+        f32x4_t grow[4];
+        if constexpr (GATED) {
+            const float gsc = gate_scan(rb);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                gcol[b] = __shfl(gsc, 16 * b + l16);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) grow[b][r] = __shfl(gsc, 16 * b + 4 * lg + r);
+            }
+            if (lg == 0) {
+                float* gh = rnb(c);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) gh[16 * b + l16] = gcol[b];
+            }
+        }
         f32x4_t eye;
 #pragma unroll
         for (int r = 0; r < 4; ++r) eye[r] = (4 * lg + r == l16) ? 1.f : 0.f;
@@ -246,8 +292,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = 4 * lg + r;
-                n[r] = (row > l16) ? -br4[b][r] * gd[b][r] : 0.f;   // N[row][l16]
-                nt[r] = (l16 > row) ? -(NORM ? br4[b][r] : bc[b]) * gd[b][r] : 0.f;  // N[l16][row]
+                // GATED: Gam[row][l16] and Gam[l16][row]; the one not selected may overflow,
+                // and is discarded, never multiplied
+                const float gn = GATED ? expf(grow[b][r] - gcol[b]) : 1.f;
+                const float gnt = GATED ? expf(gcol[b] - grow[b][r]) : 1.f;
+                n[r] = (row > l16) ? -br4[b][r] * (gn * gd[b][r]) : 0.f;   // N[row][l16]
+                nt[r] = (l16 > row) ? -(NORM ? br4[b][r] : bc[b]) * (gnt * gd[b][r]) : 0.f;  // N[l16][row]
             }
             cn[b] = cvt4(n);
             cnt[b] = cvt4(nt);
@@ -271,8 +321,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             // cet = (I + N)^T as an accumulator, rebuilt from cnt's source values
             f32x4_t nt;
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                nt[r] = (l16 > 4 * lg + r) ? -(NORM ? br4[b][r] : bc[b]) * gd[b][r] : 0.f;
+            for (int r = 0; r < 4; ++r) {
+                const float gnt = GATED ? expf(gcol[b] - grow[b][r]) : 1.f;
+                nt[r] = (l16 > 4 * lg + r) ? -(NORM ? br4[b][r] : bc[b]) * (gnt * gd[b][r]) : 0.f;
+            }
             cet[b] = cvt4(nt + eye);
             n4[b] = mfma16(cn2t[b], cn2[b], zero);
             n4t[b] = mfma16(cn2[b], cn2t[b], zero);
@@ -301,9 +353,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
         // A_ik as an A operand: upper tile (k, i) of K K^T, rows scaled by beta_{16i+l16}
         // (NORM: by r_{16i+l16}, and its columns 16k + 4g + r by r_{16k+4g+r})
+        // (GATED: entry (16i + l16, 16k + 4g + r) by Gam, i > k)
         auto a_op = [&](int x, int i, int k) {
-            if constexpr (NORM) return cvt4(rc[i] * (rr4[k] * gu[x]));
-            else return cvt4(bc[i] * gu[x]);
+            if constexpr (NORM) {
+                return cvt4(rc[i] * (rr4[k] * gu[x]));
+            } else if constexpr (GATED) {
+                f32x4_t e;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) e[r] = expf(gcol[i] - grow[k][r]);
+                return cvt4(bc[i] * (e * gu[x]));
+            } else {
+                return cvt4(bc[i] * gu[x]);
+            }
         };
         const u32x2_t cd0 = cvt4(dd[0]), cd1 = cvt4(dd[1]), cd2 = cvt4(dd[2]);
         const u32x2_t cdt1 = cvt4(ddt[1]), cdt2 = cvt4(ddt[2]), cdt3 = cvt4(ddt[3]);
@@ -385,6 +446,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 if (lg == 0) rn[16 * i + l16] = rq[i];
             }
         }
+        float pgc[4];    // GATED: G_{16i + l16}
+        f32x4_t pgr[4];  // GATED: G_{16j + 4lg + r}
+        if constexpr (GATED) {
+            const float gsc = gate_scan(rb);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                pgc[b] = __shfl(gsc, 16 * b + l16);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) pgr[b][r] = __shfl(gsc, 16 * b + 4 * lg + r);
+            }
+        }
         int x = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -392,6 +464,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int j = 0; j <= i; ++j, ++x) {
                 f32x4_t t = p[x];
                 if constexpr (NORM) t = t * rq[i];
+                if constexpr (GATED) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        // Gam[16i + l16][16j + 4g + r]; above the diagonal (i == j) it is masked
+                        const float e = expf(pgc[i] - pgr[j][r]);
+                        t[r] = (i > j || l16 >= 4 * lg + r) ? t[r] * e : 0.f;
+                    }
+                }
                 if (i == j) {  // keep t >= s: row l16, column 4g+r
 #pragma unroll
                     for (int r = 0; r < 4; ++r) t[r] = (l16 >= 4 * lg + r) ? t[r] : 0.f;
@@ -461,12 +541,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         u32x2_t vv2 = lds_v_issue<DV>(Vs, 2, w, lane), vv3 = lds_v_issue<DV>(Vs, 3, w, lane);
         lds_wait(vv0, vv1, vv2, vv3);
         const u32x2_t vv[4] = {vv0, vv1, vv2, vv3};
-        f32x4_t R[4], rk4[4];
+        f32x4_t R[4], rk4[4], gk4[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             if constexpr (NORM) {
                 rk4[m] = *reinterpret_cast<const f32x4_t*>(rnb(c) + 16 * m + 4 * lg);
                 R[m] = widen4(vv[m]) - rk4[m] * X[m];
+            } else if constexpr (GATED) {
+                gk4[m] = *reinterpret_cast<const f32x4_t*>(rnb(c) + 16 * m + 4 * lg);  // G_t
+                f32x4_t e;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) e[r] = expf(gk4[m][r]);
+                const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + 16 * m + 4 * lg);
+                R[m] = bs * (widen4(vv[m]) - e * X[m]);
             } else {
                 const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + 16 * m + 4 * lg);
                 R[m] = bs * (widen4(vv[m]) - X[m]);
@@ -484,6 +571,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int m = 0; m < 4; ++m) U[m] = rk4[m] * U[m];  // diag(r) U
         }
         const bf16x8_t Ub0 = acc_to_b(U[0], U[1]), Ub1 = acc_to_b(U[2], U[3]);
+        // GATED: the state update takes diag(e^(G_C - G)) U, and S decays by e^(G_C)
+        bf16x8_t Us0 = Ub0, Us1 = Ub1;
+        if constexpr (GATED) {
+            const float gC = rnb(c)[kC - 1];
+            f32x4_t Ud[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                f32x4_t e;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) e[r] = expf(gC - gk4[m][r]);
+                Ud[m] = e * U[m];
+            }
+            Us0 = acc_to_b(Ud[0], Ud[1]);
+            Us1 = acc_to_b(Ud[2], Ud[3]);
+            const float eC = expf(gC);
+#pragma unroll
+            for (int md = 0; md < D / 16; ++md) S[md] = eC * S[md];
+        }
         // S += K^T U (K^T operands by transpose reads of the token rows)
 #pragma unroll
         for (int h4 = 0; h4 < D / 64; ++h4) {
@@ -495,8 +600,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const u32x4_t f0[4] = {a0, a1, a2, a3}, f1[4] = {b0, b1, b2, b3};
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
-                S[4 * h4 + x] = mfma32(__builtin_bit_cast(bf16x8_t, f0[x]), Ub0, S[4 * h4 + x]);
-                S[4 * h4 + x] = mfma32(__builtin_bit_cast(bf16x8_t, f1[x]), Ub1, S[4 * h4 + x]);
+                S[4 * h4 + x] = mfma32(__builtin_bit_cast(bf16x8_t, f0[x]), Us0, S[4 * h4 + x]);
+                S[4 * h4 + x] = mfma32(__builtin_bit_cast(bf16x8_t, f1[x]), Us1, S[4 * h4 + x]);
             }
         }
         // O^T = Y^T + U^T P^T (U tiles as the A operand give U^T; the packed P rows are the
@@ -504,6 +609,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         if constexpr (NORM) {
 #pragma unroll
             for (int m = 0; m < 4; ++m) Y[m] = Y[m] * rnb(c)[kC + 16 * m + l16];  // diag(rq) Q S
+        }
+        if constexpr (GATED) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) Y[m] = Y[m] * expf(rnb(c)[16 * m + l16]);  // diag(e^G) Q S
         }
         f32x4_t O[4];
         O[0] = mfma32(Ub0, packed_a(Pp, 0, lane), Y[0]);
@@ -574,11 +683,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
-template <int D, int DV, bool OB, bool HIST, bool NORM = false>
+template <int D, int DV, bool OB, bool HIST, bool NORM = false, bool GATED = false>
 hipError_t launch_t(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
-    using G = Geo<D, DV>;
-    constexpr int kBytes = NORM ? G::BYTES_NORM : G::BYTES;
-    auto kern = delta_chunked_kernel<D, DV, OB, HIST, NORM>;
+    using G = Geo<D, DV, GATED>;
+    constexpr int kBytes = (NORM || GATED) ? G::BYTES_NORM : G::BYTES;
+    auto kern = delta_chunked_kernel<D, DV, OB, HIST, NORM, GATED>;
     // the dynamic-LDS limit is a per-device function attribute
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -595,12 +704,15 @@ hipError_t launch_t(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
     const int slots = (n_pairs + 7) / 8;
     const dim3 grid(static_cast<unsigned>(slots * 8 * n_tiles));
     hipLaunchKernelGGL(kern, grid, dim3(256), kBytes, st, a.q, a.k, a.v, a.beta, a.s0, a.o,
-                       a.s_out, s_hist, a.cu_seqlens, n_pairs, a.T, a.H, n_tiles);
+                       a.s_out, s_hist, a.cu_seqlens, n_pairs, a.T, a.H, n_tiles, a.g);
     return hipGetLastError();
 }
 
 template <int D, int DV>
 hipError_t launch_dv(const ChunkedArgs& a, hipStream_t st) {
+    if (a.g)
+        return a.out_bf16 ? launch_t<D, DV, true, false, false, true>(a, nullptr, st)
+                          : launch_t<D, DV, false, false, false, true>(a, nullptr, st);
     if (a.norm)
         return a.out_bf16 ? launch_t<D, DV, true, false, true>(a, nullptr, st)
                           : launch_t<D, DV, false, false, true>(a, nullptr, st);

@@ -18,6 +18,11 @@
 // The model's linear attention (model/__init__.py:393-432) runs here too:
 // with l2norm, each staged q and k row is divided by max(||row||_2, 1e-6)
 // (its _l2_normalize, :203-205) before use, and a NULL beta means beta = 1.
+//
+// Gated variant (log-gates g, alpha = exp(g) per token and head):
+//   S_t = alpha_t (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T,
+// i.e. u = beta (v - alpha k^T S), S = alpha S + k u^T.  Without g, alpha = 1
+// and the arithmetic is exactly the ungated step.
 
 #include "pm_common.h"
 #include "pm_internal.h"
@@ -33,13 +38,15 @@ template <int RPT, typename InT, typename OutT>
 __global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel(
     const InT* __restrict__ q, const InT* __restrict__ k, const InT* __restrict__ v,
     const float* __restrict__ beta, const float* s0, OutT* __restrict__ o, float* s_out,
-    const int32_t* __restrict__ cu_seqlens, int T, int H, int D, int RS, int l2norm) {
+    const int32_t* __restrict__ cu_seqlens, int T, int H, int D, int RS, int l2norm,
+    const float* __restrict__ gate) {
     extern __shared__ float lds[];
     const int DP = RS * RPT;  // padded row count per column
     float* sk = lds;                          // [kRecSteps][DP]
     float* sq = sk + kRecSteps * DP;          // [kRecSteps][DP]
     float* sv = sq + kRecSteps * DP;          // [kRecSteps][DP]
     float* sb = sv + kRecSteps * DP;          // [kRecSteps]
+    float* sa = sb + kRecSteps;               // [kRecSteps] alpha
 
     const int pair = blockIdx.x;
     const int seq = pair / H, h = pair % H;
@@ -85,8 +92,11 @@ __global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel
             sq[idx] = qv;
             sv[idx] = vv;
         }
-        for (int j = tid; j < kRecSteps; j += blockDim.x)
-            sb[j] = (j >= nst) ? 0.f : beta ? beta[static_cast<size_t>(tok0 + t0 + j) * H + h] : 1.f;
+        for (int j = tid; j < kRecSteps; j += blockDim.x) {
+            const size_t a = static_cast<size_t>(tok0 + t0 + j) * H + h;
+            sb[j] = (j >= nst) ? 0.f : beta ? beta[a] : 1.f;
+            sa[j] = (j < nst && gate) ? expf(gate[a]) : 1.f;
+        }
         __syncthreads();
         if (l2norm) {
             // one wave per staged row (k rows, then q rows): x / max(||x||, 1e-6)
@@ -109,9 +119,10 @@ __global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel
 #pragma unroll
             for (int i = 0; i < RPT; ++i) ks = fmaf(kr[i], S[i], ks);
             for (int m = 1; m < RS; m <<= 1) ks += __shfl_xor(ks, m);
-            const float u = sb[j] * ((col_ok ? sv[j * DP + e] : 0.f) - ks);
+            const float al = sa[j];
+            const float u = sb[j] * ((col_ok ? sv[j * DP + e] : 0.f) - al * ks);
 #pragma unroll
-            for (int i = 0; i < RPT; ++i) S[i] = fmaf(kr[i], u, S[i]);
+            for (int i = 0; i < RPT; ++i) S[i] = fmaf(kr[i], u, al * S[i]);
             float os = 0.f;
 #pragma unroll
             for (int i = 0; i < RPT; ++i) os = fmaf(qr[i], S[i], os);
@@ -142,11 +153,11 @@ static void recurrent_geometry(int D, int* rpt, int* rs) {
 template <int RPT, typename InT, typename OutT>
 static hipError_t launch_rec_t(const RecurrentArgs& a, int rs, hipStream_t st) {
     const int threads = ((a.D * rs + 63) / 64) * 64;
-    const size_t lds = sizeof(float) * (3 * kRecSteps * rs * RPT + kRecSteps);
+    const size_t lds = sizeof(float) * (3 * kRecSteps * rs * RPT + 2 * kRecSteps);
     hipLaunchKernelGGL((delta_recurrent_kernel<RPT, InT, OutT>), dim3(a.n_pairs), dim3(threads),
                        lds, st, static_cast<const InT*>(a.q), static_cast<const InT*>(a.k),
                        static_cast<const InT*>(a.v), a.beta, a.s0, static_cast<OutT*>(a.o),
-                       a.s_out, a.cu_seqlens, a.T, a.H, a.D, rs, a.l2norm ? 1 : 0);
+                       a.s_out, a.cu_seqlens, a.T, a.H, a.D, rs, a.l2norm ? 1 : 0, a.g);
     return hipGetLastError();
 }
 

@@ -25,7 +25,8 @@ namespace pm {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <int D, typename InT>
+// GATED: S' = alpha (S - beta k (k^T S)) + beta k v^T with alpha = exp(g[b, h]).
+template <int D, typename InT, bool GATED>
 __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
                                                          const InT* __restrict__ q,
                                                          const InT* __restrict__ k,
@@ -33,7 +34,8 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
                                                          const float* __restrict__ beta,
                                                          float* __restrict__ o,
                                                          const int32_t* __restrict__ slots,
-                                                         int H, int n_slots) {
+                                                         int H, int n_slots,
+                                                         const float* __restrict__ gate) {
     constexpr int NT = 256;
     constexpr int CG = D / 4;      // column groups of 4
     constexpr int RG = NT / CG;    // row groups
@@ -93,12 +95,15 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
     for (int j = 1; j < NW; ++j) ks += red[0][j][cg];
 
     const f32x4 vv = {sv[4 * cg], sv[4 * cg + 1], sv[4 * cg + 2], sv[4 * cg + 3]};
-    const f32x4 u = b * (vv - ks);
+    float al = 1.f;
+    if constexpr (GATED) al = expf(gate[pair]);
+    const f32x4 u = GATED ? b * (vv - al * ks) : b * (vv - ks);
     f32x4 op = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
         const int row = rg + RG * i;
-        S[i] += sk[row] * u;
+        if constexpr (GATED) S[i] = al * S[i] + sk[row] * u;
+        else S[i] += sk[row] * u;
         op += sq[row] * S[i];
         __builtin_nontemporal_store(S[i], sp + row * CG + cg);
     }
@@ -121,18 +126,23 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
 
 bool step_supported(int D) { return D == 32 || D == 64 || D == 128; }
 
-template <int D>
-static hipError_t launch_step_d(const StepArgs& a, hipStream_t st) {
+template <int D, bool GATED>
+static hipError_t launch_step_g(const StepArgs& a, hipStream_t st) {
     if (a.in_bf16) {
-        hipLaunchKernelGGL((delta_step_kernel<D, uint16_t>), dim3(a.n_pairs), dim3(256), 0, st,
+        hipLaunchKernelGGL((delta_step_kernel<D, uint16_t, GATED>), dim3(a.n_pairs), dim3(256), 0, st,
                            a.s, static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.k),
-                           static_cast<const uint16_t*>(a.v), a.beta, a.o, a.slots, a.H, a.n_slots);
+                           static_cast<const uint16_t*>(a.v), a.beta, a.o, a.slots, a.H, a.n_slots, a.g);
     } else {
-        hipLaunchKernelGGL((delta_step_kernel<D, float>), dim3(a.n_pairs), dim3(256), 0, st, a.s,
+        hipLaunchKernelGGL((delta_step_kernel<D, float, GATED>), dim3(a.n_pairs), dim3(256), 0, st, a.s,
                            static_cast<const float*>(a.q), static_cast<const float*>(a.k),
-                           static_cast<const float*>(a.v), a.beta, a.o, a.slots, a.H, a.n_slots);
+                           static_cast<const float*>(a.v), a.beta, a.o, a.slots, a.H, a.n_slots, a.g);
     }
     return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_step_d(const StepArgs& a, hipStream_t st) {
+    return a.g ? launch_step_g<D, true>(a, st) : launch_step_g<D, false>(a, st);
 }
 
 hipError_t launch_step(const StepArgs& a, hipStream_t st) {

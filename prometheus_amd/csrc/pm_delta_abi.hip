@@ -86,7 +86,8 @@ int check_dtypes(int in_dtype, int out_dtype) {
 // Common forward dispatch. cu == nullptr: fixed length (n_seq = B, T).
 int forward(const void* q, const void* k, const void* v, const float* beta, const float* s0,
             void* o, float* s_out, const int32_t* cu, int n_seq, int T, int total_T, int H,
-            int D, int in_dtype, int out_dtype, int chunk, hipStream_t st) {
+            int D, int in_dtype, int out_dtype, int chunk, hipStream_t st,
+            const float* g = nullptr) {
     const bool varlen = cu != nullptr;
     const long n_pairs = static_cast<long>(n_seq) * H;
     const long n_tok = varlen ? static_cast<long>(total_T) : static_cast<long>(n_seq) * T;
@@ -123,6 +124,7 @@ int forward(const void* q, const void* k, const void* v, const float* beta, cons
                           static_cast<const uint16_t*>(v), beta, s0, o, s_out, cu, n_seq,
                           varlen ? total_T : T, H, D,
                           out_dtype == PM_DTYPE_BF16, g_tile.load()};
+        a.g = g;
         hipError_t e = pm::launch_chunked(a, st);
         return e == hipSuccess ? 0 : hip_fail(e, "chunked forward launch");
     }
@@ -130,8 +132,41 @@ int forward(const void* q, const void* k, const void* v, const float* beta, cons
     pm::RecurrentArgs a{q, k, v, beta, s0, o, s_out, cu, static_cast<int>(n_pairs),
                         varlen ? total_T : T, H, D,
                         in_bf16, out_dtype == PM_DTYPE_BF16};
+    a.g = g;
     hipError_t e = pm::launch_recurrent(a, st);
     return e == hipSuccess ? 0 : hip_fail(e, "recurrent forward launch");
+}
+
+// The decode step, plain (g == NULL) or gated.
+int step(float* s_inout, const void* q, const void* k, const void* v, const float* beta,
+         const float* g, float* o, int B, int H, int D, int in_dtype, void* stream) {
+    g_err[0] = '\0';
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (B < 0 || H < 0) return fail(PM_E_SHAPE, "B, H must be >= 0 (got %d, %d)", B, H);
+    if (D < 1 || D > PM_DELTA_MAX_D)
+        return fail(PM_E_SHAPE, "D must be in [1, %d] (got %d)", PM_DELTA_MAX_D, D);
+    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16)
+        return fail(PM_E_DTYPE, "in_dtype %d is not PM_DTYPE_F32 or PM_DTYPE_BF16", in_dtype);
+    const long n_pairs = static_cast<long>(B) * H;
+    if (n_pairs == 0) return 0;
+    if (n_pairs > (1L << 30)) return fail(PM_E_SHAPE, "problem too large");
+    if (!s_inout || !q || !k || !v || !beta || !o)
+        return fail(PM_E_NULL, "s_inout, q, k, v, beta and o must be non-NULL");
+    if (pm::step_supported(D) && aligned(s_inout, 16) && aligned(o, 16)) {
+        pm::StepArgs a{s_inout, q, k, v, beta, o, static_cast<int>(n_pairs), D,
+                       in_dtype == PM_DTYPE_BF16};
+        a.g = g;
+        hipError_t e = pm::launch_step(a, st);
+        return e == hipSuccess ? 0 : hip_fail(e, "decode step launch");
+    }
+    if (!aligned(s_inout, 4) || !aligned(o, 4))
+        return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
+    // a (B, H, D) token is a length-1 (B, 1, H, D) sequence; K4 runs it in place
+    pm::RecurrentArgs a{q, k, v, beta, s_inout, o, s_inout, nullptr, static_cast<int>(n_pairs), 1,
+                        H, D, in_dtype == PM_DTYPE_BF16, false};
+    a.g = g;
+    hipError_t e = pm::launch_recurrent(a, st);
+    return e == hipSuccess ? 0 : hip_fail(e, "decode step launch");
 }
 
 }  // namespace
@@ -328,31 +363,31 @@ int pm_linear_attention(const void* q, const void* k, const void* v, const float
 
 int pm_delta_step(float* s_inout, const void* q, const void* k, const void* v,
                   const float* beta, float* o, int B, int H, int D, int in_dtype, void* stream) {
+    return step(s_inout, q, k, v, beta, nullptr, o, B, H, D, in_dtype, stream);
+}
+
+int pm_gated_delta_step(float* s_inout, const void* q, const void* k, const void* v,
+                        const float* beta, const float* g, float* o, int B, int H, int D,
+                        int in_dtype, void* stream) {
     g_err[0] = '\0';
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (B < 0 || H < 0) return fail(PM_E_SHAPE, "B, H must be >= 0 (got %d, %d)", B, H);
+    if (static_cast<long>(B) * H > 0 && !g) return fail(PM_E_NULL, "g is NULL");
+    if (g && !aligned(g, 4)) return fail(PM_E_ALIGN, "g must be 4-byte aligned");
+    return step(s_inout, q, k, v, beta, g, o, B, H, D, in_dtype, stream);
+}
+
+int pm_gated_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
+                       const float* g, const float* s0, void* o, float* s_out, int B, int T, int H,
+                       int D, int in_dtype, int out_dtype, void* stream) {
+    g_err[0] = '\0';
+    if (B < 0 || T < 0 || H < 0)
+        return fail(PM_E_SHAPE, "B, T, H must be >= 0 (got %d, %d, %d)", B, T, H);
     if (D < 1 || D > PM_DELTA_MAX_D)
         return fail(PM_E_SHAPE, "D must be in [1, %d] (got %d)", PM_DELTA_MAX_D, D);
-    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16)
-        return fail(PM_E_DTYPE, "in_dtype %d is not PM_DTYPE_F32 or PM_DTYPE_BF16", in_dtype);
-    const long n_pairs = static_cast<long>(B) * H;
-    if (n_pairs == 0) return 0;
-    if (n_pairs > (1L << 30)) return fail(PM_E_SHAPE, "problem too large");
-    if (!s_inout || !q || !k || !v || !beta || !o)
-        return fail(PM_E_NULL, "s_inout, q, k, v, beta and o must be non-NULL");
-    if (pm::step_supported(D) && aligned(s_inout, 16) && aligned(o, 16)) {
-        pm::StepArgs a{s_inout, q, k, v, beta, o, static_cast<int>(n_pairs), D,
-                       in_dtype == PM_DTYPE_BF16};
-        hipError_t e = pm::launch_step(a, st);
-        return e == hipSuccess ? 0 : hip_fail(e, "decode step launch");
-    }
-    if (!aligned(s_inout, 4) || !aligned(o, 4))
-        return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
-    // a (B, H, D) token is a length-1 (B, 1, H, D) sequence; K4 runs it in place
-    pm::RecurrentArgs a{q, k, v, beta, s_inout, o, s_inout, nullptr, static_cast<int>(n_pairs), 1,
-                        H, D, in_dtype == PM_DTYPE_BF16, false};
-    hipError_t e = pm::launch_recurrent(a, st);
-    return e == hipSuccess ? 0 : hip_fail(e, "decode step launch");
+    if (int rc = check_dtypes(in_dtype, out_dtype)) return rc;
+    if (static_cast<long>(B) * T * H > 0 && !g) return fail(PM_E_NULL, "g is NULL");
+    if (g && !aligned(g, 4)) return fail(PM_E_ALIGN, "g must be 4-byte aligned");
+    return forward(q, k, v, beta, s0, o, s_out, nullptr, B, T, 0, H, D, in_dtype, out_dtype, 64,
+                   static_cast<hipStream_t>(stream), g);
 }
 
 }  // extern "C"

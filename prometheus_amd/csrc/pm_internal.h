@@ -23,6 +23,7 @@ struct RecurrentArgs {
     int T, H, D;
     bool in_bf16, out_bf16;
     bool l2norm = false;  // q and k divided by max(||.||_2, 1e-6) per token on load
+    const float* g = nullptr;  // gated variant: log-gates per (token, head), alpha = exp(g)
 };
 hipError_t launch_recurrent(const RecurrentArgs& a, hipStream_t st);
 
@@ -41,6 +42,7 @@ struct StepArgs {
     // leaves the pool untouched and gets a zero output row.
     const int32_t* slots = nullptr;
     int H = 1, n_slots = 0;
+    const float* g = nullptr;  // gated variant: log-gate per (b, h), alpha = exp(g)
 };
 bool step_supported(int D);
 hipError_t launch_step(const StepArgs& a, hipStream_t st);
@@ -62,6 +64,9 @@ struct ChunkedArgs {
     // The model's linear attention: beta = 1 (beta unused) and q, k divided by
     // max(||.||, 1e-6) per token inside the kernel.
     bool norm = false;
+    // Gated variant (not with norm): log-gates per (token, head), alpha = exp(g)
+    // (g <= 0 keeps every in-chunk decay factor at most 1).
+    const float* g = nullptr;
 };
 bool chunked_supported(int D, int H);  // D in {64, 128}, H*D <= 2^24
 hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st);

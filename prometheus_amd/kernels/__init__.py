@@ -432,6 +432,75 @@ def delta_rule_step(q, k, v, beta, state):
     return call.out(o)
 
 
+# ---------------------------------------------------------------------------
+# gated variant (no reference code: the model's intent, spec/03-model.md:12)
+# ---------------------------------------------------------------------------
+
+
+def chunked_gated_delta_rule(q, k, v, beta, g, state=None, config=None, *, out_dtype=None):
+    """Gated delta rule (Gated DeltaNet) with a log-gate per token and head.
+
+    ``S_t = exp(g_t) (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T``,
+    ``o_t = q_t S_t``. q, k, v, beta, state and the return value as
+    ``chunked_delta_rule``; g: (batch, seq, heads) fp32 log-gates (g = 0 gives
+    ``chunked_delta_rule``). bf16 q/k/v with dim 64 or 128 run the chunked
+    MFMA kernel with the in-chunk decays folded into its tiles; other inputs
+    run the fp32 per-token kernel.
+    """
+    cfg = LinearAttnConfig() if config is None else config
+    _check_chunk(cfg)
+    batch, seq, heads, dim = _validate(q, k, v, beta, state)
+    if _shape(g) != (batch, seq, heads):
+        raise KernelError(f"g shape {_shape(g)} != {(batch, seq, heads)}")
+    odt = _out_dtype(out_dtype)
+    if _on_host(q, k, v, beta, state):
+        _check_beta_host(beta)
+    call = _Call(q, k, v, beta, g, state)
+    cdt = _qkv_dtype(q, k, v)
+    with torch.cuda.device(call.device):
+        qd, kd, vd = call.dev(q, cdt), call.dev(k, cdt), call.dev(v, cdt)
+        bd, gd = call.dev(beta, torch.float32), call.dev(g, torch.float32)
+        sd = call.dev(state, torch.float32)
+        o = torch.empty((batch, seq, heads, dim), dtype=odt, device=call.device)
+        s_out = torch.empty((batch, heads, dim, dim), dtype=torch.float32, device=call.device)
+        rc = _native.lib().pm_gated_delta_fwd(
+            _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(gd), _ptr(sd), _ptr(o), _ptr(s_out),
+            batch, seq, heads, dim, _code(cdt), _code(odt), _stream(call.device),
+        )
+        _native.check(rc)
+    return call.out(o), call.out(s_out)
+
+
+def gated_delta_rule_step(q, k, v, beta, g, state):
+    """One gated step for (B, H, D) tokens, g (B, H); ``state`` updated in place as in
+    ``delta_rule_step``: ``S' = exp(g) (S - beta k (k^T S)) + beta k v^T``, ``o = q S'``."""
+    qs = _shape(q)
+    if len(qs) != 3 or _shape(k) != qs or _shape(v) != qs:
+        raise KernelError(f"q, k, v must all have shape (B, H, D); got {qs}")
+    batch, heads, dim = qs
+    if _shape(beta) != (batch, heads) or _shape(g) != (batch, heads):
+        raise KernelError(f"beta and g must be {(batch, heads)}; got {_shape(beta)}, {_shape(g)}")
+    if state is None or _shape(state) != (batch, heads, dim, dim):
+        raise KernelError(f"state shape {_shape(state) if state is not None else None} != "
+                          f"{(batch, heads, dim, dim)}")
+    if dim > _native.MAX_D:
+        raise KernelError(f"head dimension {dim} exceeds the supported maximum {_native.MAX_D}")
+    if not (isinstance(state, torch.Tensor) and state.device.type == "cuda"
+            and state.dtype == torch.float32 and state.is_contiguous()):
+        raise KernelError("state must be a contiguous fp32 GPU tensor (updated in place)")
+    call = _Call(q, k, v, beta, g, state)
+    cdt = _qkv_dtype(q, k, v)
+    with torch.cuda.device(call.device):
+        qd, kd, vd = call.dev(q, cdt), call.dev(k, cdt), call.dev(v, cdt)
+        bd, gd = call.dev(beta, torch.float32), call.dev(g, torch.float32)
+        o = torch.empty((batch, heads, dim), dtype=torch.float32, device=call.device)
+        rc = _native.lib().pm_gated_delta_step(_ptr(state), _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd),
+                                               _ptr(gd), _ptr(o), batch, heads, dim, _code(cdt),
+                                               _stream(call.device))
+        _native.check(rc)
+    return call.out(o)
+
+
 __all__ = [
     "DEFAULT_CHUNK",
     "KernelError",
@@ -442,4 +511,6 @@ __all__ = [
     "chunked_delta_rule_bwd",
     "chunked_delta_rule_varlen",
     "delta_rule_step",
+    "chunked_gated_delta_rule",
+    "gated_delta_rule_step",
 ]

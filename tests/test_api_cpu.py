@@ -325,3 +325,20 @@ def test_slot_decode_abi_validation_without_gpu():
     assert call(4, 2, 2, 64, pool=ctypes.c_void_p(8)) == _native.E_ALIGN
     assert call(4, 2, 2, 64, o=ctypes.c_void_p(8)) == _native.E_ALIGN
     assert call(4, 0, 2, 64) == 0  # nothing to do
+
+
+def test_gated_validation_without_gpu():
+    q = np.zeros((1, 4, 2, 8), np.float32)
+    b = np.zeros((1, 4, 2), np.float32)
+    with pytest.raises(kernels.KernelError):
+        kernels.chunked_gated_delta_rule(q, q, q, b, np.zeros((1, 4, 3), np.float32))
+    with pytest.raises(kernels.KernelError):
+        kernels.gated_delta_rule_step(q[:, 0], q[:, 0], q[:, 0], b[:, 0], np.zeros((1, 3), np.float32),
+                                      np.zeros((1, 2, 8, 8), np.float32))
+    lib = _native.lib()
+    p = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    assert lib.pm_gated_delta_fwd(p, p, p, p, None, None, p, p, 1, 4, 2, 8, 0, 0, None) == _native.E_NULL
+    assert lib.pm_gated_delta_fwd(p, p, p, p, ctypes.c_void_p(2), None, p, p, 1, 4, 2, 8, 0, 0,
+                                  None) == _native.E_ALIGN
+    assert lib.pm_gated_delta_fwd(p, p, p, p, p, None, p, p, 1, 4, 2, 300, 0, 0, None) == _native.E_SHAPE
+    assert lib.pm_gated_delta_step(p, p, p, p, p, None, p, 1, 2, 8, 0, None) == _native.E_NULL

@@ -16,8 +16,9 @@ algorithm, OpenMP over the 64 (b, h) sequences, on this host). The decode
 step (cfg4: B=256 H=32 D=128, fp32 state updated in place) is measured in
 the same run and reported under ``decode`` (with the same batch through a
 serving state cache under ``decode.state_cache``), the backward at cfg1
-under ``backward``, and the model's linear attention at the cfg1 shape
-under ``model_linear_attention``.
+under ``backward``, the model's linear attention at the cfg1 shape
+under ``model_linear_attention``, and the gated variant at cfg1 under
+``gated``.
 """
 
 from __future__ import annotations
@@ -105,6 +106,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--decode-steps", type=int, default=64)
+    ap.add_argument("--gated-calls", type=int, default=10,
+                    help="timed pm_gated_delta_fwd calls at cfg1 (0 skips)")
     ap.add_argument("--model-calls", type=int, default=2,
                     help="timed pm_linear_attention calls at the cfg1 shape (0 skips)")
     ap.add_argument("--bwd-steps", type=int, default=3,
@@ -329,6 +332,43 @@ def main():
             del qm, km, vm
         del om, sm
 
+    # the gated delta rule at cfg1 (pm_gated_delta_fwd): cfg1's inputs plus log-gates
+    # -0.1 |N(0, 1)| per token and head, on the chunked kernel
+    gated = None
+    if args.gated_calls > 0:
+        q, k, v, beta = sets[0]
+        g.manual_seed(8)
+        gates = -0.1 * torch.randn((B, T, H), generator=g, device=dev).abs()
+        og = torch.empty((B, T, H, D), device=dev)
+        sg = torch.empty((B, H, D, D), device=dev)
+
+        def gfwd():
+            rc = lib.pm_gated_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
+                                        gates.data_ptr(), None, og.data_ptr(), sg.data_ptr(), B, T, H,
+                                        D, _native.DTYPE_BF16, _native.DTYPE_F32, stream.cuda_stream)
+            _native.check(rc)
+
+        gfwd()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.gated_calls):
+            gfwd()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        g_ms = e0.elapsed_time(e1) / args.gated_calls
+        gb = fwd_bytes(B, T, H, D) + 4 * B * T * H
+        gated = {
+            "workload": "cfg1 gated delta rule (log-gates -0.1|N(0,1)|), bf16 q/k/v, chunked kernel",
+            "calls": args.gated_calls,
+            "ms_per_call": g_ms,
+            "tokens_per_s": tokens / (g_ms * 1e-3),
+            "roofline": {"bound": "hbm", "achieved": gb / (g_ms * 1e-3) / 1e9,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gb / (g_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        }
+        del og, sg, gates
+
     # backward at cfg1 (chunked_delta_rule_bwd through the C ABI): bf16 q/k/v, zero S0,
     # random go and gS, fp32 gradients
     backward = None
@@ -410,6 +450,7 @@ def main():
         "parity": parity,
         "decode": decode,
         "model_linear_attention": model_la,
+        "gated": gated,
         "backward": backward,
     }
     print(json.dumps(line), flush=True)

@@ -77,7 +77,7 @@ struct Geo {
     static constexpr int TP = 2 * 6 * 1024;
     static constexpr int BYTES = NRAW * RAW + 2 * TP;
     // NORM / GATED modes: per chunk parity, 128 floats handed from the producers to the
-    // chain after the TP buffers (NORM: 1/||k_t||, 1/||q_t||; GATED: the cumulative gates)
+    // chain after the TP buffers (NORM: 1/||k_t||, 1/||q_t||; GATED: e^(G_t), e^(G_C - G_t))
     static constexpr int RN = BYTES;
     static constexpr int BYTES_NORM = BYTES + 2 * 512;
     static_assert(D == 64 || D == 128, "D");
@@ -110,7 +110,7 @@ struct Geo {
 //   O = diag(e^G) Q S + (Gam * lower_incl(Q K^T)) U,
 //   S <- e^(G_C) S + K^T diag(e^(G_C - G)) U.
 // Each producer scans the chunk's gates itself (one wave, shuffles); the T
-// producer hands G to the chain.  Entries above the diagonal are selected
+// producer hands e^(G_t) and e^(G_C - G_t) to the chain.  Entries above the diagonal are selected
 // away, never multiplied, so their (possibly overflowing) exponents are
 // harmless; any g works, and g <= 0 keeps every factor at most 1.
 template <int D, int DV, bool OUT_BF16, bool HIST, bool NORM, bool GATED>
@@ -196,9 +196,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             copy_to_lds(make_rsrc(gate + (tok0 + base) * H + h, n_b), rbuf + G::R_GS, 4,
                         static_cast<unsigned>(lane * H * 4));
     };
-    // GATED: inclusive scan of the chunk's log-gates (rows past the end read 0): lane t gets G_t
+    // GATED: inclusive scan of the chunk's log-gates (rows past the end read 0), in the
+    // base-2 domain: lane t gets G_t * log2(e), so that every decay is one v_exp_f32 (2^x)
     auto gate_scan = [&](const unsigned char* rb) {
-        float x = reinterpret_cast<const float*>(rb + G::R_GS)[lane];
+        float x = reinterpret_cast<const float*>(rb + G::R_GS)[lane] * 1.44269504088896341f;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const float y = __shfl_up(x, off);
@@ -263,7 +264,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             }
         }
         // GATED: G of the rows this lane holds in A-operand form (gcol, 16b + l16) and in
-        // accumulator form (grow, 16b + 4lg + r); the chain gets G through LDS
+        // accumulator form (grow, 16b + 4lg + r); the chain gets e^(G_t) and e^(G_C - G_t)
+        // through LDS (lane t computes token t's pair)
         float gcol[4];
         f32x4_t grow[4];
         if constexpr (GATED) {
@@ -274,11 +276,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
                 for (int r = 0; r < 4; ++r) grow[b][r] = __shfl(gsc, 16 * b + 4 * lg + r);
             }
-            if (lg == 0) {
-                float* gh = rnb(c);
-#pragma unroll
-                for (int b = 0; b < 4; ++b) gh[16 * b + l16] = gcol[b];
-            }
+            float* gh = rnb(c);
+            gh[lane] = exp2_hw(gsc);
+            gh[kC + lane] = exp2_hw(__shfl(gsc, kC - 1) - gsc);
         }
         f32x4_t eye;
 #pragma unroll
@@ -292,12 +292,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = 4 * lg + r;
-                // GATED: Gam[row][l16] and Gam[l16][row]; the one not selected may overflow,
-                // and is discarded, never multiplied
-                const float gn = GATED ? expf(grow[b][r] - gcol[b]) : 1.f;
-                const float gnt = GATED ? expf(gcol[b] - grow[b][r]) : 1.f;
-                n[r] = (row > l16) ? -br4[b][r] * (gn * gd[b][r]) : 0.f;   // N[row][l16]
-                nt[r] = (l16 > row) ? -(NORM ? br4[b][r] : bc[b]) * (gnt * gd[b][r]) : 0.f;  // N[l16][row]
+                // GATED: Gam between row and l16, from the later token to the earlier one
+                // (the diagonal, masked below, takes 2^0)
+                const float dlt = grow[b][r] - gcol[b];
+                const float gm = GATED ? exp2_hw(row > l16 ? dlt : -dlt) : 1.f;
+                n[r] = (row > l16) ? -br4[b][r] * (gm * gd[b][r]) : 0.f;   // N[row][l16]
+                nt[r] = (l16 > row) ? -(NORM ? br4[b][r] : bc[b]) * (gm * gd[b][r]) : 0.f;  // N[l16][row]
             }
             cn[b] = cvt4(n);
             cnt[b] = cvt4(nt);
@@ -322,7 +322,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             f32x4_t nt;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float gnt = GATED ? expf(gcol[b] - grow[b][r]) : 1.f;
+                const float gnt = GATED ? exp2_hw(l16 > 4 * lg + r ? gcol[b] - grow[b][r] : 0.f) : 1.f;
                 nt[r] = (l16 > 4 * lg + r) ? -(NORM ? br4[b][r] : bc[b]) * (gnt * gd[b][r]) : 0.f;
             }
             cet[b] = cvt4(nt + eye);
@@ -360,7 +360,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             } else if constexpr (GATED) {
                 f32x4_t e;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) e[r] = expf(gcol[i] - grow[k][r]);
+                for (int r = 0; r < 4; ++r) e[r] = exp2_hw(gcol[i] - grow[k][r]);
                 return cvt4(bc[i] * (e * gu[x]));
             } else {
                 return cvt4(bc[i] * gu[x]);
@@ -468,8 +468,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         // Gam[16i + l16][16j + 4g + r]; above the diagonal (i == j) it is masked
-                        const float e = expf(pgc[i] - pgr[j][r]);
-                        t[r] = (i > j || l16 >= 4 * lg + r) ? t[r] * e : 0.f;
+                        const bool keep = i > j || l16 >= 4 * lg + r;
+                        t[r] = keep ? t[r] * exp2_hw(keep ? pgc[i] - pgr[j][r] : 0.f) : 0.f;
                     }
                 }
                 if (i == j) {  // keep t >= s: row l16, column 4g+r
@@ -548,10 +548,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 rk4[m] = *reinterpret_cast<const f32x4_t*>(rnb(c) + 16 * m + 4 * lg);
                 R[m] = widen4(vv[m]) - rk4[m] * X[m];
             } else if constexpr (GATED) {
-                gk4[m] = *reinterpret_cast<const f32x4_t*>(rnb(c) + 16 * m + 4 * lg);  // G_t
-                f32x4_t e;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) e[r] = expf(gk4[m][r]);
+                const f32x4_t e = *reinterpret_cast<const f32x4_t*>(rnb(c) + 16 * m + 4 * lg);  // e^(G_t)
+                gk4[m] = *reinterpret_cast<const f32x4_t*>(rnb(c) + kC + 16 * m + 4 * lg);      // e^(G_C - G_t)
                 const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + 16 * m + 4 * lg);
                 R[m] = bs * (widen4(vv[m]) - e * X[m]);
             } else {
@@ -574,18 +572,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // GATED: the state update takes diag(e^(G_C - G)) U, and S decays by e^(G_C)
         bf16x8_t Us0 = Ub0, Us1 = Ub1;
         if constexpr (GATED) {
-            const float gC = rnb(c)[kC - 1];
-            f32x4_t Ud[4];
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                f32x4_t e;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) e[r] = expf(gC - gk4[m][r]);
-                Ud[m] = e * U[m];
-            }
-            Us0 = acc_to_b(Ud[0], Ud[1]);
-            Us1 = acc_to_b(Ud[2], Ud[3]);
-            const float eC = expf(gC);
+            Us0 = acc_to_b(gk4[0] * U[0], gk4[1] * U[1]);
+            Us1 = acc_to_b(gk4[2] * U[2], gk4[3] * U[3]);
+            const float eC = rnb(c)[kC - 1];  // e^(G_C)
 #pragma unroll
             for (int md = 0; md < D / 16; ++md) S[md] = eC * S[md];
         }
@@ -612,7 +601,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
         if constexpr (GATED) {
 #pragma unroll
-            for (int m = 0; m < 4; ++m) Y[m] = Y[m] * expf(rnb(c)[16 * m + l16]);  // diag(e^G) Q S
+            for (int m = 0; m < 4; ++m) Y[m] = Y[m] * rnb(c)[16 * m + l16];  // diag(e^G) Q S
         }
         f32x4_t O[4];
         O[0] = mfma32(Ub0, packed_a(Pp, 0, lane), Y[0]);

@@ -207,6 +207,9 @@ __device__ __forceinline__ void lds_barrier() {
 // Wait for this wave's outstanding buffer loads (and so its LDS copies).
 __device__ __forceinline__ void wait_copies() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// 2^x in one v_exp_f32 (about 1 ulp; 0 for x below the fp32 range).
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // T = (I + A)^-1, A = strict_lower(diag(beta) K K^T), for one 64-token chunk
 // by one wave: K token rows in the swizzled tile at rb + R_KS, beta (fp32) at
 // rb + R_BS; T lands in Tp in the packed operand layout (6 blocks of 1 KiB).

@@ -21,10 +21,11 @@
 //      (bf16, as rows of S^T);
 //   2. bwd_prep_kernel, one wave per chunk: T (the forward's builder), and
 //      T^T and P^T, in packed MFMA operand order;
-//   3. bwd_rev_kernel walks the chunks backwards per (b, h, 64 columns of
+//   3. bwd_rev_kernel walks the chunks backwards per (b, h, 32 columns of
 //      d_v) carrying G in fp32 MFMA accumulators (the columns of G are
-//      independent), writes G_c (bf16, rows of G^T), W (bf16, rows of W^T),
-//      dV and finally dS_0;
+//      independent) in two waves, while two more waves copy the next chunk;
+//      it writes G_c (bf16, rows of G^T), W (bf16, rows of W^T), dV and
+//      finally dS_0;
 //   4. bwd_grad_kernel, one workgroup per chunk, all chunks in parallel:
 //      dQ, dK and dbeta from S_c, G_c, W and the chunk's q/k/v/beta.
 // Numerics as in the forward: bf16 operands, fp32 accumulation; G and the
@@ -205,16 +206,24 @@ struct RevGeo {
     static constexpr int QS = KS + kC * D * 2;
     static constexpr int TT = QS + kC * D * 2;  // packed T^T, then packed P^T
     static constexpr int PT = TT + kPacked * 2;
-    static constexpr int NC = 64;                // columns per workgroup (16 per wave)
+    static constexpr int NC = 32;                // columns per workgroup (16 per chain wave)
     static constexpr int DO = PT + kPacked * 2;  // dO tile, fp32 [t][NC], 16-byte chunks swizzled
     static constexpr int BS = DO + kC * NC * 4;
     static constexpr int BUF = BS + kC * 4;
-    static constexpr int BYTES = 2 * BUF;
-    static_assert(BUF % 16 == 0, "layout");
+    static constexpr int NBUF = 3;  // the loaders run two chunks ahead
+    static constexpr int BYTES = NBUF * BUF;
+    // copy instructions one loader wave issues per chunk (loader 1 adds beta's)
+    static constexpr int N_KQ = kC * D * 2 / 1024, N_TP = 4 * kPacked / 1024, N_DO = kC * NC * 4 / 1024;
+    static constexpr int COPIES = N_KQ / 2 * 2 + N_TP / 2 + N_DO / 2;
+    static_assert(N_KQ % 2 == 0 && N_TP % 2 == 0 && N_DO % 2 == 0, "copies split evenly");
+    static_assert(COPIES + 1 <= 63, "vmcnt range");
+    static_assert(BUF % 16 == 0 && BYTES <= 160 * 1024, "layout");
 };
-// dO tile: 16-byte chunk p of token row t sits at chunk p ^ fdo(t); the operand reads
-// (rows 4g + i, 16 consecutive columns per lane group g) then hit 64 distinct banks.
-__device__ __forceinline__ int fdo(int t) { return 4 * ((t >> 2) & 3); }
+// dO tile (rows of 32 fp32 = 128 bytes, half the banks): 16-byte chunk p of token row t
+// sits at chunk p ^ fdo(t).  The operand reads touch rows 4g + i (same parity) and 16
+// consecutive columns per lane group g; the XOR puts odd and even g in different
+// bank halves (2-way, the least two 128-byte rows of one parity allow).
+__device__ __forceinline__ int fdo(int t) { return 4 * ((t >> 2) & 1); }
 
 template <int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_rev_kernel(
@@ -235,7 +244,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = static_cast<int>(uniform(static_cast<unsigned>(tid >> 6)));
     const int l16 = lane & 15, lg = lane >> 4;
-    const int j = tile * G::NC + 16 * w + l16;  // this lane's column of G
+    // waves 0 and 1 carry G (16 columns each) and store; waves 2 and 3 only copy the next
+    // chunk into LDS and wait for it, so no wave waits on the others' stores
+    const bool chain = w < 2;
+    const int j = tile * G::NC + 16 * (w & 1) + l16;  // this lane's column of G (chain waves)
     const size_t tstride = static_cast<size_t>(H) * D;
     const size_t sbase = static_cast<size_t>(pair) * D * D;
 
@@ -244,40 +256,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int md = 0; md < D / 16; ++md)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            Gm[md][r] = gs ? gs[sbase + static_cast<size_t>(s_row_d(md, 4 * lg + r)) * D + j] : 0.f;
+            Gm[md][r] = (chain && gs) ? gs[sbase + static_cast<size_t>(s_row_d(md, 4 * lg + r)) * D + j] : 0.f;
     bf16x8_t Gb[D / 32];
 #pragma unroll
     for (int kb = 0; kb < D / 32; ++kb) Gb[kb] = acc_to_b(Gm[2 * kb], Gm[2 * kb + 1]);
 
     const int col0 = tile * G::NC;
-    auto buf = [&](int c) { return smem + ((n_ch - 1 - c) & 1) * G::BUF; };
+    auto buf = [&](int c) { return smem + ((n_ch - 1 - c) % G::NBUF) * G::BUF; };
     auto issue = [&](int c) {
         const int base = c * kC, clen = min(kC, T - base);
         const size_t row0 = (tok0 + base) * tstride + static_cast<size_t>(h) * D;
         const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
         unsigned char* b = uniform_ptr(buf(c));
+        const int lw = w - 2;  // loader index
         copy_rows<D>(make_rsrc(k + row0, n_kq), b + G::KS, kC * D * 2 / 1024,
-                     static_cast<unsigned>(tstride * 2), w, 4, lane);
+                     static_cast<unsigned>(tstride * 2), lw, 2, lane);
         copy_rows<D>(make_rsrc(q + row0, n_kq), b + G::QS, kC * D * 2 / 1024,
-                     static_cast<unsigned>(tstride * 2), w, 4, lane);
+                     static_cast<unsigned>(tstride * 2), lw, 2, lane);
         copy_flat(make_rsrc(tp_ws + (static_cast<size_t>(pair) * n_ch + c) * 3 * kPacked + kPacked,
                             4 * kPacked),
-                  b + G::TT, 4 * kPacked / 1024, w, 4, lane);
+                  b + G::TT, 4 * kPacked / 1024, lw, 2, lane);
         // dO (fp32): rows of NC values from column col0; a NULL go reads as zeros
         const unsigned n_do = go ? static_cast<unsigned>(((clen - 1) * tstride + G::NC) * 4) : 0u;
         const __amdgpu_buffer_rsrc_t rd = make_rsrc(go ? go + row0 + col0 : go, n_do);
-        for (int ii = w; ii < kC * G::NC * 4 / 1024; ii += 4) {
+        for (int ii = lw; ii < kC * G::NC * 4 / 1024; ii += 2) {
             const int pos = 1024 * ii + 16 * lane;  // byte in the LDS tile
             const int r = pos / (G::NC * 4), p = (pos % (G::NC * 4)) / 16;
             copy_to_lds(rd, b + G::DO + 1024 * ii, 16,
                         static_cast<unsigned>(r * tstride * 4) + 16u * static_cast<unsigned>(p ^ fdo(r)));
         }
-        if (w == 3)
+        if (lw == 1)
             copy_to_lds(make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4)),
                         b + G::BS, 4, static_cast<unsigned>(lane * H * 4));
     };
     // dO as a B operand over tokens 32kb + {4g..4g+3, 16+4g..16+4g+3}, column j
-    const int jl = 16 * w + l16;  // column within the tile
+    const int jl = 16 * (w & 1) + l16;  // column within the tile
     auto do_op = [&](const float* Ds, int kb) {
         float f[8];
 #pragma unroll
@@ -289,14 +302,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         return as_b(v);
     };
 
+    // One LDS-only barrier per chunk: by then the loaders have waited for the copies of the
+    // chunk the chain takes next, and the chain's stores need not complete.  The loaders
+    // keep the chunk after that in flight: a loader wave issues nothing but these copies,
+    // so waiting until G::COPIES (+1 for the beta copy) are outstanding completes exactly
+    // the older chunk's.
+    auto wait_older = [&] {
+        if (w == 3)
+            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(G::COPIES + 1) : "memory");
+        else
+            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(G::COPIES) : "memory");
+    };
     if (n_ch > 0) {
-        issue(n_ch - 1);
-        wait_copies();
-        __syncthreads();
+        if (!chain) {
+            issue(n_ch - 1);
+            if (n_ch > 1) {
+                issue(n_ch - 2);
+                wait_older();
+            } else {
+                wait_copies();
+            }
+        }
+        lds_barrier();
     }
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
     for (int c = n_ch - 1; c >= 0; --c) {
-        if (c > 0) issue(c - 1);
+        if (!chain) {
+            if (c > 0) {  // make chunk c - 1 ready; put c - 2 in flight
+                if (c >= 2) {
+                    issue(c - 2);
+                    wait_older();
+                } else {
+                    wait_copies();
+                }
+                lds_barrier();
+            }
+            continue;
+        }
         unsigned char* b = buf(c);
         const uint16_t* Ks = reinterpret_cast<const uint16_t*>(b + G::KS);
         const uint16_t* Qs = reinterpret_cast<const uint16_t*>(b + G::QS);
@@ -379,16 +421,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
 #pragma unroll
         for (int kb = 0; kb < D / 32; ++kb) Gb[kb] = acc_to_b(Gm[2 * kb], Gm[2 * kb + 1]);
-        if (c > 0) {
-            wait_copies();
-            __syncthreads();
-        }
+        if (c > 0) lds_barrier();
     }
+    if (chain) {
 #pragma unroll
-    for (int md = 0; md < D / 16; ++md)
+        for (int md = 0; md < D / 16; ++md)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            gs0[sbase + static_cast<size_t>(s_row_d(md, 4 * lg + r)) * D + j] = Gm[md][r];
+            for (int r = 0; r < 4; ++r)
+                gs0[sbase + static_cast<size_t>(s_row_d(md, 4 * lg + r)) * D + j] = Gm[md][r];
+    }
 }
 
 // ---------------------------------------------------------------------------

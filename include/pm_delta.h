@@ -178,8 +178,8 @@ size_t pm_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype);
  * Two kernels, chosen as the forward's are (pm_delta_set_path):
  *   - bf16 q/k/v with D in {64, 128}: the chunked backward on bf16 MFMA
  *     (the forward's chunked kernel in reverse; bf16 parity, rel-L2 <= 2e-2
- *     against the fp32 reference).  q, k, v, go and workspace 16-byte
- *     aligned.  Workspace, per (b, h) and 64-token chunk: the chunk's start
+ *     against the fp32 reference).  q, k, v, go, gq, gk, gv and
+ *     workspace 16-byte aligned.  Workspace, per (b, h) and 64-token chunk: the chunk's start
  *     state and end state gradient and W (bf16), and three packed 64x64
  *     operands: 2 * B * H * ceil(T / 64) * (2 * D * D + 64 * D + 9216) bytes.
  *   - otherwise the per-token fp32 backward (fp32 parity).  Workspace:

@@ -379,18 +379,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         W[1] = mfma32(packed_a(TTp, qblk_u(1, 1), lane), Yb1, mfma32(packed_a(TTp, qblk_u(1, 0), lane), Yb0, zero));
         W[2] = mfma32(packed_a(TTp, qblk_u(2, 1), lane), Yb1, zero);
         W[3] = mfma32(packed_a(TTp, qblk_u(3, 1), lane), Yb1, zero);
-        // dV = beta W; W^T rows for the gradient kernel
+        // W^T = Y^T T, the same product with the operands swapped: lane (g, l16) holds
+        // W[16m + l16][4g .. 4g+3] of its 16 columns, so dV = beta W goes out in 16-byte rows
+        f32x4_t WT[4];
+        WT[0] = mfma32(Yb1, packed_a(TTp, qblk_u(0, 1), lane), mfma32(Yb0, packed_a(TTp, qblk_u(0, 0), lane), zero));
+        WT[1] = mfma32(Yb1, packed_a(TTp, qblk_u(1, 1), lane), mfma32(Yb0, packed_a(TTp, qblk_u(1, 0), lane), zero));
+        WT[2] = mfma32(Yb1, packed_a(TTp, qblk_u(2, 1), lane), zero);
+        WT[3] = mfma32(Yb1, packed_a(TTp, qblk_u(3, 1), lane), zero);
+        // W^T rows (bf16) for the gradient kernel; the state update takes -beta W
         f32x4_t NBW[4];
         uint16_t* wp = w_hist + (static_cast<size_t>(pair) * n_ch + c) * D * kC + static_cast<size_t>(j) * kC;
+        const size_t vcol = static_cast<size_t>(h) * D + tile * G::NC + 16 * (w & 1) + 4 * lg;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int t0 = 16 * m + 4 * lg;
-            const f32x4_t bw = *reinterpret_cast<const f32x4_t*>(Bs + t0) * W[m];
-            NBW[m] = -bw;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (t0 + r < clen) gv[(tok0 + base + t0 + r) * tstride + static_cast<size_t>(h) * D + j] = bw[r];
+            NBW[m] = -(*reinterpret_cast<const f32x4_t*>(Bs + t0) * W[m]);
             *reinterpret_cast<u32x2_t*>(wp + t0) = cvt4(W[m]);
+            const int t = 16 * m + l16;
+            if (t < clen)
+                *reinterpret_cast<f32x4_t*>(gv + (tok0 + base + t) * tstride + vcol) = Bs[t] * WT[m];
         }
         // G += Q^T dO - K^T diag(beta) W
         const bf16x8_t nb0 = acc_to_b(NBW[0], NBW[1]), nb1 = acc_to_b(NBW[2], NBW[3]);
@@ -641,9 +648,10 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int dd = 0; dd < JW; ++dd) {
-                dQ[m][dd] = mfma32(fdo[m], as_b(fst[dd]), dQ[m][dd]);
-                dKa[m][dd] = mfma32(as_b(fu[m]), as_b(fgt[dd]), dKa[m][dd]);
-                dKb[m][dd] = mfma32(as_b(fw[m]), as_b(fst[dd]), dKb[m][dd]);
+                // operands swapped: the tiles hold dQ^T, dK^T (lane: 4 consecutive d of a token)
+                dQ[m][dd] = mfma32(as_b(fst[dd]), fdo[m], dQ[m][dd]);
+                dKa[m][dd] = mfma32(as_b(fgt[dd]), as_b(fu[m]), dKa[m][dd]);
+                dKb[m][dd] = mfma32(as_b(fst[dd]), as_b(fw[m]), dKb[m][dd]);
             }
 #pragma unroll
         for (int x = 0; x < kTiles; ++x) {
@@ -772,28 +780,25 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int dd = 0; dd < JW; ++dd) {
-                dQ[m][dd] = mfma32(as_b(fpc[m]), as_b(fkc[dd]), dQ[m][dd]);
-                dKc[m][dd] = mfma32(fpr[m], as_b(fqc[dd]), dKc[m][dd]);
-                dKc[m][dd] = mfma32(far[m], as_b(fkc[dd]), dKc[m][dd]);
-                dKc[m][dd] = mfma32(as_b(fac[m]), as_b(fkc[dd]), dKc[m][dd]);
+                dQ[m][dd] = mfma32(as_b(fkc[dd]), as_b(fpc[m]), dQ[m][dd]);
+                dKc[m][dd] = mfma32(as_b(fqc[dd]), fpr[m], dKc[m][dd]);
+                dKc[m][dd] = mfma32(as_b(fkc[dd]), far[m], dKc[m][dd]);
+                dKc[m][dd] = mfma32(as_b(fkc[dd]), as_b(fac[m]), dKc[m][dd]);
             }
     }
-    // outputs
+    // outputs: lane (g, l16) holds d = 16 dt + 4g + [0, 4) of token 16m + l16 (16-byte stores)
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        const int t0 = 16 * m + 4 * lg;
-        const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + t0);
+        const int t = 16 * m + l16;
+        const float bt = Bs[t];
 #pragma unroll
         for (int dd = 0; dd < JW; ++dd) {
-            const int d = 16 * (JW * w + dd) + l16;
-            const f32x4_t kk = dKa[m][dd] - bs * dKb[m][dd] + dKc[m][dd];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (t0 + r < clen) {
-                    const size_t a = row0 + (t0 + r) * tstride + d;
-                    gq[a] = dQ[m][dd][r];
-                    gk[a] = kk[r];
-                }
+            const int d0 = 16 * (JW * w + dd) + 4 * lg;
+            const f32x4_t kk = dKa[m][dd] - bt * dKb[m][dd] + dKc[m][dd];
+            if (t < clen) {
+                const size_t a = row0 + t * tstride + d0;
+                *reinterpret_cast<f32x4_t*>(gq + a) = dQ[m][dd];
+                *reinterpret_cast<f32x4_t*>(gk + a) = kk;
             }
         }
     }

@@ -224,10 +224,11 @@ int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
                     "chunked backward needs bf16 inputs and D in {64, 128} (got in_dtype %d, D %d)",
                     in_dtype, D);
     if (chunked && n_tok > 0) {
-        const void* v16[] = {q, k, v, go, workspace};
+        const void* v16[] = {q, k, v, go, gq, gk, gv, workspace};
         for (const void* p : v16)
             if (p && !aligned(p, 16))
-                return fail(PM_E_ALIGN, "chunked backward: q, k, v, go and workspace must be 16-byte aligned");
+                return fail(PM_E_ALIGN,
+                            "chunked backward: q, k, v, go, gq, gk, gv and workspace must be 16-byte aligned");
     }
     const size_t need = bwd_ws_bytes(B, T, H, D, in_dtype);
     if (need > 0 && (!workspace || ws_bytes < need))

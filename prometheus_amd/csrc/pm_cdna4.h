@@ -213,6 +213,10 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // T = (I + A)^-1, A = strict_lower(diag(beta) K K^T), for one 64-token chunk
 // by one wave: K token rows in the swizzled tile at rb + R_KS, beta (fp32) at
 // rb + R_BS; T lands in Tp in the packed operand layout (6 blocks of 1 KiB).
+// The backward's prep kernel calls this.  The forward kernel keeps the same
+// algebra inline in its T producer, with its NORM and GATED scalings: called
+// through this function instead, it compiled to 5 more VGPRs and about 190
+// more instructions, in its most time-critical role.
 template <int D, int R_KS, int R_BS>
 __device__ __forceinline__ void build_t_packed(const unsigned char* rb, uint16_t* Tp, int lane) {
     const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + R_KS);

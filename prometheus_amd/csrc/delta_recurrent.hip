@@ -10,7 +10,7 @@
 //
 // Mapping: one workgroup per (sequence, head).  Thread (e, r) holds rows
 // [r*RPT, r*RPT + RPT) of column e of S in registers (RS = row slices per
-// column, adjacent lanes, reduced with cross-lane shuffles).  Tokens are
+// column, adjacent lanes, reduced with DPP quad permutes).  Tokens are
 // staged into LDS STEPS at a time so the inner loop has no barriers.
 // S is read once at the start and written once at the end, so s0 may alias
 // s_out (the decode step runs in place).
@@ -30,6 +30,33 @@
 namespace pm {
 
 constexpr int kRecSteps = 16;
+
+// Sum over the RS adjacent lanes that hold one column (RS in {1, 2, 4}): DPP quad
+// permutes, no LDS round trip.
+__device__ __forceinline__ float quad_xor(float x, int ctrl) {
+    const int xi = __float_as_int(x);
+    return __int_as_float(ctrl == 1 ? __builtin_amdgcn_update_dpp(xi, xi, 0xB1, 0xF, 0xF, false)
+                                    : __builtin_amdgcn_update_dpp(xi, xi, 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float col_sum(float x, int RS) {
+    if (RS >= 2) x += quad_xor(x, 1);  // lanes i, i ^ 1
+    if (RS >= 4) x += quad_xor(x, 2);  // lanes i, i ^ 2
+    return x;
+}
+// Dot product of a row slice with four independent accumulators (RPT % 4 == 0), so the
+// dependent chain is RPT / 4 FMAs long.
+template <int RPT>
+__device__ __forceinline__ float dot4(const float* a, const float (&b)[RPT]) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < RPT; i += 4) {
+        s0 = fmaf(a[i], b[i], s0);
+        s1 = fmaf(a[i + 1], b[i + 1], s1);
+        s2 = fmaf(a[i + 2], b[i + 2], s2);
+        s3 = fmaf(a[i + 3], b[i + 3], s3);
+    }
+    return (s0 + s1) + (s2 + s3);
+}
 
 // D <= 128 runs at most 512 threads (RPT 32, 4 slices); only D > 128 needs
 // 1024 threads, where the 64-row slices do not fit the register budget and
@@ -115,18 +142,12 @@ __global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel
         for (int j = 0; j < nst; ++j) {
             const float* kr = sk + j * DP + r * RPT;
             const float* qr = sq + j * DP + r * RPT;
-            float ks = 0.f;
-#pragma unroll
-            for (int i = 0; i < RPT; ++i) ks = fmaf(kr[i], S[i], ks);
-            for (int m = 1; m < RS; m <<= 1) ks += __shfl_xor(ks, m);
+            const float ks = col_sum(dot4<RPT>(kr, S), RS);
             const float al = sa[j];
             const float u = sb[j] * ((col_ok ? sv[j * DP + e] : 0.f) - al * ks);
 #pragma unroll
             for (int i = 0; i < RPT; ++i) S[i] = fmaf(kr[i], u, al * S[i]);
-            float os = 0.f;
-#pragma unroll
-            for (int i = 0; i < RPT; ++i) os = fmaf(qr[i], S[i], os);
-            for (int m = 1; m < RS; m <<= 1) os += __shfl_xor(os, m);
+            const float os = col_sum(dot4<RPT>(qr, S), RS);
             if (r == 0 && col_ok)
                 o[(static_cast<size_t>(tok0 + t0 + j) * H + h) * D + e] = from_f32<OutT>(os);
         }
@@ -142,6 +163,7 @@ __global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel
 }
 
 // Picks rows-per-thread and the row-slice count for head dimension D.
+// (RS <= 4 for every D <= 256, as col_sum needs.)
 static void recurrent_geometry(int D, int* rpt, int* rs) {
     int r = (D <= 8) ? 8 : (D <= 16) ? 16 : (D <= 128) ? 32 : 64;
     int s = 1;

@@ -47,6 +47,24 @@ constexpr int kRpt = 16;      // elements of a row or column slice per thread
 constexpr int kTileCols = 32; // columns per workgroup when D > 32
 static_assert(kCk % kBwdSteps == 0, "checkpoint interval");
 
+// Sum over the RS adjacent lanes (RS a power of two <= 16, aligned to RS inside a
+// 16-lane row) with DPP adds; every lane of the group ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float bwd_dpp_add(float x) {
+    const int xi = __float_as_int(x);
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, xi, CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_sum(float x, int RS) {
+    if (RS >= 2) x = bwd_dpp_add<0xB1>(x);   // lane ^ 1
+    if (RS >= 4) x = bwd_dpp_add<0x4E>(x);   // lane ^ 2
+    if (RS >= 8) x = bwd_dpp_add<0x141>(x);  // lane 7 - i of each 8
+    if (RS >= 16) x = bwd_dpp_add<0x140>(x); // lane 15 - i
+    return x;
+}
+// Workgroup barrier for LDS traffic only: global stores still in flight are not
+// waited for (no other thread reads them).
+__device__ __forceinline__ void lds_sync() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 struct BwdGeo {
     int nc, n_tiles;  // tile columns, tiles per (b, h)
     int rsc, rsr;     // row slices per column (column layout), column slices per row (row layout)
@@ -119,7 +137,7 @@ __global__ __launch_bounds__(512) void delta_bwd_ckpt_kernel(
             float ks = 0.f;
 #pragma unroll
             for (int i = 0; i < kRpt; ++i) ks = fmaf(kr[i], S[i], ks);
-            for (int m = 1; m < RS; m <<= 1) ks += __shfl_xor(ks, m);
+            ks = lane_sum(ks, RS);
             const int t = t0 + j;
             const float u = (ok ? sv[j * NC + e] : 0.f) - ks;
             if (r == 0 && ok) u_p[static_cast<size_t>(t) * D + col] = u;
@@ -160,7 +178,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
     float* su = sg + kBwdSteps * CP;    // [kBwdSteps][CP]  u (tile columns)
     float* sw = su + kBwdSteps * CP;    // [2][CP]          w, by token parity
     float* sb = sw + 2 * CP;            // [kBwdSteps]
-    float* sgb = sb + kBwdSteps;        // [kBwdSteps][NWV] gbeta partial sums
+    float* sgb = sb + kBwdSteps;        // [kBwdSteps][D] gbeta terms k[d] x[d]
 
     const int tile = blockIdx.x % n_tiles, pair = blockIdx.x / n_tiles, col0 = tile * NC;
     const int seq = pair / H, h = pair % H;
@@ -256,11 +274,9 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                     wp = fmaf(Gc[i], kc[i], wp);
                     xp = fmaf(Gr[i], ur[i], xp);
                 }
-                for (int m = 1; m < RSC; m <<= 1) wp += __shfl_xor(wp, m);
-                for (int m = 1; m < RSR; m <<= 1) {
-                    gqp += __shfl_xor(gqp, m);
-                    xp += __shfl_xor(xp, m);
-                }
+                wp = lane_sum(wp, RSC);
+                gqp = lane_sum(gqp, RSR);
+                xp = lane_sum(xp, RSR);
                 float* swp = sw + (t & 1) * CP;
                 const size_t orow = (static_cast<size_t>(tok0 + t) * H + h) * D;
                 if (rc == 0 && ok_c) {
@@ -272,17 +288,16 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 const float bkd = b * kd;
 #pragma unroll
                 for (int i = 0; i < kRpt; ++i) Sr[i] = fmaf(-bkd, ur[i], Sr[i]);
-                __syncthreads();  // w visible to the row layout
+                lds_sync();  // w visible to the row layout
                 const float* wr = swp + rr * kRpt;  // w[col0 + rr*R + i]
                 float yp = 0.f;
 #pragma unroll
                 for (int i = 0; i < kRpt; ++i) yp = fmaf(Sr[i], wr[i], yp);
-                for (int m = 1; m < RSR; m <<= 1) yp += __shfl_xor(yp, m);
-                if (rr == 0 && ok_r) gk_t[orow + d] = b * (xp - yp);
-                // gbeta = k . x, reduced over the rows held by this wave, then over waves
-                float gbp = (rr == 0 && ok_r) ? kd * xp : 0.f;
-                for (int m = 1; m < 64; m <<= 1) gbp += __shfl_xor(gbp, m);
-                if (lane == 0) sgb[j * NWV + wave] = gbp;
+                yp = lane_sum(yp, RSR);
+                if (rr == 0 && ok_r) {
+                    gk_t[orow + d] = b * (xp - yp);
+                    sgb[j * D + d] = kd * xp;  // gbeta = k . x, summed at the block end
+                }
                 // G -= b k w^T (both layouts)
 #pragma unroll
                 for (int i = 0; i < kRpt; ++i) {
@@ -291,10 +306,12 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 }
             }
             __syncthreads();
-            for (int j = tid; j < nst; j += blockDim.x) {
+            // gbeta of the block's tokens: one wave per token
+            for (int j = wave; j < nst; j += NWV) {
                 float sum = 0.f;
-                for (int x = 0; x < NWV; ++x) sum += sgb[j * NWV + x];
-                gb_t[static_cast<size_t>(tok0 + lo + j) * H + h] = sum;
+                for (int x = lane; x < D; x += 64) sum += sgb[j * D + x];
+                for (int m = 1; m < 64; m <<= 1) sum += __shfl_xor(sum, m);
+                if (lane == 0) gb_t[static_cast<size_t>(tok0 + lo + j) * H + h] = sum;
             }
         }
     }
@@ -364,7 +381,7 @@ static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
     float* gb = split ? part + static_cast<size_t>(2 * g.n_tiles) * e : a.gbeta;
     const int dp = g.rsc * kRpt, cp = g.rsr * kRpt;
     const size_t lds_b = sizeof(float) * (2 * kBwdSteps * dp + 2 * kBwdSteps * cp + 2 * cp +
-                                          kBwdSteps + kBwdSteps * (g.threads / 64));
+                                          kBwdSteps + kBwdSteps * a.D);
     hipLaunchKernelGGL((delta_bwd_kernel<InT>), dim3(grid), dim3(g.threads), lds_b, st,
                        static_cast<const InT*>(a.q), static_cast<const InT*>(a.k), a.beta, a.go,
                        a.gs, u_ws, ck_ws, gq, gk, a.gv, gb, a.gs0, a.T, a.H, a.D, g.nc, g.n_tiles,

@@ -8,12 +8,29 @@
 // own tests use D = 2..8), the varlen form of those, and pm_delta_step for
 // D outside the specialised decode kernel.
 //
-// Mapping: one workgroup per (sequence, head).  Thread (e, r) holds rows
-// [r*RPT, r*RPT + RPT) of column e of S in registers (RS = row slices per
-// column, adjacent lanes, reduced with DPP quad permutes).  Tokens are
-// staged into LDS STEPS at a time so the inner loop has no barriers.
-// S is read once at the start and written once at the end, so s0 may alias
-// s_out (the decode step runs in place).
+// Mapping.  Given k, v and beta, the columns of S evolve independently
+// (column e: kS_e = k . S[:, e], u_e = beta (v_e - kS_e), S[:, e] += k u_e,
+// o_e = q . S[:, e]), so each (sequence, head) is split into column groups of
+// CW = 256 / RS columns, one 256-thread workgroup per group.  Thread (el, r)
+// holds rows [r*RPT, r*RPT + RPT) of column c*CW + el in registers; the RS
+// row slices of a column are adjacent lanes of one 16-lane DPP row and are
+// summed with DPP (no LDS round trip).  A column's arithmetic depends on RPT
+// and RS only (fixed by D), never on the group width or the grid.
+//
+// Per token, k.S and q.S are both taken from the state before the update, and
+//   o = q.S_new = alpha (q.S) + (q.k) u
+// with q.k formed once per token while staging: the two dot products and their
+// lane sums run side by side, and only the rank-1 update waits for u.
+//
+// Tokens are staged into LDS 16 at a time, double-buffered with one barrier
+// per block: the q/k/v/beta/gate loads of block b + 1 are issued into
+// registers before block b's token loop and written to LDS after it, and a
+// block's outputs leave through LDS as row segments one block later.  Row
+// slices sit at a stride of RPT + 4 floats, so the 16-byte slice reads of a
+// wave hit distinct banks.  Workgroups of one (sequence, head) are numbered
+// 8 apart, so they run on one XCD and share its L2 copy of q and k.
+// S is read once at the start and written once at the end, column group by
+// column group, so s0 may alias s_out (the decode step runs in place).
 //
 // The model's linear attention (model/__init__.py:393-432) runs here too:
 // with l2norm, each staged q and k row is divided by max(||row||_2, 1e-6)
@@ -21,7 +38,7 @@
 //
 // Gated variant (log-gates g, alpha = exp(g) per token and head):
 //   S_t = alpha_t (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T,
-// i.e. u = beta (v - alpha k^T S), S = alpha S + k u^T.  Without g, alpha = 1
+// i.e. u = beta (v - alpha k^T S), S = alpha S + k u^T.  With g = 0, alpha = 1
 // and the arithmetic is exactly the ungated step.
 
 #include "pm_common.h"
@@ -29,53 +46,136 @@
 
 namespace pm {
 
-constexpr int kRecSteps = 16;
+constexpr int kRecSteps = 16;     // tokens per staged block
+constexpr int kRecThreads = 256;  // threads per workgroup
 
-// Sum over the RS adjacent lanes that hold one column (RS in {1, 2, 4}): DPP quad
-// permutes, no LDS round trip.
-__device__ __forceinline__ float quad_xor(float x, int ctrl) {
+// x plus the value of the lane selected by a DPP control inside each 16-lane row
+// (old = 0 and full masks, so the permute folds into one v_add_f32_dpp).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
     const int xi = __float_as_int(x);
-    return __int_as_float(ctrl == 1 ? __builtin_amdgcn_update_dpp(xi, xi, 0xB1, 0xF, 0xF, false)
-                                    : __builtin_amdgcn_update_dpp(xi, xi, 0x4E, 0xF, 0xF, false));
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, xi, CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ float col_sum(float x, int RS) {
-    if (RS >= 2) x += quad_xor(x, 1);  // lanes i, i ^ 1
-    if (RS >= 4) x += quad_xor(x, 2);  // lanes i, i ^ 2
-    return x;
+// Sums over the RS adjacent lanes that hold one column (RS a power of two <= 16,
+// aligned to RS inside a 16-lane row), for two values at once.  Each step adds the
+// same two values on both partner lanes, so every lane of the group ends with the
+// same bits.
+template <int RS>
+__device__ __forceinline__ void col_sum2(float& a, float& b) {
+    if constexpr (RS >= 2) a = dpp_add<0xB1>(a), b = dpp_add<0xB1>(b);    // lane ^ 1
+    if constexpr (RS >= 4) a = dpp_add<0x4E>(a), b = dpp_add<0x4E>(b);    // lane ^ 2
+    if constexpr (RS >= 8) a = dpp_add<0x141>(a), b = dpp_add<0x141>(b);  // 7 - i in each 8
+    if constexpr (RS >= 16) a = dpp_add<0x140>(a), b = dpp_add<0x140>(b); // 15 - i
 }
-// Dot product of a row slice with four independent accumulators (RPT % 4 == 0), so the
-// dependent chain is RPT / 4 FMAs long.
+// Dot products of two row slices with one column slice, four independent
+// accumulators each (RPT % 4 == 0), so the dependent chains are RPT / 4 FMAs long.
 template <int RPT>
-__device__ __forceinline__ float dot4(const float* a, const float (&b)[RPT]) {
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+__device__ __forceinline__ void dot4x2(const float (&a)[RPT], const float (&b)[RPT], const float (&s)[RPT],
+                                       float& da, float& db) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
 #pragma unroll
     for (int i = 0; i < RPT; i += 4) {
-        s0 = fmaf(a[i], b[i], s0);
-        s1 = fmaf(a[i + 1], b[i + 1], s1);
-        s2 = fmaf(a[i + 2], b[i + 2], s2);
-        s3 = fmaf(a[i + 3], b[i + 3], s3);
+        a0 = fmaf(a[i], s[i], a0);
+        b0 = fmaf(b[i], s[i], b0);
+        a1 = fmaf(a[i + 1], s[i + 1], a1);
+        b1 = fmaf(b[i + 1], s[i + 1], b1);
+        a2 = fmaf(a[i + 2], s[i + 2], a2);
+        b2 = fmaf(b[i + 2], s[i + 2], b2);
+        a3 = fmaf(a[i + 3], s[i + 3], a3);
+        b3 = fmaf(b[i + 3], s[i + 3], b3);
     }
-    return (s0 + s1) + (s2 + s3);
+    da = (a0 + a1) + (a2 + a3);
+    db = (b0 + b1) + (b2 + b3);
 }
 
-// D <= 128 runs at most 512 threads (RPT 32, 4 slices); only D > 128 needs
-// 1024 threads, where the 64-row slices do not fit the register budget and
-// part of S spills (a rare shape, kept for generality).
-template <int RPT, typename InT, typename OutT>
-__global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel(
+// Four consecutive elements of a q or k row as loaded, converted only when
+// written to LDS (so the loads stay in flight across a token loop).  With
+// vec, one 16-byte (fp32) or 8-byte (bf16, two packed pairs in w[0..1])
+// load; otherwise up to four element loads.  Elements past the row are 0.
+template <typename InT>
+struct Raw4;
+template <>
+struct Raw4<float> {
+    float x[4];
+    __device__ __forceinline__ void load(const float* p, int n, bool vec) {
+        if (vec) {
+            if (n > 0) {
+                const float4 t = *reinterpret_cast<const float4*>(p);
+                x[0] = t.x, x[1] = t.y, x[2] = t.z, x[3] = t.w;
+            } else {
+                x[0] = x[1] = x[2] = x[3] = 0.f;
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[c] = c < n ? p[c] : 0.f;
+        }
+    }
+    __device__ __forceinline__ void get(float (&y)[4], bool) const {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) y[c] = x[c];
+    }
+};
+template <>
+struct Raw4<uint16_t> {
+    uint32_t w[4];
+    __device__ __forceinline__ void load(const uint16_t* p, int n, bool vec) {
+        if (vec) {
+            if (n > 0) {
+                const uint2 t = *reinterpret_cast<const uint2*>(p);
+                w[0] = t.x, w[1] = t.y;
+            } else {
+                w[0] = w[1] = 0u;
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) w[c] = c < n ? p[c] : 0u;
+        }
+    }
+    __device__ __forceinline__ void get(float (&y)[4], bool vec) const {
+        if (vec) {
+            y[0] = __uint_as_float(w[0] << 16), y[1] = __uint_as_float(w[0] & 0xffff0000u);
+            y[2] = __uint_as_float(w[1] << 16), y[3] = __uint_as_float(w[1] & 0xffff0000u);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) y[c] = __uint_as_float(w[c] << 16);
+        }
+    }
+};
+
+// LDS floats of one staging buffer: k and q rows [kRecSteps][RS * (RPT + 4)],
+// v and the outputs [kRecSteps][CW], and per token {beta, q.k, alpha, 0}.
+template <int RPT, int RS>
+struct RecGeo {
+    static constexpr int CW = kRecThreads / RS;  // columns per workgroup
+    static constexpr int DP = RS * RPT;          // padded row length
+    static constexpr int SL = RPT + 4;           // LDS stride of a row slice
+    static constexpr int DPL = RS * SL;          // LDS row length
+    static constexpr int BUF = 2 * kRecSteps * DPL + 2 * kRecSteps * CW + 4 * kRecSteps;
+    static constexpr size_t BYTES = 2 * BUF * sizeof(float);
+};
+
+// One (sequence, head) column group per workgroup; blockIdx = (slot * ncg + c) * 8 + x
+// for pair = pair0 + slot * 8 + x and column group c.
+template <int RPT, int RS, bool GATED, typename InT, typename OutT>
+__global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
     const InT* __restrict__ q, const InT* __restrict__ k, const InT* __restrict__ v,
     const float* __restrict__ beta, const float* s0, OutT* __restrict__ o, float* s_out,
-    const int32_t* __restrict__ cu_seqlens, int T, int H, int D, int RS, int l2norm,
-    const float* __restrict__ gate) {
-    extern __shared__ float lds[];
-    const int DP = RS * RPT;  // padded row count per column
-    float* sk = lds;                          // [kRecSteps][DP]
-    float* sq = sk + kRecSteps * DP;          // [kRecSteps][DP]
-    float* sv = sq + kRecSteps * DP;          // [kRecSteps][DP]
-    float* sb = sv + kRecSteps * DP;          // [kRecSteps]
-    float* sa = sb + kRecSteps;               // [kRecSteps] alpha
+    const int32_t* __restrict__ cu_seqlens, int pair0, int n_pairs, int ncg, int T, int H, int D,
+    int l2norm, int vec, const float* __restrict__ gate) {
+    using G = RecGeo<RPT, RS>;
+    constexpr int CW = G::CW, DP = G::DP, SL = G::SL, DPL = G::DPL;
+    constexpr int KB = kRecSteps, NT = kRecThreads;
+    constexpr int NG = KB * DP / 4;           // 4-element groups in a staged q or k block
+    constexpr int NPF = (NG + NT - 1) / NT;   // groups per thread
+    constexpr int NPV = KB * CW / NT;         // staged v elements per thread (16 / RS)
+    static_assert(RPT % 4 == 0 && RS <= 16 && NPV * NT == KB * CW, "recurrent geometry");
+    extern __shared__ float4 lds4[];
+    float* const lds = reinterpret_cast<float*>(lds4);
 
-    const int pair = blockIdx.x;
+    const int xs = blockIdx.x & 7, rest = blockIdx.x >> 3;
+    const int c = rest % ncg;
+    const int pair = pair0 + (rest / ncg) * 8 + xs;
+    if (pair >= n_pairs) return;  // whole workgroup, before any barrier
     const int seq = pair / H, h = pair % H;
     long tok0;
     int len;
@@ -91,8 +191,8 @@ __global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel
     }
 
     const int tid = threadIdx.x;
-    const int e = tid / RS;
-    const int r = tid % RS;
+    const int el = tid / RS, r = tid % RS;
+    const int e = c * CW + el;
     const bool col_ok = e < D;
     const size_t sbase = static_cast<size_t>(pair) * D * D;
 
@@ -103,54 +203,163 @@ __global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel
         S[i] = (s0 && col_ok && d < D) ? s0[sbase + static_cast<size_t>(d) * D + e] : 0.0f;
     }
 
-    for (int t0 = 0; t0 < len; t0 += kRecSteps) {
-        const int nst = min(kRecSteps, len - t0);
-        __syncthreads();
-        for (int idx = tid; idx < kRecSteps * DP; idx += blockDim.x) {
-            const int j = idx / DP, d = idx % DP;
-            float kv = 0.f, qv = 0.f, vv = 0.f;
-            if (j < nst && d < D) {
-                const size_t a = (static_cast<size_t>(tok0 + t0 + j) * H + h) * D + d;
-                kv = to_f32(k[a]);
-                qv = to_f32(q[a]);
-                vv = to_f32(v[a]);
-            }
-            sk[idx] = kv;
-            sq[idx] = qv;
-            sv[idx] = vv;
-        }
-        for (int j = tid; j < kRecSteps; j += blockDim.x) {
-            const size_t a = static_cast<size_t>(tok0 + t0 + j) * H + h;
-            sb[j] = (j >= nst) ? 0.f : beta ? beta[a] : 1.f;
-            sa[j] = (j < nst && gate) ? expf(gate[a]) : 1.f;
-        }
-        __syncthreads();
-        if (l2norm) {
-            // one wave per staged row (k rows, then q rows): x / max(||x||, 1e-6)
-            const int lane = tid & 63, nw = blockDim.x >> 6;
-            for (int row = tid >> 6; row < 2 * nst; row += nw) {
-                float* x = (row < nst ? sk : sq) + (row % nst) * DP;
-                float ss = 0.f;
-                for (int d = lane; d < D; d += 64) ss = fmaf(x[d], x[d], ss);
-                for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
-                const float den = fmaxf(sqrtf(ss), 1e-6f);
-                for (int d = lane; d < D; d += 64) x[d] = x[d] / den;
-            }
-            __syncthreads();
-        }
+    auto row = [&](int t) { return (static_cast<size_t>(tok0 + t) * H + h) * D; };
 
-        for (int j = 0; j < nst; ++j) {
-            const float* kr = sk + j * DP + r * RPT;
-            const float* qr = sq + j * DP + r * RPT;
-            const float ks = col_sum(dot4<RPT>(kr, S), RS);
-            const float al = sa[j];
-            const float u = sb[j] * ((col_ok ? sv[j * DP + e] : 0.f) - al * ks);
+    // ---- prefetch registers for one block ----
+    Raw4<InT> pk[NPF], pq[NPF];
+    InT pv[NPV];
+    float pb = 0.f, pg = 0.f;
+    auto prefetch = [&](int t0, int nst) {
 #pragma unroll
-            for (int i = 0; i < RPT; ++i) S[i] = fmaf(kr[i], u, al * S[i]);
-            const float os = col_sum(dot4<RPT>(qr, S), RS);
-            if (r == 0 && col_ok)
-                o[(static_cast<size_t>(tok0 + t0 + j) * H + h) * D + e] = from_f32<OutT>(os);
+        for (int s = 0; s < NPF; ++s) {
+            const int grp = s * NT + tid;
+            const int j = grp * 4 / DP, d = grp * 4 % DP;
+            int n = 0;
+            size_t a = 0;
+            if (grp < NG && j < nst) {
+                n = max(0, min(4, D - d));
+                a = row(t0 + j) + d;
+            }
+            pk[s].load(k + a, n, vec);
+            pq[s].load(q + a, n, vec);
         }
+#pragma unroll
+        for (int s = 0; s < NPV; ++s) {
+            const int idx = s * NT + tid;
+            const int j = idx / CW, e2 = c * CW + idx % CW;
+            pv[s] = (j < nst && e2 < D) ? v[row(t0 + j) + e2] : InT(0);
+        }
+        if (tid < KB) {
+            const size_t a = static_cast<size_t>(tok0 + t0 + tid) * H + h;
+            pb = tid < nst ? (beta ? beta[a] : 1.f) : 0.f;
+            if constexpr (GATED) pg = tid < nst ? gate[a] : 0.f;
+        }
+    };
+
+    // ---- registers -> LDS buffer (q and k rows normalised first under l2norm) ----
+    auto stage = [&](float* buf) {
+        float* sk = buf;
+        float* sq = sk + KB * DPL;
+        float* sv = sq + KB * DPL;
+        float* sc = sv + 2 * KB * CW;  // [KB] x {beta, q.k, alpha, 0}
+#pragma unroll
+        for (int s = 0; s < NPF; ++s) {
+            const int grp = s * NT + tid;
+            const int j = grp * 4 / DP, d = grp * 4 % DP;
+            float xk[4], xq[4];
+            pk[s].get(xk, vec);
+            pq[s].get(xq, vec);
+            if (l2norm) {
+                // a row is DP / 4 adjacent lanes (DP / 4 divides 64)
+                float ssk = 0.f, ssq = 0.f;
+#pragma unroll
+                for (int c2 = 0; c2 < 4; ++c2) {
+                    ssk = fmaf(xk[c2], xk[c2], ssk);
+                    ssq = fmaf(xq[c2], xq[c2], ssq);
+                }
+#pragma unroll
+                for (int m = 1; m < DP / 4; m <<= 1) {
+                    ssk += __shfl_xor(ssk, m);
+                    ssq += __shfl_xor(ssq, m);
+                }
+                const float dk = fmaxf(sqrtf(ssk), 1e-6f), dq = fmaxf(sqrtf(ssq), 1e-6f);
+#pragma unroll
+                for (int c2 = 0; c2 < 4; ++c2) {
+                    xk[c2] = xk[c2] / dk;
+                    xq[c2] = xq[c2] / dq;
+                }
+            }
+            float qk = 0.f;
+#pragma unroll
+            for (int c2 = 0; c2 < 4; ++c2) qk = fmaf(xq[c2], xk[c2], qk);
+#pragma unroll
+            for (int m = 1; m < DP / 4; m <<= 1) qk += __shfl_xor(qk, m);
+            if (grp < NG) {
+                const int pos = j * DPL + (d / RPT) * SL + d % RPT;
+                *reinterpret_cast<float4*>(sk + pos) = make_float4(xk[0], xk[1], xk[2], xk[3]);
+                *reinterpret_cast<float4*>(sq + pos) = make_float4(xq[0], xq[1], xq[2], xq[3]);
+                if (d == 0) sc[4 * j + 1] = qk;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < NPV; ++s) sv[s * NT + tid] = to_f32(pv[s]);
+        if (tid < KB) {
+            sc[4 * tid] = pb;
+            sc[4 * tid + 2] = GATED ? expf(pg) : 1.f;  // alpha: 1 past the sequence end
+        }
+    };
+
+    // ---- the recurrence over one staged block ----
+    auto tokens = [&](const float* buf, int nst) {
+        const float* sk = buf;
+        const float* sq = sk + KB * DPL;
+        const float* sv = sq + KB * DPL;
+        float* so = const_cast<float*>(sv) + KB * CW;
+        const float4* sc = reinterpret_cast<const float4*>(so + KB * CW);
+        auto body = [&](int j) {
+            float kk[RPT], qq[RPT];
+            const float4* kp = reinterpret_cast<const float4*>(sk + j * DPL + r * SL);
+            const float4* qp = reinterpret_cast<const float4*>(sq + j * DPL + r * SL);
+#pragma unroll
+            for (int i = 0; i < RPT / 4; ++i) {
+                const float4 t = kp[i], w = qp[i];
+                kk[4 * i] = t.x, kk[4 * i + 1] = t.y, kk[4 * i + 2] = t.z, kk[4 * i + 3] = t.w;
+                qq[4 * i] = w.x, qq[4 * i + 1] = w.y, qq[4 * i + 2] = w.z, qq[4 * i + 3] = w.w;
+            }
+            float ks, qs;
+            dot4x2<RPT>(kk, qq, S, ks, qs);
+            col_sum2<RS>(ks, qs);
+            const float4 cj = sc[j];  // beta, q.k, alpha
+            const float vv = sv[j * CW + el];
+            float os;
+            if constexpr (GATED) {
+                const float u = cj.x * (vv - cj.z * ks);
+                os = fmaf(cj.y, u, cj.z * qs);
+#pragma unroll
+                for (int i = 0; i < RPT; ++i) S[i] = fmaf(kk[i], u, cj.z * S[i]);
+            } else {
+                const float u = cj.x * (vv - ks);
+                os = fmaf(cj.y, u, qs);
+#pragma unroll
+                for (int i = 0; i < RPT; ++i) S[i] = fmaf(kk[i], u, S[i]);
+            }
+            so[j * CW + el] = os;  // the RS lanes of a column store the same bits
+        };
+        if (nst == KB) {
+#pragma unroll
+            for (int j = 0; j < KB; ++j) body(j);
+        } else {
+            for (int j = 0; j < nst; ++j) body(j);
+        }
+    };
+
+    // ---- a block's outputs, from LDS, as row segments of CW columns ----
+    auto store_o = [&](const float* buf, int t0, int nst) {
+        const float* so = buf + 2 * KB * DPL + KB * CW;
+#pragma unroll
+        for (int s = 0; s < NPV; ++s) {
+            const int idx = s * NT + tid;
+            const int j = idx / CW, e2 = c * CW + idx % CW;
+            if (j < nst && e2 < D) o[row(t0 + j) + e2] = from_f32<OutT>(so[idx]);
+        }
+    };
+
+    const int nblk = (len + KB - 1) / KB;
+    if (nblk > 0) prefetch(0, min(KB, len));
+    for (int b = 0; b < nblk; ++b) {
+        float* buf = lds + (b & 1) * G::BUF;
+        const int t0 = b * KB, nst = min(KB, len - t0);
+        // buf was last read by block b - 2's token loop, before the previous barrier
+        stage(buf);
+        __syncthreads();
+        if (b + 1 < nblk) prefetch(t0 + KB, min(KB, len - t0 - KB));
+        if (b > 0) store_o(lds + ((b - 1) & 1) * G::BUF, t0 - KB, KB);
+        tokens(buf, nst);
+    }
+    if (nblk > 0) {
+        __syncthreads();
+        const int t0 = (nblk - 1) * KB;
+        store_o(lds + ((nblk - 1) & 1) * G::BUF, t0, len - t0);
     }
 
     if (col_ok) {
@@ -162,36 +371,70 @@ __global__ __launch_bounds__(RPT >= 64 ? 1024 : 512) void delta_recurrent_kernel
     }
 }
 
-// Picks rows-per-thread and the row-slice count for head dimension D.
-// (RS <= 4 for every D <= 256, as col_sum needs.)
+// Rows per thread and row slices per column for head dimension D: RPT 8 up to
+// D = 128, 16 above; RS the smallest power of two with RS * RPT >= D (<= 16).
 static void recurrent_geometry(int D, int* rpt, int* rs) {
-    int r = (D <= 8) ? 8 : (D <= 16) ? 16 : (D <= 128) ? 32 : 64;
+    const int r = D <= 128 ? 8 : 16;
     int s = 1;
     while (r * s < D) s <<= 1;
     *rpt = r;
     *rs = s;
 }
 
-template <int RPT, typename InT, typename OutT>
-static hipError_t launch_rec_t(const RecurrentArgs& a, int rs, hipStream_t st) {
-    const int threads = ((a.D * rs + 63) / 64) * 64;
-    const size_t lds = sizeof(float) * (3 * kRecSteps * rs * RPT + 2 * kRecSteps);
-    hipLaunchKernelGGL((delta_recurrent_kernel<RPT, InT, OutT>), dim3(a.n_pairs), dim3(threads),
-                       lds, st, static_cast<const InT*>(a.q), static_cast<const InT*>(a.k),
-                       static_cast<const InT*>(a.v), a.beta, a.s0, static_cast<OutT*>(a.o),
-                       a.s_out, a.cu_seqlens, a.T, a.H, a.D, rs, a.l2norm ? 1 : 0, a.g);
-    return hipGetLastError();
+static bool is_aligned(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+template <int RPT, int RS, bool GATED, typename InT, typename OutT>
+static hipError_t launch_rec_t(const RecurrentArgs& a, hipStream_t st) {
+    using G = RecGeo<RPT, RS>;
+    auto kern = delta_recurrent_kernel<RPT, RS, GATED, InT, OutT>;
+    if (G::BYTES > 64 * 1024) {
+        // the dynamic-LDS limit is a per-device function attribute
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        static bool attr_set[64] = {};
+        if (dev < 0 || dev >= 64 || !attr_set[dev]) {
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(G::BYTES));
+            if (e != hipSuccess) return e;
+            if (dev >= 0 && dev < 64) attr_set[dev] = true;
+        }
+    }
+    const int ncg = (a.D + G::CW - 1) / G::CW;
+    // 16-byte (fp32) or 8-byte (bf16) row loads when every q/k row group is aligned
+    const size_t vb = sizeof(InT) * 4;
+    const int vec = (a.D % 4 == 0) && is_aligned(a.q, vb) && is_aligned(a.k, vb);
+    // at most 2^22 workgroups (2^30 work-items) per launch
+    const long per = ((1L << 22) / (8L * ncg)) * 8;
+    for (long p0 = 0; p0 < a.n_pairs; p0 += per) {
+        const long np = a.n_pairs - p0 < per ? a.n_pairs - p0 : per;
+        const dim3 grid(static_cast<unsigned>((np + 7) / 8 * 8 * ncg));
+        hipLaunchKernelGGL(kern, grid, dim3(kRecThreads), G::BYTES, st, static_cast<const InT*>(a.q),
+                           static_cast<const InT*>(a.k), static_cast<const InT*>(a.v), a.beta, a.s0,
+                           static_cast<OutT*>(a.o), a.s_out, a.cu_seqlens, static_cast<int>(p0), a.n_pairs,
+                           ncg, a.T, a.H, a.D, a.l2norm ? 1 : 0, vec, a.g);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+template <int RPT, int RS, typename InT, typename OutT>
+static hipError_t launch_rec_g(const RecurrentArgs& a, hipStream_t st) {
+    return a.g ? launch_rec_t<RPT, RS, true, InT, OutT>(a, st) : launch_rec_t<RPT, RS, false, InT, OutT>(a, st);
 }
 
 template <typename InT, typename OutT>
 static hipError_t launch_rec_io(const RecurrentArgs& a, hipStream_t st) {
     int rpt, rs;
     recurrent_geometry(a.D, &rpt, &rs);
-    switch (rpt) {
-        case 8: return launch_rec_t<8, InT, OutT>(a, rs, st);
-        case 16: return launch_rec_t<16, InT, OutT>(a, rs, st);
-        case 32: return launch_rec_t<32, InT, OutT>(a, rs, st);
-        default: return launch_rec_t<64, InT, OutT>(a, rs, st);
+    if (rpt == 16) return launch_rec_g<16, 16, InT, OutT>(a, st);
+    switch (rs) {
+        case 1: return launch_rec_g<8, 1, InT, OutT>(a, st);
+        case 2: return launch_rec_g<8, 2, InT, OutT>(a, st);
+        case 4: return launch_rec_g<8, 4, InT, OutT>(a, st);
+        case 8: return launch_rec_g<8, 8, InT, OutT>(a, st);
+        default: return launch_rec_g<8, 16, InT, OutT>(a, st);
     }
 }
 

@@ -17,8 +17,9 @@ step (cfg4: B=256 H=32 D=128, fp32 state updated in place) is measured in
 the same run and reported under ``decode`` (with the same batch through a
 serving state cache under ``decode.state_cache``), the backward at cfg1
 under ``backward``, the model's linear attention at the cfg1 shape
-under ``model_linear_attention``, and the gated variant at cfg1 under
-``gated``.
+under ``model_linear_attention``, the cfg1 forward with fp32 q/k/v (the
+per-token kernel) under ``fp32_forward``, and the gated variant at cfg1
+under ``gated``.
 """
 
 from __future__ import annotations
@@ -37,6 +38,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, vendor figure
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, vendor figure
+FP32_VALU_PEAK_TFLOPS = 157.3  # MI355X fp32 vector, vendor figure (packed FMA; half without)
 CHUNK = 64
 CALIB_COPY_BYTES = 1 << 30  # bytes read (and written) by one calibration copy launch
 CPU_SAMPLE_S = 10.0  # seconds of CPU work timed for cpu_baseline (whole cfg1 batches)
@@ -332,6 +334,43 @@ def main():
             del qm, km, vm
         del om, sm
 
+    # the same cfg1 forward with fp32 q/k/v (the reference's dtype): the per-token kernel
+    fp32_fwd = None
+    if args.model_calls > 0:
+        q, k, v, beta = (x.float() for x in sets[0])
+        of = torch.empty((B, T, H, D), device=dev)
+        sf = torch.empty((B, H, D, D), device=dev)
+
+        def ffwd():
+            rc = lib.pm_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), None,
+                                  of.data_ptr(), sf.data_ptr(), B, T, H, D, _native.DTYPE_F32,
+                                  _native.DTYPE_F32, CHUNK, None, 0, stream.cuda_stream)
+            _native.check(rc)
+
+        ffwd()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        calls = args.model_calls * 2
+        e0.record(stream)
+        for _ in range(calls):
+            ffwd()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        f_ms = e0.elapsed_time(e1) / calls
+        fb = fwd_bytes(B, T, H, D, s_in=4, s_out=4)
+        fflop = 6 * B * T * H * D * D  # k.S, q.S and the rank-1 update, 2 flops per FMA
+        fp32_fwd = {
+            "workload": "cfg1 forward with fp32 q/k/v (pm_delta_fwd, per-token fp32 kernel)",
+            "calls": calls,
+            "ms_per_call": f_ms,
+            "tokens_per_s": tokens / (f_ms * 1e-3),
+            "roofline": {"bound": "valu", "achieved": fflop / (f_ms * 1e-3) / 1e12,
+                         "peak": FP32_VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": fflop / (f_ms * 1e-3) / 1e12 / FP32_VALU_PEAK_TFLOPS},
+            "hbm_gbs": fb / (f_ms * 1e-3) / 1e9,
+        }
+        del q, k, v, beta, of, sf
+
     # the gated delta rule at cfg1 (pm_gated_delta_fwd): cfg1's inputs plus log-gates
     # -0.1 |N(0, 1)| per token and head, on the chunked kernel
     gated = None
@@ -450,6 +489,7 @@ def main():
         "parity": parity,
         "decode": decode,
         "model_linear_attention": model_la,
+        "fp32_forward": fp32_fwd,
         "gated": gated,
         "backward": backward,
     }

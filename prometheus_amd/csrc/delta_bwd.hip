@@ -27,9 +27,9 @@
 // sums), so with several tiles each writes its partial sums and a final
 // pass adds them (in a fixed order: results do not depend on scheduling).
 //
-// K5a (checkpoint pass) runs the forward recurrence for its columns, one
-// thread per (column, slice of RPT rows), writing u and the block-end
-// states.  K5b (reverse pass) holds three fp32 matrices of the tile on chip:
+// K5a (checkpoint pass) runs the forward recurrence in the per-token
+// forward kernel's layout (column groups of 256 threads), writing u and the
+// block-end states.  K5b (reverse pass) holds three fp32 matrices of the tile on chip:
 // G by columns (thread (e, rc): rows rc*RPT.. of column e, for w = G^T k),
 // G by rows and S by rows (thread (d, rr): tile columns rr*RPT.. of row d,
 // for x = G u, S go and S w); every product is a per-thread partial sum
@@ -38,12 +38,13 @@
 
 #include "pm_common.h"
 #include "pm_internal.h"
+#include "pm_rec.h"
 
 namespace pm {
 
 constexpr int kBwdSteps = 8;  // tokens staged in LDS at a time
 constexpr int kCk = 8;        // tokens between state checkpoints (multiple of kBwdSteps)
-constexpr int kRpt = 16;      // elements of a row or column slice per thread
+constexpr int kRpt = 8;       // elements of a row or column slice per thread
 constexpr int kTileCols = 32; // columns per workgroup when D > 32
 static_assert(kCk % kBwdSteps == 0, "checkpoint interval");
 
@@ -87,75 +88,231 @@ static BwdGeo bwd_geo(int D) {
 }
 
 // ---------------- K5a: forward pass writing u and block-end states ----------------
-template <typename InT>
-__global__ __launch_bounds__(512) void delta_bwd_ckpt_kernel(
+// The forward recurrence in the per-token forward kernel's layout (256 threads per
+// group of CW = 256 / RS columns, thread (el, r) holding rows [r*RPT, r*RPT + RPT)
+// of its column, DPP column sums, tokens staged 16 at a time with the next block's
+// loads in flight), writing u_t = v_t - S_{t-1}^T k_t per token (through LDS, one
+// block later) and S after every kCk-th token and after the last.
+template <int RPT, int RS, typename InT>
+__global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
     const InT* __restrict__ k, const InT* __restrict__ v, const float* __restrict__ beta,
-    const float* __restrict__ s0, float* __restrict__ u_ws, float* __restrict__ ck_ws, int T,
-    int H, int D, int NC, int n_tiles, int RS) {
-    extern __shared__ float lds[];
-    const int DP = RS * kRpt;
-    float* sk = lds;                  // [kBwdSteps][DP]
-    float* sv = sk + kBwdSteps * DP;  // [kBwdSteps][NC]
-    float* sb = sv + kBwdSteps * NC;  // [kBwdSteps]
+    const float* __restrict__ s0, float* __restrict__ u_ws, float* __restrict__ ck_ws, int pair0,
+    int n_pairs, int ncg, int T, int H, int D, int vec) {
+    using G = RecGeo<RPT, RS>;
+    constexpr int CW = G::CW, DP = G::DP, SL = G::SL, DPL = G::DPL;
+    constexpr int KB = kRecSteps, NT = kRecThreads;
+    constexpr int NG = KB * DP / 4, NPF = (NG + NT - 1) / NT, NPV = KB * CW / NT;
+    constexpr int BUF = KB * DPL + 2 * KB * CW + 4 * KB;  // k rows, v, u, beta
+    static_assert(KB % kCk == 0, "checkpoints fall inside a staged block");
+    extern __shared__ float4 lds4[];
+    float* const lds = reinterpret_cast<float*>(lds4);
 
-    const int pair = blockIdx.x / n_tiles, col0 = (blockIdx.x % n_tiles) * NC;
+    const int xs = blockIdx.x & 7, rest = blockIdx.x >> 3;
+    const int c = rest % ncg;
+    const int pair = pair0 + (rest / ncg) * 8 + xs;
+    if (pair >= n_pairs) return;  // whole workgroup, before any barrier
     const int seq = pair / H, h = pair % H;
     const long tok0 = static_cast<long>(seq) * T;
     const int tid = threadIdx.x;
-    const int e = tid / RS, r = tid % RS;  // tile column e, rows r*kRpt..
-    const int col = col0 + e;
-    const bool ok = e < NC && col < D;
+    const int el = tid / RS, r = tid % RS;
+    const int e = c * CW + el;
+    const bool col_ok = e < D;
     const size_t sbase = static_cast<size_t>(pair) * D * D;
     const int n_ck = (T + kCk - 1) / kCk;
     float* u_p = u_ws + static_cast<size_t>(pair) * T * D;
     float* ck_p = ck_ws + static_cast<size_t>(pair) * n_ck * D * D;
 
-    float S[kRpt];  // S[r*kRpt + i][col]
+    float S[RPT];  // S[r*RPT + i][e]
 #pragma unroll
-    for (int i = 0; i < kRpt; ++i) {
-        const int d = r * kRpt + i;
-        S[i] = (s0 && ok && d < D) ? s0[sbase + static_cast<size_t>(d) * D + col] : 0.f;
+    for (int i = 0; i < RPT; ++i) {
+        const int d = r * RPT + i;
+        S[i] = (s0 && col_ok && d < D) ? s0[sbase + static_cast<size_t>(d) * D + e] : 0.f;
     }
-    for (int t0 = 0; t0 < T; t0 += kBwdSteps) {
-        const int nst = min(kBwdSteps, T - t0);
-        __syncthreads();
-        for (int idx = tid; idx < kBwdSteps * DP; idx += blockDim.x) {
-            const int j = idx / DP, d = idx % DP;
-            sk[idx] = (j < nst && d < D)
-                          ? to_f32(k[(static_cast<size_t>(tok0 + t0 + j) * H + h) * D + d]) : 0.f;
+    auto row = [&](int t) { return (static_cast<size_t>(tok0 + t) * H + h) * D; };
+
+    Raw4<InT> pk[NPF];
+    InT pv[NPV];
+    float pb = 0.f;
+    auto prefetch = [&](int t0, int nst) {
+#pragma unroll
+        for (int s = 0; s < NPF; ++s) {
+            const int grp = s * NT + tid;
+            const int j = grp * 4 / DP, d = grp * 4 % DP;
+            int n = 0;
+            size_t a = 0;
+            if (grp < NG && j < nst) {
+                n = max(0, min(4, D - d));
+                a = row(t0 + j) + d;
+            }
+            pk[s].load(k + a, n, vec);
         }
-        for (int idx = tid; idx < kBwdSteps * NC; idx += blockDim.x) {
-            const int j = idx / NC, c = idx % NC;
-            sv[idx] = (j < nst && col0 + c < D)
-                          ? to_f32(v[(static_cast<size_t>(tok0 + t0 + j) * H + h) * D + col0 + c]) : 0.f;
+#pragma unroll
+        for (int s = 0; s < NPV; ++s) {
+            const int idx = s * NT + tid;
+            const int j = idx / CW, e2 = c * CW + idx % CW;
+            pv[s] = (j < nst && e2 < D) ? v[row(t0 + j) + e2] : InT(0);
         }
-        for (int j = tid; j < kBwdSteps; j += blockDim.x)
-            sb[j] = (j < nst) ? beta[static_cast<size_t>(tok0 + t0 + j) * H + h] : 0.f;
-        __syncthreads();
-        for (int j = 0; j < nst; ++j) {
-            const float* kr = sk + j * DP + r * kRpt;
-            float ks = 0.f;
+        if (tid < KB) pb = tid < nst ? beta[static_cast<size_t>(tok0 + t0 + tid) * H + h] : 0.f;
+    };
+    auto stage = [&](float* buf) {
+        float* sk = buf;
+        float* sv = sk + KB * DPL;
+        float* sb = sv + 2 * KB * CW;
 #pragma unroll
-            for (int i = 0; i < kRpt; ++i) ks = fmaf(kr[i], S[i], ks);
-            ks = lane_sum(ks, RS);
-            const int t = t0 + j;
-            const float u = (ok ? sv[j * NC + e] : 0.f) - ks;
-            if (r == 0 && ok) u_p[static_cast<size_t>(t) * D + col] = u;
-            const float bu = sb[j] * u;
-#pragma unroll
-            for (int i = 0; i < kRpt; ++i) S[i] = fmaf(kr[i], bu, S[i]);
-            if ((t + 1) % kCk == 0 || t + 1 == T) {
-                float* c = ck_p + static_cast<size_t>(t / kCk) * D * D;
-                if (ok) {
-#pragma unroll
-                    for (int i = 0; i < kRpt; ++i) {
-                        const int d = r * kRpt + i;
-                        if (d < D) c[static_cast<size_t>(d) * D + col] = S[i];
-                    }
-                }
+        for (int s = 0; s < NPF; ++s) {
+            const int grp = s * NT + tid;
+            const int j = grp * 4 / DP, d = grp * 4 % DP;
+            float xk[4];
+            pk[s].get(xk, vec);
+            if (grp < NG) {
+                const int pos = j * DPL + (d / RPT) * SL + d % RPT;
+                *reinterpret_cast<float4*>(sk + pos) = make_float4(xk[0], xk[1], xk[2], xk[3]);
             }
         }
+#pragma unroll
+        for (int s = 0; s < NPV; ++s) sv[s * NT + tid] = to_f32(pv[s]);
+        if (tid < KB) sb[tid] = pb;
+    };
+    auto checkpoint = [&](int t) {
+        float* cp = ck_p + static_cast<size_t>(t / kCk) * D * D;
+        if (col_ok) {
+#pragma unroll
+            for (int i = 0; i < RPT; ++i) {
+                const int d = r * RPT + i;
+                if (d < D) cp[static_cast<size_t>(d) * D + e] = S[i];
+            }
+        }
+    };
+    auto tokens = [&](float* buf, int t0, int nst, int len) {
+        const float* sk = buf;
+        const float* sv = sk + KB * DPL;
+        float* su = buf + KB * DPL + KB * CW;
+        const float* sb = su + KB * CW;
+        auto body = [&](int j) {
+            float kk[RPT];
+            const float4* kp = reinterpret_cast<const float4*>(sk + j * DPL + r * SL);
+#pragma unroll
+            for (int i = 0; i < RPT / 4; ++i) {
+                const float4 t = kp[i];
+                kk[4 * i] = t.x, kk[4 * i + 1] = t.y, kk[4 * i + 2] = t.z, kk[4 * i + 3] = t.w;
+            }
+            const float ks = col_sum<RS>(dot4<RPT>(kk, S));
+            const float u = sv[j * CW + el] - ks;
+            su[j * CW + el] = u;  // the RS lanes of a column store the same bits
+            const float bu = sb[j] * u;
+#pragma unroll
+            for (int i = 0; i < RPT; ++i) S[i] = fmaf(kk[i], bu, S[i]);
+            // t0 is a multiple of kCk
+            if ((j + 1) % kCk == 0 || t0 + j + 1 == len) checkpoint(t0 + j);
+        };
+        if (nst == KB) {
+#pragma unroll
+            for (int j = 0; j < KB; ++j) body(j);
+        } else {
+            for (int j = 0; j < nst; ++j) body(j);
+        }
+    };
+    auto store_u = [&](const float* buf, int t0, int nst) {
+        const float* su = buf + KB * DPL + KB * CW;
+#pragma unroll
+        for (int s = 0; s < NPV; ++s) {
+            const int idx = s * NT + tid;
+            const int j = idx / CW, e2 = c * CW + idx % CW;
+            if (j < nst && e2 < D) u_p[static_cast<size_t>(t0 + j) * D + e2] = su[idx];
+        }
+    };
+
+    const int len = T;
+    const int nblk = (len + KB - 1) / KB;
+    if (nblk > 0) prefetch(0, min(KB, len));
+    for (int b = 0; b < nblk; ++b) {
+        float* buf = lds + (b & 1) * BUF;
+        const int t0 = b * KB, nst = min(KB, len - t0);
+        stage(buf);
+        __syncthreads();
+        if (b + 1 < nblk) prefetch(t0 + KB, min(KB, len - t0 - KB));
+        if (b > 0) store_u(lds + ((b - 1) & 1) * BUF, t0 - KB, KB);
+        tokens(buf, t0, nst, len);
     }
+    if (nblk > 0) {
+        __syncthreads();
+        const int t0 = (nblk - 1) * KB;
+        store_u(lds + ((nblk - 1) & 1) * BUF, t0, len - t0);
+    }
+}
+
+template <int RPT, int RS, typename InT>
+static hipError_t launch_ckpt_t(const BwdArgs& a, float* u_ws, float* ck_ws, hipStream_t st) {
+    using G = RecGeo<RPT, RS>;
+    constexpr size_t kBytes = 2 * sizeof(float) * (kRecSteps * G::DPL + 2 * kRecSteps * G::CW + 4 * kRecSteps);
+    auto kern = delta_bwd_ckpt_kernel<RPT, RS, InT>;
+    if (kBytes > 64 * 1024) {
+        // the dynamic-LDS limit is a per-device function attribute
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        static bool attr_set[64] = {};
+        if (dev < 0 || dev >= 64 || !attr_set[dev]) {
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kBytes));
+            if (e != hipSuccess) return e;
+            if (dev >= 0 && dev < 64) attr_set[dev] = true;
+        }
+    }
+    const int ncg = (a.D + G::CW - 1) / G::CW;
+    const size_t vb = sizeof(InT) * 4;
+    const int vec = (a.D % 4 == 0) && reinterpret_cast<uintptr_t>(a.k) % vb == 0;
+    // at most 2^22 workgroups (2^30 work-items) per launch
+    const long per = ((1L << 22) / (8L * ncg)) * 8;
+    for (long p0 = 0; p0 < a.n_pairs; p0 += per) {
+        const long np = a.n_pairs - p0 < per ? a.n_pairs - p0 : per;
+        const dim3 grid(static_cast<unsigned>((np + 7) / 8 * 8 * ncg));
+        hipLaunchKernelGGL(kern, grid, dim3(kRecThreads), kBytes, st, static_cast<const InT*>(a.k),
+                           static_cast<const InT*>(a.v), a.beta, a.s0, u_ws, ck_ws, static_cast<int>(p0),
+                           a.n_pairs, ncg, a.T, a.H, a.D, vec);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// RPT 8 and RS the smallest power of two with 8 RS >= D (D <= 128).
+template <typename InT>
+static hipError_t launch_ckpt(const BwdArgs& a, float* u_ws, float* ck_ws, hipStream_t st) {
+    int rs = 1;
+    while (8 * rs < a.D) rs <<= 1;
+    switch (rs) {
+        case 1: return launch_ckpt_t<8, 1, InT>(a, u_ws, ck_ws, st);
+        case 2: return launch_ckpt_t<8, 2, InT>(a, u_ws, ck_ws, st);
+        case 4: return launch_ckpt_t<8, 4, InT>(a, u_ws, ck_ws, st);
+        case 8: return launch_ckpt_t<8, 8, InT>(a, u_ws, ck_ws, st);
+        default: return launch_ckpt_t<8, 16, InT>(a, u_ws, ck_ws, st);
+    }
+}
+
+// LDS layout of K5b's staged vectors: slice i of kRpt elements starts at i * kSl, so
+// slices are 16-byte aligned and the slices read by one wave start in different banks.
+constexpr int kSl = kRpt + 4;
+__device__ __forceinline__ int spad(int x) { return (x / kRpt) * kSl + x % kRpt; }
+__device__ __forceinline__ void load_slice(const float* p, float (&x)[kRpt]) {
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+#pragma unroll
+    for (int i = 0; i < kRpt / 4; ++i) {
+        const float4 t = p4[i];
+        x[4 * i] = t.x, x[4 * i + 1] = t.y, x[4 * i + 2] = t.z, x[4 * i + 3] = t.w;
+    }
+}
+// Dot product of two register slices, four independent accumulators.
+__device__ __forceinline__ float slice_dot(const float (&a)[kRpt], const float (&b)[kRpt]) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < kRpt; i += 4) {
+        s0 = fmaf(a[i], b[i], s0);
+        s1 = fmaf(a[i + 1], b[i + 1], s1);
+        s2 = fmaf(a[i + 2], b[i + 2], s2);
+        s3 = fmaf(a[i + 3], b[i + 3], s3);
+    }
+    return (s0 + s1) + (s2 + s3);
 }
 
 // ---------------- K5b: reverse pass over one column tile ----------------
@@ -171,13 +328,15 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
     extern __shared__ float lds[];
     const int DP = RSC * kRpt;   // padded rows (column layout)
     const int CP = RSR * kRpt;   // padded tile columns (row layout)
+    const int DPL = RSC * kSl;   // their LDS strides (spad positions)
+    const int CPL = RSR * kSl;
     const int NWV = blockDim.x / 64;
-    float* sk = lds;                    // [kBwdSteps][DP]  k
-    float* sq = sk + kBwdSteps * DP;    // [kBwdSteps][DP]  q
-    float* sg = sq + kBwdSteps * DP;    // [kBwdSteps][CP]  go (tile columns)
-    float* su = sg + kBwdSteps * CP;    // [kBwdSteps][CP]  u (tile columns)
-    float* sw = su + kBwdSteps * CP;    // [2][CP]          w, by token parity
-    float* sb = sw + 2 * CP;            // [kBwdSteps]
+    float* sk = lds;                    // [kBwdSteps][DPL]  k
+    float* sq = sk + kBwdSteps * DPL;   // [kBwdSteps][DPL]  q
+    float* sg = sq + kBwdSteps * DPL;   // [kBwdSteps][CPL]  go (tile columns)
+    float* su = sg + kBwdSteps * CPL;   // [kBwdSteps][CPL]  u (tile columns)
+    float* sw = su + kBwdSteps * CPL;   // [2][CPL]          w, by token parity
+    float* sb = sw + 2 * CPL;           // [kBwdSteps]
     float* sgb = sb + kBwdSteps;        // [kBwdSteps][D] gbeta terms k[d] x[d]
 
     const int tile = blockIdx.x % n_tiles, pair = blockIdx.x / n_tiles, col0 = tile * NC;
@@ -199,7 +358,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
     float* gb_t = gb + tile * part_stride_b;
 
     // w's padding entries (tile columns past NC or D) are read as zeros, never written
-    for (int x = tid; x < 2 * CP; x += blockDim.x) sw[x] = 0.f;
+    for (int x = tid; x < 2 * CPL; x += blockDim.x) sw[x] = 0.f;
 
     float Gc[kRpt], Gr[kRpt], Sr[kRpt];  // G[rc*R+i][col0+e], G[d][col0+rr*R+i], S[d][col0+rr*R+i]
 #pragma unroll
@@ -231,8 +390,8 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                     kv = to_f32(k[a]);
                     qv = to_f32(q[a]);
                 }
-                sk[idx] = kv;
-                sq[idx] = qv;
+                sk[j * DPL + spad(x)] = kv;
+                sq[j * DPL + spad(x)] = qv;
             }
             for (int idx = tid; idx < kBwdSteps * CP; idx += blockDim.x) {
                 const int j = idx / CP, c = idx % CP;
@@ -242,8 +401,8 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                     gv_ = go ? go[a] : 0.f;
                     uv = u_p[static_cast<size_t>(lo + j) * D + col0 + c];
                 }
-                sg[idx] = gv_;
-                su[idx] = uv;
+                sg[j * CPL + spad(c)] = gv_;
+                su[j * CPL + spad(c)] = uv;
             }
             for (int j = tid; j < kBwdSteps; j += blockDim.x)
                 sb[j] = (j < nst) ? beta[static_cast<size_t>(tok0 + lo + j) * H + h] : 0.f;
@@ -252,35 +411,31 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
             for (int j = nst - 1; j >= 0; --j) {
                 const int t = lo + j;
                 const float b = sb[j];
-                const float* kc = sk + j * DP + rc * kRpt;  // k[rc*R + i]      (column layout)
-                const float* qc = sq + j * DP + rc * kRpt;  // q[rc*R + i]
-                const float* gr = sg + j * CP + rr * kRpt;  // go[col0 + rr*R + i] (row layout)
-                const float* ur = su + j * CP + rr * kRpt;  // u[col0 + rr*R + i]
-                const float ge = ok_c ? sg[j * CP + e] : 0.f;  // go[col0 + e]
-                const float kd = ok_r ? sk[j * DP + d] : 0.f;  // k[d]
-                const float qd = ok_r ? sq[j * DP + d] : 0.f;  // q[d]
+                float kc[kRpt], qc[kRpt], gr[kRpt], ur[kRpt];
+                load_slice(sk + j * DPL + rc * kSl, kc);  // k[rc*R + i]      (column layout)
+                load_slice(sq + j * DPL + rc * kSl, qc);  // q[rc*R + i]
+                load_slice(sg + j * CPL + rr * kSl, gr);  // go[col0 + rr*R + i] (row layout)
+                load_slice(su + j * CPL + rr * kSl, ur);  // u[col0 + rr*R + i]
+                const float ge = ok_c ? sg[j * CPL + spad(e)] : 0.f;  // go[col0 + e]
+                const float kd = ok_r ? sk[j * DPL + spad(d)] : 0.f;  // k[d]
+                const float qd = ok_r ? sq[j * DPL + spad(d)] : 0.f;  // q[d]
                 // G += q go^T (both layouts); S_t go over the tile's columns (row layout)
-                float gqp = 0.f;
 #pragma unroll
                 for (int i = 0; i < kRpt; ++i) {
                     Gc[i] = fmaf(qc[i], ge, Gc[i]);
                     Gr[i] = fmaf(qd, gr[i], Gr[i]);
-                    gqp = fmaf(Sr[i], gr[i], gqp);
                 }
+                float gqp = slice_dot(gr, Sr);
                 // w = G^T k (column layout), x = G u over the tile's columns (row layout)
-                float wp = 0.f, xp = 0.f;
-#pragma unroll
-                for (int i = 0; i < kRpt; ++i) {
-                    wp = fmaf(Gc[i], kc[i], wp);
-                    xp = fmaf(Gr[i], ur[i], xp);
-                }
+                float wp = slice_dot(kc, Gc);
+                float xp = slice_dot(ur, Gr);
                 wp = lane_sum(wp, RSC);
                 gqp = lane_sum(gqp, RSR);
                 xp = lane_sum(xp, RSR);
-                float* swp = sw + (t & 1) * CP;
+                float* swp = sw + (t & 1) * CPL;
                 const size_t orow = (static_cast<size_t>(tok0 + t) * H + h) * D;
                 if (rc == 0 && ok_c) {
-                    swp[e] = wp;
+                    swp[spad(e)] = wp;
                     gv[orow + col0 + e] = b * wp;
                 }
                 if (rr == 0 && ok_r) gq_t[orow + d] = gqp;
@@ -289,11 +444,9 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
 #pragma unroll
                 for (int i = 0; i < kRpt; ++i) Sr[i] = fmaf(-bkd, ur[i], Sr[i]);
                 lds_sync();  // w visible to the row layout
-                const float* wr = swp + rr * kRpt;  // w[col0 + rr*R + i]
-                float yp = 0.f;
-#pragma unroll
-                for (int i = 0; i < kRpt; ++i) yp = fmaf(Sr[i], wr[i], yp);
-                yp = lane_sum(yp, RSR);
+                float wr[kRpt];
+                load_slice(swp + rr * kSl, wr);  // w[col0 + rr*R + i]
+                const float yp = lane_sum(slice_dot(wr, Sr), RSR);
                 if (rr == 0 && ok_r) {
                     gk_t[orow + d] = b * (xp - yp);
                     sgb[j * D + d] = kd * xp;  // gbeta = k . x, summed at the block end
@@ -366,20 +519,14 @@ static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
     float* part = ck_ws + static_cast<size_t>(a.n_pairs) * n_ck * a.D * a.D;
     const unsigned grid = static_cast<unsigned>(a.n_pairs) * g.n_tiles;
 
-    // K5a: one thread per (tile column, slice of kRpt rows)
-    const int threads_a = ((g.nc * g.rsc + 63) / 64) * 64;
-    const size_t lds_a = sizeof(float) * (kBwdSteps * g.rsc * kRpt + kBwdSteps * g.nc + kBwdSteps);
-    hipLaunchKernelGGL((delta_bwd_ckpt_kernel<InT>), dim3(grid), dim3(threads_a), lds_a, st,
-                       static_cast<const InT*>(a.k), static_cast<const InT*>(a.v), a.beta, a.s0,
-                       u_ws, ck_ws, a.T, a.H, a.D, g.nc, g.n_tiles, g.rsc);
-    hipError_t err = hipGetLastError();
+    hipError_t err = launch_ckpt<InT>(a, u_ws, ck_ws, st);
     if (err != hipSuccess) return err;
 
     const bool split = g.n_tiles > 1;
     float* gq = split ? part : a.gq;
     float* gk = split ? part + static_cast<size_t>(g.n_tiles) * e : a.gk;
     float* gb = split ? part + static_cast<size_t>(2 * g.n_tiles) * e : a.gbeta;
-    const int dp = g.rsc * kRpt, cp = g.rsr * kRpt;
+    const int dp = g.rsc * kSl, cp = g.rsr * kSl;
     const size_t lds_b = sizeof(float) * (2 * kBwdSteps * dp + 2 * kBwdSteps * cp + 2 * cp +
                                           kBwdSteps + kBwdSteps * a.D);
     hipLaunchKernelGGL((delta_bwd_kernel<InT>), dim3(grid), dim3(g.threads), lds_b, st,

@@ -48,20 +48,6 @@ constexpr int kRpt = 8;       // elements of a row or column slice per thread
 constexpr int kTileCols = 32; // columns per workgroup when D > 32
 static_assert(kCk % kBwdSteps == 0, "checkpoint interval");
 
-// Sum over the RS adjacent lanes (RS a power of two <= 16, aligned to RS inside a
-// 16-lane row) with DPP adds; every lane of the group ends with the same bits.
-template <int CTRL>
-__device__ __forceinline__ float bwd_dpp_add(float x) {
-    const int xi = __float_as_int(x);
-    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, xi, CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float lane_sum(float x, int RS) {
-    if (RS >= 2) x = bwd_dpp_add<0xB1>(x);   // lane ^ 1
-    if (RS >= 4) x = bwd_dpp_add<0x4E>(x);   // lane ^ 2
-    if (RS >= 8) x = bwd_dpp_add<0x141>(x);  // lane 7 - i of each 8
-    if (RS >= 16) x = bwd_dpp_add<0x140>(x); // lane 15 - i
-    return x;
-}
 // Workgroup barrier for LDS traffic only: global stores still in flight are not
 // waited for (no other thread reads them).
 __device__ __forceinline__ void lds_sync() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
@@ -318,13 +304,14 @@ __device__ __forceinline__ float slice_dot(const float (&a)[kRpt], const float (
 // ---------------- K5b: reverse pass over one column tile ----------------
 // gq/gk/gb receive this tile's sums over its columns: the outputs themselves
 // when n_tiles == 1, else this tile's slot of the partial-sum buffers.
-template <typename InT>
+// RSC row slices per column (column layout), RSR column slices per row (row layout).
+template <typename InT, int RSC, int RSR>
 __global__ __launch_bounds__(512) void delta_bwd_kernel(
     const InT* __restrict__ q, const InT* __restrict__ k, const float* __restrict__ beta,
     const float* __restrict__ go, const float* __restrict__ gs, const float* __restrict__ u_ws,
     const float* __restrict__ ck_ws, float* __restrict__ gq, float* __restrict__ gk,
     float* __restrict__ gv, float* __restrict__ gb, float* __restrict__ gs0, int T, int H, int D,
-    int NC, int n_tiles, int RSC, int RSR, size_t part_stride_e, size_t part_stride_b) {
+    int NC, int n_tiles, size_t part_stride_e, size_t part_stride_b) {
     extern __shared__ float lds[];
     const int DP = RSC * kRpt;   // padded rows (column layout)
     const int CP = RSR * kRpt;   // padded tile columns (row layout)
@@ -408,17 +395,21 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 sb[j] = (j < nst) ? beta[static_cast<size_t>(tok0 + lo + j) * H + h] : 0.f;
             __syncthreads();
 
-            for (int j = nst - 1; j >= 0; --j) {
-                const int t = lo + j;
-                const float b = sb[j];
-                float kc[kRpt], qc[kRpt], gr[kRpt], ur[kRpt];
+            // a token's operands; the next token's are loaded while this one finishes
+            float b, ge, kd, qd, kc[kRpt], qc[kRpt], gr[kRpt], ur[kRpt];
+            auto load_tok = [&](int j) {
+                b = sb[j];
                 load_slice(sk + j * DPL + rc * kSl, kc);  // k[rc*R + i]      (column layout)
                 load_slice(sq + j * DPL + rc * kSl, qc);  // q[rc*R + i]
                 load_slice(sg + j * CPL + rr * kSl, gr);  // go[col0 + rr*R + i] (row layout)
                 load_slice(su + j * CPL + rr * kSl, ur);  // u[col0 + rr*R + i]
-                const float ge = ok_c ? sg[j * CPL + spad(e)] : 0.f;  // go[col0 + e]
-                const float kd = ok_r ? sk[j * DPL + spad(d)] : 0.f;  // k[d]
-                const float qd = ok_r ? sq[j * DPL + spad(d)] : 0.f;  // q[d]
+                ge = ok_c ? sg[j * CPL + spad(e)] : 0.f;  // go[col0 + e]
+                kd = ok_r ? sk[j * DPL + spad(d)] : 0.f;  // k[d]
+                qd = ok_r ? sq[j * DPL + spad(d)] : 0.f;  // q[d]
+            };
+            if (nst > 0) load_tok(nst - 1);
+            for (int j = nst - 1; j >= 0; --j) {
+                const int t = lo + j;
                 // G += q go^T (both layouts); S_t go over the tile's columns (row layout)
 #pragma unroll
                 for (int i = 0; i < kRpt; ++i) {
@@ -429,9 +420,9 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 // w = G^T k (column layout), x = G u over the tile's columns (row layout)
                 float wp = slice_dot(kc, Gc);
                 float xp = slice_dot(ur, Gr);
-                wp = lane_sum(wp, RSC);
-                gqp = lane_sum(gqp, RSR);
-                xp = lane_sum(xp, RSR);
+                wp = col_sum<RSC>(wp);
+                gqp = col_sum<RSR>(gqp);
+                xp = col_sum<RSR>(xp);
                 float* swp = sw + (t & 1) * CPL;
                 const size_t orow = (static_cast<size_t>(tok0 + t) * H + h) * D;
                 if (rc == 0 && ok_c) {
@@ -443,18 +434,24 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 const float bkd = b * kd;
 #pragma unroll
                 for (int i = 0; i < kRpt; ++i) Sr[i] = fmaf(-bkd, ur[i], Sr[i]);
+                // what the rest of this token needs from its operands
+                const float bt = b, kdt = kd;
+                float bk[kRpt];
+#pragma unroll
+                for (int i = 0; i < kRpt; ++i) bk[i] = -b * kc[i];
                 lds_sync();  // w visible to the row layout
                 float wr[kRpt];
                 load_slice(swp + rr * kSl, wr);  // w[col0 + rr*R + i]
-                const float yp = lane_sum(slice_dot(wr, Sr), RSR);
+                if (j > 0) load_tok(j - 1);
+                const float yp = col_sum<RSR>(slice_dot(wr, Sr));
                 if (rr == 0 && ok_r) {
-                    gk_t[orow + d] = b * (xp - yp);
-                    sgb[j * D + d] = kd * xp;  // gbeta = k . x, summed at the block end
+                    gk_t[orow + d] = bt * (xp - yp);
+                    sgb[j * D + d] = kdt * xp;  // gbeta = k . x, summed at the block end
                 }
                 // G -= b k w^T (both layouts)
 #pragma unroll
                 for (int i = 0; i < kRpt; ++i) {
-                    Gc[i] = fmaf(-b * kc[i], wp, Gc[i]);
+                    Gc[i] = fmaf(bk[i], wp, Gc[i]);
                     Gr[i] = fmaf(-bkd, wr[i], Gr[i]);
                 }
             }
@@ -529,10 +526,19 @@ static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
     const int dp = g.rsc * kSl, cp = g.rsr * kSl;
     const size_t lds_b = sizeof(float) * (2 * kBwdSteps * dp + 2 * kBwdSteps * cp + 2 * cp +
                                           kBwdSteps + kBwdSteps * a.D);
-    hipLaunchKernelGGL((delta_bwd_kernel<InT>), dim3(grid), dim3(g.threads), lds_b, st,
-                       static_cast<const InT*>(a.q), static_cast<const InT*>(a.k), a.beta, a.go,
-                       a.gs, u_ws, ck_ws, gq, gk, a.gv, gb, a.gs0, a.T, a.H, a.D, g.nc, g.n_tiles,
-                       g.rsc, g.rsr, split ? e : 0, split ? bt : 0);
+    // with kRpt 8 and tiles of min(D, 32) columns, RSR = min(RSC, 4) for every D <= 128
+    if (g.rsr != (g.rsc < 4 ? g.rsc : 4) || g.rsc > 16) return hipErrorInvalidValue;
+    auto kern = delta_bwd_kernel<InT, 16, 4>;
+    switch (g.rsc) {
+        case 1: kern = delta_bwd_kernel<InT, 1, 1>; break;
+        case 2: kern = delta_bwd_kernel<InT, 2, 2>; break;
+        case 4: kern = delta_bwd_kernel<InT, 4, 4>; break;
+        case 8: kern = delta_bwd_kernel<InT, 8, 4>; break;
+        default: break;
+    }
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(g.threads), lds_b, st, static_cast<const InT*>(a.q),
+                       static_cast<const InT*>(a.k), a.beta, a.go, a.gs, u_ws, ck_ws, gq, gk, a.gv, gb,
+                       a.gs0, a.T, a.H, a.D, g.nc, g.n_tiles, split ? e : 0, split ? bt : 0);
     err = hipGetLastError();
     if (err != hipSuccess || !split) return err;
     if ((err = launch_reduce(a.gq, gq, e, e, g.n_tiles, st)) != hipSuccess) return err;

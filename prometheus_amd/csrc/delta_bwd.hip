@@ -46,7 +46,7 @@ constexpr int kBwdSteps = 8;  // tokens staged in LDS at a time
 constexpr int kCk = 8;        // tokens between state checkpoints (multiple of kBwdSteps)
 constexpr int kRpt = 8;       // elements of a row or column slice per thread
 constexpr int kTileCols = 32; // columns per workgroup when D > 32
-static_assert(kCk % kBwdSteps == 0, "checkpoint interval");
+static_assert(kCk == kBwdSteps, "the reverse pass stages one checkpoint block at a time");
 
 // Workgroup barrier for LDS traffic only: global stores still in flight are not
 // waited for (no other thread reads them).
@@ -313,18 +313,21 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
     float* __restrict__ gv, float* __restrict__ gb, float* __restrict__ gs0, int T, int H, int D,
     int NC, int n_tiles, size_t part_stride_e, size_t part_stride_b) {
     extern __shared__ float lds[];
-    const int DP = RSC * kRpt;   // padded rows (column layout)
-    const int CP = RSR * kRpt;   // padded tile columns (row layout)
-    const int DPL = RSC * kSl;   // their LDS strides (spad positions)
-    const int CPL = RSR * kSl;
-    const int NWV = blockDim.x / 64;
-    float* sk = lds;                    // [kBwdSteps][DPL]  k
-    float* sq = sk + kBwdSteps * DPL;   // [kBwdSteps][DPL]  q
-    float* sg = sq + kBwdSteps * DPL;   // [kBwdSteps][CPL]  go (tile columns)
-    float* su = sg + kBwdSteps * CPL;   // [kBwdSteps][CPL]  u (tile columns)
-    float* sw = su + kBwdSteps * CPL;   // [2][CPL]          w, by token parity
-    float* sb = sw + 2 * CPL;           // [kBwdSteps]
-    float* sgb = sb + kBwdSteps;        // [kBwdSteps][D] gbeta terms k[d] x[d]
+    constexpr int DP = RSC * kRpt;   // padded rows (column layout)
+    constexpr int CP = RSR * kRpt;   // padded tile columns (row layout)
+    constexpr int DPL = RSC * kSl;   // their LDS strides (spad positions)
+    constexpr int CPL = RSR * kSl;
+    constexpr int KB = kBwdSteps;
+    // per-thread staging slots, for the fewest threads a launch of this geometry has
+    constexpr int NTMIN = 32 * RSC < 64 ? 64 : 32 * RSC;
+    constexpr int MK = (KB * DP + NTMIN - 1) / NTMIN, MG = (KB * CP + NTMIN - 1) / NTMIN;
+    constexpr int SB = 2 * KB * DPL + 2 * KB * CPL + KB;  // one staging buffer
+    const int NT = blockDim.x, NWV = NT / 64;
+    // outputs of a block, written out one block later: by block parity,
+    // [KB][D] gbeta terms k[d] x[d], [KB][D] gq, [KB][D] gk, [KB][NC] gv
+    const int OB = 3 * KB * D + KB * NC;
+    float* sw = lds + 2 * SB;           // [2][CPL]       w, by token parity
+    float* so0 = sw + 2 * CPL;          // [2][OB]
 
     const int tile = blockIdx.x % n_tiles, pair = blockIdx.x / n_tiles, col0 = tile * NC;
     const int seq = pair / H, h = pair % H;
@@ -345,7 +348,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
     float* gb_t = gb + tile * part_stride_b;
 
     // w's padding entries (tile columns past NC or D) are read as zeros, never written
-    for (int x = tid; x < 2 * CPL; x += blockDim.x) sw[x] = 0.f;
+    for (int x = tid; x < 2 * CPL; x += NT) sw[x] = 0.f;
 
     float Gc[kRpt], Gr[kRpt], Sr[kRpt];  // G[rc*R+i][col0+e], G[d][col0+rr*R+i], S[d][col0+rr*R+i]
 #pragma unroll
@@ -356,45 +359,108 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                     ? gs[sbase + static_cast<size_t>(d) * D + col0 + c] : 0.f;
     }
 
-    for (int blk = n_ck - 1; blk >= 0; --blk) {
-        const int t_lo = blk * kCk, t_hi = min(T, t_lo + kCk);
-        {
-            const float* cp = ck_p + static_cast<size_t>(blk) * D * D;
+    // ---- one checkpoint block's inputs, loaded a block ahead into registers ----
+    InT pk[MK], pq[MK];
+    float pg[MG], pu[MG], ps[kRpt], pb = 0.f;
+    auto prefetch = [&](int blk) {
+        const int lo = blk * kCk, nst = min(T, lo + kCk) - lo;
 #pragma unroll
-            for (int i = 0; i < kRpt; ++i) {
-                const int c = rr * kRpt + i;
-                Sr[i] = (ok_r && c < NC && col0 + c < D) ? cp[static_cast<size_t>(d) * D + col0 + c] : 0.f;
+        for (int s = 0; s < MK; ++s) {
+            const int idx = s * NT + tid;
+            const int j = idx / DP, x = idx % DP;
+            const bool ok = idx < KB * DP && j < nst && x < D;
+            const size_t a = ok ? (static_cast<size_t>(tok0 + lo + j) * H + h) * D + x : 0;
+            pk[s] = ok ? k[a] : InT(0);
+            pq[s] = ok ? q[a] : InT(0);
+        }
+#pragma unroll
+        for (int s = 0; s < MG; ++s) {
+            const int idx = s * NT + tid;
+            const int j = idx / CP, c = idx % CP;
+            const bool ok = idx < KB * CP && j < nst && c < NC && col0 + c < D;
+            pg[s] = (ok && go) ? go[(static_cast<size_t>(tok0 + lo + j) * H + h) * D + col0 + c] : 0.f;
+            pu[s] = ok ? u_p[static_cast<size_t>(lo + j) * D + col0 + c] : 0.f;
+        }
+        if (tid < KB) pb = tid < nst ? beta[static_cast<size_t>(tok0 + lo + tid) * H + h] : 0.f;
+        const float* cp = ck_p + static_cast<size_t>(blk) * D * D;
+#pragma unroll
+        for (int i = 0; i < kRpt; ++i) {
+            const int c = rr * kRpt + i;
+            ps[i] = (ok_r && c < NC && col0 + c < D) ? cp[static_cast<size_t>(d) * D + col0 + c] : 0.f;
+        }
+    };
+    auto stage = [&](float* buf) {
+        float* sk = buf;
+        float* sq = sk + KB * DPL;
+        float* sg = sq + KB * DPL;
+        float* su = sg + KB * CPL;
+        float* sb = su + KB * CPL;
+#pragma unroll
+        for (int s = 0; s < MK; ++s) {
+            const int idx = s * NT + tid;
+            if (idx < KB * DP) {
+                const int pos = (idx / DP) * DPL + spad(idx % DP);
+                sk[pos] = to_f32(pk[s]);
+                sq[pos] = to_f32(pq[s]);
             }
         }
-        for (int hi = t_hi; hi > t_lo; hi -= kBwdSteps) {
-            const int lo = max(t_lo, hi - kBwdSteps), nst = hi - lo;
-            __syncthreads();
-            for (int idx = tid; idx < kBwdSteps * DP; idx += blockDim.x) {
-                const int j = idx / DP, x = idx % DP;
-                float kv = 0.f, qv = 0.f;
-                if (j < nst && x < D) {
-                    const size_t a = (static_cast<size_t>(tok0 + lo + j) * H + h) * D + x;
-                    kv = to_f32(k[a]);
-                    qv = to_f32(q[a]);
-                }
-                sk[j * DPL + spad(x)] = kv;
-                sq[j * DPL + spad(x)] = qv;
+#pragma unroll
+        for (int s = 0; s < MG; ++s) {
+            const int idx = s * NT + tid;
+            if (idx < KB * CP) {
+                const int pos = (idx / CP) * CPL + spad(idx % CP);
+                sg[pos] = pg[s];
+                su[pos] = pu[s];
             }
-            for (int idx = tid; idx < kBwdSteps * CP; idx += blockDim.x) {
-                const int j = idx / CP, c = idx % CP;
-                float gv_ = 0.f, uv = 0.f;
-                if (j < nst && c < NC && col0 + c < D) {
-                    const size_t a = (static_cast<size_t>(tok0 + lo + j) * H + h) * D + col0 + c;
-                    gv_ = go ? go[a] : 0.f;
-                    uv = u_p[static_cast<size_t>(lo + j) * D + col0 + c];
-                }
-                sg[j * CPL + spad(c)] = gv_;
-                su[j * CPL + spad(c)] = uv;
-            }
-            for (int j = tid; j < kBwdSteps; j += blockDim.x)
-                sb[j] = (j < nst) ? beta[static_cast<size_t>(tok0 + lo + j) * H + h] : 0.f;
-            __syncthreads();
+        }
+        if (tid < KB) sb[tid] = pb;
+#pragma unroll
+        for (int i = 0; i < kRpt; ++i) Sr[i] = ps[i];
+    };
+    // a block's outputs: gq, gk and gv rows, and gbeta (one wave per token)
+    auto flush_out = [&](const float* so, int lo, int nst) {
+        const float* soq = so + KB * D;
+        const float* sok = soq + KB * D;
+        const float* sov = sok + KB * D;
+        for (int idx = tid; idx < nst * D; idx += NT) {
+            const int j = idx / D, x = idx % D;
+            const size_t a = (static_cast<size_t>(tok0 + lo + j) * H + h) * D + x;
+            gq_t[a] = soq[idx];
+            gk_t[a] = sok[idx];
+        }
+        for (int idx = tid; idx < nst * NC; idx += NT) {
+            const int j = idx / NC, c = idx % NC;
+            if (col0 + c < D) gv[(static_cast<size_t>(tok0 + lo + j) * H + h) * D + col0 + c] = sov[idx];
+        }
+        for (int j = wave; j < nst; j += NWV) {
+            float sum = 0.f;
+            for (int x = lane; x < D; x += 64) sum += so[j * D + x];
+            for (int m = 1; m < 64; m <<= 1) sum += __shfl_xor(sum, m);
+            if (lane == 0) gb_t[static_cast<size_t>(tok0 + lo + j) * H + h] = sum;
+        }
+    };
 
+    if (n_ck > 0) prefetch(n_ck - 1);
+    for (int blk = n_ck - 1, it = 0; blk >= 0; --blk, ++it) {
+        float* buf = lds + (it & 1) * SB;
+        const int lo = blk * kCk, nst = min(T, lo + kCk) - lo;
+        // buf was last read by the token loop two blocks back, before the previous barrier
+        stage(buf);
+        __syncthreads();
+        // the previous block's stores go out before this block's loads, so that waiting
+        // for the loads never waits for stores issued after them
+        if (it > 0) flush_out(so0 + ((it - 1) & 1) * OB, lo + kCk, min(T, lo + 2 * kCk) - lo - kCk);
+        if (blk > 0) prefetch(blk - 1);
+        const float* sk = buf;
+        const float* sq = sk + KB * DPL;
+        const float* sg = sq + KB * DPL;
+        const float* su = sg + KB * CPL;
+        const float* sb = su + KB * CPL;
+        float* sgb = so0 + (it & 1) * OB;  // gbeta terms, then gq, gk, gv
+        float* soq = sgb + KB * D;
+        float* sok = soq + KB * D;
+        float* sov = sok + KB * D;
+        {
             // a token's operands; the next token's are loaded while this one finishes
             float b, ge, kd, qd, kc[kRpt], qc[kRpt], gr[kRpt], ur[kRpt];
             auto load_tok = [&](int j) {
@@ -424,12 +490,11 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 gqp = col_sum<RSR>(gqp);
                 xp = col_sum<RSR>(xp);
                 float* swp = sw + (t & 1) * CPL;
-                const size_t orow = (static_cast<size_t>(tok0 + t) * H + h) * D;
                 if (rc == 0 && ok_c) {
                     swp[spad(e)] = wp;
-                    gv[orow + col0 + e] = b * wp;
+                    sov[j * NC + e] = b * wp;
                 }
-                if (rr == 0 && ok_r) gq_t[orow + d] = gqp;
+                if (rr == 0 && ok_r) soq[j * D + d] = gqp;
                 // S_{t-1} = S_t - b k u^T (row layout)
                 const float bkd = b * kd;
 #pragma unroll
@@ -445,8 +510,8 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 if (j > 0) load_tok(j - 1);
                 const float yp = col_sum<RSR>(slice_dot(wr, Sr));
                 if (rr == 0 && ok_r) {
-                    gk_t[orow + d] = bt * (xp - yp);
-                    sgb[j * D + d] = kdt * xp;  // gbeta = k . x, summed at the block end
+                    sok[j * D + d] = bt * (xp - yp);
+                    sgb[j * D + d] = kdt * xp;  // gbeta = k . x, summed when written out
                 }
                 // G -= b k w^T (both layouts)
 #pragma unroll
@@ -455,15 +520,11 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                     Gr[i] = fmaf(-bkd, wr[i], Gr[i]);
                 }
             }
-            __syncthreads();
-            // gbeta of the block's tokens: one wave per token
-            for (int j = wave; j < nst; j += NWV) {
-                float sum = 0.f;
-                for (int x = lane; x < D; x += 64) sum += sgb[j * D + x];
-                for (int m = 1; m < 64; m <<= 1) sum += __shfl_xor(sum, m);
-                if (lane == 0) gb_t[static_cast<size_t>(tok0 + lo + j) * H + h] = sum;
-            }
         }
+    }
+    if (n_ck > 0) {
+        __syncthreads();
+        flush_out(so0 + ((n_ck - 1) & 1) * OB, 0, min(T, kCk));
     }
     if (ok_c) {
 #pragma unroll
@@ -524,8 +585,8 @@ static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
     float* gk = split ? part + static_cast<size_t>(g.n_tiles) * e : a.gk;
     float* gb = split ? part + static_cast<size_t>(2 * g.n_tiles) * e : a.gbeta;
     const int dp = g.rsc * kSl, cp = g.rsr * kSl;
-    const size_t lds_b = sizeof(float) * (2 * kBwdSteps * dp + 2 * kBwdSteps * cp + 2 * cp +
-                                          kBwdSteps + kBwdSteps * a.D);
+    const size_t lds_b = sizeof(float) * (2 * (2 * kBwdSteps * dp + 2 * kBwdSteps * cp + kBwdSteps) +
+                                          2 * cp + 2 * (3 * kBwdSteps * a.D + kBwdSteps * g.nc));
     // with kRpt 8 and tiles of min(D, 32) columns, RSR = min(RSC, 4) for every D <= 128
     if (g.rsr != (g.rsc < 4 ? g.rsc : 4) || g.rsc > 16) return hipErrorInvalidValue;
     auto kern = delta_bwd_kernel<InT, 16, 4>;

@@ -449,7 +449,35 @@ def main():
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": bb / (bwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
         }
-        del go, gs, gq, gk, gv, gb, gs0, ws
+        del ws
+        # the same backward with fp32 q/k/v (the reference's dtype): the per-token kernels
+        q, k, v = (x.float() for x in (q, k, v))
+        ws_bytes = lib.pm_delta_bwd_workspace_bytes(B, T, H, D, _native.DTYPE_F32)
+        ws = torch.empty(((ws_bytes + 3) // 4,), device=dev)
+
+        def bwd32():
+            rc = lib.pm_delta_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), None,
+                                  go.data_ptr(), gs.data_ptr(), gq.data_ptr(), gk.data_ptr(),
+                                  gv.data_ptr(), gb.data_ptr(), gs0.data_ptr(), B, T, H, D,
+                                  _native.DTYPE_F32, ws.data_ptr(), ws_bytes, stream.cuda_stream)
+            _native.check(rc)
+
+        bwd32()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.bwd_steps):
+            bwd32()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        b32_ms = e0.elapsed_time(e1) / args.bwd_steps
+        backward["fp32"] = {
+            "workload": "cfg1 backward with fp32 q/k/v (per-token fp32 kernels)",
+            "calls": args.bwd_steps,
+            "ms_per_call": b32_ms,
+            "tokens_per_s": tokens / (b32_ms * 1e-3),
+            "workspace_bytes": ws_bytes,
+        }
+        del go, gs, gq, gk, gv, gb, gs0, ws, q, k, v
 
     if args.calib_copy:
         n = CALIB_COPY_BYTES // 4

@@ -497,6 +497,19 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
     float* db2 = db1 + 4 * kC;                             // [wave][t]: sum_s dA (k_t . k_s)
 
     {
+        // dO (fp32) first, into registers: its loads are in flight with the copies below,
+        // and waiting for them never waits for a copy issued after them
+        // (buffer loads: rows past the chunk's end, and a NULL go, read as zeros)
+        constexpr int NDO = kC * D / 4 / 256;
+        const __amdgpu_buffer_rsrc_t rgo =
+            make_rsrc(go ? go + row0 : nullptr, go ? static_cast<unsigned>(((clen - 1) * tstride + D) * 4) : 0u);
+        f32x4_t xdo[NDO];
+#pragma unroll
+        for (int i = 0; i < NDO; ++i) {
+            const int e = tid + 256 * i, t = e / (D / 4), d = 4 * (e % (D / 4));
+            xdo[i] = __builtin_bit_cast(
+                f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rgo, static_cast<unsigned>((t * tstride + d) * 4), 0, 0));
+        }
         const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
         const unsigned rb = static_cast<unsigned>(tstride * 2);
         copy_rows<D>(make_rsrc(k + row0, n_kq), smem + G::KS, kC * D * 2 / 1024, rb, w, 4, lane);
@@ -509,12 +522,11 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         if (w == 3)
             copy_to_lds(make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4)),
                         smem + G::BS, 4, static_cast<unsigned>(lane * H * 4));
-        // dO (fp32) -> bf16 token rows
-        for (int e = tid; e < kC * D / 4; e += 256) {
-            const int t = e / (D / 4), d = 4 * (e % (D / 4));
-            f32x4_t x = {0.f, 0.f, 0.f, 0.f};
-            if (go && t < clen) x = *reinterpret_cast<const f32x4_t*>(go + row0 + t * tstride + d);
-            *reinterpret_cast<u32x2_t*>(DOs + swz<D>(t, d)) = cvt4(x);
+        // dO -> bf16 token rows
+#pragma unroll
+        for (int i = 0; i < NDO; ++i) {
+            const int e = tid + 256 * i, t = e / (D / 4), d = 4 * (e % (D / 4));
+            *reinterpret_cast<u32x2_t*>(DOs + swz<D>(t, d)) = cvt4(xdo[i]);
         }
         wait_copies();
         __syncthreads();

@@ -110,8 +110,9 @@ def test_finite_differences_of_the_gpu_forward():
         np.testing.assert_allclose(fd, float(np.sum(gx * d)), rtol=1e-3, atol=1e-3, err_msg=name)
 
 
-@pytest.mark.parametrize("shape", [(1, 1, 1, 8), (2, 63, 2, 16), (1, 65, 2, 48), (1, 200, 2, 64),
-                                   (2, 130, 1, 128), (1, 17, 2, 33), (1, 20, 1, 100)])
+@pytest.mark.parametrize("shape", [(1, 1, 1, 8), (2, 63, 2, 16), (1, 41, 2, 24), (2, 9, 3, 32),
+                                   (1, 65, 2, 48), (1, 200, 2, 64), (2, 130, 1, 128), (1, 17, 2, 33),
+                                   (1, 20, 1, 100)])
 @pytest.mark.parametrize("state", [True, False])
 def test_shapes_across_checkpoint_blocks(shape, state):
     x = synth.fwd_inputs(shape, seed=sum(shape) + state, dtype="fp32",

@@ -117,6 +117,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_cfg1.json"),
                     help="JSON with measured HBM bytes per launch (from rocprofv3 --pmc)")
+    ap.add_argument("--mfma-counters", default=os.path.join(ROOT, "profiles", "mfma_cfg1.json"),
+                    help="JSON with rocprofv3 MfmaUtil / MfmaFlopsBF16 for the forward kernel")
     ap.add_argument("--tile", type=int, default=0, help="d_v tile of the chunked kernel (0 auto)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run 3 launches of a plain 1 GiB fp32 elementwise copy (torch.neg, "
@@ -184,6 +186,15 @@ def main():
     if os.path.exists(args.traffic):
         with open(args.traffic) as f:
             traffic = json.load(f).get("bytes_per_launch")
+    # MFMA counters of the same kernel and workload, from a rocprofv3 --pmc run (the file
+    # records the command): busy fraction of the MFMA pipes and executed bf16 MFMA flops
+    mfma_counters = None
+    if os.path.exists(args.mfma_counters):
+        with open(args.mfma_counters) as f:
+            mc = json.load(f)
+        mfma_counters = {"mfma_util_pct": mc.get("mfma_util_pct"),
+                         "executed_bf16_mfma_flop": mc.get("executed_bf16_mfma_flop"),
+                         "executed_over_algorithmic": mc.get("executed_over_algorithmic")}
 
     # parity of the timed output against the C restatement (which is also the CPU baseline)
     cpu = None
@@ -508,7 +519,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic},
         "mfma": {"achieved_tflops": tflops, "peak_tflops": BF16_PEAK_TFLOPS,
-                 "frac": tflops / BF16_PEAK_TFLOPS, "algorithmic_gflop": flops / 1e9},
+                 "frac": tflops / BF16_PEAK_TFLOPS, "algorithmic_gflop": flops / 1e9,
+                 "counters": mfma_counters},
         "attainable_roofline_frac": max(flops / (BF16_PEAK_TFLOPS * 1e12),
                                         nbytes / (HBM_PEAK_GBS * 1e9)) / (kern_ms * 1e-3),
         "kernel_us": kern_ms * 1e3,

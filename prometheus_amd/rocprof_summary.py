@@ -3,6 +3,8 @@
     python -m prometheus_amd.rocprof_summary stats DIR --cmd "..." [--bench-log LOG] -o OUT.md
     python -m prometheus_amd.rocprof_summary traffic FETCH_DIR WRITE_DIR --kernel NAME
         --cmd-fetch "..." --cmd-write "..." -o OUT.json
+    python -m prometheus_amd.rocprof_summary mfma DIR --kernel NAME --cmd "..."
+        [--algorithmic-flop F] -o OUT.json
 
 ``stats`` turns ``*_kernel_stats.csv`` (from ``--kernel-trace --stats``) into a
 short markdown table.  ``traffic`` reads two ``--pmc`` runs (``FETCH_SIZE``,
@@ -10,6 +12,10 @@ then ``WRITE_SIZE``; both in KiB per dispatch) of a command that also ran
 ``bench.py --calib-copy`` (a plain elementwise fp32 copy of a known 1 GiB), and
 scales the kernel's per-dispatch counters by ``known bytes / counted bytes``
 of that copy, giving the HBM bytes one launch of the kernel moves.
+``mfma`` reads one ``--pmc MfmaUtil MfmaFlopsBF16`` run (rocprofv3's derived
+counters: MFMA busy cycles over GUI-active cycles times SIMDs, and
+``SQ_INSTS_VALU_MFMA_MOPS_BF16 * 512``) and records their per-dispatch mean
+for the kernel, beside its algorithmic flops.
 """
 
 from __future__ import annotations
@@ -59,9 +65,22 @@ def stats(args) -> None:
         for ln in open(args.bench_log):
             if ln.startswith("{"):
                 d = json.loads(ln)
+                extra = ""
+                for key, label in (("fp32_forward", "fp32 forward"), ("gated", "gated forward")):
+                    if d.get(key):
+                        extra += f"; {label} = {d[key]['ms_per_call']:.3f} ms"
+                if d.get("model_linear_attention"):
+                    m = d["model_linear_attention"]
+                    extra += (f"; model linear attention bf16 / fp32 = {m['bf16']['ms_per_call']:.3f} / "
+                              f"{m['fp32']['ms_per_call']:.3f} ms")
+                if d.get("backward"):
+                    b = d["backward"]
+                    extra += f"; backward bf16 = {b['ms_per_call']:.3f} ms"
+                    if b.get("fp32"):
+                        extra += f", fp32 = {b['fp32']['ms_per_call']:.3f} ms"
                 out += [f"bench.py line from the same run: kernel_us (HIP events, mean per launch) = "
                         f"{d['kernel_us']:.1f}; decode us_per_step = "
-                        f"{d['decode']['us_per_step']:.1f}; value = {d['value']:.4g} {d['unit']}", ""]
+                        f"{d['decode']['us_per_step']:.1f}; value = {d['value']:.4g} {d['unit']}{extra}", ""]
     out += ["| kernel | calls | avg us | min us | max us | total % |",
             "|---|---:|---:|---:|---:|---:|"]
     for r in rows[: args.top]:
@@ -135,6 +154,29 @@ def traffic(args) -> None:
     print(json.dumps(res, indent=1))
 
 
+def mfma(args) -> None:
+    kname, util = _pick(_per_dispatch(args.dir, "MfmaUtil"), args.kernel)
+    _, flop = _pick(_per_dispatch(args.dir, "MfmaFlopsBF16"), args.kernel)
+    res = {
+        "kernel": kname,
+        "dispatches": len(util),
+        "mfma_util_pct": statistics.mean(util),
+        "mfma_util_pct_per_dispatch": util,
+        "executed_bf16_mfma_flop": statistics.mean(flop),
+        "algorithmic_flop": args.algorithmic_flop,
+        "counters": {
+            "MfmaUtil": "reduce(SQ_VALU_MFMA_BUSY_CYCLES,sum)/(reduce(GRBM_GUI_ACTIVE,max)*SIMD_NUM)*100",
+            "MfmaFlopsBF16": "SQ_INSTS_VALU_MFMA_MOPS_BF16*512"},
+        "command": args.cmd,
+    }
+    if args.algorithmic_flop:
+        res["executed_over_algorithmic"] = res["executed_bf16_mfma_flop"] / args.algorithmic_flop
+    with open(args.out, "w") as f:
+        json.dump(res, f, indent=1)
+        f.write("\n")
+    print(json.dumps(res, indent=1))
+
+
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd_name", required=True)
@@ -152,8 +194,14 @@ def main(argv=None) -> None:
     t.add_argument("--cmd-write", required=True)
     t.add_argument("--algorithmic-bytes", type=float, default=None)
     t.add_argument("-o", "--out", required=True)
+    m = sub.add_parser("mfma")
+    m.add_argument("dir")
+    m.add_argument("--kernel", required=True)
+    m.add_argument("--cmd", required=True)
+    m.add_argument("--algorithmic-flop", type=float, default=None)
+    m.add_argument("-o", "--out", required=True)
     args = ap.parse_args(argv)
-    (stats if args.cmd_name == "stats" else traffic)(args)
+    {"stats": stats, "traffic": traffic, "mfma": mfma}[args.cmd_name](args)
 
 
 if __name__ == "__main__":

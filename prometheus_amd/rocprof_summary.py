@@ -78,7 +78,7 @@ def stats(args) -> None:
                     extra += f"; backward bf16 = {b['ms_per_call']:.3f} ms"
                     if b.get("fp32"):
                         extra += f", fp32 = {b['fp32']['ms_per_call']:.3f} ms"
-                out += [f"bench.py line from the same run: kernel_us (HIP events, mean per launch) = "
+                out += [f"bench.py line from the same run: kernel_us (HIP events over the timed launches, per launch) = "
                         f"{d['kernel_us']:.1f}; decode us_per_step = "
                         f"{d['decode']['us_per_step']:.1f}; value = {d['value']:.4g} {d['unit']}{extra}", ""]
     out += ["| kernel | calls | avg us | min us | max us | total % |",

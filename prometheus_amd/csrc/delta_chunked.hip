@@ -80,6 +80,9 @@ struct Geo {
     // chain after the TP buffers (NORM: 1/||k_t||, 1/||q_t||; GATED: e^(G_t), e^(G_C - G_t))
     static constexpr int RN = BYTES;
     static constexpr int BYTES_NORM = BYTES + 2 * 512;
+    // GATED: one 64-float scratch per producer for the scanned gates, after RN
+    static constexpr int GS = BYTES_NORM;
+    static constexpr int BYTES_GATED = BYTES_NORM + 2 * 256;
     static_assert(D == 64 || D == 128, "D");
     static_assert(DV == 16 || DV == 32, "DV");
     static_assert(NI_V >= 1 && RAW % 16 == 0, "RAW layout");
@@ -159,6 +162,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         return reinterpret_cast<uint16_t*>(smem + G::NRAW * G::RAW + (c & 1) * G::TP);
     };
     auto rnb = [&](int c) { return reinterpret_cast<float*>(smem + G::RN + (c & 1) * 512); };
+    // GATED: producer pw's scanned gates, written and read back by that wave only
+    auto gsb = [&](int p) { return reinterpret_cast<float*>(smem + G::GS + p * 256); };
 
     // ---------------- loader: chunk c's K, Q, V tile and beta, HBM -> LDS ----------------
     // Copy instruction i, lane L fills LDS bytes [1024 i + 16 L, +16) of the tile: row r,
@@ -206,6 +211,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             if (lane >= off) x += y;
         }
         return x;
+    };
+    // GATED: the scanned gates of token 16b + l16 (col) and of tokens 16b + 4lg + [0, 4)
+    // (row), through this producer's LDS scratch (one write, eight reads; a wave's LDS
+    // operations complete in order, so no wait or barrier is needed)
+    auto gate_bcast = [&](float gsc, float (&col)[4], f32x4_t (&row)[4]) {
+        float* sg = gsb(pw);
+        sg[lane] = gsc;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            col[b] = sg[16 * b + l16];
+            row[b] = *reinterpret_cast<const f32x4_t*>(sg + 16 * b + 4 * lg);
+        }
     };
 
     // ---------------- producer 0: T = (I + A)^-1 in packed operand order ----------------
@@ -270,15 +287,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         f32x4_t grow[4];
         if constexpr (GATED) {
             const float gsc = gate_scan(rb);
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                gcol[b] = __shfl(gsc, 16 * b + l16);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) grow[b][r] = __shfl(gsc, 16 * b + 4 * lg + r);
-            }
+            gate_bcast(gsc, gcol, grow);
             float* gh = rnb(c);
             gh[lane] = exp2_hw(gsc);
-            gh[kC + lane] = exp2_hw(__shfl(gsc, kC - 1) - gsc);
+            const float gC = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gsc), kC - 1));
+            gh[kC + lane] = exp2_hw(gC - gsc);
         }
         f32x4_t eye;
 #pragma unroll
@@ -286,6 +299,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // diagonal inverses D_b = (I+N)(I+N^2)(I+N^4)(I+N^8), N = -L_b (dd = D_b, ddt = D_b^T),
         // one level at a time over the four independent blocks
         u32x2_t cn[4], cnt[4];
+        f32x4_t ntg[4];  // GATED: N^T's entries, reused for (I + N)^T below
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             f32x4_t n, nt;
@@ -301,6 +315,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             }
             cn[b] = cvt4(n);
             cnt[b] = cvt4(nt);
+            if constexpr (GATED) ntg[b] = nt;
         }
         f32x4_t n2[4], n2t[4];
 #pragma unroll
@@ -318,12 +333,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         f32x4_t n4[4], n4t[4], ft[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            // cet = (I + N)^T as an accumulator, rebuilt from cnt's source values
+            // cet = (I + N)^T as an accumulator, rebuilt from cnt's source values (GATED:
+            // kept, as rebuilding would repeat the decays' exponentials)
             f32x4_t nt;
+            if constexpr (GATED) {
+                nt = ntg[b];
+            } else {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float gnt = GATED ? exp2_hw(l16 > 4 * lg + r ? gcol[b] - grow[b][r] : 0.f) : 1.f;
-                nt[r] = (l16 > 4 * lg + r) ? -(NORM ? br4[b][r] : bc[b]) * (gnt * gd[b][r]) : 0.f;
+                for (int r = 0; r < 4; ++r)
+                    nt[r] = (l16 > 4 * lg + r) ? -(NORM ? br4[b][r] : bc[b]) * gd[b][r] : 0.f;
             }
             cet[b] = cvt4(nt + eye);
             n4[b] = mfma16(cn2t[b], cn2[b], zero);
@@ -448,15 +466,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
         float pgc[4];    // GATED: G_{16i + l16}
         f32x4_t pgr[4];  // GATED: G_{16j + 4lg + r}
-        if constexpr (GATED) {
-            const float gsc = gate_scan(rb);
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                pgc[b] = __shfl(gsc, 16 * b + l16);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) pgr[b][r] = __shfl(gsc, 16 * b + 4 * lg + r);
-            }
-        }
+        if constexpr (GATED) gate_bcast(gate_scan(rb), pgc, pgr);
         int x = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -675,7 +685,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 template <int D, int DV, bool OB, bool HIST, bool NORM = false, bool GATED = false>
 hipError_t launch_t(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
     using G = Geo<D, DV, GATED>;
-    constexpr int kBytes = (NORM || GATED) ? G::BYTES_NORM : G::BYTES;
+    constexpr int kBytes = GATED ? G::BYTES_GATED : NORM ? G::BYTES_NORM : G::BYTES;
     auto kern = delta_chunked_kernel<D, DV, OB, HIST, NORM, GATED>;
     // the dynamic-LDS limit is a per-device function attribute
     int dev = 0;

@@ -256,28 +256,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // NORM: beta = 1, and r_t = 1 / max(||k_t||, 1e-6) on both sides of every Gram entry
         f32x4_t br4[4], rr4[4];
         float bc[4], rc[4];
+        if constexpr (NORM) {
+            float* rn = rnb(c);
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            if constexpr (NORM) {
+            for (int b = 0; b < 4; ++b) {
                 // ||k_t||^2, t = 16b + l16, is entry (l16, l16) of the diagonal tile: lane
                 // (l16 / 4, l16), component l16 % 4
                 const int c4 = l16 & 3;
                 const float dg = c4 == 0 ? gd[b].x : c4 == 1 ? gd[b].y : c4 == 2 ? gd[b].z : gd[b].w;
                 rc[b] = 1.f / fmaxf(sqrtf(__shfl(dg, 16 * (l16 >> 2) + l16)), 1e-6f);  // row 16b + l16
-#pragma unroll
-                for (int r = 0; r < 4; ++r) rr4[b][r] = __shfl(rc[b], 20 * lg + r);  // row 16b + 4lg + r
-                br4[b] = rr4[b] * rc[b];  // N[row][l16] and N[l16][row] carry r_row r_l16
                 bc[b] = 1.f;
-            } else {
-                br4[b] = *reinterpret_cast<const f32x4_t*>(Bs + 16 * b + 4 * lg);
-                bc[b] = Bs[16 * b + l16];
             }
-        }
-        if constexpr (NORM) {
-            float* rn = rnb(c);
+            // r for the chain, and read back for the rows 16b + 4lg + [0, 4) this lane
+            // holds in accumulator form (a wave's LDS operations complete in order)
             if (lg == 0) {
 #pragma unroll
                 for (int b = 0; b < 4; ++b) rn[16 * b + l16] = rc[b];
+            }
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                rr4[b] = *reinterpret_cast<const f32x4_t*>(rn + 16 * b + 4 * lg);
+                br4[b] = rr4[b] * rc[b];  // N[row][l16] and N[l16][row] carry r_row r_l16
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                br4[b] = *reinterpret_cast<const f32x4_t*>(Bs + 16 * b + 4 * lg);
+                bc[b] = Bs[16 * b + l16];
             }
         }
         // GATED: G of the rows this lane holds in A-operand form (gcol, 16b + l16) and in

@@ -92,7 +92,8 @@ struct Geo {
 // HIST: the backward's state recompute.  Instead of O and the final state,
 // each chain wave writes the state at the start of every chunk, rounded to
 // bf16, as rows of S^T: s_hist[(pair * n_chunks + c) * D * D + col * D + d]
-// (fixed-length batches only).
+// (fixed-length batches only).  With no O to form, Q is not copied and P is
+// not built.
 //
 // NORM: the model's linear attention (model/__init__.py:393-432): beta = 1
 // and q, k divided by max(||.||, 1e-6) per token, without rewriting them.
@@ -187,7 +188,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const int r = pos / D, p = (pos % D) / 8;
             const unsigned vo = static_cast<unsigned>(r * tstride * 2) + 16u * (p ^ kq_f<D>(r));
             copy_to_lds(rk, rbuf + G::R_KS + 1024 * i, 16, vo);
-            copy_to_lds(rq, rbuf + G::R_QS + 1024 * i, 16, vo);
+            if constexpr (!HIST) copy_to_lds(rq, rbuf + G::R_QS + 1024 * i, 16, vo);  // HIST: no O
         }
 #pragma unroll
         for (int i = 0; i < G::NI_V; ++i) {
@@ -666,7 +667,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 if (loader && c + 1 < n_chunks) issue_copies(c + 1);
                 if (pw == 0) {
                     build_t(c);
-                } else if (pw == 1) {
+                } else if (pw == 1 && !HIST) {  // HIST computes no O, so no P
                     build_p(c);
                 }
                 if (loader) wait_copies();

@@ -466,20 +466,15 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
     const float* __restrict__ beta, const float* __restrict__ go, const uint16_t* __restrict__ s_hist,
     const uint16_t* __restrict__ g_hist, const uint16_t* __restrict__ w_hist,
     const uint16_t* __restrict__ tp_ws, float* __restrict__ gq, float* __restrict__ gk,
-    float* __restrict__ gbeta, int T, int H, int n_ch) {
+    float* __restrict__ gbeta, int T, int H, int n_ch, int n_total) {
     using G = GradGeo<D>;
     constexpr int JW = G::JW;
+    constexpr int NDO = kC * D / 4 / 256;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    const int pair = blockIdx.x / n_ch, c = blockIdx.x % n_ch;
-    const int seq = pair / H, h = pair % H;
-    const long tok0 = static_cast<long>(seq) * T;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = static_cast<int>(uniform(static_cast<unsigned>(tid >> 6)));
     const int l16 = lane & 15, lg = lane >> 4;
-    const int base = c * kC, clen = min(kC, T - base);
     const size_t tstride = static_cast<size_t>(H) * D;
-    const size_t row0 = (tok0 + base) * tstride + static_cast<size_t>(h) * D;
-    const size_t cidx = static_cast<size_t>(pair) * n_ch + c;
 
     uint16_t* Ks = reinterpret_cast<uint16_t*>(smem + G::KS);
     uint16_t* Qs = reinterpret_cast<uint16_t*>(smem + G::QS);
@@ -496,331 +491,389 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
     float* db1 = reinterpret_cast<float*>(smem + G::DB);  // [wave][t]: W . (V - K S)
     float* db2 = db1 + 4 * kC;                             // [wave][t]: sum_s dA (k_t . k_s)
 
-    {
-        // dO (fp32) first, into registers: its loads are in flight with the copies below,
-        // and waiting for them never waits for a copy issued after them
-        // (buffer loads: rows past the chunk's end, and a NULL go, read as zeros)
-        constexpr int NDO = kC * D / 4 / 256;
-        const __amdgpu_buffer_rsrc_t rgo =
-            make_rsrc(go ? go + row0 : nullptr, go ? static_cast<unsigned>(((clen - 1) * tstride + D) * 4) : 0u);
-        f32x4_t xdo[NDO];
+    // Persistent: workgroup b takes chunks b, b + gridDim.x, ...  Phase 3 reads only K, Q,
+    // G^T's space (dP^T, dA^T) and beta, so the next chunk's V, S^T, W^T, T and dO are
+    // fetched while it runs, and only K, Q, G^T and beta are copied between chunks.
+    struct Ref {
+        long tok0;
+        int h, base, clen;
+        size_t row0, cidx;
+    };
+    auto ref_of = [&](int idx) {
+        Ref r;
+        const int pair = idx / n_ch, c = idx % n_ch;
+        r.h = pair % H;
+        r.tok0 = static_cast<long>(pair / H) * T;
+        r.base = c * kC;
+        r.clen = min(kC, T - r.base);
+        r.row0 = (r.tok0 + r.base) * tstride + static_cast<size_t>(r.h) * D;
+        r.cidx = static_cast<size_t>(pair) * n_ch + c;
+        return r;
+    };
+    // dO (fp32) into registers with buffer loads (rows past the chunk's end, and a NULL
+    // go, read as zeros); written to LDS as bf16 token rows once they have landed
+    f32x4_t xdo[NDO];
+    auto load_do = [&](const Ref& r) {
+        const __amdgpu_buffer_rsrc_t rgo = make_rsrc(
+            go ? go + r.row0 : nullptr, go ? static_cast<unsigned>(((r.clen - 1) * tstride + D) * 4) : 0u);
 #pragma unroll
         for (int i = 0; i < NDO; ++i) {
             const int e = tid + 256 * i, t = e / (D / 4), d = 4 * (e % (D / 4));
             xdo[i] = __builtin_bit_cast(
                 f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rgo, static_cast<unsigned>((t * tstride + d) * 4), 0, 0));
         }
-        const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
-        const unsigned rb = static_cast<unsigned>(tstride * 2);
-        copy_rows<D>(make_rsrc(k + row0, n_kq), smem + G::KS, kC * D * 2 / 1024, rb, w, 4, lane);
-        copy_rows<D>(make_rsrc(q + row0, n_kq), smem + G::QS, kC * D * 2 / 1024, rb, w, 4, lane);
-        copy_rows<D>(make_rsrc(v + row0, n_kq), smem + G::VS, kC * D * 2 / 1024, rb, w, 4, lane);
-        copy_rows<D>(make_rsrc(s_hist + cidx * D * D, D * D * 2), smem + G::ST, D * D * 2 / 1024, D * 2, w, 4, lane);
-        copy_rows<D>(make_rsrc(g_hist + cidx * D * D, D * D * 2), smem + G::GT, D * D * 2 / 1024, D * 2, w, 4, lane);
-        copy_rows<kC>(make_rsrc(w_hist + cidx * D * kC, D * kC * 2), smem + G::WT, D * kC * 2 / 1024, kC * 2, w, 4, lane);
-        copy_flat(make_rsrc(tp_ws + cidx * 3 * kPacked, kPacked * 2), smem + G::TP, kPacked * 2 / 1024, w, 4, lane);
-        if (w == 3)
-            copy_to_lds(make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4)),
-                        smem + G::BS, 4, static_cast<unsigned>(lane * H * 4));
-        // dO -> bf16 token rows
+    };
+    auto store_do = [&]() {
 #pragma unroll
         for (int i = 0; i < NDO; ++i) {
             const int e = tid + 256 * i, t = e / (D / 4), d = 4 * (e % (D / 4));
             *reinterpret_cast<u32x2_t*>(DOs + swz<D>(t, d)) = cvt4(xdo[i]);
         }
-        wait_copies();
-        __syncthreads();
-    }
-    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    };
+    // the inputs phase 3 does not read: V (later U^T), S^T, W^T, T
+    auto copy_a = [&](const Ref& r) {
+        const unsigned n_kq = static_cast<unsigned>(((r.clen - 1) * tstride + D) * 2);
+        const unsigned rb = static_cast<unsigned>(tstride * 2);
+        copy_rows<D>(make_rsrc(v + r.row0, n_kq), smem + G::VS, kC * D * 2 / 1024, rb, w, 4, lane);
+        copy_rows<D>(make_rsrc(s_hist + r.cidx * D * D, D * D * 2), smem + G::ST, D * D * 2 / 1024, D * 2, w, 4, lane);
+        copy_rows<kC>(make_rsrc(w_hist + r.cidx * D * kC, D * kC * 2), smem + G::WT, D * kC * 2 / 1024, kC * 2, w, 4,
+                      lane);
+        copy_flat(make_rsrc(tp_ws + r.cidx * 3 * kPacked, kPacked * 2), smem + G::TP, kPacked * 2 / 1024, w, 4, lane);
+    };
+    // the inputs phase 3 reads: K, Q, G^T, beta
+    auto copy_b = [&](const Ref& r) {
+        const unsigned n_kq = static_cast<unsigned>(((r.clen - 1) * tstride + D) * 2);
+        const unsigned rb = static_cast<unsigned>(tstride * 2);
+        copy_rows<D>(make_rsrc(k + r.row0, n_kq), smem + G::KS, kC * D * 2 / 1024, rb, w, 4, lane);
+        copy_rows<D>(make_rsrc(q + r.row0, n_kq), smem + G::QS, kC * D * 2 / 1024, rb, w, 4, lane);
+        copy_rows<D>(make_rsrc(g_hist + r.cidx * D * D, D * D * 2), smem + G::GT, D * D * 2 / 1024, D * 2, w, 4, lane);
+        if (w == 3)
+            copy_to_lds(make_rsrc(beta + (r.tok0 + r.base) * H + r.h, static_cast<unsigned>(((r.clen - 1) * H + 1) * 4)),
+                        smem + G::BS, 4, static_cast<unsigned>(lane * H * 4));
+    };
 
-    // ---- phase 1: R' = V - K S and U = T diag(beta) R' for this wave's columns ----
-    f32x4_t U[4][JW];
-    {
-        f32x4_t X[4][JW];
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int jj = 0; jj < JW; ++jj) X[m][jj] = zero;
-#pragma unroll
-        for (int kb = 0; kb < D / 32; ++kb) {
-            bf16x8_t fk[4], fs[JW];
-#pragma unroll
-            for (int m = 0; m < 4; ++m) fk[m] = lds_op_kq<D>(Ks, 16 * m + l16, kb, lg);
-#pragma unroll
-            for (int jj = 0; jj < JW; ++jj) fs[jj] = lds_op_kq<D>(St, 16 * (JW * w + jj) + l16, kb, lg);
+    int idx = blockIdx.x;
+    if (idx >= n_total) return;  // whole workgroup, before any barrier
+    Ref cur = ref_of(idx);
+    load_do(cur);
+    copy_b(cur);
+    copy_a(cur);
+    store_do();
+    wait_copies();
+    __syncthreads();
+    for (;;) {
+        const long tok0 = cur.tok0;
+        const int h = cur.h, base = cur.base, clen = cur.clen;
+        const size_t row0 = cur.row0;
+        const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+
+        // ---- phase 1: R' = V - K S and U = T diag(beta) R' for this wave's columns ----
+        f32x4_t U[4][JW];
+        {
+            f32x4_t X[4][JW];
 #pragma unroll
             for (int m = 0; m < 4; ++m)
 #pragma unroll
-                for (int jj = 0; jj < JW; ++jj) X[m][jj] = mfma32(fk[m], fs[jj], X[m][jj]);
-        }
-        f32x4_t dbp[4];
+                for (int jj = 0; jj < JW; ++jj) X[m][jj] = zero;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) dbp[m] = zero;
+            for (int kb = 0; kb < D / 32; ++kb) {
+                bf16x8_t fk[4], fs[JW];
 #pragma unroll
-        for (int jj = 0; jj < JW; ++jj) {
-            const int jt = JW * w + jj, jcol = 16 * jt + l16;
-            u32x2_t vv0 = lds_acc_issue<D>(Vs, 0, 16 * jt, lane), vv1 = lds_acc_issue<D>(Vs, 16, 16 * jt, lane);
-            u32x2_t vv2 = lds_acc_issue<D>(Vs, 32, 16 * jt, lane), vv3 = lds_acc_issue<D>(Vs, 48, 16 * jt, lane);
-            lds_wait(vv0, vv1, vv2, vv3);
-            const u32x2_t vv[4] = {vv0, vv1, vv2, vv3};
-            f32x4_t R[4];
+                for (int m = 0; m < 4; ++m) fk[m] = lds_op_kq<D>(Ks, 16 * m + l16, kb, lg);
+#pragma unroll
+                for (int jj = 0; jj < JW; ++jj) fs[jj] = lds_op_kq<D>(St, 16 * (JW * w + jj) + l16, kb, lg);
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+#pragma unroll
+                    for (int jj = 0; jj < JW; ++jj) X[m][jj] = mfma32(fk[m], fs[jj], X[m][jj]);
+            }
+            f32x4_t dbp[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) dbp[m] = zero;
+#pragma unroll
+            for (int jj = 0; jj < JW; ++jj) {
+                const int jt = JW * w + jj, jcol = 16 * jt + l16;
+                u32x2_t vv0 = lds_acc_issue<D>(Vs, 0, 16 * jt, lane), vv1 = lds_acc_issue<D>(Vs, 16, 16 * jt, lane);
+                u32x2_t vv2 = lds_acc_issue<D>(Vs, 32, 16 * jt, lane), vv3 = lds_acc_issue<D>(Vs, 48, 16 * jt, lane);
+                lds_wait(vv0, vv1, vv2, vv3);
+                const u32x2_t vv[4] = {vv0, vv1, vv2, vv3};
+                f32x4_t R[4];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const int t0 = 16 * m + 4 * lg;
+                    const f32x4_t rp = widen4(vv[m]) - X[m][jj];  // V - K S
+                    const f32x4_t wv = widen4(*reinterpret_cast<const u32x2_t*>(Wt + swz<kC>(jcol, t0)));
+                    dbp[m] += wv * rp;
+                    R[m] = *reinterpret_cast<const f32x4_t*>(Bs + t0) * rp;
+                }
+                const bf16x8_t Rb0 = acc_to_b(R[0], R[1]), Rb1 = acc_to_b(R[2], R[3]);
+                U[0][jj] = mfma32(packed_a(Tp, 0, lane), Rb0, zero);
+                U[1][jj] = mfma32(packed_a(Tp, 1, lane), Rb0, zero);
+                U[2][jj] = mfma32(packed_a(Tp, 3, lane), Rb1, mfma32(packed_a(Tp, 2, lane), Rb0, zero));
+                U[3][jj] = mfma32(packed_a(Tp, 5, lane), Rb1, mfma32(packed_a(Tp, 4, lane), Rb0, zero));
+            }
+            // dbeta, first term: sum over this wave's columns (lanes l16, then its tiles)
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                const int t0 = 16 * m + 4 * lg;
-                const f32x4_t rp = widen4(vv[m]) - X[m][jj];  // V - K S
-                const f32x4_t wv = widen4(*reinterpret_cast<const u32x2_t*>(Wt + swz<kC>(jcol, t0)));
-                dbp[m] += wv * rp;
-                R[m] = *reinterpret_cast<const f32x4_t*>(Bs + t0) * rp;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x = dbp[m][r];
+                    x += __shfl_xor(x, 1);
+                    x += __shfl_xor(x, 2);
+                    x += __shfl_xor(x, 4);
+                    x += __shfl_xor(x, 8);
+                    dbp[m][r] = x;
+                }
+                if (l16 == 0) *reinterpret_cast<f32x4_t*>(db1 + w * kC + 16 * m + 4 * lg) = dbp[m];
             }
-            const bf16x8_t Rb0 = acc_to_b(R[0], R[1]), Rb1 = acc_to_b(R[2], R[3]);
-            U[0][jj] = mfma32(packed_a(Tp, 0, lane), Rb0, zero);
-            U[1][jj] = mfma32(packed_a(Tp, 1, lane), Rb0, zero);
-            U[2][jj] = mfma32(packed_a(Tp, 3, lane), Rb1, mfma32(packed_a(Tp, 2, lane), Rb0, zero));
-            U[3][jj] = mfma32(packed_a(Tp, 5, lane), Rb1, mfma32(packed_a(Tp, 4, lane), Rb0, zero));
         }
-        // dbeta, first term: sum over this wave's columns (lanes l16, then its tiles)
+        __syncthreads();  // V is dead: its space takes U^T
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int jj = 0; jj < JW; ++jj)
+                *reinterpret_cast<u32x2_t*>(Ut + swz<kC>(16 * (JW * w + jj) + l16, 16 * m + 4 * lg)) = cvt4(U[m][jj]);
+        __syncthreads();
+
+        // ---- phase 2: products contracting over the d_v index j ----
+        // dQ1 = dO S^T, dKa = U G^T, dKb = W S^T for this wave's d tiles; the lower
+        // 16x16 tiles (m, st), m >= st, numbered 0..9 row by row, go to waves by number mod 4:
+        // dP = dO U^T, dA = -W U^T, KK = K K^T.
+        f32x4_t dQ[4][JW], dKa[4][JW], dKb[4][JW];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int dd = 0; dd < JW; ++dd) {
+                dQ[m][dd] = zero;
+                dKa[m][dd] = zero;
+                dKb[m][dd] = zero;
+            }
+        constexpr int kTiles = 3;  // wave w takes lower tiles w, w + 4, w + 8
+        auto tile_m = [](int idx) { return idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0; };
+        auto tile_s = [&](int idx) { const int m = tile_m(idx); return idx - m * (m + 1) / 2; };
+        const int nt = w < 2 ? 3 : 2;
+        int tm[kTiles], ts[kTiles];
+#pragma unroll
+        for (int x = 0; x < kTiles; ++x) {
+            const int idx = min(w + 4 * x, 9);
+            tm[x] = tile_m(idx);
+            ts[x] = tile_s(idx);
+        }
+        f32x4_t dP[kTiles], dA[kTiles], KK[kTiles];
+#pragma unroll
+        for (int x = 0; x < kTiles; ++x) dP[x] = dA[x] = KK[x] = zero;
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb) {
+            u32x4_t fu[4], fw[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                fu[m] = lds_col_issue<kC>(Ut, 32 * kb, 16 * m, lane);
+                fw[m] = lds_col_issue<kC>(Wt, 32 * kb, 16 * m, lane);
+            }
+            u32x4_t fst[JW], fgt[JW];
+#pragma unroll
+            for (int dd = 0; dd < JW; ++dd) {
+                fst[dd] = lds_col_issue<D>(St, 32 * kb, 16 * (JW * w + dd), lane);
+                fgt[dd] = lds_col_issue<D>(Gt, 32 * kb, 16 * (JW * w + dd), lane);
+            }
+            bf16x8_t fdo[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) fdo[m] = lds_op_kq<D>(DOs, 16 * m + l16, kb, lg);
+            lds_wait_all();
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                tie(fu[m]);
+                tie(fw[m]);
+            }
+#pragma unroll
+            for (int dd = 0; dd < JW; ++dd) {
+                tie(fst[dd]);
+                tie(fgt[dd]);
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int dd = 0; dd < JW; ++dd) {
+                    // operands swapped: the tiles hold dQ^T, dK^T (lane: 4 consecutive d of a token)
+                    dQ[m][dd] = mfma32(as_b(fst[dd]), fdo[m], dQ[m][dd]);
+                    dKa[m][dd] = mfma32(as_b(fgt[dd]), as_b(fu[m]), dKa[m][dd]);
+                    dKb[m][dd] = mfma32(as_b(fst[dd]), as_b(fw[m]), dKb[m][dd]);
+                }
+#pragma unroll
+            for (int x = 0; x < kTiles; ++x) {
+                if (x < nt) {
+                    // select row block tm[x] and column block ts[x] without dynamic register indexing
+                    bf16x8_t ado = fdo[0];
+                    u32x4_t aw = fw[0], bu = fu[0];
+#pragma unroll
+                    for (int m = 1; m < 4; ++m) {
+                        if (tm[x] == m) {
+                            ado = fdo[m];
+                            aw = fw[m];
+                        }
+                        if (ts[x] == m) bu = fu[m];
+                    }
+                    dP[x] = mfma32(ado, as_b(bu), dP[x]);
+                    dA[x] = mfma32(as_b(aw), as_b(bu), dA[x]);
+                }
+            }
+        }
+#pragma unroll
+        for (int x = 0; x < kTiles; ++x) {
+            if (x < nt) {
+#pragma unroll
+                for (int kb = 0; kb < D / 32; ++kb)
+                    KK[x] = mfma32(lds_op_kq<D>(Ks, 16 * tm[x] + l16, kb, lg), lds_op_kq<D>(Ks, 16 * ts[x] + l16, kb, lg), KK[x]);
+            }
+        }
+        // masks, dbeta second term, beta dA
+        f32x4_t db2p[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) db2p[m] = zero;
+#pragma unroll
+        for (int x = 0; x < kTiles; ++x) {
+            if (x < nt) {
+                const int m = tm[x], st = ts[x];
+                const int t0 = 16 * m + 4 * lg, s = 16 * st + l16;
+                const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + t0);
+                f32x4_t e = zero;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (t0 + r < s) dP[x][r] = 0.f;
+                    const float a = (t0 + r > s) ? -dA[x][r] : 0.f;
+                    e[r] = a * KK[x][r];
+                    dA[x][r] = bs[r] * a;
+                }
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm)
+                    if (mm == m) db2p[mm] += e;
+            }
+        }
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float x = dbp[m][r];
+                float x = db2p[m][r];
                 x += __shfl_xor(x, 1);
                 x += __shfl_xor(x, 2);
                 x += __shfl_xor(x, 4);
                 x += __shfl_xor(x, 8);
-                dbp[m][r] = x;
+                db2p[m][r] = x;
             }
-            if (l16 == 0) *reinterpret_cast<f32x4_t*>(db1 + w * kC + 16 * m + 4 * lg) = dbp[m];
+            if (l16 == 0) *reinterpret_cast<f32x4_t*>(db2 + w * kC + 16 * m + 4 * lg) = db2p[m];
         }
-    }
-    __syncthreads();  // V is dead: its space takes U^T
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int jj = 0; jj < JW; ++jj)
-            *reinterpret_cast<u32x2_t*>(Ut + swz<kC>(16 * (JW * w + jj) + l16, 16 * m + 4 * lg)) = cvt4(U[m][jj]);
-    __syncthreads();
-
-    // ---- phase 2: products contracting over the d_v index j ----
-    // dQ1 = dO S^T, dKa = U G^T, dKb = W S^T for this wave's d tiles; the lower
-    // 16x16 tiles (m, st), m >= st, numbered 0..9 row by row, go to waves by number mod 4:
-    // dP = dO U^T, dA = -W U^T, KK = K K^T.
-    f32x4_t dQ[4][JW], dKa[4][JW], dKb[4][JW];
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int dd = 0; dd < JW; ++dd) {
-            dQ[m][dd] = zero;
-            dKa[m][dd] = zero;
-            dKb[m][dd] = zero;
-        }
-    constexpr int kTiles = 3;  // wave w takes lower tiles w, w + 4, w + 8
-    auto tile_m = [](int idx) { return idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0; };
-    auto tile_s = [&](int idx) { const int m = tile_m(idx); return idx - m * (m + 1) / 2; };
-    const int nt = w < 2 ? 3 : 2;
-    int tm[kTiles], ts[kTiles];
-#pragma unroll
-    for (int x = 0; x < kTiles; ++x) {
-        const int idx = min(w + 4 * x, 9);
-        tm[x] = tile_m(idx);
-        ts[x] = tile_s(idx);
-    }
-    f32x4_t dP[kTiles], dA[kTiles], KK[kTiles];
-#pragma unroll
-    for (int x = 0; x < kTiles; ++x) dP[x] = dA[x] = KK[x] = zero;
-#pragma unroll
-    for (int kb = 0; kb < D / 32; ++kb) {
-        u32x4_t fu[4], fw[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            fu[m] = lds_col_issue<kC>(Ut, 32 * kb, 16 * m, lane);
-            fw[m] = lds_col_issue<kC>(Wt, 32 * kb, 16 * m, lane);
-        }
-        u32x4_t fst[JW], fgt[JW];
-#pragma unroll
-        for (int dd = 0; dd < JW; ++dd) {
-            fst[dd] = lds_col_issue<D>(St, 32 * kb, 16 * (JW * w + dd), lane);
-            fgt[dd] = lds_col_issue<D>(Gt, 32 * kb, 16 * (JW * w + dd), lane);
-        }
-        bf16x8_t fdo[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) fdo[m] = lds_op_kq<D>(DOs, 16 * m + l16, kb, lg);
-        lds_wait_all();
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            tie(fu[m]);
-            tie(fw[m]);
-        }
-#pragma unroll
-        for (int dd = 0; dd < JW; ++dd) {
-            tie(fst[dd]);
-            tie(fgt[dd]);
-        }
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int dd = 0; dd < JW; ++dd) {
-                // operands swapped: the tiles hold dQ^T, dK^T (lane: 4 consecutive d of a token)
-                dQ[m][dd] = mfma32(as_b(fst[dd]), fdo[m], dQ[m][dd]);
-                dKa[m][dd] = mfma32(as_b(fgt[dd]), as_b(fu[m]), dKa[m][dd]);
-                dKb[m][dd] = mfma32(as_b(fst[dd]), as_b(fw[m]), dKb[m][dd]);
-            }
+        __syncthreads();  // G^T is dead: its space takes dP^T and (beta dA)^T
 #pragma unroll
         for (int x = 0; x < kTiles; ++x) {
             if (x < nt) {
-                // select row block tm[x] and column block ts[x] without dynamic register indexing
-                bf16x8_t ado = fdo[0];
-                u32x4_t aw = fw[0], bu = fu[0];
-#pragma unroll
-                for (int m = 1; m < 4; ++m) {
-                    if (tm[x] == m) {
-                        ado = fdo[m];
-                        aw = fw[m];
+                const int o = swz<kC>(16 * ts[x] + l16, 16 * tm[x] + 4 * lg);
+                *reinterpret_cast<u32x2_t*>(dPt + o) = cvt4(dP[x]);
+                *reinterpret_cast<u32x2_t*>(dAt + o) = cvt4(dA[x]);
+            }
+        }
+        {
+            // the upper tiles (m < st) are zero; 6 of them, numbered row by row, by number mod 4
+            int idx = 0;
+            const u32x2_t z2 = {0u, 0u};
+            for (int m = 0; m < 4; ++m)
+                for (int st = m + 1; st < 4; ++st, ++idx)
+                    if ((idx & 3) == w) {
+                        const int o = swz<kC>(16 * st + l16, 16 * m + 4 * lg);
+                        *reinterpret_cast<u32x2_t*>(dPt + o) = z2;
+                        *reinterpret_cast<u32x2_t*>(dAt + o) = z2;
                     }
-                    if (ts[x] == m) bu = fu[m];
-                }
-                dP[x] = mfma32(ado, as_b(bu), dP[x]);
-                dA[x] = mfma32(as_b(aw), as_b(bu), dA[x]);
-            }
         }
-    }
-#pragma unroll
-    for (int x = 0; x < kTiles; ++x) {
-        if (x < nt) {
-#pragma unroll
-            for (int kb = 0; kb < D / 32; ++kb)
-                KK[x] = mfma32(lds_op_kq<D>(Ks, 16 * tm[x] + l16, kb, lg), lds_op_kq<D>(Ks, 16 * ts[x] + l16, kb, lg), KK[x]);
-        }
-    }
-    // masks, dbeta second term, beta dA
-    f32x4_t db2p[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) db2p[m] = zero;
-#pragma unroll
-    for (int x = 0; x < kTiles; ++x) {
-        if (x < nt) {
-            const int m = tm[x], st = ts[x];
-            const int t0 = 16 * m + 4 * lg, s = 16 * st + l16;
-            const f32x4_t bs = *reinterpret_cast<const f32x4_t*>(Bs + t0);
-            f32x4_t e = zero;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (t0 + r < s) dP[x][r] = 0.f;
-                const float a = (t0 + r > s) ? -dA[x][r] : 0.f;
-                e[r] = a * KK[x][r];
-                dA[x][r] = bs[r] * a;
-            }
-#pragma unroll
-            for (int mm = 0; mm < 4; ++mm)
-                if (mm == m) db2p[mm] += e;
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float x = db2p[m][r];
-            x += __shfl_xor(x, 1);
-            x += __shfl_xor(x, 2);
-            x += __shfl_xor(x, 4);
-            x += __shfl_xor(x, 8);
-            db2p[m][r] = x;
-        }
-        if (l16 == 0) *reinterpret_cast<f32x4_t*>(db2 + w * kC + 16 * m + 4 * lg) = db2p[m];
-    }
-    __syncthreads();  // G^T is dead: its space takes dP^T and (beta dA)^T
-#pragma unroll
-    for (int x = 0; x < kTiles; ++x) {
-        if (x < nt) {
-            const int o = swz<kC>(16 * ts[x] + l16, 16 * tm[x] + 4 * lg);
-            *reinterpret_cast<u32x2_t*>(dPt + o) = cvt4(dP[x]);
-            *reinterpret_cast<u32x2_t*>(dAt + o) = cvt4(dA[x]);
-        }
-    }
-    {
-        // the upper tiles (m < st) are zero; 6 of them, numbered row by row, by number mod 4
-        int idx = 0;
-        const u32x2_t z2 = {0u, 0u};
-        for (int m = 0; m < 4; ++m)
-            for (int st = m + 1; st < 4; ++st, ++idx)
-                if ((idx & 3) == w) {
-                    const int o = swz<kC>(16 * st + l16, 16 * m + 4 * lg);
-                    *reinterpret_cast<u32x2_t*>(dPt + o) = z2;
-                    *reinterpret_cast<u32x2_t*>(dAt + o) = z2;
-                }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    // ---- phase 3: products contracting over tokens ----
-    // dQ += dP K;  dKc = dP^T Q + (beta dA)^T K + (beta dA) K
-    f32x4_t dKc[4][JW];
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int dd = 0; dd < JW; ++dd) dKc[m][dd] = zero;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-        u32x4_t fkc[JW], fqc[JW], fpc[4], fac[4];
-#pragma unroll
-        for (int dd = 0; dd < JW; ++dd) {
-            fkc[dd] = lds_col_issue<D>(Ks, 32 * kb, 16 * (JW * w + dd), lane);
-            fqc[dd] = lds_col_issue<D>(Qs, 32 * kb, 16 * (JW * w + dd), lane);
+        // the next chunk's V, S^T, W^T, T and dO, into space phase 3 does not read
+        const int nidx = idx + static_cast<int>(gridDim.x);
+        const bool more = nidx < n_total;
+        Ref nxt{};
+        if (more) {
+            nxt = ref_of(nidx);
+            load_do(nxt);
+            copy_a(nxt);
         }
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            fpc[m] = lds_col_issue<kC>(dPt, 32 * kb, 16 * m, lane);
-            fac[m] = lds_col_issue<kC>(dAt, 32 * kb, 16 * m, lane);
-        }
-        bf16x8_t fpr[4], far[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            fpr[m] = lds_op_kq<kC>(dPt, 16 * m + l16, kb, lg);
-            far[m] = lds_op_kq<kC>(dAt, 16 * m + l16, kb, lg);
-        }
-        lds_wait_all();
-#pragma unroll
-        for (int dd = 0; dd < JW; ++dd) {
-            tie(fkc[dd]);
-            tie(fqc[dd]);
-        }
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            tie(fpc[m]);
-            tie(fac[m]);
-        }
+
+        // ---- phase 3: products contracting over tokens ----
+        // dQ += dP K;  dKc = dP^T Q + (beta dA)^T K + (beta dA) K
+        f32x4_t dKc[4][JW];
 #pragma unroll
         for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int dd = 0; dd < JW; ++dd) dKc[m][dd] = zero;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            u32x4_t fkc[JW], fqc[JW], fpc[4], fac[4];
 #pragma unroll
             for (int dd = 0; dd < JW; ++dd) {
-                dQ[m][dd] = mfma32(as_b(fkc[dd]), as_b(fpc[m]), dQ[m][dd]);
-                dKc[m][dd] = mfma32(as_b(fqc[dd]), fpr[m], dKc[m][dd]);
-                dKc[m][dd] = mfma32(as_b(fkc[dd]), far[m], dKc[m][dd]);
-                dKc[m][dd] = mfma32(as_b(fkc[dd]), as_b(fac[m]), dKc[m][dd]);
+                fkc[dd] = lds_col_issue<D>(Ks, 32 * kb, 16 * (JW * w + dd), lane);
+                fqc[dd] = lds_col_issue<D>(Qs, 32 * kb, 16 * (JW * w + dd), lane);
             }
-    }
-    // outputs: lane (g, l16) holds d = 16 dt + 4g + [0, 4) of token 16m + l16 (16-byte stores)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const int t = 16 * m + l16;
-        const float bt = Bs[t];
+            for (int m = 0; m < 4; ++m) {
+                fpc[m] = lds_col_issue<kC>(dPt, 32 * kb, 16 * m, lane);
+                fac[m] = lds_col_issue<kC>(dAt, 32 * kb, 16 * m, lane);
+            }
+            bf16x8_t fpr[4], far[4];
 #pragma unroll
-        for (int dd = 0; dd < JW; ++dd) {
-            const int d0 = 16 * (JW * w + dd) + 4 * lg;
-            const f32x4_t kk = dKa[m][dd] - bt * dKb[m][dd] + dKc[m][dd];
-            if (t < clen) {
-                const size_t a = row0 + t * tstride + d0;
-                *reinterpret_cast<f32x4_t*>(gq + a) = dQ[m][dd];
-                *reinterpret_cast<f32x4_t*>(gk + a) = kk;
+            for (int m = 0; m < 4; ++m) {
+                fpr[m] = lds_op_kq<kC>(dPt, 16 * m + l16, kb, lg);
+                far[m] = lds_op_kq<kC>(dAt, 16 * m + l16, kb, lg);
+            }
+            lds_wait_all();
+#pragma unroll
+            for (int dd = 0; dd < JW; ++dd) {
+                tie(fkc[dd]);
+                tie(fqc[dd]);
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                tie(fpc[m]);
+                tie(fac[m]);
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int dd = 0; dd < JW; ++dd) {
+                    dQ[m][dd] = mfma32(as_b(fkc[dd]), as_b(fpc[m]), dQ[m][dd]);
+                    dKc[m][dd] = mfma32(as_b(fqc[dd]), fpr[m], dKc[m][dd]);
+                    dKc[m][dd] = mfma32(as_b(fkc[dd]), far[m], dKc[m][dd]);
+                    dKc[m][dd] = mfma32(as_b(fkc[dd]), as_b(fac[m]), dKc[m][dd]);
+                }
+        }
+        // outputs: lane (g, l16) holds d = 16 dt + 4g + [0, 4) of token 16m + l16 (16-byte stores)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int t = 16 * m + l16;
+            const float bt = Bs[t];
+#pragma unroll
+            for (int dd = 0; dd < JW; ++dd) {
+                const int d0 = 16 * (JW * w + dd) + 4 * lg;
+                const f32x4_t kk = dKa[m][dd] - bt * dKb[m][dd] + dKc[m][dd];
+                if (t < clen) {
+                    const size_t a = row0 + t * tstride + d0;
+                    *reinterpret_cast<f32x4_t*>(gq + a) = dQ[m][dd];
+                    *reinterpret_cast<f32x4_t*>(gk + a) = kk;
+                }
             }
         }
-    }
-    if (tid < clen) {
-        float s = 0.f;
+        if (tid < clen) {
+            float s = 0.f;
 #pragma unroll
-        for (int x = 0; x < 4; ++x) s += db1[x * kC + tid];
+            for (int x = 0; x < 4; ++x) s += db1[x * kC + tid];
 #pragma unroll
-        for (int x = 0; x < 4; ++x) s += db2[x * kC + tid];
-        gbeta[(tok0 + base + tid) * H + h] = s;
+            for (int x = 0; x < 4; ++x) s += db2[x * kC + tid];
+            gbeta[(tok0 + base + tid) * H + h] = s;
+        }
+        if (!more) break;
+        __syncthreads();  // phase 3's reads of K, Q, dP^T, dA^T, beta and the dbeta sums are done
+        copy_b(nxt);
+        store_do();
+        wait_copies();
+        __syncthreads();
+        idx = nidx;
+        cur = nxt;
     }
 }
 
@@ -862,9 +915,17 @@ hipError_t launch_d(const BwdArgs& a, hipStream_t st) {
                        a.n_pairs, a.T, a.H, n_ch, n_tiles);
     if ((e = hipGetLastError()) != hipSuccess || n_ch == 0) return e;
     if ((e = set_lds(bwd_grad_kernel<D>, GradGeo<D>::BYTES)) != hipSuccess) return e;
-    hipLaunchKernelGGL(bwd_grad_kernel<D>, dim3(static_cast<unsigned>(a.n_pairs) * n_ch), dim3(256),
-                       GradGeo<D>::BYTES, st, q, k, v, a.beta, a.go, s_hist, g_hist, w_hist, tp, a.gq, a.gk,
-                       a.gbeta, a.T, a.H, n_ch);
+    // persistent: one workgroup per CU (its LDS allows no more), each taking every
+    // gridDim.x-th chunk
+    int dev = 0, n_cu = 0;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+    if ((e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+    const long n_total = static_cast<long>(a.n_pairs) * n_ch;
+    if (n_total > (1L << 30)) return hipErrorInvalidValue;  // chunk indices stay in int
+    const long grid = n_total < n_cu ? n_total : (n_cu > 0 ? n_cu : 1);
+    hipLaunchKernelGGL(bwd_grad_kernel<D>, dim3(static_cast<unsigned>(grid)), dim3(256), GradGeo<D>::BYTES, st, q,
+                       k, v, a.beta, a.go, s_hist, g_hist, w_hist, tp, a.gq, a.gk, a.gbeta, a.T, a.H, n_ch,
+                       static_cast<int>(n_total));
     return hipGetLastError();
 }
 

@@ -372,6 +372,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         Y[1] = mfma32(packed_a(PTp, qblk_u(1, 1), lane), d1, mfma32(packed_a(PTp, qblk_u(1, 0), lane), d0, Y[1]));
         Y[2] = mfma32(packed_a(PTp, qblk_u(2, 1), lane), d1, Y[2]);
         Y[3] = mfma32(packed_a(PTp, qblk_u(3, 1), lane), d1, Y[3]);
+        // G += Q^T dO: it does not depend on W, so its products fill the wait for Y and W
+        // (Y took G through Gb, so Gm is free to change)
+#pragma unroll
+        for (int h4 = 0; h4 < D / 64; ++h4) {
+            u32x4_t e0 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 0, lane), f0 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 0, lane);
+            u32x4_t e1 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 1, lane), f1 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 1, lane);
+            u32x4_t e2 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 2, lane), f2 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 2, lane);
+            u32x4_t e3 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 3, lane), f3 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 3, lane);
+            lds_wait(e0, f0, e1, f1, e2, f2, e3, f3);
+            const u32x4_t qa[4] = {e0, e1, e2, e3}, qb[4] = {f0, f1, f2, f3};
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                Gm[4 * h4 + x] = mfma32(as_b(qa[x]), d0, Gm[4 * h4 + x]);
+                Gm[4 * h4 + x] = mfma32(as_b(qb[x]), d1, Gm[4 * h4 + x]);
+            }
+        }
         // W = T^T Y
         const bf16x8_t Yb0 = acc_to_b(Y[0], Y[1]), Yb1 = acc_to_b(Y[2], Y[3]);
         f32x4_t W[4];
@@ -399,7 +415,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             if (t < clen)
                 *reinterpret_cast<f32x4_t*>(gv + (tok0 + base + t) * tstride + vcol) = Bs[t] * WT[m];
         }
-        // G += Q^T dO - K^T diag(beta) W
+        // G -= K^T diag(beta) W (Q^T dO was added above)
         const bf16x8_t nb0 = acc_to_b(NBW[0], NBW[1]), nb1 = acc_to_b(NBW[2], NBW[3]);
 #pragma unroll
         for (int h4 = 0; h4 < D / 64; ++h4) {
@@ -408,22 +424,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             u32x4_t a2 = lds_kt_issue<D, 0>(Ks, 4 * h4 + 2, lane), b2 = lds_kt_issue<D, 32>(Ks, 4 * h4 + 2, lane);
             u32x4_t a3 = lds_kt_issue<D, 0>(Ks, 4 * h4 + 3, lane), b3 = lds_kt_issue<D, 32>(Ks, 4 * h4 + 3, lane);
             lds_wait(a0, b0, a1, b1, a2, b2, a3, b3);
-            u32x4_t e0 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 0, lane), f0 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 0, lane);
-            u32x4_t e1 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 1, lane), f1 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 1, lane);
-            u32x4_t e2 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 2, lane), f2 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 2, lane);
-            u32x4_t e3 = lds_kt_issue<D, 0>(Qs, 4 * h4 + 3, lane), f3 = lds_kt_issue<D, 32>(Qs, 4 * h4 + 3, lane);
             const u32x4_t ka[4] = {a0, a1, a2, a3}, kb_[4] = {b0, b1, b2, b3};
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
                 Gm[4 * h4 + x] = mfma32(as_b(ka[x]), nb0, Gm[4 * h4 + x]);
                 Gm[4 * h4 + x] = mfma32(as_b(kb_[x]), nb1, Gm[4 * h4 + x]);
-            }
-            lds_wait(e0, f0, e1, f1, e2, f2, e3, f3);
-            const u32x4_t qa[4] = {e0, e1, e2, e3}, qb[4] = {f0, f1, f2, f3};
-#pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                Gm[4 * h4 + x] = mfma32(as_b(qa[x]), d0, Gm[4 * h4 + x]);
-                Gm[4 * h4 + x] = mfma32(as_b(qb[x]), d1, Gm[4 * h4 + x]);
             }
         }
 #pragma unroll

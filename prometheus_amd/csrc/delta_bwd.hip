@@ -29,12 +29,18 @@
 //
 // K5a (checkpoint pass) runs the forward recurrence in the per-token
 // forward kernel's layout (column groups of 256 threads), writing u and the
-// block-end states.  K5b (reverse pass) holds three fp32 matrices of the tile on chip:
-// G by columns (thread (e, rc): rows rc*RPT.. of column e, for w = G^T k),
-// G by rows and S by rows (thread (d, rr): tile columns rr*RPT.. of row d,
-// for x = G u, S go and S w); every product is a per-thread partial sum
-// reduced over adjacent lanes.  w moves from the column to the row layout
-// through LDS: one barrier per token.
+// block-end states.  K5b (reverse pass) holds three fp32 matrices of the
+// tile on chip: G by columns (thread (e, rc): rows rc*8.. of column e, for
+// w = G^T k), G by rows and S by rows (thread (d, rr): tile columns rr*8..
+// of row d, for x = G u, S go and S w); every product is a per-thread
+// partial sum reduced over adjacent lanes with DPP.  w moves from the
+// column to the row layout through LDS: one LDS-only barrier per token,
+// after which the next token's operands are read.  A checkpoint block's
+// inputs (k, q, go, u, beta and the checkpoint) are loaded into registers
+// one block ahead and staged into double-buffered LDS (slices at a stride
+// of kRpt + 4 floats: 16-byte reads in distinct banks); the block's outputs
+// collect in LDS and go out coalesced at the next block, before that
+// block's loads, so that waiting for loads never waits for stores.
 
 #include "pm_common.h"
 #include "pm_internal.h"

@@ -26,8 +26,9 @@
 //      independent) in two waves, while two more waves copy the next chunk;
 //      it writes G_c (bf16, rows of G^T), W (bf16, rows of W^T), dV and
 //      finally dS_0;
-//   4. bwd_grad_kernel, one workgroup per chunk, all chunks in parallel:
-//      dQ, dK and dbeta from S_c, G_c, W and the chunk's q/k/v/beta.
+//   4. bwd_grad_kernel, all chunks in parallel (one persistent workgroup
+//      per CU, the next chunk's inputs fetched during the last phase): dQ,
+//      dK and dbeta from S_c, G_c, W and the chunk's q/k/v/beta.
 // Numerics as in the forward: bf16 operands, fp32 accumulation; G and the
 // outputs stay fp32.
 //

@@ -188,7 +188,7 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
                 const float4 t = kp[i];
                 kk[4 * i] = t.x, kk[4 * i + 1] = t.y, kk[4 * i + 2] = t.z, kk[4 * i + 3] = t.w;
             }
-            const float ks = col_sum<RS>(dot4<RPT>(kk, S));
+            const float ks = col_sum<RS>(row_dot<RPT>(kk, S));
             const float u = sv[j * CW + el] - ks;
             su[j * CW + el] = u;  // the RS lanes of a column store the same bits
             const float bu = sb[j] * u;
@@ -294,18 +294,8 @@ __device__ __forceinline__ void load_slice(const float* p, float (&x)[kRpt]) {
         x[4 * i] = t.x, x[4 * i + 1] = t.y, x[4 * i + 2] = t.z, x[4 * i + 3] = t.w;
     }
 }
-// Dot product of two register slices, four independent accumulators.
-__device__ __forceinline__ float slice_dot(const float (&a)[kRpt], const float (&b)[kRpt]) {
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-#pragma unroll
-    for (int i = 0; i < kRpt; i += 4) {
-        s0 = fmaf(a[i], b[i], s0);
-        s1 = fmaf(a[i + 1], b[i + 1], s1);
-        s2 = fmaf(a[i + 2], b[i + 2], s2);
-        s3 = fmaf(a[i + 3], b[i + 3], s3);
-    }
-    return (s0 + s1) + (s2 + s3);
-}
+// Dot product of two register slices, one accumulator (see row_dot).
+__device__ __forceinline__ float slice_dot(const float (&a)[kRpt], const float (&b)[kRpt]) { return row_dot<kRpt>(a, b); }
 
 // ---------------- K5b: reverse pass over one column tile ----------------
 // gq/gk/gb receive this tile's sums over its columns: the outputs themselves

@@ -200,7 +200,7 @@ __global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
                 qq[4 * i] = w.x, qq[4 * i + 1] = w.y, qq[4 * i + 2] = w.z, qq[4 * i + 3] = w.w;
             }
             float ks, qs;
-            dot4x2<RPT>(kk, qq, S, ks, qs);
+            row_dot2<RPT>(kk, qq, S, ks, qs);
             col_sum2<RS>(ks, qs);
             const float4 cj = sc[j];  // beta, q.k, alpha
             const float vv = sv[j * CW + el];

@@ -38,38 +38,28 @@ __device__ __forceinline__ float col_sum(float a) {
     if constexpr (RS >= 16) a = dpp_add<0x140>(a);
     return a;
 }
-// Dot product of a row slice with a column slice, four independent accumulators.
+// Dot products of row slices with a column slice, one accumulator each.  The
+// recurrence kernels are bound by VALU issue (wave64 FP32 at 4 cycles an
+// instruction), so the adds that would join split accumulators cost more
+// than the shorter dependent chains save.
 template <int RPT>
-__device__ __forceinline__ float dot4(const float (&a)[RPT], const float (&s)[RPT]) {
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+__device__ __forceinline__ float row_dot(const float (&a)[RPT], const float (&s)[RPT]) {
+    float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < RPT; i += 4) {
-        a0 = fmaf(a[i], s[i], a0);
-        a1 = fmaf(a[i + 1], s[i + 1], a1);
-        a2 = fmaf(a[i + 2], s[i + 2], a2);
-        a3 = fmaf(a[i + 3], s[i + 3], a3);
-    }
-    return (a0 + a1) + (a2 + a3);
+    for (int i = 0; i < RPT; ++i) acc = fmaf(a[i], s[i], acc);
+    return acc;
 }
-// Dot products of two row slices with one column slice, four independent
-// accumulators each (RPT % 4 == 0), so the dependent chains are RPT / 4 FMAs long.
 template <int RPT>
-__device__ __forceinline__ void dot4x2(const float (&a)[RPT], const float (&b)[RPT], const float (&s)[RPT],
-                                       float& da, float& db) {
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+__device__ __forceinline__ void row_dot2(const float (&a)[RPT], const float (&b)[RPT], const float (&s)[RPT],
+                                        float& da, float& db) {
+    float x = 0.f, y = 0.f;
 #pragma unroll
-    for (int i = 0; i < RPT; i += 4) {
-        a0 = fmaf(a[i], s[i], a0);
-        b0 = fmaf(b[i], s[i], b0);
-        a1 = fmaf(a[i + 1], s[i + 1], a1);
-        b1 = fmaf(b[i + 1], s[i + 1], b1);
-        a2 = fmaf(a[i + 2], s[i + 2], a2);
-        b2 = fmaf(b[i + 2], s[i + 2], b2);
-        a3 = fmaf(a[i + 3], s[i + 3], a3);
-        b3 = fmaf(b[i + 3], s[i + 3], b3);
+    for (int i = 0; i < RPT; ++i) {
+        x = fmaf(a[i], s[i], x);
+        y = fmaf(b[i], s[i], y);
     }
-    da = (a0 + a1) + (a2 + a3);
-    db = (b0 + b1) + (b2 + b3);
+    da = x;
+    db = y;
 }
 
 // Four consecutive elements of a q or k row as loaded, converted only when

@@ -205,13 +205,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // GATED: inclusive scan of the chunk's log-gates (rows past the end read 0), in the
     // base-2 domain: lane t gets G_t * log2(e), so that every decay is one v_exp_f32 (2^x)
     auto gate_scan = [&](const unsigned char* rb) {
-        float x = reinterpret_cast<const float*>(rb + G::R_GS)[lane] * 1.44269504088896341f;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float y = __shfl_up(x, off);
-            if (lane >= off) x += y;
-        }
-        return x;
+        return wave_prefix_sum(reinterpret_cast<const float*>(rb + G::R_GS)[lane] * 1.44269504088896341f);
     };
     // GATED: the scanned gates of token 16b + l16 (col) and of tokens 16b + 4lg + [0, 4)
     // (row), through this producer's LDS scratch (one write, eight reads; a wave's LDS

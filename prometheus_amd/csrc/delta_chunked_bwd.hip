@@ -623,12 +623,7 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
             for (int m = 0; m < 4; ++m) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float x = dbp[m][r];
-                    x += __shfl_xor(x, 1);
-                    x += __shfl_xor(x, 2);
-                    x += __shfl_xor(x, 4);
-                    x += __shfl_xor(x, 8);
-                    dbp[m][r] = x;
+                    dbp[m][r] = row16_sum(dbp[m][r]);
                 }
                 if (l16 == 0) *reinterpret_cast<f32x4_t*>(db1 + w * kC + 16 * m + 4 * lg) = dbp[m];
             }
@@ -759,12 +754,7 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         for (int m = 0; m < 4; ++m) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float x = db2p[m][r];
-                x += __shfl_xor(x, 1);
-                x += __shfl_xor(x, 2);
-                x += __shfl_xor(x, 4);
-                x += __shfl_xor(x, 8);
-                db2p[m][r] = x;
+                db2p[m][r] = row16_sum(db2p[m][r]);
             }
             if (l16 == 0) *reinterpret_cast<f32x4_t*>(db2 + w * kC + 16 * m + 4 * lg) = db2p[m];
         }

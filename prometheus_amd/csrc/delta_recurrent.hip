@@ -150,11 +150,8 @@ __global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
                     ssk = fmaf(xk[c2], xk[c2], ssk);
                     ssq = fmaf(xq[c2], xq[c2], ssq);
                 }
-#pragma unroll
-                for (int m = 1; m < DP / 4; m <<= 1) {
-                    ssk += __shfl_xor(ssk, m);
-                    ssq += __shfl_xor(ssq, m);
-                }
+                ssk = lane_sum<DP / 4>(ssk);
+                ssq = lane_sum<DP / 4>(ssq);
                 const float dk = fmaxf(sqrtf(ssk), 1e-6f), dq = fmaxf(sqrtf(ssq), 1e-6f);
 #pragma unroll
                 for (int c2 = 0; c2 < 4; ++c2) {
@@ -165,8 +162,7 @@ __global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
             float qk = 0.f;
 #pragma unroll
             for (int c2 = 0; c2 < 4; ++c2) qk = fmaf(xq[c2], xk[c2], qk);
-#pragma unroll
-            for (int m = 1; m < DP / 4; m <<= 1) qk += __shfl_xor(qk, m);
+            qk = lane_sum<DP / 4>(qk);
             if (grp < NG) {
                 const int pos = j * DPL + (d / RPT) * SL + d % RPT;
                 *reinterpret_cast<float4*>(sk + pos) = make_float4(xk[0], xk[1], xk[2], xk[3]);

@@ -38,6 +38,17 @@ __device__ __forceinline__ float col_sum(float a) {
     if constexpr (RS >= 16) a = dpp_add<0x140>(a);
     return a;
 }
+// Sum over aligned groups of N adjacent lanes (N a power of two <= 64), every lane
+// of a group ending with the same bits: DPP inside 16-lane rows (col_sum), then
+// one lane permute per doubling beyond 16.
+template <int N>
+__device__ __forceinline__ float lane_sum(float x) {
+    x = col_sum<(N < 16 ? N : 16)>(x);
+    if constexpr (N >= 32) x += __shfl_xor(x, 16);
+    if constexpr (N >= 64) x += __shfl_xor(x, 32);
+    return x;
+}
+
 // Dot products of row slices with a column slice, one accumulator each.  The
 // recurrence kernels are bound by VALU issue (wave64 FP32 at 4 cycles an
 // instruction), so the adds that would join split accumulators cost more

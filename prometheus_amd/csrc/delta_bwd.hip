@@ -431,8 +431,8 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
         for (int j = wave; j < nst; j += NWV) {
             float sum = 0.f;
             for (int x = lane; x < D; x += 64) sum += so[j * D + x];
-            for (int m = 1; m < 64; m <<= 1) sum += __shfl_xor(sum, m);
-            if (lane == 0) gb_t[static_cast<size_t>(tok0 + lo + j) * H + h] = sum;
+            sum = wave_sum_row3(sum);
+            if (lane == 63) gb_t[static_cast<size_t>(tok0 + lo + j) * H + h] = sum;
         }
     };
 

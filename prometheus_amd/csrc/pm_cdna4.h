@@ -205,32 +205,6 @@ __device__ __forceinline__ void lds_barrier() {
     __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 // Wait for this wave's outstanding buffer loads (and so its LDS copies).
-// x plus the value DPP control CTRL selects, in the 16-lane rows ROW_MASK enables
-// (other rows, and lanes whose source is outside their row, add 0).
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_add_rows(float x) {
-    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
-}
-// Sum over each 16-lane row without LDS, every lane of the row ending with the same
-// bits: quad_perm [1,0,3,2] and [2,3,0,1], then row_half_mirror and row_mirror.
-__device__ __forceinline__ float row16_sum(float x) {
-    x = dpp_add_rows<0xB1, 0xF>(x);
-    x = dpp_add_rows<0x4E, 0xF>(x);
-    x = dpp_add_rows<0x141, 0xF>(x);
-    return dpp_add_rows<0x140, 0xF>(x);
-}
-// Inclusive prefix sum over the wave's 64 lanes without LDS: row_shr 1, 2, 4, 8
-// inside each row, then row_bcast:15 adds row 0's (row 2's) total to row 1 (row 3),
-// and row_bcast:31 adds rows 0-1's total to rows 2 and 3.
-__device__ __forceinline__ float wave_prefix_sum(float x) {
-    x = dpp_add_rows<0x111, 0xF>(x);
-    x = dpp_add_rows<0x112, 0xF>(x);
-    x = dpp_add_rows<0x114, 0xF>(x);
-    x = dpp_add_rows<0x118, 0xF>(x);
-    x = dpp_add_rows<0x142, 0xA>(x);
-    return dpp_add_rows<0x143, 0xC>(x);
-}
-
 __device__ __forceinline__ void wait_copies() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // 2^x in one v_exp_f32 (about 1 ulp; 0 for x below the fp32 range).

@@ -7,8 +7,15 @@
 //   16x16x16: same with slot s <-> 4g+s;
 //   both:     accumulator lane l, element i -> C[4(l/16)+i][l%16].
 // The host compares C with a NumPy product; any wrong assumption shows.
+//
+// dpp_probe runs the DPP lane reductions of pm_common.h / pm_rec.h on one
+// wave's 64 values: out[64 j + lane] for j = 0 prefix sum, 1 row16_sum,
+// 2 wave_sum_row3, 3..8 lane_sum<2, 4, 8, 16, 32, 64>.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "pm_common.h"
+#include "pm_rec.h"
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
@@ -44,6 +51,27 @@ extern "C" int mfma_probe(const uint16_t* a32, const uint16_t* b32, float* c32,
                           const uint16_t* a16, const uint16_t* b16, float* c16) {
     hipLaunchKernelGGL(probe32, dim3(1), dim3(64), 0, 0, a32, b32, c32);
     hipLaunchKernelGGL(probe16, dim3(1), dim3(64), 0, 0, a16, b16, c16);
+    if (hipGetLastError() != hipSuccess) return 1;
+    return hipDeviceSynchronize() == hipSuccess ? 0 : 2;
+}
+
+__global__ void dpp_probe_kernel(const float* x, float* out) {
+    const int l = threadIdx.x;
+    const float v = x[l];
+    out[l] = pm::wave_prefix_sum(v);
+    out[64 + l] = pm::row16_sum(v);
+    out[128 + l] = pm::wave_sum_row3(v);
+    out[192 + l] = pm::lane_sum<2>(v);
+    out[256 + l] = pm::lane_sum<4>(v);
+    out[320 + l] = pm::lane_sum<8>(v);
+    out[384 + l] = pm::lane_sum<16>(v);
+    out[448 + l] = pm::lane_sum<32>(v);
+    out[512 + l] = pm::lane_sum<64>(v);
+}
+
+// x: 64 floats, out: 9 x 64 floats (device pointers).
+extern "C" int dpp_probe(const float* x, float* out) {
+    hipLaunchKernelGGL(dpp_probe_kernel, dim3(1), dim3(64), 0, 0, x, out);
     if (hipGetLastError() != hipSuccess) return 1;
     return hipDeviceSynchronize() == hipSuccess ? 0 : 2;
 }

@@ -94,6 +94,29 @@ def test_mfma_layout_probe():
     np.testing.assert_allclose(_np(c16), e16, rtol=1e-5, atol=1e-5)
 
 
+def test_dpp_lane_reductions_probe():
+    """The DPP reductions the kernels use (gate scan, row and wave sums, lane-group
+    sums), on one wave: against NumPy, and every lane of a group with the same bits."""
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(__file__), "hip", "libmfma_probe.so"))
+    x = np.random.default_rng(3).standard_normal(64).astype(np.float32)
+    dx = torch.from_numpy(x).cuda()
+    out = torch.full((9, 64), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    assert lib.dpp_probe(ctypes.c_void_p(dx.data_ptr()), ctypes.c_void_p(out.data_ptr())) == 0
+    r = _np(out)
+    x64 = x.astype(np.float64)
+    np.testing.assert_allclose(r[0], np.cumsum(x64), rtol=1e-5, atol=1e-5)
+    rows = np.repeat(x64.reshape(4, 16).sum(axis=1), 16)
+    np.testing.assert_allclose(r[1], rows, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(r[2][48:], np.full(16, x64.sum()), rtol=1e-5, atol=1e-5)
+    for j, n in enumerate((2, 4, 8, 16, 32, 64), start=3):
+        groups = r[j].reshape(64 // n, n)
+        np.testing.assert_allclose(groups[:, 0], x64.reshape(64 // n, n).sum(axis=1), rtol=1e-5, atol=1e-5)
+        assert (groups == groups[:, :1]).all(), f"lane_sum<{n}>: lanes of a group differ"
+    r1 = r[1].reshape(4, 16)
+    assert (r1 == r1[:, :1]).all(), "row16_sum: lanes of a row differ"
+
+
 # ---------------------------------------------------------------------------
 # the reference's own cases (fp32 -> per-token kernel)
 # ---------------------------------------------------------------------------

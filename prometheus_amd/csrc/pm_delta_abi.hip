@@ -14,8 +14,6 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include <atomic>
-
 #include "pm_common.h"
 #include "pm_internal.h"
 #include "../../include/pm_delta.h"
@@ -57,8 +55,11 @@ hipError_t launch_copy_f32(float* dst, const float* src, size_t n, hipStream_t s
 namespace {
 
 thread_local char g_err[512] = "";
-std::atomic<int> g_path{0};
-std::atomic<int> g_tile{0};
+// Kernel-selection knobs (pm_delta_set_path / pm_delta_set_tile): per calling
+// thread, so that a workspace-size query and the call it sizes always see the
+// same setting, whatever other threads select meanwhile.
+thread_local int g_path = 0;
+thread_local int g_tile = 0;
 
 int fail(int code, const char* fmt, ...) {
     va_list ap;
@@ -108,13 +109,13 @@ int forward(const void* q, const void* k, const void* v, const float* beta, cons
         return e == hipSuccess ? 0 : hip_fail(e, "state copy");
     }
 
-    const int path = g_path.load();
+    const int path = g_path;
     const bool in_bf16 = in_dtype == PM_DTYPE_BF16;
     const bool want_chunked = path != 1;
     const bool can_chunked = in_bf16 && pm::chunked_supported(D, H) && aligned(q, 16) &&
                              aligned(k, 16) && aligned(v, 16) &&
                              (out_dtype == PM_DTYPE_F32 ? aligned(o, 16) : aligned(o, 8));
-    if (path == 2 && !can_chunked)
+    if (path >= 2 && !can_chunked)
         return fail(PM_E_UNSUPPORTED,
                     "chunked kernel needs bf16 inputs, D in {64, 128} and 16-byte aligned "
                     "q/k/v/o (got in_dtype %d, D %d)",
@@ -123,8 +124,9 @@ int forward(const void* q, const void* k, const void* v, const float* beta, cons
         pm::ChunkedArgs a{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                           static_cast<const uint16_t*>(v), beta, s0, o, s_out, cu, n_seq,
                           varlen ? total_T : T, H, D,
-                          out_dtype == PM_DTYPE_BF16, g_tile.load()};
+                          out_dtype == PM_DTYPE_BF16, g_tile};
         a.g = g;
+        a.pipeline = path == 3;
         hipError_t e = pm::launch_chunked(a, st);
         return e == hipSuccess ? 0 : hip_fail(e, "chunked forward launch");
     }
@@ -169,6 +171,18 @@ int step(float* s_inout, const void* q, const void* k, const void* v, const floa
     return e == hipSuccess ? 0 : hip_fail(e, "decode step launch");
 }
 
+// Which backward serves (B, T, H, D, in_dtype) under the current path setting:
+// the chunked kernel for bf16 inputs with D in {64, 128}, else the per-token one.
+bool bwd_chunked(int H, int D, int in_dtype) {
+    return g_path != 1 && in_dtype == PM_DTYPE_BF16 && pm::chunked_bwd_supported(D, H);
+}
+
+size_t bwd_ws_bytes(int B, int T, int H, int D, int in_dtype) {
+    const long n_pairs = static_cast<long>(B) * H;
+    if (bwd_chunked(H, D, in_dtype)) return pm::chunked_bwd_ws(n_pairs, T, D).bytes;
+    return sizeof(float) * pm::bwd_workspace_floats(n_pairs, T, D);
+}
+
 }  // namespace
 
 extern "C" {
@@ -178,18 +192,6 @@ int pm_abi_version(void) { return PM_DELTA_ABI_VERSION; }
 const char* pm_last_error(void) { return g_err; }
 
 size_t pm_delta_workspace_bytes(int, int, int, int, int) { return 0; }
-
-// Which backward serves (B, T, H, D, in_dtype) under the current path setting:
-// the chunked kernel for bf16 inputs with D in {64, 128}, else the per-token one.
-bool bwd_chunked(int H, int D, int in_dtype) {
-    return g_path.load() != 1 && in_dtype == PM_DTYPE_BF16 && pm::chunked_bwd_supported(D, H);
-}
-
-size_t bwd_ws_bytes(int B, int T, int H, int D, int in_dtype) {
-    const long n_pairs = static_cast<long>(B) * H;
-    if (bwd_chunked(H, D, in_dtype)) return pm::chunked_bwd_ws(n_pairs, T, D).bytes;
-    return sizeof(float) * pm::bwd_workspace_floats(n_pairs, T, D);
-}
 
 size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype) {
     if (B < 0 || T < 0 || H < 0 || D < 1 || D > pm::kBwdMaxD) return 0;
@@ -219,7 +221,7 @@ int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
     for (const void* p : f32s)
         if (p && !aligned(p, 4)) return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
     const bool chunked = bwd_chunked(H, D, in_dtype);
-    if (g_path.load() == 2 && !chunked)
+    if (g_path >= 2 && !chunked)
         return fail(PM_E_UNSUPPORTED,
                     "chunked backward needs bf16 inputs and D in {64, 128} (got in_dtype %d, D %d)",
                     in_dtype, D);
@@ -243,14 +245,18 @@ int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
 }
 
 int pm_delta_set_path(int path) {
-    if (path < 0 || path > 2) return fail(PM_E_UNSUPPORTED, "path %d not in {0, 1, 2}", path);
-    return g_path.exchange(path);
+    if (path < 0 || path > 3) return fail(PM_E_UNSUPPORTED, "path %d not in {0, 1, 2, 3}", path);
+    const int old = g_path;
+    g_path = path;
+    return old;
 }
 
 int pm_delta_set_tile(int dv_tile) {
     if (dv_tile != 0 && dv_tile != 16 && dv_tile != 32 && dv_tile != 64)
         return fail(PM_E_UNSUPPORTED, "dv_tile %d not in {0, 16, 32, 64}", dv_tile);
-    return g_tile.exchange(dv_tile);
+    const int old = g_tile;
+    g_tile = dv_tile;
+    return old;
 }
 
 int pm_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
@@ -340,11 +346,11 @@ int pm_linear_attention(const void* q, const void* k, const void* v, const float
                           : pm::launch_fill_zero(s_out, s_elems, st);
         return e == hipSuccess ? 0 : hip_fail(e, "state copy");
     }
-    const int path = g_path.load();
+    const int path = g_path;
     const bool can_chunked = in_dtype == PM_DTYPE_BF16 && pm::chunked_supported(D, H) &&
                              aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
                              (out_dtype == PM_DTYPE_F32 ? aligned(o, 16) : aligned(o, 8));
-    if (path == 2 && !can_chunked)
+    if (path >= 2 && !can_chunked)
         return fail(PM_E_UNSUPPORTED,
                     "chunked kernel needs bf16 inputs, D in {64, 128} and 16-byte aligned "
                     "q/k/v/o (got in_dtype %d, D %d)",
@@ -352,7 +358,7 @@ int pm_linear_attention(const void* q, const void* k, const void* v, const float
     if (path != 1 && can_chunked) {
         pm::ChunkedArgs a{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                           static_cast<const uint16_t*>(v), nullptr, s0, o, s_out, nullptr, B, T, H, D,
-                          out_dtype == PM_DTYPE_BF16, g_tile.load(), true};
+                          out_dtype == PM_DTYPE_BF16, g_tile, true};
         hipError_t e = pm::launch_chunked(a, st);
         return e == hipSuccess ? 0 : hip_fail(e, "chunked linear attention launch");
     }

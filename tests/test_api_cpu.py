@@ -264,10 +264,11 @@ def test_path_and_tile_switches():
     old = _native.set_path(1)
     try:
         assert _native.set_path(2) == 1
+        assert _native.set_path(3) == 2
     finally:
         _native.set_path(old)
     with pytest.raises(_native.NativeError):
-        _native.set_path(3)
+        _native.set_path(4)
     old = _native.set_tile(32)
     try:
         assert _native.set_tile(16) == 32
@@ -342,3 +343,52 @@ def test_gated_validation_without_gpu():
                                   None) == _native.E_ALIGN
     assert lib.pm_gated_delta_fwd(p, p, p, p, p, None, p, p, 1, 4, 2, 300, 0, 0, None) == _native.E_SHAPE
     assert lib.pm_gated_delta_step(p, p, p, p, p, None, p, 1, 2, 8, 0, None) == _native.E_NULL
+
+
+def test_selection_knobs_are_per_thread():
+    """pm_delta_set_path / pm_delta_set_tile act on the calling thread only, so a
+    workspace-size query and the call it sizes agree whatever another thread
+    selects meanwhile (no GPU needed: both calls are host-only)."""
+    import threading
+
+    L = _native.lib()
+    B, T, H, D = 2, 300, 4, 128
+    bf16 = _native.DTYPE_BF16
+    chunked = L.pm_delta_bwd_workspace_bytes(B, T, H, D, bf16)
+    L.pm_delta_set_path(1)
+    try:
+        per_token = L.pm_delta_bwd_workspace_bytes(B, T, H, D, bf16)
+    finally:
+        L.pm_delta_set_path(0)
+    assert chunked != per_token and chunked > 0 and per_token > 0
+
+    barrier = threading.Barrier(2)
+    seen = {}
+
+    def worker(path, key):
+        L.pm_delta_set_path(path)
+        barrier.wait()  # both threads have selected before either queries
+        sizes = [L.pm_delta_bwd_workspace_bytes(B, T, H, D, bf16) for _ in range(200)]
+        barrier.wait()
+        seen[key] = (L.pm_delta_set_path(0), set(sizes))
+
+    threads = [threading.Thread(target=worker, args=(1, "a")), threading.Thread(target=worker, args=(2, "b"))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert seen["a"] == (1, {per_token})
+    assert seen["b"] == (2, {chunked})
+    assert L.pm_delta_set_path(0) == 0  # this thread never selected anything
+
+
+def test_no_unprefixed_exports():
+    """The library exports exactly the pm_* entry points of include/pm_delta.h (no
+    internal helper leaks as an unprefixed C symbol)."""
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--defined-only", _native.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    names = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    c_names = {n for n in names if not n.startswith("_Z")}
+    assert c_names - {"_init", "_fini"} == set(_native.EXPORTS), sorted(c_names)

@@ -208,19 +208,24 @@ const char* pm_last_error(void);
 int pm_abi_version(void);
 
 /*
- * Kernel selection for pm_delta_fwd, pm_delta_fwd_varlen and pm_delta_bwd,
- * for tests and benchmarks: 0 = automatic (chunked MFMA kernel where the
- * shape and dtype allow, else the per-token kernel), 1 = always the
- * per-token kernel, 2 = chunked kernel required (PM_E_UNSUPPORTED when it
- * cannot serve the call).  The previous value is returned.  Process-wide.
+ * Kernel selection for pm_delta_fwd, pm_delta_fwd_varlen, pm_delta_bwd and
+ * pm_linear_attention, for tests and benchmarks: 0 = automatic (chunked MFMA
+ * kernel where the shape and dtype allow, else the per-token kernel), 1 =
+ * always the per-token kernel, 2 = chunked kernel required
+ * (PM_E_UNSUPPORTED when it cannot serve the call), 3 = as 2, with the plain
+ * forward on the deep four-wave pipeline kernel (copies two stages ahead, T
+ * built over two stages; bitwise the same results as the default kernel).  The
+ * previous value is returned.  The setting is per calling thread: a
+ * workspace-size query and the call it sizes, made on one thread, always see
+ * the same setting.
  */
 int pm_delta_set_path(int path);
 
 /*
  * Column-tile width (d_v columns per workgroup) the chunked kernel uses:
  * 0 = automatic (32 when B*H*(D/32) >= 256, else 16), else 16, 32 or 64;
- * 64 is accepted and served with 32-column workgroups (a 64-column
- * workgroup would leave no producer waves).  Returns the previous value.
+ * 64 is accepted and served with 32-column workgroups.  Returns the previous
+ * value.  Per calling thread, as pm_delta_set_path.
  */
 int pm_delta_set_tile(int dv_tile);
 

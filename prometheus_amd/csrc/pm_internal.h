@@ -67,9 +67,14 @@ struct ChunkedArgs {
     // Gated variant (not with norm): log-gates per (token, head), alpha = exp(g)
     // (g <= 0 keeps every in-chunk decay factor at most 1).
     const float* g = nullptr;
+    // Plain forward only: run the deep four-wave pipeline (delta_chunked_pipe.hip)
+    // instead of the single-stage kernel.  Same results, bit for bit.
+    bool pipeline = false;
 };
 bool chunked_supported(int D, int H);  // D in {64, 128}, H*D <= 2^24
 hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st);
+// The plain forward (no norm, no gates) as the deep four-wave pipeline, dv in {16, 32}.
+hipError_t launch_chunked_pipe(const ChunkedArgs& a, int dv, hipStream_t st);
 // The same kernel writing, instead of O and the final state, the state at
 // the start of every chunk as bf16 rows of S^T (fixed-length batches only):
 // s_hist holds n_seq*H x ceil(T/64) x D x D values.

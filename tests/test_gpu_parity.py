@@ -474,3 +474,40 @@ def test_cfg4_decode_steps_vs_c_oracle():
         e_o = cref.delta_step(s_cpu, x.q_bits, x.k_bits, x.v_bits, x.beta, threads=CPU_THREADS)
         assert_f32_parity(_np(o), e_o, f"cfg4 step {t} o")
     assert_f32_parity(_np(s_dev), s_cpu, "cfg4 final S")
+
+
+@pytest.mark.parametrize("shape,tile,s0_std,out16", [
+    ((1, 64, 1, 128), 0, None, False), ((2, 150, 2, 128), 0, 0.02, False), ((1, 1, 3, 128), 32, None, False),
+    ((2, 257, 3, 64), 0, 0.02, False), ((3, 300, 2, 128), 16, 0.02, True), ((1, 130, 4, 64), 32, None, True),
+    ((4, 1024, 16, 128), 0, None, False),
+])
+def test_pipeline_form_is_bitwise_the_default(shape, tile, s0_std, out16):
+    """pm_delta_set_path(3) runs the plain forward on the deep four-wave pipeline
+    kernel; every product is formed in the same order, so O and S equal the
+    default kernel's bit for bit (tails, D 64/128, both tile widths, S0, bf16 O)."""
+    x, (q, k, v, b, s0) = _bf16_case(shape, seed=sum(shape) + tile, s0_std=s0_std)
+    odt = torch.bfloat16 if out16 else None
+    with _path(2, tile):
+        o2, s2 = kernels.chunked_delta_rule(q, k, v, b, s0, out_dtype=odt)
+    with _path(3, tile):
+        o3, s3 = kernels.chunked_delta_rule(q, k, v, b, s0, out_dtype=odt)
+    torch.cuda.synchronize()
+    assert torch.equal(o2, o3) and torch.equal(s2, s3)
+    if shape[1] <= 300:
+        e_o, e_s = ref.wy_chunked_fwd(x.q, x.k, x.v, x.beta, x.s0, chunk=64)
+        assert_bf16_parity(_np(o3.float()), e_o, "pipeline O")
+        assert_bf16_parity(_np(s3), e_s, "pipeline S")
+
+
+def test_pipeline_form_varlen_is_bitwise_the_default():
+    lens = np.array([64, 1, 0, 130, 700, 3000, 257])
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    n = int(cu[-1])
+    x, (q, k, v, b, _) = _bf16_case((n, 4, 128), seed=91)
+    for tile in (0, 16):
+        with _path(2, tile):
+            o2, s2 = kernels.chunked_delta_rule_varlen(q, k, v, b, cu)
+        with _path(3, tile):
+            o3, s3 = kernels.chunked_delta_rule_varlen(q, k, v, b, cu)
+        torch.cuda.synchronize()
+        assert torch.equal(o2, o3) and torch.equal(s2, s3)

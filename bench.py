@@ -102,6 +102,15 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def cpu_threads() -> int:
+    """Threads for the CPU baseline: OMP_NUM_THREADS when the environment sets it (the
+    GPU box sets it to its CPU share), else every CPU this process may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return max(1, len(os.sched_getaffinity(0)))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -119,6 +128,8 @@ def main():
                     help="JSON with measured HBM bytes per launch (from rocprofv3 --pmc)")
     ap.add_argument("--mfma-counters", default=os.path.join(ROOT, "profiles", "mfma_cfg1.json"),
                     help="JSON with rocprofv3 MfmaUtil / MfmaFlopsBF16 for the forward kernel")
+    ap.add_argument("--decode-traffic", default=os.path.join(ROOT, "profiles", "traffic_cfg4_decode.json"),
+                    help="JSON with measured HBM bytes per decode-step launch (rocprofv3 --pmc)")
     ap.add_argument("--tile", type=int, default=0, help="d_v tile of the chunked kernel (0 auto)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run 3 launches of a plain 1 GiB fp32 elementwise copy (torch.neg, "
@@ -132,7 +143,7 @@ def main():
 
     import torch
 
-    from prometheus_amd import _native
+    from prometheus_amd import _native, synth
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -196,6 +207,54 @@ def main():
                          "executed_bf16_mfma_flop": mc.get("executed_bf16_mfma_flop"),
                          "executed_over_algorithmic": mc.get("executed_over_algorithmic")}
 
+    def time_fwd(out_code, out_t, calls=10):
+        q, k, v, beta = sets[0]
+
+        def f():
+            rc = lib.pm_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), None,
+                                  out_t.data_ptr(), s.data_ptr(), B, T, H, D, _native.DTYPE_BF16,
+                                  out_code, CHUNK, None, 0, stream.cuda_stream)
+            _native.check(rc)
+
+        f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(calls):
+            f()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / calls
+
+    # the opt-in bf16 output (out_dtype=bf16): 273.7 MB instead of 340.8 MB per call
+    o16 = torch.empty((B, T, H, D), dtype=torch.bfloat16, device=dev)
+    b16_ms = time_fwd(_native.DTYPE_BF16, o16)
+    b16_bytes = fwd_bytes(B, T, H, D, s_out=2)
+    bf16_out = {
+        "workload": "cfg1 forward, bf16 O (pm_delta_fwd out_dtype bf16)",
+        "kernel_us": b16_ms * 1e3,
+        "tokens_per_s": tokens / (b16_ms * 1e-3),
+        "algorithmic_bytes": b16_bytes,
+        "roofline": {"bound": "hbm", "achieved": b16_bytes / (b16_ms * 1e-3) / 1e9,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": b16_bytes / (b16_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        "mfma": {"achieved_tflops": flops / (b16_ms * 1e-3) / 1e12, "peak_tflops": BF16_PEAK_TFLOPS,
+                 "frac": flops / (b16_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS},
+    }
+    del o16
+    # the deep-pipeline form of the chunked kernel (pm_delta_set_path(3)): bitwise the same
+    # results; reported beside the default
+    old_path = _native.set_path(3)
+    try:
+        pipe_ms = time_fwd(_native.DTYPE_F32, o)
+    finally:
+        _native.set_path(old_path)
+    pipeline_form = {"workload": "cfg1 forward, chunked kernel in its deep-pipeline form (path 3)",
+                     "kernel_us": pipe_ms * 1e3,
+                     "roofline_frac": nbytes / (pipe_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    launch(last)  # the output the parity check reads
+    torch.cuda.synchronize()
+
     # parity of the timed output against the C restatement (which is also the CPU baseline)
     cpu = None
     parity = None
@@ -204,7 +263,7 @@ def main():
 
         q, k, v, beta = sets[last]
         hq, hk, hv, hb = bits(q), bits(k), bits(v), beta.cpu().numpy()
-        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        threads = cpu_threads()
         print(f"[bench] CPU baseline on {threads} threads", file=sys.stderr, flush=True)
         cref.delta_fwd(hq[:, :64], hk[:, :64], hv[:, :64], hb[:, :64], None, threads=threads)
         # the full batch, repeated for about CPU_SAMPLE_S seconds of CPU work
@@ -222,8 +281,21 @@ def main():
         cpu = {"value": tokens / cpu_s, "unit": "tokens/s", "cores": threads, "kind": "port",
                "sample": f"full cfg1 batch (B4 T4096 H16 D128, bf16 inputs upcast to fp32), "
                          f"{reps} repeats, {cpu_s:.3f} s each; C restatement of the reference's per-token rank-1 "
-                         f"recurrence (oracle/delta_ref.c), OpenMP over 64 (b,h) sequences; "
-                         f"CPU: {cpu_model()}"}
+                         f"recurrence (oracle/delta_ref.c), OpenMP over 64 (b,h) sequences",
+               "cpu_model": cpu_model(),
+               "affinity_cpus": len(os.sched_getaffinity(0)),
+               "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
+               "threads_used": threads,
+               "threads_rule": "OMP_NUM_THREADS when set (the box's CPU share), else the affinity count"}
+        # the other BASELINE configurations on the same CPU path, per call / per step
+        x0 = synth.fwd_inputs((1, 256, 4, 64), seed=0, dtype="fp32")
+        t1 = time.perf_counter()
+        reps0 = 0
+        while time.perf_counter() - t1 < 1.0:
+            cref.delta_fwd(x0.q, x0.k, x0.v, x0.beta, None, threads=threads)
+            reps0 += 1
+        cpu["cfg0_ms_per_call"] = (time.perf_counter() - t1) * 1e3 / reps0
+        cpu["cfg0_tokens_per_s"] = 256 / ((time.perf_counter() - t1) / reps0)
 
     # decode step, cfg4: B256 H32 D128, fp32 state updated in place, 64 steps
     Bd, Hd = 256, 32
@@ -248,6 +320,8 @@ def main():
                                stream.cuda_stream)
         _native.check(rc)
 
+    # the state before any step, for the parity check of the whole in-place sequence
+    state0_host = state.cpu().numpy() if not args.no_cpu_baseline else None
     for i in range(4):
         step(i)
     torch.cuda.synchronize()
@@ -260,6 +334,10 @@ def main():
     torch.cuda.synchronize()
     step_ms = float(np.mean([a.elapsed_time(b) for a, b in dev_]))
     dbytes = step_bytes(Bd, Hd, D)
+    dtraffic = None
+    if os.path.exists(args.decode_traffic):
+        with open(args.decode_traffic) as f:
+            dtraffic = json.load(f).get("bytes_per_launch")
     decode = {
         "workload": "cfg4 decode step B256 H32 D128, bf16 token, fp32 state in place",
         "steps": args.decode_steps,
@@ -267,8 +345,30 @@ def main():
         "tokens_per_s": Bd / (step_ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": dbytes / (step_ms * 1e-3) / 1e9,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": dbytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+                     "frac": dbytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "traffic": dtraffic},
     }
+    if state0_host is not None:
+        # every step the GPU ran (4 untimed + the timed ones), replayed on the C restatement
+        from oracle import cref
+
+        threads = cpu_threads()
+        s_ref = state0_host
+        htoks = [(bits(a), bits(b_), bits(c_), d_.cpu().numpy()) for a, b_, c_, d_ in toks]
+        n_all = 4 + args.decode_steps
+        t1 = time.perf_counter()
+        for i in range(n_all):
+            e_od = cref.delta_step(s_ref, *htoks[i % 2], threads=threads)
+        cpu_step_s = (time.perf_counter() - t1) / n_all
+        rel = lambda a, b: float(np.linalg.norm((a - b).ravel()) / np.linalg.norm(b.ravel()))  # noqa
+        decode["parity"] = {"steps_checked": n_all, "rel_l2_final_state": rel(state.cpu().numpy(), s_ref),
+                            "rel_l2_last_o": rel(od.cpu().numpy(), e_od), "bound": 1e-5}
+        decode["parity"]["ok"] = (decode["parity"]["rel_l2_final_state"] <= 1e-5
+                                  and decode["parity"]["rel_l2_last_o"] <= 1e-5)
+        if cpu is not None:
+            cpu["cfg4_ms_per_step"] = cpu_step_s * 1e3
+            cpu["cfg4_tokens_per_s"] = Bd / cpu_step_s
+        del s_ref
 
     # the same decode through a serving state cache: a pool of 2*B slots, the batch's
     # requests on a random half of them (pm_delta_step_slots)
@@ -528,6 +628,8 @@ def main():
         "cpu_baseline": cpu,
         "parity": parity,
         "decode": decode,
+        "bf16_out": bf16_out,
+        "pipeline_form": pipeline_form,
         "model_linear_attention": model_la,
         "fp32_forward": fp32_fwd,
         "gated": gated,
@@ -535,6 +637,8 @@ def main():
     }
     print(json.dumps(line), flush=True)
     if parity is not None and not parity["ok"]:
+        sys.exit(3)
+    if decode.get("parity") is not None and not decode["parity"]["ok"]:
         sys.exit(3)
 
 

@@ -459,10 +459,13 @@ def test_step_matches_forward_with_state(dim):
 
 
 def test_cfg4_decode_steps_vs_c_oracle():
+    """BASELINE cfg4 in full: B256 H32 D128, 64 consecutive in-place steps, o checked
+    at every step and the state after the last one."""
     from oracle import cref
 
     c = synth.CONFIGS[4]
-    bsz, heads, dim, steps = c["B"], c["H"], c["D"], 8
+    bsz, heads, dim, steps = c["B"], c["H"], c["D"], c["steps"]
+    assert steps == 64
     rng = np.random.default_rng(4)
     s0 = rng.normal(0.0, c["s0_std"], (bsz, heads, dim, dim)).astype(np.float32)
     s_dev = _dev(s0)

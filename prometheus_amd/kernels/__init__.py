@@ -188,6 +188,10 @@ def _ptr(t) -> int | None:
     return None if t is None or t.numel() == 0 else t.data_ptr()
 
 
+def _aligned16(t):
+    return t if t is None or t.numel() == 0 or t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -221,6 +225,38 @@ def _forward(q, k, v, beta, state, chunk: int, out_dtype):
     return call, (qd, kd, vd, bd, sd), o, s_out
 
 
+def _wants_grad(*xs) -> bool:
+    return torch.is_grad_enabled() and any(isinstance(x, torch.Tensor) and x.requires_grad for x in xs)
+
+
+class _ChunkedDeltaRule(torch.autograd.Function):
+    """``chunked_delta_rule`` as a differentiable op: the forward kernel, and
+    ``chunked_delta_rule_bwd`` (pm_delta_bwd) as its backward -- the torch form of
+    the reference's ``jax.custom_vjp`` (kernels/__init__.py:591-658).  The config
+    is not differentiated; a ``state=None`` input has no gradient.  Gradients
+    come back in each input's dtype and device (autograd's contract); they are
+    computed in fp32 as the backward's outputs are."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, state, chunk, out_dtype):
+        call, (qd, kd, vd, bd, sd), o, s = _forward(q, k, v, beta, state, chunk, out_dtype)
+        ctx.save_for_backward(qd, kd, vd, bd, sd)
+        ctx.chunk = chunk
+        ctx.like = [(x.dtype, x.device) if isinstance(x, torch.Tensor) else None
+                    for x in (q, k, v, beta, state)]
+        return call.out(o), call.out(s)
+
+    @staticmethod
+    def backward(ctx, go, gs):
+        qd, kd, vd, bd, sd = ctx.saved_tensors
+        res = _DeltaResidual(q=qd, k=kd, v=vd, beta=bd, state0=sd, chunk=ctx.chunk)
+        grads = chunked_delta_rule_bwd(res, (go, gs))
+        out = []
+        for g, like, need in zip(grads, ctx.like, ctx.needs_input_grad[:5]):
+            out.append(g.to(device=like[1], dtype=like[0]) if (like is not None and need) else None)
+        return (*out, None, None)
+
+
 def chunked_delta_rule(q, k, v, beta, state=None, config=None, *, out_dtype=None):
     """Gated delta-rule linear attention (``kernels/__init__.py:591-619``).
 
@@ -228,9 +264,17 @@ def chunked_delta_rule(q, k, v, beta, state=None, config=None, *, out_dtype=None
     state: (batch, heads, dim, dim) recurrent state, zeros if None.
     Returns ``(output, next_state)``; output shaped like v (fp32 unless
     ``out_dtype`` asks for bf16), next_state fp32.
+
+    Differentiable like the reference's ``custom_vjp``: when autograd records
+    and a torch input requires grad, ``torch.autograd.grad`` / ``backward``
+    through ``(output, next_state)`` runs ``chunked_delta_rule_bwd`` (the
+    fused reverse kernels), never an unrolled graph of the recurrence.
     """
     cfg = LinearAttnConfig() if config is None else config
     chunk = _check_chunk(cfg)
+    if _wants_grad(q, k, v, beta, state):
+        _validate(q, k, v, beta, state)
+        return _ChunkedDeltaRule.apply(q, k, v, beta, state, chunk, out_dtype)
     call, _, o, s = _forward(q, k, v, beta, state, chunk, out_dtype)
     return call.out(o), call.out(s)
 
@@ -283,6 +327,9 @@ def chunked_delta_rule_bwd(residual: _DeltaResidual, grads):
         qd, kd, vd = call.dev(q, cdt), call.dev(k, cdt), call.dev(v, cdt)
         bd, sd = call.dev(beta, f32), call.dev(s0, f32)
         god, gsd = call.dev(go, f32), call.dev(gs, f32)
+        # the chunked backward reads q, k, v and dO with 16-byte vector loads: a view at an
+        # odd offset is copied to a fresh (aligned) buffer rather than refused
+        qd, kd, vd, god = (_aligned16(x) for x in (qd, kd, vd, god))
         gq = torch.empty((batch, seq, heads, dim), dtype=f32, device=call.device)
         gk, gv = torch.empty_like(gq), torch.empty_like(gq)
         gb = torch.empty((batch, seq, heads), dtype=f32, device=call.device)

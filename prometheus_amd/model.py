@@ -26,7 +26,7 @@ import numpy as np
 import torch
 
 from prometheus_amd import _native
-from prometheus_amd.kernels import _Call, _code, _ptr, _stream
+from prometheus_amd.kernels import _Call, _code, _DeltaResidual, _ptr, _stream, chunked_delta_rule_bwd
 
 __all__ = ["linear_attention", "_linear_attn"]
 
@@ -51,8 +51,61 @@ def _dtype(q, k, v) -> torch.dtype:
     return torch.float32
 
 
+def _l2n(x):
+    """``x / max(||x||, 1e-6)`` over the last axis (model/__init__.py:203-205)."""
+    return x / torch.clamp_min(torch.linalg.vector_norm(x, dim=-1, keepdim=True), 1e-6)
+
+
+def _run_linear_attention(qd, kd, vd, sd, cdt, device):
+    batch, seq, heads, dim = qd.shape
+    o = torch.empty(qd.shape, dtype=torch.float32, device=device)
+    s_out = torch.empty((batch, heads, dim, dim), dtype=torch.float32, device=device)
+    rc = _native.lib().pm_linear_attention(
+        _ptr(qd), _ptr(kd), _ptr(vd), _ptr(sd), _ptr(o), _ptr(s_out),
+        batch, seq, heads, dim, _code(cdt), _native.DTYPE_F32, _stream(device),
+    )
+    _native.check(rc)
+    return o, s_out
+
+
+class _LinearAttention(torch.autograd.Function):
+    """The fused kernel forward; the backward runs ``chunked_delta_rule_bwd`` (the
+    reverse kernels) on the normalised rows with beta = 1, then differentiates the
+    normalisation ``x / max(||x||, 1e-6)`` with torch.  bf16 q/k run the chunked
+    bf16 backward on bf16-rounded normalised rows; fp32 q/k the fp32 backward."""
+
+    @staticmethod
+    def forward(ctx, qd, kd, vd, sd, cdt):
+        o, s_out = _run_linear_attention(qd, kd, vd, sd, cdt, qd.device)
+        ctx.save_for_backward(qd, kd, vd, sd)
+        ctx.cdt = cdt
+        return o, s_out
+
+    @staticmethod
+    def backward(ctx, go, gs):
+        qd, kd, vd, sd = ctx.saved_tensors
+        with torch.enable_grad():
+            qf = qd.detach().float().requires_grad_(True)
+            kf = kd.detach().float().requires_grad_(True)
+            qn, kn = _l2n(qf), _l2n(kf)
+        ones = torch.ones(qd.shape[:3], dtype=torch.float32, device=qd.device)
+        s0 = sd if sd is not None else torch.zeros(
+            (qd.shape[0], qd.shape[2], qd.shape[3], qd.shape[3]), dtype=torch.float32, device=qd.device)
+        res = _DeltaResidual(q=qn.detach().to(ctx.cdt), k=kn.detach().to(ctx.cdt), v=vd, beta=ones,
+                             state0=s0, chunk=64)
+        gqn, gkn, gv, _, gs0 = chunked_delta_rule_bwd(res, (go, gs))
+        gq, gk = torch.autograd.grad((qn, kn), (qf, kf), (gqn, gkn))
+        need = ctx.needs_input_grad
+        return (gq.to(qd.dtype) if need[0] else None, gk.to(kd.dtype) if need[1] else None,
+                gv.to(vd.dtype) if need[2] else None, gs0 if (sd is not None and need[3]) else None, None)
+
+
 def linear_attention(q, k, v, state=None):
-    """Causal delta rule with beta = 1 on L2-normalised q, k; returns (output, next_state)."""
+    """Causal delta rule with beta = 1 on L2-normalised q, k; returns (output, next_state).
+
+    Differentiable when autograd records and a torch input requires grad (the
+    reference differentiates it with JAX autodiff through its scan).
+    """
     qs, squeeze = _heads(q)
     ks, _ = _heads(k)
     vs, _ = _heads(v)
@@ -69,16 +122,15 @@ def linear_attention(q, k, v, state=None):
         raise ValueError(f"head dimension {dim} not in [1, 256]")
     call = _Call(q, k, v, state)
     cdt = _dtype(q, k, v)
+    grad = torch.is_grad_enabled() and any(isinstance(x, torch.Tensor) and x.requires_grad
+                                           for x in (q, k, v, state))
     with torch.cuda.device(call.device):
         qd, kd, vd = (call.dev(x, cdt).reshape(qs) for x in (q, k, v))
         sd = None if state is None else call.dev(state, torch.float32).reshape(batch, heads, dim, dim)
-        o = torch.empty(qs, dtype=torch.float32, device=call.device)
-        s_out = torch.empty((batch, heads, dim, dim), dtype=torch.float32, device=call.device)
-        rc = _native.lib().pm_linear_attention(
-            _ptr(qd), _ptr(kd), _ptr(vd), _ptr(sd), _ptr(o), _ptr(s_out),
-            batch, seq, heads, dim, _code(cdt), _native.DTYPE_F32, _stream(call.device),
-        )
-        _native.check(rc)
+        if grad:
+            o, s_out = _LinearAttention.apply(qd, kd, vd, sd, cdt)
+        else:
+            o, s_out = _run_linear_attention(qd, kd, vd, sd, cdt, call.device)
     if squeeze:
         o, s_out = o[:, :, 0, :], s_out[:, 0]
     return call.out(o), call.out(s_out)

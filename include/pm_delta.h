@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 5
+#define PM_DELTA_ABI_VERSION 6
 
 /* element types */
 #define PM_DTYPE_F32 0
@@ -200,6 +200,24 @@ int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
 /* Workspace bytes pm_delta_bwd needs for these shapes and in_dtype under the
  * current path setting (0 for invalid shapes, dtypes or D > 128). */
 size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype);
+
+/*
+ * pm_delta_bwd without a caller workspace and without any allocation.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving or training loops,
+ * harnesses that forbid hipMalloc).  The kernels and results are those of
+ * pm_delta_bwd; the workspace is a fixed scratch array inside the library,
+ * one per GPU, held until the process ends: PM_DELTA_NOALLOC_SCRATCH_BYTES.
+ * A call whose pm_delta_bwd_workspace_bytes exceeds it returns
+ * PM_E_WORKSPACE before launching anything.  Every call on one GPU uses that
+ * GPU's scratch: calls that overlap on one GPU (other streams, other threads)
+ * race and must be ordered by the caller.  Arguments as pm_delta_bwd.
+ */
+#define PM_DELTA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int pm_delta_bwd_noalloc(const void* q, const void* k, const void* v, const float* beta,
+                         const float* s0, const float* go, const float* gs, float* gq, float* gk,
+                         float* gv, float* gbeta, float* gs0, int B, int T, int H, int D,
+                         int in_dtype, void* stream);
 
 /* Thread-local message for the last nonzero return on this thread. */
 const char* pm_last_error(void);

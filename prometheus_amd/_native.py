@@ -18,11 +18,12 @@ import torch  # noqa: F401  (see module docstring: must precede CDLL)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpmdelta.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256
 MAX_D_BWD = 128
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 E_NULL, E_SHAPE, E_DTYPE, E_ALIGN, E_WORKSPACE, E_UNSUPPORTED = -1, -2, -3, -4, -5, -6
 
@@ -38,6 +39,7 @@ EXPORTS = (
     "pm_delta_workspace_bytes",
     "pm_delta_bwd",
     "pm_delta_bwd_workspace_bytes",
+    "pm_delta_bwd_noalloc",
     "pm_last_error",
     "pm_abi_version",
     "pm_delta_set_path",
@@ -92,6 +94,8 @@ def lib() -> ctypes.CDLL:
         L.pm_delta_bwd.restype = i
         L.pm_delta_bwd_workspace_bytes.argtypes = [i, i, i, i, i]
         L.pm_delta_bwd_workspace_bytes.restype = sz
+        L.pm_delta_bwd_noalloc.argtypes = [vp] * 12 + [i] * 5 + [vp]
+        L.pm_delta_bwd_noalloc.restype = i
         L.pm_last_error.argtypes = []
         L.pm_last_error.restype = ctypes.c_char_p
         L.pm_abi_version.argtypes = []

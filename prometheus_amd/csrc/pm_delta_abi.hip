@@ -14,6 +14,9 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "pm_common.h"
 #include "pm_internal.h"
 #include "../../include/pm_delta.h"
@@ -67,6 +70,39 @@ int fail(int code, const char* fmt, ...) {
     vsnprintf(g_err, sizeof g_err, fmt, ap);
     va_end(ap);
     return code;
+}
+
+// Scratch of pm_delta_bwd_noalloc: a file-scope device array, one copy per GPU,
+// held until the process ends.  Host code never uses `scratch` itself (its
+// host-side name is not a device address): the device address comes from
+// hipGetSymbolAddress, once per device with that device current.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+__device__ __attribute__((aligned(256))) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int hip_fail(hipError_t e, const char* what);
+
+// Device address of this GPU's scratch (looked up on the first call on the device).
+int scratch_address(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(PM_E_UNSUPPORTED, "device %d beyond %d", dev, kMaxDevices);
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+            if (!p) return fail(PM_E_NULL, "hipGetSymbolAddress(scratch) gave NULL");
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return 0;
 }
 
 int hip_fail(hipError_t e, const char* what) {
@@ -242,6 +278,31 @@ int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
     hipError_t e = chunked ? pm::launch_bwd_chunked(a, static_cast<hipStream_t>(stream))
                            : pm::launch_bwd(a, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? 0 : hip_fail(e, "backward launch");
+}
+
+int pm_delta_bwd_noalloc(const void* q, const void* k, const void* v, const float* beta,
+                         const float* s0, const float* go, const float* gs, float* gq, float* gk,
+                         float* gv, float* gbeta, float* gs0, int B, int T, int H, int D,
+                         int in_dtype, void* stream) {
+    g_err[0] = '\0';
+    if (B < 0 || T < 0 || H < 0)
+        return fail(PM_E_SHAPE, "B, T, H must be >= 0 (got %d, %d, %d)", B, T, H);
+    if (D < 1 || D > pm::kBwdMaxD)
+        return fail(PM_E_SHAPE, "backward D must be in [1, %d] (got %d)", pm::kBwdMaxD, D);
+    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16)
+        return fail(PM_E_DTYPE, "in_dtype %d is not PM_DTYPE_F32 or PM_DTYPE_BF16", in_dtype);
+    const size_t need = bwd_ws_bytes(B, T, H, D, in_dtype);
+    if (need > kNoAllocScratchBytes)
+        return fail(PM_E_WORKSPACE,
+                    "the backward needs %zu bytes of workspace; the no-allocation entry point holds "
+                    "%zu (use pm_delta_bwd with a caller workspace)",
+                    need, kNoAllocScratchBytes);
+    void* ws = nullptr;
+    if (need > 0 && static_cast<long>(B) * H > 0) {
+        if (int rc = scratch_address(&ws)) return rc;
+    }
+    return pm_delta_bwd(q, k, v, beta, s0, go, gs, gq, gk, gv, gbeta, gs0, B, T, H, D, in_dtype, ws,
+                        ws ? kNoAllocScratchBytes : 0, stream);
 }
 
 int pm_delta_set_path(int path) {

@@ -392,3 +392,20 @@ def test_no_unprefixed_exports():
     names = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
     c_names = {n for n in names if not n.startswith("_Z")}
     assert c_names - {"_init", "_fini"} == set(_native.EXPORTS), sorted(c_names)
+
+
+def test_noalloc_backward_rejects_sizes_beyond_its_scratch():
+    """pm_delta_bwd_noalloc refuses (PM_E_WORKSPACE, before any device work) a call
+    whose workspace would exceed the library's fixed scratch, and validates its
+    arguments like pm_delta_bwd."""
+    L = _native.lib()
+    p = ctypes.c_void_p(16)  # never dereferenced
+    ptrs = [p] * 12
+    B, T, H, D = 4, 4096, 16, 128
+    assert L.pm_delta_bwd_workspace_bytes(B, T, H, D, _native.DTYPE_BF16) > _native.NOALLOC_SCRATCH_BYTES
+    assert L.pm_delta_bwd_noalloc(*ptrs, B, T, H, D, _native.DTYPE_BF16, None) == _native.E_WORKSPACE
+    assert b"no-allocation" in L.pm_last_error()
+    assert L.pm_delta_bwd_noalloc(*ptrs, 1, 8, 1, 129, _native.DTYPE_F32, None) == _native.E_SHAPE
+    assert L.pm_delta_bwd_noalloc(*ptrs, 1, 8, 1, 8, 7, None) == _native.E_DTYPE
+    # nothing to do: B*H == 0 returns before any device work
+    assert L.pm_delta_bwd_noalloc(*([None] * 12), 0, 8, 1, 8, _native.DTYPE_F32, None) == 0

@@ -207,13 +207,14 @@ def main():
                          "executed_bf16_mfma_flop": mc.get("executed_bf16_mfma_flop"),
                          "executed_over_algorithmic": mc.get("executed_over_algorithmic")}
 
-    def time_fwd(out_code, out_t, calls=10):
+    def time_fwd(out_code, out_t, calls=10, ws=None):
         q, k, v, beta = sets[0]
 
         def f():
             rc = lib.pm_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), None,
                                   out_t.data_ptr(), s.data_ptr(), B, T, H, D, _native.DTYPE_BF16,
-                                  out_code, CHUNK, None, 0, stream.cuda_stream)
+                                  out_code, CHUNK, None if ws is None else ws.data_ptr(),
+                                  0 if ws is None else ws.numel(), stream.cuda_stream)
             _native.check(rc)
 
         f()
@@ -242,16 +243,20 @@ def main():
                  "frac": flops / (b16_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS},
     }
     del o16
-    # the deep-pipeline form of the chunked kernel (pm_delta_set_path(3)): bitwise the same
-    # results; reported beside the default
+    # the split form of the chunked kernel (T diag(beta) by a parallel pass into a workspace,
+    # then the chunk recurrence), forced at cfg1 with pm_delta_set_path(3); by default it runs
+    # only where the chunked kernel takes 16-column tiles, where it is the faster form
     old_path = _native.set_path(3)
     try:
-        pipe_ms = time_fwd(_native.DTYPE_F32, o)
+        ws_split = torch.empty(lib.pm_delta_workspace_bytes(B, T, H, D, _native.DTYPE_BF16),
+                               dtype=torch.uint8, device=dev)
+        split_ms = time_fwd(_native.DTYPE_F32, o, ws=ws_split)
     finally:
         _native.set_path(old_path)
-    pipeline_form = {"workload": "cfg1 forward, chunked kernel in its deep-pipeline form (path 3)",
-                     "kernel_us": pipe_ms * 1e3,
-                     "roofline_frac": nbytes / (pipe_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    del ws_split
+    split_form = {"workload": "cfg1 forward, chunked kernel in split form (path 3, prep + recurrence)",
+                  "kernel_us": split_ms * 1e3,
+                  "roofline_frac": nbytes / (split_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
     launch(last)  # the output the parity check reads
     torch.cuda.synchronize()
 
@@ -629,7 +634,7 @@ def main():
         "parity": parity,
         "decode": decode,
         "bf16_out": bf16_out,
-        "pipeline_form": pipeline_form,
+        "split_form": split_form,
         "model_linear_attention": model_la,
         "fp32_forward": fp32_fwd,
         "gated": gated,

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 6
+#define PM_DELTA_ABI_VERSION 7
 
 /* element types */
 #define PM_DTYPE_F32 0
@@ -70,8 +70,16 @@ extern "C" {
  * chunk >= 1 is accepted as in the reference (:676-677); like the
  * reference it does not change the mathematical result (:92).
  * T == 0 gives no output rows and s_out = s0 (or zeros).
- * workspace/ws_bytes: pass NULL/0; no kernel of this build needs one
- * (pm_delta_workspace_bytes returns 0), kept for ABI stability.
+ * workspace/ws_bytes: optional device memory (16-byte aligned) of at least
+ * pm_delta_workspace_bytes(B, T, H, D, in_dtype) bytes, which is nonzero
+ * exactly when the call would run the split form of the chunked kernel: a
+ * parallel pass builds every chunk's T diag(beta), T = (I + A)^-1, into the
+ * workspace and the chunk recurrence loads it instead of building it.  By
+ * default (pm_delta_set_path(0)) that is the case for bf16 inputs at D in
+ * {64, 128} when B*H*(D/32) < 256 (the chunked kernel's 16-column tiles),
+ * where the split form is the faster one.  Without the workspace the
+ * single-stage chunked kernel runs, which needs none; the two agree within
+ * the bf16 parity bound.  The library never allocates.
  */
 int pm_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
                  const float* s0, void* o, float* s_out, int B, int T, int H, int D,
@@ -85,6 +93,7 @@ int pm_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
  * No reference counterpart: the reference's equivalent is n_seqs separate
  * chunked_delta_rule calls (kernels/__init__.py:591-619) with B=1.
  * s0 may be NULL (zeros) or (n_seqs, H, D, D).
+ * workspace/ws_bytes as pm_delta_fwd, sized by pm_delta_varlen_workspace_bytes.
  */
 int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float* beta,
                         const int32_t* cu_seqlens, int n_seqs, int total_T,
@@ -161,8 +170,17 @@ int pm_linear_attention(const void* q, const void* k, const void* v, const float
                         float* s_out, int B, int T, int H, int D, int in_dtype, int out_dtype,
                         void* stream);
 
-/* Workspace bytes pm_delta_fwd would need (0 in this build). */
+/*
+ * Workspace bytes pm_delta_fwd uses for the split form of the chunked
+ * kernel (6 KiB per (b, h) and 64-token chunk); 0 when the call, under the
+ * calling thread's pm_delta_set_path / pm_delta_set_tile setting, would not
+ * run the split form.  No reference counterpart: the reference's scan keeps
+ * no per-chunk state (kernels/__init__.py:421-458).
+ */
 size_t pm_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype);
+/* The same for pm_delta_fwd_varlen (6 KiB per head per slot, with
+ * ceil(total_T / 64) + n_seqs slots). */
+size_t pm_delta_varlen_workspace_bytes(int n_seqs, int total_T, int H, int D, int in_dtype);
 
 /*
  * Reverse mode of the forward: gradients of L with respect to (q, k, v,
@@ -228,12 +246,13 @@ int pm_abi_version(void);
 /*
  * Kernel selection for pm_delta_fwd, pm_delta_fwd_varlen, pm_delta_bwd and
  * pm_linear_attention, for tests and benchmarks: 0 = automatic (chunked MFMA
- * kernel where the shape and dtype allow, else the per-token kernel), 1 =
- * always the per-token kernel, 2 = chunked kernel required
- * (PM_E_UNSUPPORTED when it cannot serve the call), 3 = as 2, with the plain
- * forward on the deep four-wave pipeline kernel (copies two stages ahead, T
- * built over two stages; bitwise the same results as the default kernel).  The
- * previous value is returned.  The setting is per calling thread: a
+ * kernel where the shape and dtype allow, else the per-token kernel; the
+ * plain forward in split form where that is faster and a workspace is
+ * given), 1 = always the per-token kernel, 2 = chunked kernel required
+ * (PM_E_UNSUPPORTED when it cannot serve the call), single-stage form, 3 = as
+ * 2, with the plain forward always in split form (PM_E_WORKSPACE without a
+ * workspace of pm_delta_workspace_bytes bytes).  The previous value is
+ * returned.  The setting is per calling thread: a
  * workspace-size query and the call it sizes, made on one thread, always see
  * the same setting.
  */

@@ -18,7 +18,7 @@ import torch  # noqa: F401  (see module docstring: must precede CDLL)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpmdelta.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256
@@ -37,6 +37,7 @@ EXPORTS = (
     "pm_gated_delta_step",
     "pm_linear_attention",
     "pm_delta_workspace_bytes",
+    "pm_delta_varlen_workspace_bytes",
     "pm_delta_bwd",
     "pm_delta_bwd_workspace_bytes",
     "pm_delta_bwd_noalloc",
@@ -90,6 +91,8 @@ def lib() -> ctypes.CDLL:
         L.pm_linear_attention.restype = i
         L.pm_delta_workspace_bytes.argtypes = [i, i, i, i, i]
         L.pm_delta_workspace_bytes.restype = sz
+        L.pm_delta_varlen_workspace_bytes.argtypes = [i, i, i, i, i]
+        L.pm_delta_varlen_workspace_bytes.restype = sz
         L.pm_delta_bwd.argtypes = [vp] * 12 + [i] * 5 + [vp, sz, vp]
         L.pm_delta_bwd.restype = i
         L.pm_delta_bwd_workspace_bytes.argtypes = [i, i, i, i, i]

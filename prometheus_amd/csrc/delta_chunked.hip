@@ -728,6 +728,8 @@ int pick_tile(int D, long n_pairs, int requested) {
 
 }  // namespace
 
+int chunked_pick_tile(int D, long n_pairs, int requested) { return pick_tile(D, n_pairs, requested); }
+
 // 32-bit buffer offsets: a chunk spans 64 token rows of H*D elements.
 bool chunked_supported(int D, int H) {
     return (D == 64 || D == 128) && H >= 1 && static_cast<long>(H) * D <= (1L << 24);
@@ -738,7 +740,6 @@ hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st) {
     if (n_pairs == 0) return hipSuccess;
     if (!chunked_supported(a.D, a.H)) return hipErrorInvalidValue;
     const int dv = pick_tile(a.D, n_pairs, a.dv_tile);
-    if (!a.norm && !a.g && a.pipeline) return launch_chunked_pipe(a, dv, st);
     if (a.D == 128) return dv == 16 ? launch_dv<128, 16>(a, st) : launch_dv<128, 32>(a, st);
     return dv == 16 ? launch_dv<64, 16>(a, st) : launch_dv<64, 32>(a, st);
 }

@@ -210,17 +210,20 @@ __device__ __forceinline__ void wait_copies() { __asm__ volatile("s_waitcnt vmcn
 // 2^x in one v_exp_f32 (about 1 ulp; 0 for x below the fp32 range).
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// T = (I + A)^-1, A = strict_lower(diag(beta) K K^T), for one 64-token chunk
-// by one wave: K token rows in the swizzled tile at rb + R_KS, beta (fp32) at
-// rb + R_BS; T lands in Tp in the packed operand layout (6 blocks of 1 KiB).
-// The backward's prep kernel calls this.  The forward kernel keeps the same
-// algebra inline in its T producer, with its NORM and GATED scalings: called
-// through this function instead, it compiled to 5 more VGPRs and about 190
-// more instructions, in its most time-critical role.
-template <int D, int R_KS, int R_BS>
-__device__ __forceinline__ void build_t_packed(const unsigned char* rb, uint16_t* Tp, int lane) {
-    const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + R_KS);
-    const float* Bs = reinterpret_cast<const float*>(rb + R_BS);
+// The ten lower 16x16 blocks of T = (I + A)^-1, A = strict_lower(diag(beta) K K^T),
+// for one 64-token chunk, each as the accumulator tile of its transpose (lane (g, l16)
+// holds T[16i + l16][16j + 4g + r], r < 4), in the order (0,0) (1,0) (1,1) (2,0) (2,1)
+// (2,2) (3,0) (3,1) (3,2) (3,3): the form store_packed_t takes.  One wave, from
+//   f[r][kb]: K token row 16 r + l16, d = 32 kb + 8 g + [0, 8) (the operand order of
+//             lds_op_kq), rows past the chunk's end zero;
+//   bc[b] = beta of token 16 b + l16;  br4[b][r] = beta of token 16 b + 4 g + r.
+// The forward kernel keeps the same algebra inline in its T producer, with its NORM and
+// GATED scalings (called through a function instead, it compiled to 5 more VGPRs and
+// about 190 more instructions, in its most time-critical role); for plain inputs the two
+// give equal bits.
+template <int D>
+__device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const float (&bc)[4],
+                                         const f32x4_t (&br4)[4], int lane, f32x4_t (&tb)[10]) {
     const int l16 = lane & 15, lg = lane >> 4;
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
     // G = K K^T: diagonal tiles gd[b] and upper tiles gu(k, i), k < i
@@ -231,25 +234,14 @@ __device__ __forceinline__ void build_t_packed(const unsigned char* rb, uint16_t
     for (int x = 0; x < 6; ++x) gu[x] = zero;
 #pragma unroll
     for (int kb = 0; kb < D / 32; ++kb) {
-        bf16x8_t f[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) f[r] = lds_op_kq<D>(Ks, 16 * r + l16, kb, lg);
-#pragma unroll
-        for (int b = 0; b < 4; ++b) gd[b] = mfma32(f[b], f[b], gd[b]);
-        gu[0] = mfma32(f[0], f[1], gu[0]);  // (0,1)
-        gu[1] = mfma32(f[0], f[2], gu[1]);  // (0,2)
-        gu[2] = mfma32(f[1], f[2], gu[2]);  // (1,2)
-        gu[3] = mfma32(f[0], f[3], gu[3]);  // (0,3)
-        gu[4] = mfma32(f[1], f[3], gu[4]);  // (1,3)
-        gu[5] = mfma32(f[2], f[3], gu[5]);  // (2,3)
-    }
-    // beta of the rows this lane holds in accumulator form (br4) and in A-operand form (bc)
-    f32x4_t br4[4];
-    float bc[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        br4[b] = *reinterpret_cast<const f32x4_t*>(Bs + 16 * b + 4 * lg);
-        bc[b] = Bs[16 * b + l16];
+        for (int b = 0; b < 4; ++b) gd[b] = mfma32(f[b][kb], f[b][kb], gd[b]);
+        gu[0] = mfma32(f[0][kb], f[1][kb], gu[0]);  // (0,1)
+        gu[1] = mfma32(f[0][kb], f[2][kb], gu[1]);  // (0,2)
+        gu[2] = mfma32(f[1][kb], f[2][kb], gu[2]);  // (1,2)
+        gu[3] = mfma32(f[0][kb], f[3][kb], gu[3]);  // (0,3)
+        gu[4] = mfma32(f[1][kb], f[3][kb], gu[4]);  // (1,3)
+        gu[5] = mfma32(f[2][kb], f[3][kb], gu[5]);  // (2,3)
     }
     f32x4_t eye;
 #pragma unroll
@@ -329,28 +321,56 @@ __device__ __forceinline__ void build_t_packed(const unsigned char* rb, uint16_t
     const u32x2_t z32 = cvt4(mfma16(a32, cd2, zero));
     const u32x2_t cx10 = cvt4(-mfma16(cdt1, z10, zero));
     const u32x2_t cx21 = cvt4(-mfma16(cdt2, z21, zero));
-    const f32x4_t x10t = -mfma16(z10, cdt1, zero);
-    const f32x4_t x21t = -mfma16(z21, cdt2, zero);
-    const f32x4_t x32t = -mfma16(z32, cdt3, zero);
+    tb[1] = -mfma16(z10, cdt1, zero);  // (1,0)
+    tb[4] = -mfma16(z21, cdt2, zero);  // (2,1)
+    tb[8] = -mfma16(z32, cdt3, zero);  // (3,2)
     // level 2
     const u32x2_t z20 = cvt4(mfma16(a21, cx10, mfma16(a20, cd0, zero)));
     const u32x2_t z31 = cvt4(mfma16(a32, cx21, mfma16(a31, cd1, zero)));
     const u32x2_t cx20 = cvt4(-mfma16(cdt2, z20, zero));
-    const f32x4_t x20t = -mfma16(z20, cdt2, zero);
-    const f32x4_t x31t = -mfma16(z31, cdt3, zero);
+    tb[3] = -mfma16(z20, cdt2, zero);  // (2,0)
+    tb[7] = -mfma16(z31, cdt3, zero);  // (3,1)
     // level 3
     const u32x2_t z30 = cvt4(mfma16(a32, cx20, mfma16(a31, cx10, mfma16(a30, cd0, zero))));
-    const f32x4_t x30t = -mfma16(z30, cdt3, zero);
-    store_packed_t(Tp, 0, 0, ddt[0], lane);
-    store_packed_t(Tp, 1, 0, x10t, lane);
-    store_packed_t(Tp, 1, 1, ddt[1], lane);
-    store_packed_t(Tp, 2, 0, x20t, lane);
-    store_packed_t(Tp, 2, 1, x21t, lane);
-    store_packed_t(Tp, 2, 2, ddt[2], lane);
-    store_packed_t(Tp, 3, 0, x30t, lane);
-    store_packed_t(Tp, 3, 1, x31t, lane);
-    store_packed_t(Tp, 3, 2, x32t, lane);
-    store_packed_t(Tp, 3, 3, ddt[3], lane);
+    tb[6] = -mfma16(z30, cdt3, zero);  // (3,0)
+    tb[0] = ddt[0];
+    tb[2] = ddt[1];
+    tb[5] = ddt[2];
+    tb[9] = ddt[3];
+}
+
+// t_blocks for one chunk by one wave from LDS: K token rows in the swizzled tile at
+// rb + R_KS, beta (fp32) at rb + R_BS; T lands in Tp in the packed operand layout
+// (6 blocks of 1 KiB).  The backward's prep kernel calls this.
+template <int D, int R_KS, int R_BS>
+__device__ __forceinline__ void build_t_packed(const unsigned char* rb, uint16_t* Tp, int lane) {
+    const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + R_KS);
+    const float* Bs = reinterpret_cast<const float*>(rb + R_BS);
+    const int l16 = lane & 15, lg = lane >> 4;
+    bf16x8_t f[4][D / 32];
+#pragma unroll
+    for (int kb = 0; kb < D / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) f[r][kb] = lds_op_kq<D>(Ks, 16 * r + l16, kb, lg);
+    f32x4_t br4[4];
+    float bc[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        br4[b] = *reinterpret_cast<const f32x4_t*>(Bs + 16 * b + 4 * lg);
+        bc[b] = Bs[16 * b + l16];
+    }
+    f32x4_t tb[10];
+    t_blocks<D>(f, bc, br4, lane, tb);
+    store_packed_t(Tp, 0, 0, tb[0], lane);
+    store_packed_t(Tp, 1, 0, tb[1], lane);
+    store_packed_t(Tp, 1, 1, tb[2], lane);
+    store_packed_t(Tp, 2, 0, tb[3], lane);
+    store_packed_t(Tp, 2, 1, tb[4], lane);
+    store_packed_t(Tp, 2, 2, tb[5], lane);
+    store_packed_t(Tp, 3, 0, tb[6], lane);
+    store_packed_t(Tp, 3, 1, tb[7], lane);
+    store_packed_t(Tp, 3, 2, tb[8], lane);
+    store_packed_t(Tp, 3, 3, tb[9], lane);
     zero_upper_half(Tp, qblk(0, 0), lane);
     zero_upper_half(Tp, qblk(2, 1), lane);
 }

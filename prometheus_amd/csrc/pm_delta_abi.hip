@@ -112,6 +112,14 @@ int hip_fail(hipError_t e, const char* what) {
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// The split form of the chunked forward runs under path 3, and by default (path 0) where
+// the chunked kernel takes 16-column tiles: fewer (b, h) pairs than fill the GPU with
+// 32-column tiles.  There its lighter memory traffic per CU wins (measured 5-25 % faster);
+// with 32-column tiles on every CU the single-stage kernel is faster.
+bool split_chosen(int path, int D, long n_pairs) {
+    return path == 3 || (path == 0 && pm::chunked_pick_tile(D, n_pairs, g_tile) == 16);
+}
+
 int check_dtypes(int in_dtype, int out_dtype) {
     if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16)
         return fail(PM_E_DTYPE, "in_dtype %d is not PM_DTYPE_F32 or PM_DTYPE_BF16", in_dtype);
@@ -124,7 +132,7 @@ int check_dtypes(int in_dtype, int out_dtype) {
 int forward(const void* q, const void* k, const void* v, const float* beta, const float* s0,
             void* o, float* s_out, const int32_t* cu, int n_seq, int T, int total_T, int H,
             int D, int in_dtype, int out_dtype, int chunk, hipStream_t st,
-            const float* g = nullptr) {
+            const float* g = nullptr, void* workspace = nullptr, size_t ws_bytes = 0) {
     const bool varlen = cu != nullptr;
     const long n_pairs = static_cast<long>(n_seq) * H;
     const long n_tok = varlen ? static_cast<long>(total_T) : static_cast<long>(n_seq) * T;
@@ -162,7 +170,18 @@ int forward(const void* q, const void* k, const void* v, const float* beta, cons
                           varlen ? total_T : T, H, D,
                           out_dtype == PM_DTYPE_BF16, g_tile};
         a.g = g;
-        a.pipeline = path == 3;
+        // the split form (T built by a parallel pass into the caller's workspace) for the
+        // plain forward where it is the faster form (split_chosen), or always under path 3
+        if (!g && split_chosen(path, D, n_pairs)) {
+            const size_t need = pm::chunked_split_ws_bytes(varlen, n_seq, varlen ? total_T : T, H);
+            if (workspace && ws_bytes >= need && aligned(workspace, 16)) {
+                hipError_t e = pm::launch_chunked_split(a, pm::chunked_pick_tile(D, n_pairs, g_tile), workspace, st);
+                return e == hipSuccess ? 0 : hip_fail(e, "chunked forward launch");
+            }
+            if (path == 3)
+                return fail(PM_E_WORKSPACE, "path 3 needs a 16-byte aligned workspace of %zu bytes (got %zu)",
+                            need, workspace ? ws_bytes : static_cast<size_t>(0));
+        }
         hipError_t e = pm::launch_chunked(a, st);
         return e == hipSuccess ? 0 : hip_fail(e, "chunked forward launch");
     }
@@ -227,7 +246,20 @@ int pm_abi_version(void) { return PM_DELTA_ABI_VERSION; }
 
 const char* pm_last_error(void) { return g_err; }
 
-size_t pm_delta_workspace_bytes(int, int, int, int, int) { return 0; }
+size_t pm_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype) {
+    if (B < 0 || T < 0 || H < 0 || in_dtype != PM_DTYPE_BF16 || !pm::chunked_supported(D, H)) return 0;
+    const long n_pairs = static_cast<long>(B) * H;
+    if (n_pairs > (1L << 30) || g_path == 1 || !split_chosen(g_path, D, n_pairs)) return 0;
+    return pm::chunked_split_ws_bytes(false, B, T, H);
+}
+
+size_t pm_delta_varlen_workspace_bytes(int n_seqs, int total_T, int H, int D, int in_dtype) {
+    if (n_seqs < 0 || total_T < 0 || H < 0 || in_dtype != PM_DTYPE_BF16 || !pm::chunked_supported(D, H))
+        return 0;
+    const long n_pairs = static_cast<long>(n_seqs) * H;
+    if (n_pairs > (1L << 30) || g_path == 1 || !split_chosen(g_path, D, n_pairs)) return 0;
+    return pm::chunked_split_ws_bytes(true, n_seqs, total_T, H);
+}
 
 size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype) {
     if (B < 0 || T < 0 || H < 0 || D < 1 || D > pm::kBwdMaxD) return 0;
@@ -324,8 +356,6 @@ int pm_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
                  const float* s0, void* o, float* s_out, int B, int T, int H, int D,
                  int in_dtype, int out_dtype, int chunk, void* workspace, size_t ws_bytes,
                  void* stream) {
-    (void)workspace;
-    (void)ws_bytes;
     g_err[0] = '\0';
     if (B < 0 || T < 0 || H < 0)
         return fail(PM_E_SHAPE, "B, T, H must be >= 0 (got %d, %d, %d)", B, T, H);
@@ -334,15 +364,13 @@ int pm_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
     if (chunk < 1) return fail(PM_E_SHAPE, "chunk must be >= 1, got %d", chunk);
     if (int rc = check_dtypes(in_dtype, out_dtype)) return rc;
     return forward(q, k, v, beta, s0, o, s_out, nullptr, B, T, 0, H, D, in_dtype, out_dtype,
-                   chunk, static_cast<hipStream_t>(stream));
+                   chunk, static_cast<hipStream_t>(stream), nullptr, workspace, ws_bytes);
 }
 
 int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float* beta,
                         const int32_t* cu_seqlens, int n_seqs, int total_T, const float* s0,
                         void* o, float* s_out, int H, int D, int in_dtype, int out_dtype,
                         int chunk, void* workspace, size_t ws_bytes, void* stream) {
-    (void)workspace;
-    (void)ws_bytes;
     g_err[0] = '\0';
     if (n_seqs < 0 || total_T < 0 || H < 0)
         return fail(PM_E_SHAPE, "n_seqs, total_T, H must be >= 0 (got %d, %d, %d)", n_seqs,
@@ -355,7 +383,7 @@ int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float
     if (cu_seqlens && !aligned(cu_seqlens, 4))
         return fail(PM_E_ALIGN, "cu_seqlens must be 4-byte aligned");
     return forward(q, k, v, beta, s0, o, s_out, cu_seqlens, n_seqs, 0, total_T, H, D, in_dtype,
-                   out_dtype, chunk, static_cast<hipStream_t>(stream));
+                   out_dtype, chunk, static_cast<hipStream_t>(stream), nullptr, workspace, ws_bytes);
 }
 
 int pm_delta_step_slots(float* pool, const int32_t* slots, int n_slots, const void* q,

@@ -67,14 +67,18 @@ struct ChunkedArgs {
     // Gated variant (not with norm): log-gates per (token, head), alpha = exp(g)
     // (g <= 0 keeps every in-chunk decay factor at most 1).
     const float* g = nullptr;
-    // Plain forward only: run the deep four-wave pipeline (delta_chunked_pipe.hip)
-    // instead of the single-stage kernel.  Same results, bit for bit.
-    bool pipeline = false;
 };
 bool chunked_supported(int D, int H);  // D in {64, 128}, H*D <= 2^24
+// d_v columns per workgroup of the chunked forward: 32 (two chain waves) unless that
+// leaves CUs idle; `requested` 16 or 32 forces it (64 is served as 32).
+int chunked_pick_tile(int D, long n_pairs, int requested);
 hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st);
-// The plain forward (no norm, no gates) as the deep four-wave pipeline, dv in {16, 32}.
-hipError_t launch_chunked_pipe(const ChunkedArgs& a, int dv, hipStream_t st);
+// The plain forward (no norm, no gates) in split form (delta_chunked_split.hip): a
+// parallel pass builds every chunk's T diag(beta) into `t_ws` (chunked_split_ws_bytes
+// bytes, 16-byte aligned), then the chunk recurrence loads it instead of building it.
+// Same algebra as the single-stage kernel, rounded differently (bf16 parity).
+size_t chunked_split_ws_bytes(bool varlen, int n_seq, int T, int H);
+hipError_t launch_chunked_split(const ChunkedArgs& a, int dv, void* t_ws, hipStream_t st);
 // The same kernel writing, instead of O and the final state, the state at
 // the start of every chunk as bf16 rows of S^T (fixed-length batches only):
 // s_hist holds n_seq*H x ceil(T/64) x D x D values.

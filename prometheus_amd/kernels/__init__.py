@@ -214,9 +214,12 @@ def _forward(q, k, v, beta, state, chunk: int, out_dtype):
         sd = call.dev(state, torch.float32)
         o = torch.empty((batch, seq, heads, dim), dtype=odt, device=call.device)
         s_out = torch.empty((batch, heads, dim, dim), dtype=torch.float32, device=call.device)
+        # the split form's T workspace, where the C ABI would use it (torch's caching allocator)
+        nbytes = _native.lib().pm_delta_workspace_bytes(batch, seq, heads, dim, _code(cdt))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=call.device) if nbytes else None
         rc = _native.lib().pm_delta_fwd(
             _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(sd), _ptr(o), _ptr(s_out),
-            batch, seq, heads, dim, _code(cdt), _code(odt), chunk, None, 0,
+            batch, seq, heads, dim, _code(cdt), _code(odt), chunk, _ptr(ws), nbytes,
             _stream(call.device),
         )
         _native.check(rc)
@@ -416,9 +419,11 @@ def chunked_delta_rule_varlen(q, k, v, beta, cu_seqlens, state=None, config=None
         cu = torch.from_numpy(cu_host.astype(np.int32)).to(call.device)
         o = torch.empty((n_tok, heads, dim), dtype=odt, device=call.device)
         s_out = torch.empty((n_seqs, heads, dim, dim), dtype=torch.float32, device=call.device)
+        nbytes = _native.lib().pm_delta_varlen_workspace_bytes(n_seqs, n_tok, heads, dim, _code(cdt))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=call.device) if nbytes else None
         rc = _native.lib().pm_delta_fwd_varlen(
             _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(cu), n_seqs, n_tok, _ptr(sd),
-            _ptr(o), _ptr(s_out), heads, dim, _code(cdt), _code(odt), chunk, None, 0,
+            _ptr(o), _ptr(s_out), heads, dim, _code(cdt), _code(odt), chunk, _ptr(ws), nbytes,
             _stream(call.device),
         )
         _native.check(rc)

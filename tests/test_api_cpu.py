@@ -260,6 +260,44 @@ def test_abi_argument_validation_without_gpu():
     assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, 1) == 0
 
 
+def test_forward_workspace_sizes_and_checks():
+    """The split form's T workspace (6 KiB per (b, h) and chunk) is asked for exactly where
+    the forward would run that form: 16-column tiles by default, always under path 3."""
+    lib = _native.lib()
+    bf16, f32 = _native.DTYPE_BF16, _native.DTYPE_F32
+    per = 6 * 1024
+    assert lib.pm_delta_workspace_bytes(1, 32768, 32, 128, bf16) == 32 * 512 * per  # cfg3: 16-col tiles
+    assert lib.pm_delta_workspace_bytes(1, 130, 2, 64, bf16) == 2 * 3 * per
+    assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, bf16) == 0  # cfg1: 32-col tiles
+    assert lib.pm_delta_workspace_bytes(1, 4096, 16, 128, f32) == 0
+    assert lib.pm_delta_workspace_bytes(1, 4096, 16, 256, bf16) == 0
+    # varlen: H x (ceil(total / 64) + n_seqs) slots
+    assert lib.pm_delta_varlen_workspace_bytes(3, 1000, 4, 128, bf16) == 4 * (16 + 3) * per
+    assert lib.pm_delta_varlen_workspace_bytes(8, 16384, 16, 128, bf16) == 0  # cfg2: 32-col tiles
+    old = _native.set_path(3)
+    try:
+        assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, bf16) == 64 * 64 * per
+        assert lib.pm_delta_varlen_workspace_bytes(8, 16384, 16, 128, bf16) == 16 * (256 + 8) * per
+        # path 3 refuses to run without the workspace (checked before any launch)
+        p = ctypes.c_void_p(256)
+        rc = lib.pm_delta_fwd(p, p, p, p, None, p, p, 1, 64, 1, 128, bf16, f32, 64, None, 0, None)
+        assert rc == _native.E_WORKSPACE and b"workspace" in lib.pm_last_error()
+        rc = lib.pm_delta_fwd(p, p, p, p, None, p, p, 1, 64, 1, 128, bf16, f32, 64, p, per - 16, None)
+        assert rc == _native.E_WORKSPACE
+    finally:
+        _native.set_path(old)
+    old = _native.set_path(1)
+    try:
+        assert lib.pm_delta_workspace_bytes(1, 32768, 32, 128, bf16) == 0
+    finally:
+        _native.set_path(old)
+    old = _native.set_tile(32)
+    try:
+        assert lib.pm_delta_workspace_bytes(1, 32768, 32, 128, bf16) == 0
+    finally:
+        _native.set_tile(old)
+
+
 def test_path_and_tile_switches():
     old = _native.set_path(1)
     try:

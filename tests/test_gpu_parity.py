@@ -324,8 +324,9 @@ def test_chunked_state_carry_is_bitwise_at_chunk_boundaries():
 
 def test_chunked_repeat_and_graph_replay_are_bitwise():
     _, (q, k, v, b, s0) = _bf16_case((2, 256, 4, 128), seed=10, s0_std=0.02)
-    o1, s1 = kernels.chunked_delta_rule(q, k, v, b, s0)
-    o2, s2 = kernels.chunked_delta_rule(q, k, v, b, s0)
+    with _path(2):  # the single-stage form (this shape's default is the split form)
+        o1, s1 = kernels.chunked_delta_rule(q, k, v, b, s0)
+        o2, s2 = kernels.chunked_delta_rule(q, k, v, b, s0)
     assert torch.equal(o1, o2) and torch.equal(s1, s2)
     lib = _native.lib()
     o = torch.empty_like(o1)
@@ -358,12 +359,14 @@ def test_chunked_repeat_and_graph_replay_are_bitwise():
         torch.cuda.synchronize()
 
 
-def test_cfg1_full_size_vs_c_oracle():
+@pytest.mark.parametrize("path", [0, 3])
+def test_cfg1_full_size_vs_c_oracle(path):
     from oracle import cref
 
     c = synth.CONFIGS[1]
     x, (q, k, v, b, _) = _bf16_case((c["B"], c["T"], c["H"], c["D"]), seed=1)
-    out, st = kernels.chunked_delta_rule(q, k, v, b)
+    with _path(path):
+        out, st = kernels.chunked_delta_rule(q, k, v, b)
     e_o, e_s = cref.delta_fwd(x.q_bits, x.k_bits, x.v_bits, x.beta, None, threads=CPU_THREADS)
     ro = assert_bf16_parity(_np(out), e_o, "cfg1 O")
     rs = assert_bf16_parity(_np(st), e_s, "cfg1 S")
@@ -482,35 +485,107 @@ def test_cfg4_decode_steps_vs_c_oracle():
 @pytest.mark.parametrize("shape,tile,s0_std,out16", [
     ((1, 64, 1, 128), 0, None, False), ((2, 150, 2, 128), 0, 0.02, False), ((1, 1, 3, 128), 32, None, False),
     ((2, 257, 3, 64), 0, 0.02, False), ((3, 300, 2, 128), 16, 0.02, True), ((1, 130, 4, 64), 32, None, True),
-    ((4, 1024, 16, 128), 0, None, False),
+    ((1, 700, 2, 128), 32, 0.02, False),
 ])
-def test_pipeline_form_is_bitwise_the_default(shape, tile, s0_std, out16):
-    """pm_delta_set_path(3) runs the plain forward on the deep four-wave pipeline
-    kernel; every product is formed in the same order, so O and S equal the
-    default kernel's bit for bit (tails, D 64/128, both tile widths, S0, bf16 O)."""
-    x, (q, k, v, b, s0) = _bf16_case(shape, seed=sum(shape) + tile, s0_std=s0_std)
+def test_split_form_vs_oracle(shape, tile, s0_std, out16):
+    """pm_delta_set_path(3): the plain forward in split form (T diag(beta) built by a parallel
+    pass into the workspace, then the chunk recurrence), against the fp64 chunked oracle at
+    the bf16 bound, and against the single-stage kernel (path 2) over tails, D 64/128, both
+    tile widths, S0 and bf16 O."""
+    x, (q, k, v, b, s0) = _bf16_case(shape, seed=sum(shape) + tile + 7, s0_std=s0_std)
     odt = torch.bfloat16 if out16 else None
-    with _path(2, tile):
-        o2, s2 = kernels.chunked_delta_rule(q, k, v, b, s0, out_dtype=odt)
     with _path(3, tile):
         o3, s3 = kernels.chunked_delta_rule(q, k, v, b, s0, out_dtype=odt)
+    with _path(2, tile):
+        o2, s2 = kernels.chunked_delta_rule(q, k, v, b, s0, out_dtype=odt)
     torch.cuda.synchronize()
-    assert torch.equal(o2, o3) and torch.equal(s2, s3)
-    if shape[1] <= 300:
-        e_o, e_s = ref.wy_chunked_fwd(x.q, x.k, x.v, x.beta, x.s0, chunk=64)
-        assert_bf16_parity(_np(o3.float()), e_o, "pipeline O")
-        assert_bf16_parity(_np(s3), e_s, "pipeline S")
+    e_o, e_s = ref.wy_chunked_fwd(x.q, x.k, x.v, x.beta, x.s0, chunk=64, dtype=np.float64)
+    ro = assert_bf16_parity(_np(o3.float()), e_o, f"split O {shape}")
+    rs = assert_bf16_parity(_np(s3), e_s, f"split S {shape}")
+    assert rel_l2(_np(o3.float()), _np(o2.float())) < 2e-2 and rel_l2(_np(s3), _np(s2)) < 2e-2
+    print(f"{shape} tile {tile}: split rel-L2 O {ro:.2e} S {rs:.2e}")
 
 
-def test_pipeline_form_varlen_is_bitwise_the_default():
+def test_split_form_default_choice_and_repeat():
+    """By default the split form runs where the chunked kernel takes 16-column tiles (here
+    B*H*(D/32) = 8 < 256): the default call equals the path-3 call bit for bit, repeats
+    bitwise, and state carry at a chunk boundary is bitwise."""
+    x, (q, k, v, b, s0) = _bf16_case((1, 640, 2, 128), seed=33, s0_std=0.02)
+    assert _native.lib().pm_delta_workspace_bytes(1, 640, 2, 128, _native.DTYPE_BF16) > 0
+    o0, s0_ = kernels.chunked_delta_rule(q, k, v, b, s0)
+    with _path(3):
+        o3, s3 = kernels.chunked_delta_rule(q, k, v, b, s0)
+    o1, s1 = kernels.chunked_delta_rule(q, k, v, b, s0)
+    assert torch.equal(o0, o3) and torch.equal(s0_, s3)
+    assert torch.equal(o0, o1) and torch.equal(s0_, s1)
+    oa, sa = kernels.chunked_delta_rule(q[:, :384].contiguous(), k[:, :384].contiguous(),
+                                        v[:, :384].contiguous(), b[:, :384].contiguous(), s0)
+    ob, sb = kernels.chunked_delta_rule(q[:, 384:].contiguous(), k[:, 384:].contiguous(),
+                                        v[:, 384:].contiguous(), b[:, 384:].contiguous(), sa)
+    assert torch.equal(torch.cat([oa, ob], dim=1), o0) and torch.equal(sb, s0_)
+
+
+def test_split_form_graph_replay_is_bitwise():
+    _, (q, k, v, b, s0) = _bf16_case((2, 256, 4, 128), seed=34, s0_std=0.02)
+    lib = _native.lib()
+    with _path(3):
+        o1, s1 = kernels.chunked_delta_rule(q, k, v, b, s0)
+        nb = lib.pm_delta_workspace_bytes(2, 256, 4, 128, _native.DTYPE_BF16)
+    assert nb == 8 * 4 * 6 * 1024
+    ws = torch.empty(nb, dtype=torch.uint8, device=q.device)
+    o = torch.empty_like(o1)
+    s = torch.empty_like(s1)
+
+    def launch():
+        st = torch.cuda.current_stream().cuda_stream
+        old = _native.set_path(3)
+        try:
+            rc = lib.pm_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), b.data_ptr(),
+                                  s0.data_ptr(), o.data_ptr(), s.data_ptr(), 2, 256, 4, 128,
+                                  _native.DTYPE_BF16, _native.DTYPE_F32, 64, ws.data_ptr(), nb, st)
+        finally:
+            _native.set_path(old)
+        _native.check(rc)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch()
+    for _ in range(3):
+        o.zero_()
+        s.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, o1) and torch.equal(s, s1)
+        kernels.chunked_delta_rule(q, k, v, b, s0)
+        torch.cuda.synchronize()
+
+
+def test_split_form_varlen_segments_and_oracle():
+    """Varlen in split form: each segment (empty, 1-token and multi-chunk ones included)
+    equals its standalone split-form call bit for bit, and matches the oracle."""
     lens = np.array([64, 1, 0, 130, 700, 3000, 257])
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     n = int(cu[-1])
     x, (q, k, v, b, _) = _bf16_case((n, 4, 128), seed=91)
     for tile in (0, 16):
-        with _path(2, tile):
-            o2, s2 = kernels.chunked_delta_rule_varlen(q, k, v, b, cu)
         with _path(3, tile):
             o3, s3 = kernels.chunked_delta_rule_varlen(q, k, v, b, cu)
-        torch.cuda.synchronize()
-        assert torch.equal(o2, o3) and torch.equal(s2, s3)
+            for i in range(cu.size - 1):
+                a, z = int(cu[i]), int(cu[i + 1])
+                oi, si = kernels.chunked_delta_rule(q[None, a:z], k[None, a:z], v[None, a:z], b[None, a:z])
+                assert torch.equal(o3[a:z], oi[0]), f"segment {i} [{a}, {z}) tile {tile}"
+                assert torch.equal(s3[i], si[0]), f"segment {i} state tile {tile}"
+    o_np, s_np = _np(o3), _np(s3)
+    for i in (0, 3, 6):
+        a, z = int(cu[i]), int(cu[i + 1])
+        e_o, e_s = ref.wy_chunked_fwd(x.q[None, a:z], x.k[None, a:z], x.v[None, a:z], x.beta[None, a:z],
+                                      None, chunk=64, dtype=np.float64)
+        assert_bf16_parity(o_np[a:z], e_o[0], f"split varlen segment {i} O")
+        assert_bf16_parity(s_np[i], e_s[0], f"split varlen segment {i} S")

@@ -12,25 +12,30 @@
 //
 // T depends on the chunk's K and beta only, so K1t builds it for every
 // (sequence, head, chunk) at once (one wave each, K rows straight from global
-// memory into MFMA operand registers) and writes it, packed in MFMA operand
-// order, to the forward's workspace (6 KiB per chunk).
+// memory into MFMA operand registers) and writes T'' = -T diag(beta), packed in
+// MFMA operand order, to the forward's workspace (6 KiB per chunk).  With it
+//   U = T'' (K S - V)
+// and the recurrence's dependent steps per chunk shrink to X = K S - V (the
+// accumulators start at -V), U = T'' bf16(X), S += K^T U.
 //
 // K1s: one 256-thread workgroup per (sequence, head, d_v tile of DV columns)
-// walks the sequence's chunks; iteration i ends with one LDS-only barrier:
+// walks the sequence's chunks; every iteration ends with one LDS-only barrier.
 //   * chain waves (DV / 16; wave w owns columns col0 + 16 w + [0, 16) of S as
-//     fp32 MFMA accumulators) run chunk i - 1 entirely from registers (K and
-//     Q operand rows, K^T, V, beta and T, loaded during iteration i - 1), with
-//     P(i - 1) read from LDS, and load chunk i's operands from LDS for the next
-//     iteration as their registers fall free;
-//   * the P wave builds P(i) = lower_incl(Q K^T) of chunk i into LDS, and
-//     copies chunk i + 2's V tile, T and beta;
-//   * the loader wave copies chunk i + 2's K and Q tiles.
-// The copies are HBM -> LDS (buffer_load ... lds); each wave waits for its
-// share of chunk i + 1's before the barrier.
-// Every copy has two iterations to land, and three chunk buffers suffice:
-// chunk i - 1 lives in the chain's registers, not in LDS.  Every product is
-// formed in the same order and rounding as the single-stage kernel, so the
-// results are equal bit for bit.
+//     fp32 MFMA accumulators) run chunk c from registers (K operand rows, K^T,
+//     V loaded from LDS during chunk c - 1; T'' loaded from the workspace two
+//     chunks ahead), hand U(c) and bf16 S_{c+1} to the output wave through LDS,
+//     and copy the V columns of chunk c + 3;
+//   * the output wave, one chunk behind, forms Y = Q S and O = Y + P U and
+//     stores O with range-checked buffer stores; it copies chunk i + 2's Q rows;
+//   * the P wave builds P = lower_incl_diag(Q K^T) into LDS and copies chunk
+//     i + 2's K rows.
+// The copies are HBM -> LDS (buffer_load ... lds); each wave waits for its own
+// share of the next chunk's before the barrier.  The chain waves issue their T
+// loads and V copies as inline asm with exact vmcnt waits (the compiler's
+// conservative waits stalled the chain on copies issued in the same iteration).
+// The products are the single-stage kernel's, except that T diag(beta) is
+// applied as one bf16 operand and U = T'' bf16(K S - V) instead of
+// T bf16(diag(beta)(V - K S)); results agree within bf16 rounding, not bitwise.
 
 #include "pm_cdna4.h"
 #include "pm_internal.h"

@@ -111,6 +111,21 @@ def cpu_threads() -> int:
     return max(1, len(os.sched_getaffinity(0)))
 
 
+def time_launches(stream, fn, n):
+    """Mean ms per call of fn(0..n-1), launched back to back on `stream` between one
+    pair of events (no event between the launches)."""
+    import torch
+
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(n):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -330,14 +345,8 @@ def main():
     for i in range(4):
         step(i)
     torch.cuda.synchronize()
-    dev_ = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in range(args.decode_steps)]
-    for i in range(args.decode_steps):
-        dev_[i][0].record(stream)
-        step(i)
-        dev_[i][1].record(stream)
-    torch.cuda.synchronize()
-    step_ms = float(np.mean([a.elapsed_time(b) for a, b in dev_]))
+    # one event pair around the back-to-back steps (as for the forward's roofline)
+    step_ms = time_launches(stream, step, args.decode_steps)
     dbytes = step_bytes(Bd, Hd, D)
     dtraffic = None
     if os.path.exists(args.decode_traffic):
@@ -391,14 +400,7 @@ def main():
     for i in range(4):
         step_slots(i)
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.decode_steps)]
-    for i in range(args.decode_steps):
-        ev[i][0].record(stream)
-        step_slots(i)
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    slot_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    slot_ms = time_launches(stream, step_slots, args.decode_steps)
     decode["state_cache"] = {
         "workload": "cfg4 decode through a 512-slot state cache (pm_delta_step_slots)",
         "us_per_step": slot_ms * 1e3,
@@ -407,6 +409,17 @@ def main():
                      "frac": dbytes / (slot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
     }
     del pool, state
+
+    # What a plain read-modify-write stream reaches on this HBM: torch's in-place
+    # elementwise multiply over a 512 MiB fp32 buffer (the bytes one decode step
+    # reads and writes back).
+    buf = torch.ones((Bd * Hd * D * D,), dtype=torch.float32, device=dev)
+    rmw_ms = time_launches(stream, lambda i: buf.mul_(0.9999999), args.decode_steps)
+    rmw_gbs = 2 * buf.numel() * 4 / (rmw_ms * 1e-3) / 1e9
+    decode["rmw_ceiling"] = {"kernel": "torch in-place mul_ over 512 MiB fp32", "achieved": rmw_gbs,
+                             "unit": "GB/s", "frac": rmw_gbs / HBM_PEAK_GBS,
+                             "decode_over_rmw": decode["roofline"]["achieved"] / rmw_gbs}
+    del buf
 
     # the model's linear attention (pm_linear_attention: q/k L2-normalised inside the
     # kernel, beta = 1) at the cfg1 shape: bf16 q/k/v on the chunked kernel, and fp32

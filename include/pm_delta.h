@@ -192,7 +192,7 @@ size_t pm_delta_varlen_workspace_bytes(int n_seqs, int total_T, int H, int D, in
  *   go (B, T, H, D) fp32 or NULL (zeros); gs (B, H, D, D) fp32 or NULL (zeros);
  *   s0 NULL means a zero initial state;
  *   gq, gk, gv (B, T, H, D), gbeta (B, T, H), gs0 (B, H, D, D): fp32 outputs.
- * q, k, v are fp32 or bf16 (in_dtype); 1 <= D <= 128.
+ * q, k, v are fp32 or bf16 (in_dtype); 1 <= D <= 256.
  * Two kernels, chosen as the forward's are (pm_delta_set_path):
  *   - bf16 q/k/v with D in {64, 128}: the chunked backward on bf16 MFMA
  *     (the forward's chunked kernel in reverse; bf16 parity, rel-L2 <= 2e-2
@@ -203,8 +203,8 @@ size_t pm_delta_varlen_workspace_bytes(int n_seqs, int total_T, int H, int D, in
  *   - otherwise the per-token fp32 backward (fp32 parity).  Workspace:
  *     per-token u = v - S^T k and the state every 8 tokens, 4 * B * H *
  *     (T * D + ceil(T / 8) * D * D) bytes, and for D > 32 the partial sums
- *     of gq, gk and gbeta over 32-column tiles of the state, 4 * B * H * T
- *     * ceil(D / 32) * (2 * D + 1) bytes more.
+ *     of gq, gk and gbeta over column tiles of the state (32 columns for
+ *     D <= 128, 16 above), 4 * B * H * T * n_tiles * (2 * D + 1) bytes more.
  * workspace: device memory of at least pm_delta_bwd_workspace_bytes(B, T,
  * H, D, in_dtype) bytes (queried under the same path setting), 4-byte
  * aligned, contents undefined on entry and exit.
@@ -216,7 +216,7 @@ int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
                  void* workspace, size_t ws_bytes, void* stream);
 
 /* Workspace bytes pm_delta_bwd needs for these shapes and in_dtype under the
- * current path setting (0 for invalid shapes, dtypes or D > 128). */
+ * current path setting (0 for invalid shapes, dtypes or D > 256). */
 size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype);
 
 /*

@@ -22,7 +22,7 @@ ABI_VERSION = 7
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256
-MAX_D_BWD = 128
+MAX_D_BWD = 256
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
 E_NULL, E_SHAPE, E_DTYPE, E_ALIGN, E_WORKSPACE, E_UNSUPPORTED = -1, -2, -3, -4, -5, -6

@@ -21,8 +21,9 @@
 // (tests/test_kernels.py:1537-1548) at 1e-6, where 16 reaches 3e-5.
 //
 // The recurrence is separable along the columns of S and G (d_v): a
-// workgroup owns a tile of NC = min(D, 32) columns of one (b, h), so B*H*
-// ceil(D/NC) workgroups run (256 at cfg1 instead of 64).  gv and gS0 are
+// workgroup owns a tile of NC columns of one (b, h) (NC = min(D, 32) for
+// D <= 128, 16 above), so B*H*ceil(D/NC) workgroups run (256 at cfg1
+// instead of 64).  gv and gS0 are
 // per column; gq, gk and gbeta sum over all columns (x, y and S go are row
 // sums), so with several tiles each writes its partial sums and a final
 // pass adds them (in a fixed order: results do not depend on scheduling).
@@ -51,7 +52,8 @@ namespace pm {
 constexpr int kBwdSteps = 8;  // tokens staged in LDS at a time
 constexpr int kCk = 8;        // tokens between state checkpoints (multiple of kBwdSteps)
 constexpr int kRpt = 8;       // elements of a row or column slice per thread
-constexpr int kTileCols = 32; // columns per workgroup when D > 32
+constexpr int kTileCols = 32; // columns per workgroup when 32 < D <= 128
+constexpr int kTileColsWide = 16;  // ... when D > 128 (512 threads: 32 row slices x 16 columns)
 static_assert(kCk == kBwdSteps, "the reverse pass stages one checkpoint block at a time");
 
 // Workgroup barrier for LDS traffic only: global stores still in flight are not
@@ -70,7 +72,7 @@ static int pow2_at_least(int x) {
 }
 static BwdGeo bwd_geo(int D) {
     BwdGeo g;
-    g.nc = D <= kTileCols ? D : kTileCols;
+    g.nc = D <= kTileCols ? D : (D <= 128 ? kTileCols : kTileColsWide);
     g.n_tiles = (D + g.nc - 1) / g.nc;
     g.rsc = pow2_at_least((D + kRpt - 1) / kRpt);
     g.rsr = pow2_at_least((g.nc + kRpt - 1) / kRpt);
@@ -268,9 +270,11 @@ static hipError_t launch_ckpt_t(const BwdArgs& a, float* u_ws, float* ck_ws, hip
     return hipSuccess;
 }
 
-// RPT 8 and RS the smallest power of two with 8 RS >= D (D <= 128).
+// RPT 8 and RS the smallest power of two with 8 RS >= D for D <= 128; RPT 16 and RS 16
+// above (the per-token forward's geometry).
 template <typename InT>
 static hipError_t launch_ckpt(const BwdArgs& a, float* u_ws, float* ck_ws, hipStream_t st) {
+    if (a.D > 128) return launch_ckpt_t<16, 16, InT>(a, u_ws, ck_ws, st);
     int rs = 1;
     while (8 * rs < a.D) rs <<= 1;
     switch (rs) {
@@ -300,8 +304,9 @@ __device__ __forceinline__ float slice_dot(const float (&a)[kRpt], const float (
 // ---------------- K5b: reverse pass over one column tile ----------------
 // gq/gk/gb receive this tile's sums over its columns: the outputs themselves
 // when n_tiles == 1, else this tile's slot of the partial-sum buffers.
-// RSC row slices per column (column layout), RSR column slices per row (row layout).
-template <typename InT, int RSC, int RSR>
+// RSC row slices per column (column layout), RSR column slices per row (row layout), NCT
+// the tile width the geometry is sized for (the fewest threads a launch has is NCT RSC).
+template <typename InT, int RSC, int RSR, int NCT>
 __global__ __launch_bounds__(512) void delta_bwd_kernel(
     const InT* __restrict__ q, const InT* __restrict__ k, const float* __restrict__ beta,
     const float* __restrict__ go, const float* __restrict__ gs, const float* __restrict__ u_ws,
@@ -315,7 +320,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
     constexpr int CPL = RSR * kSl;
     constexpr int KB = kBwdSteps;
     // per-thread staging slots, for the fewest threads a launch of this geometry has
-    constexpr int NTMIN = 32 * RSC < 64 ? 64 : 32 * RSC;
+    constexpr int NTMIN = NCT * RSC < 64 ? 64 : NCT * RSC;
     constexpr int MK = (KB * DP + NTMIN - 1) / NTMIN, MG = (KB * CP + NTMIN - 1) / NTMIN;
     constexpr int SB = 2 * KB * DPL + 2 * KB * CPL + KB;  // one staging buffer
     const int NT = blockDim.x, NWV = NT / 64;
@@ -482,7 +487,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 // w = G^T k (column layout), x = G u over the tile's columns (row layout)
                 float wp = slice_dot(kc, Gc);
                 float xp = slice_dot(ur, Gr);
-                wp = col_sum<RSC>(wp);
+                wp = lane_sum<RSC>(wp);
                 gqp = col_sum<RSR>(gqp);
                 xp = col_sum<RSR>(xp);
                 float* swp = sw + (t & 1) * CPL;
@@ -607,15 +612,38 @@ static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
     const int dp = g.rsc * kSl, cp = g.rsr * kSl;
     const size_t lds_b = sizeof(float) * (2 * (2 * kBwdSteps * dp + 2 * kBwdSteps * cp + kBwdSteps) +
                                           2 * cp + 2 * (3 * kBwdSteps * a.D + kBwdSteps * g.nc));
-    // with kRpt 8 and tiles of min(D, 32) columns, RSR = min(RSC, 4) for every D <= 128
-    if (g.rsr != (g.rsc < 4 ? g.rsc : 4) || g.rsc > 16) return hipErrorInvalidValue;
-    auto kern = delta_bwd_kernel<InT, 16, 4>;
+    // with kRpt 8 and tiles of min(D, 32) columns, RSR = min(RSC, 4) for every D <= 128;
+    // above, 16-column tiles: RSC 32, RSR 2
+    const bool wide = a.D > 128;
+    if (wide ? (g.rsc != 32 || g.rsr != 2 || g.nc != kTileColsWide)
+             : (g.rsr != (g.rsc < 4 ? g.rsc : 4) || g.rsc > 16))
+        return hipErrorInvalidValue;
+    auto kern = delta_bwd_kernel<InT, 16, 4, kTileCols>;
     switch (g.rsc) {
-        case 1: kern = delta_bwd_kernel<InT, 1, 1>; break;
-        case 2: kern = delta_bwd_kernel<InT, 2, 2>; break;
-        case 4: kern = delta_bwd_kernel<InT, 4, 4>; break;
-        case 8: kern = delta_bwd_kernel<InT, 8, 4>; break;
+        case 1: kern = delta_bwd_kernel<InT, 1, 1, kTileCols>; break;
+        case 2: kern = delta_bwd_kernel<InT, 2, 2, kTileCols>; break;
+        case 4: kern = delta_bwd_kernel<InT, 4, 4, kTileCols>; break;
+        case 8: kern = delta_bwd_kernel<InT, 8, 4, kTileCols>; break;
+        case 32: kern = delta_bwd_kernel<InT, 32, 2, kTileColsWide>; break;
         default: break;
+    }
+    if (wide) {
+        // the dynamic-LDS limit is a per-device function attribute: set it once, to what
+        // the largest D (256) of this kernel needs
+        const int dp_w = 32 * kSl, cp_w = 2 * kSl;
+        const size_t lds_max = sizeof(float) * (2 * (2 * kBwdSteps * dp_w + 2 * kBwdSteps * cp_w + kBwdSteps) +
+                                                2 * cp_w + 2 * (3 * kBwdSteps * 256 + kBwdSteps * kTileColsWide));
+        if (lds_b > lds_max) return hipErrorInvalidValue;
+        int dev = 0;
+        if ((err = hipGetDevice(&dev)) != hipSuccess) return err;
+        static bool attr_set[2][64] = {};
+        const int which = sizeof(InT) == 2 ? 1 : 0;
+        if (dev < 0 || dev >= 64 || !attr_set[which][dev]) {
+            err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_max));
+            if (err != hipSuccess) return err;
+            if (dev >= 0 && dev < 64) attr_set[which][dev] = true;
+        }
     }
     hipLaunchKernelGGL(kern, dim3(grid), dim3(g.threads), lds_b, st, static_cast<const InT*>(a.q),
                        static_cast<const InT*>(a.k), a.beta, a.go, a.gs, u_ws, ck_ws, gq, gk, a.gv, gb,

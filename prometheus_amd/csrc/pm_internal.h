@@ -85,10 +85,11 @@ hipError_t launch_chunked_split(const ChunkedArgs& a, int dv, void* t_ws, hipStr
 hipError_t launch_chunked_states(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st);
 
 // Reverse mode (K5, fp32): fixed-length batch of n_pairs = B*H sequences of
-// T tokens, D <= 128.  workspace holds bwd_workspace_floats(n_pairs, T, D)
+// T tokens, D <= 256.  workspace holds bwd_workspace_floats(n_pairs, T, D)
 // floats: u (n_pairs x T x D), the checkpoints (n_pairs x ceil(T/8) x D x D),
-// then for D > 32 the per-column-tile partial sums of gq, gk (ceil(D/32) x
-// n_pairs x T x D each) and gbeta (ceil(D/32) x n_pairs x T).
+// then for D > 32 the per-column-tile partial sums of gq, gk (n_tiles x
+// n_pairs x T x D each) and gbeta (n_tiles x n_pairs x T), n_tiles = ceil(D/32)
+// for D <= 128 and ceil(D/16) above.
 struct BwdArgs {
     const void* q;
     const void* k;
@@ -106,7 +107,7 @@ struct BwdArgs {
     int n_pairs, T, H, D;
     bool in_bf16;
 };
-constexpr int kBwdMaxD = 128;
+constexpr int kBwdMaxD = 256;
 size_t bwd_workspace_floats(long n_pairs, int T, int D);
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t st);
 

@@ -5,6 +5,7 @@
         --cmd-fetch "..." --cmd-write "..." -o OUT.json
     python -m prometheus_amd.rocprof_summary mfma DIR --kernel NAME --cmd "..."
         [--algorithmic-flop F] -o OUT.json
+    python -m prometheus_amd.rocprof_summary counters DIR --kernel NAME --cmd "..." -o OUT.md
 
 ``stats`` turns ``*_kernel_stats.csv`` (from ``--kernel-trace --stats``) into a
 short markdown table.  ``traffic`` reads two ``--pmc`` runs (``FETCH_SIZE``,
@@ -15,7 +16,9 @@ of that copy, giving the HBM bytes one launch of the kernel moves.
 ``mfma`` reads one ``--pmc MfmaUtil MfmaFlopsBF16`` run (rocprofv3's derived
 counters: MFMA busy cycles over GUI-active cycles times SIMDs, and
 ``SQ_INSTS_VALU_MFMA_MOPS_BF16 * 512``) and records their per-dispatch mean
-for the kernel, beside its algorithmic flops.
+for the kernel, beside its algorithmic flops.  ``counters`` reads any one
+``--pmc`` run and tabulates the per-dispatch mean of every counter it holds
+for the kernel (SQ counters are summed over the chip), with the LDS ratios.
 """
 
 from __future__ import annotations
@@ -177,6 +180,41 @@ def mfma(args) -> None:
     print(json.dumps(res, indent=1))
 
 
+def counters(args) -> None:
+    path = _one(os.path.join(args.dir, "**", "*counter_collection.csv"))
+    names = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] not in names:
+                names.append(r["Counter_Name"])
+    vals = {}
+    kname = None
+    for n in names:
+        kname, v = _pick(_per_dispatch(args.dir, n), args.kernel)
+        vals[n] = statistics.mean(v)
+    lines = ["# rocprofv3 counters: " + kname, "", "Command:", "", "```", args.cmd, "```", "",
+             "Per-dispatch mean over the kernel's dispatches (SQ counters summed over the chip).",
+             "", "| counter | per dispatch |", "|---|---:|"]
+    lines += [f"| `{n}` | {vals[n]:.4g} |" for n in names]
+    ratios = []
+    if "SQ_WAIT_INST_LDS" in vals and "SQ_WAVE_CYCLES" in vals and vals["SQ_WAVE_CYCLES"]:
+        ratios.append(("wave-cycles waiting to issue an LDS instruction / wave-cycles",
+                       vals["SQ_WAIT_INST_LDS"] / vals["SQ_WAVE_CYCLES"]))
+    if "SQ_WAIT_ANY" in vals and "SQ_WAVE_CYCLES" in vals and vals["SQ_WAVE_CYCLES"]:
+        ratios.append(("wave-cycles waiting on anything / wave-cycles", vals["SQ_WAIT_ANY"] / vals["SQ_WAVE_CYCLES"]))
+    if "SQ_LDS_BANK_CONFLICT" in vals and "SQ_LDS_IDX_ACTIVE" in vals and vals["SQ_LDS_IDX_ACTIVE"]:
+        ratios.append(("LDS bank-conflict cycles / LDS active cycles",
+                       vals["SQ_LDS_BANK_CONFLICT"] / vals["SQ_LDS_IDX_ACTIVE"]))
+    if "SQ_ACTIVE_INST_LDS" in vals and "SQ_WAVE_CYCLES" in vals and vals["SQ_WAVE_CYCLES"]:
+        ratios.append(("wave-cycles with an LDS instruction in flight / wave-cycles",
+                       vals["SQ_ACTIVE_INST_LDS"] / vals["SQ_WAVE_CYCLES"]))
+    if ratios:
+        lines += ["", "| ratio | value |", "|---|---:|"] + [f"| {a} | {b:.3f} |" for a, b in ratios]
+    with open(args.out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd_name", required=True)
@@ -200,8 +238,13 @@ def main(argv=None) -> None:
     m.add_argument("--cmd", required=True)
     m.add_argument("--algorithmic-flop", type=float, default=None)
     m.add_argument("-o", "--out", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("dir")
+    c.add_argument("--kernel", required=True)
+    c.add_argument("--cmd", required=True)
+    c.add_argument("-o", "--out", required=True)
     args = ap.parse_args(argv)
-    {"stats": stats, "traffic": traffic, "mfma": mfma}[args.cmd_name](args)
+    {"stats": stats, "traffic": traffic, "mfma": mfma, "counters": counters}[args.cmd_name](args)
 
 
 if __name__ == "__main__":

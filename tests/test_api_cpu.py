@@ -101,13 +101,13 @@ def test_bwd_shape_checks_raise_before_any_device_work():
         kernels.chunked_delta_rule_bwd(r, (np.zeros((1, 3, 2, 5), np.float32), None))
     with pytest.raises(kernels.KernelError):
         kernels.chunked_delta_rule_bwd(r, (None, np.zeros((1, 2, 4, 3), np.float32)))
-    big = _residual(d=129)
+    big = _residual(d=257)
     with pytest.raises(kernels.KernelError):
         kernels.chunked_delta_rule_bwd(big, (None, None))
 
 
 def _per_token_ws(b, t, h, d):
-    n_ck, n_tiles = -(-t // 8), -(-d // 32)
+    n_ck, n_tiles = -(-t // 8), -(-d // (32 if d <= 128 else 16))
     part = n_tiles * t * (2 * d + 1) if n_tiles > 1 else 0
     return 4 * b * h * (t * d + n_ck * d * d + part)
 
@@ -129,7 +129,10 @@ def test_bwd_workspace_bytes():
         assert lib.pm_delta_bwd_workspace_bytes(2, 130, 3, 64, bf16) == _per_token_ws(2, 130, 3, 64)
     finally:
         _native.set_path(old)
-    assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 129, f32) == 0
+    assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 257, f32) == 0
+    # D above 128: 16-column tiles
+    assert lib.pm_delta_bwd_workspace_bytes(1, 20, 2, 160, f32) == _per_token_ws(1, 20, 2, 160)
+    assert lib.pm_delta_bwd_workspace_bytes(1, 20, 2, 256, bf16) == _per_token_ws(1, 20, 2, 256)
     assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 0, f32) == 0
     assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 8, 3) == 0
 
@@ -144,7 +147,7 @@ def test_bwd_abi_argument_validation_without_gpu():
         return f(*q, gs0, b, t, h, d, dt, ws, nbytes, None)
 
     assert call(1, 4, 1, 0, 0, p, 1 << 20) == _native.E_SHAPE
-    assert call(1, 4, 1, 129, 0, p, 1 << 20) == _native.E_SHAPE
+    assert call(1, 4, 1, 257, 0, p, 1 << 20) == _native.E_SHAPE
     assert b"backward D" in lib.pm_last_error()
     assert call(-1, 4, 1, 8, 0, p, 1 << 20) == _native.E_SHAPE
     assert call(1, 4, 1, 8, 3, p, 1 << 20) == _native.E_DTYPE
@@ -443,7 +446,7 @@ def test_noalloc_backward_rejects_sizes_beyond_its_scratch():
     assert L.pm_delta_bwd_workspace_bytes(B, T, H, D, _native.DTYPE_BF16) > _native.NOALLOC_SCRATCH_BYTES
     assert L.pm_delta_bwd_noalloc(*ptrs, B, T, H, D, _native.DTYPE_BF16, None) == _native.E_WORKSPACE
     assert b"no-allocation" in L.pm_last_error()
-    assert L.pm_delta_bwd_noalloc(*ptrs, 1, 8, 1, 129, _native.DTYPE_F32, None) == _native.E_SHAPE
+    assert L.pm_delta_bwd_noalloc(*ptrs, 1, 8, 1, 257, _native.DTYPE_F32, None) == _native.E_SHAPE
     assert L.pm_delta_bwd_noalloc(*ptrs, 1, 8, 1, 8, 7, None) == _native.E_DTYPE
     # nothing to do: B*H == 0 returns before any device work
     assert L.pm_delta_bwd_noalloc(*([None] * 12), 0, 8, 1, 8, _native.DTYPE_F32, None) == 0

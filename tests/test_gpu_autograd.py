@@ -62,6 +62,20 @@ def test_autograd_is_the_bwd_kernel_fp32():
         assert_f32_parity(_np(got), e_ref, f"autograd {name} vs delta_vjp")
 
 
+def test_autograd_head_dim_160_fp32():
+    """A head dimension above 128: the per-token forward and backward (16-column tiles)."""
+    x = synth.fwd_inputs((1, 40, 2, 160), seed=160, dtype="fp32", s0_std=0.02)
+    rng = np.random.default_rng(160)
+    go = rng.standard_normal(x.q.shape).astype(np.float32)
+    gs = rng.standard_normal(x.s0.shape).astype(np.float32) * 0.05
+    leaves = [_leaf(a) for a in (x.q, x.k, x.v, x.beta, x.s0)]
+    y, ns = kernels.chunked_delta_rule(*leaves)
+    grads = torch.autograd.grad((y, ns), leaves, (torch.from_numpy(go).cuda(), torch.from_numpy(gs).cuda()))
+    exp = ref.delta_vjp(x.q, x.k, x.v, x.beta, go, gs, x.s0)
+    for name, got, e_ref in zip(("gq", "gk", "gv", "gbeta", "gstate"), grads, exp):
+        assert_f32_parity(_np(got), e_ref, f"autograd D160 {name} vs delta_vjp")
+
+
 def test_autograd_gpu_v1_case():
     """tests/test_kernels.py:1551-1581: rng(64), (2, 8, 2, 4), chunk 64, against the
     bwd entry point and the NumPy-style VJP."""

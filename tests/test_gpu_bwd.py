@@ -7,7 +7,8 @@ random go / gs (tests/test_kernels_delta_fwd_jit.py:284-347, seeds 105 and
 106), the finite-difference test of the gradients (tests/test_kernels.py:
 409-432, seed 18), plus the shapes this build adds: head dimensions up to
 128 with padded row slices and ragged 32-column tiles of the state,
-sequences across several checkpoint blocks, bf16 q/k/v, missing cotangents, T = 0 and repeatability.
+sequences across several checkpoint blocks, head dimensions 129-256 on 16-column
+tiles, bf16 q/k/v, missing cotangents, T = 0 and repeatability.
 
 Tolerance: fp32 (tests/parity.py), rel-L2 <= 1e-5 and max-abs <= 1e-4
 (scaled), against the fp64 oracle on the same (for bf16: bf16-rounded)
@@ -124,6 +125,36 @@ def test_shapes_across_checkpoint_blocks(shape, state):
     got = kernels.chunked_delta_rule_bwd(_residual(x.q, x.k, x.v, x.beta, x.s0),
                                          (_dev(go), _dev(gs)))
     _check(got, ref.delta_vjp(x.q, x.k, x.v, x.beta, go, gs, x.s0), str(shape))
+
+
+@pytest.mark.parametrize("shape", [(1, 20, 2, 160), (1, 17, 1, 256), (2, 9, 1, 129), (1, 33, 1, 200)])
+@pytest.mark.parametrize("state", [True, False])
+def test_head_dims_above_128(shape, state):
+    """Head dimensions the forward serves above 128 (up to 256): 16-column tiles of
+    the state, 32 row slices per column."""
+    x = synth.fwd_inputs(shape, seed=sum(shape) + state, dtype="fp32",
+                         s0_std=0.02 if state else None)
+    rng = np.random.default_rng(sum(shape))
+    b, t, h, d = shape
+    go = rng.standard_normal(shape).astype(np.float32)
+    gs = (rng.standard_normal((b, h, d, d)) * 0.05).astype(np.float32)
+    got = kernels.chunked_delta_rule_bwd(_residual(x.q, x.k, x.v, x.beta, x.s0),
+                                         (_dev(go), _dev(gs)))
+    _check(got, ref.delta_vjp(x.q, x.k, x.v, x.beta, go, gs, x.s0), str(shape))
+
+
+def test_bf16_inputs_d256_against_rounded_values():
+    x = synth.fwd_inputs((1, 24, 2, 256), seed=11, dtype="bf16", s0_std=0.02)
+    rng = np.random.default_rng(11)
+    go = rng.standard_normal(x.q.shape).astype(np.float32)
+
+    def bf(bits):
+        return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+    res = kernels._DeltaResidual(q=bf(x.q_bits), k=bf(x.k_bits), v=bf(x.v_bits), beta=_dev(x.beta),
+                                 state0=_dev(x.s0), chunk=64)
+    got = kernels.chunked_delta_rule_bwd(res, (_dev(go), None))
+    _check(got, ref.delta_vjp(x.q, x.k, x.v, x.beta, go, None, x.s0), "bf16 D256")
 
 
 def test_bf16_inputs_against_rounded_values():

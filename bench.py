@@ -18,7 +18,7 @@ the same run and reported under ``decode`` (with the same batch through a
 serving state cache under ``decode.state_cache``), the backward at cfg1
 under ``backward``, the model's linear attention at the cfg1 shape
 under ``model_linear_attention``, the cfg1 forward with fp32 q/k/v (the
-per-token kernel) under ``fp32_forward``, and the gated variant at cfg1
+fp32 chunked forward, and the per-token kernel beside it) under ``fp32_forward``, and the gated variant at cfg1
 under ``gated``.
 """
 
@@ -39,6 +39,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, vendor figure
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, vendor figure
 FP32_VALU_PEAK_TFLOPS = 157.3  # MI355X fp32 vector, vendor figure (packed FMA; half without)
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA, vendor figure
 CHUNK = 64
 CALIB_COPY_BYTES = 1 << 30  # bytes read (and written) by one calibration copy launch
 CPU_SAMPLE_S = 10.0  # seconds of CPU work timed for cpu_baseline (whole cfg1 batches)
@@ -469,36 +470,50 @@ def main():
         q, k, v, beta = (x.float() for x in sets[0])
         of = torch.empty((B, T, H, D), device=dev)
         sf = torch.empty((B, H, D, D), device=dev)
+        nbf = lib.pm_delta_workspace_bytes(B, T, H, D, _native.DTYPE_F32)
+        wsf = torch.empty(nbf, dtype=torch.uint8, device=dev) if nbf else None
 
-        def ffwd():
+        def ffwd(ws):
             rc = lib.pm_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), None,
                                   of.data_ptr(), sf.data_ptr(), B, T, H, D, _native.DTYPE_F32,
-                                  _native.DTYPE_F32, CHUNK, None, 0, stream.cuda_stream)
+                                  _native.DTYPE_F32, CHUNK, None if ws is None else ws.data_ptr(),
+                                  0 if ws is None else ws.numel(), stream.cuda_stream)
             _native.check(rc)
 
-        ffwd()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        calls = args.model_calls * 2
-        e0.record(stream)
-        for _ in range(calls):
-            ffwd()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        f_ms = e0.elapsed_time(e1) / calls
+        def time_ffwd(ws, calls):
+            ffwd(ws)
+            return time_launches(stream, lambda i: ffwd(ws), calls)
+
+        calls = args.model_calls * 5
+        f_ms = time_ffwd(wsf, calls)  # the default: the fp32 chunked forward on fp32 MFMA
+        old_path = _native.set_path(1)
+        try:
+            r_ms = time_ffwd(None, args.model_calls * 2)  # the per-token VALU kernel
+        finally:
+            _native.set_path(old_path)
         fb = fwd_bytes(B, T, H, D, s_in=4, s_out=4)
-        fflop = 6 * B * T * H * D * D  # k.S, q.S and the rank-1 update, 2 flops per FMA
+        cflop = fwd_flops(B, T, H, D, chunk=16)  # the chunked form at 16-token chunks
+        rflop = 6 * B * T * H * D * D  # per token: k.S, q.S and the rank-1 update, 2 flops per FMA
         fp32_fwd = {
-            "workload": "cfg1 forward with fp32 q/k/v (pm_delta_fwd, per-token fp32 kernel)",
+            "workload": "cfg1 forward with fp32 q/k/v (pm_delta_fwd, fp32 chunked forward on fp32 MFMA)",
             "calls": calls,
             "ms_per_call": f_ms,
             "tokens_per_s": tokens / (f_ms * 1e-3),
-            "roofline": {"bound": "valu", "achieved": fflop / (f_ms * 1e-3) / 1e12,
-                         "peak": FP32_VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": fflop / (f_ms * 1e-3) / 1e12 / FP32_VALU_PEAK_TFLOPS},
+            "workspace_bytes": nbf,
+            "roofline": {"bound": "mfma", "achieved": cflop / (f_ms * 1e-3) / 1e12,
+                         "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": cflop / (f_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+                         "algorithmic_gflop": cflop / 1e9},
             "hbm_gbs": fb / (f_ms * 1e-3) / 1e9,
+            "per_token": {
+                "kernel": "per-token fp32 VALU kernel (pm_delta_set_path 1)",
+                "ms_per_call": r_ms,
+                "roofline": {"bound": "valu", "achieved": rflop / (r_ms * 1e-3) / 1e12,
+                             "peak": FP32_VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": rflop / (r_ms * 1e-3) / 1e12 / FP32_VALU_PEAK_TFLOPS},
+            },
         }
-        del q, k, v, beta, of, sf
+        del q, k, v, beta, of, sf, wsf
 
     # the gated delta rule at cfg1 (pm_gated_delta_fwd): cfg1's inputs plus log-gates
     # -0.1 |N(0, 1)| per token and head, on the chunked kernel

@@ -175,21 +175,10 @@ struct SplitGeo {
     static_assert(RAW % 16 == 0 && BYTES <= 160 * 1024, "LDS layout");
 };
 
-// Wait until at most N vector-memory operations of this wave are outstanding
-// (they complete in issue order).
-template <int N>
-__device__ __forceinline__ void wait_vm_n() {
-    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Vector-memory operations the compiler does not see.  A chain wave issues its T loads and
-// its share of the copies this way, and orders them with its own exact vmcnt waits: the
-// compiler's wait insertion, merging loop iterations conservatively, would otherwise wait
-// for copies issued in the same iteration.
-__device__ __forceinline__ void dma16_asm(__amdgpu_buffer_rsrc_t rs, const void* lds_dst, unsigned voffset) {
-    const unsigned m0 = uniform(lds_addr(lds_dst));
-    __asm__ volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rs), "{m0}"(m0) : "memory");
-}
+// A chain wave issues its T loads and its share of the copies as inline asm (dma16_asm,
+// load16_asm), which the compiler does not see, and orders them with its own exact vmcnt
+// waits: the compiler's wait insertion, merging loop iterations conservatively, would
+// otherwise wait for copies issued in the same iteration.
 __device__ __forceinline__ bf16x8_t load16_asm(__amdgpu_buffer_rsrc_t rs, unsigned voffset) {
     u32x4_t r;
     __asm__ volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(r) : "v"(voffset), "s"(rs) : "memory");

@@ -206,6 +206,19 @@ __device__ __forceinline__ void lds_barrier() {
 }
 // Wait for this wave's outstanding buffer loads (and so its LDS copies).
 __device__ __forceinline__ void wait_copies() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (they complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vm_n() {
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// A 16-byte-per-lane buffer -> LDS copy that the compiler does not see (lane L's
+// bytes land at lds_dst + 16 L): no compiler-inserted waits before later LDS reads;
+// the caller waits with wait_vm_n and a barrier.
+__device__ __forceinline__ void dma16_asm(__amdgpu_buffer_rsrc_t rs, const void* lds_dst, unsigned voffset) {
+    const unsigned m0 = uniform(lds_addr(lds_dst));
+    __asm__ volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rs), "{m0}"(m0) : "memory");
+}
 
 // 2^x in one v_exp_f32 (about 1 ulp; 0 for x below the fp32 range).
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -159,11 +159,27 @@ int forward(const void* q, const void* k, const void* v, const float* beta, cons
     const bool can_chunked = in_bf16 && pm::chunked_supported(D, H) && aligned(q, 16) &&
                              aligned(k, 16) && aligned(v, 16) &&
                              (out_dtype == PM_DTYPE_F32 ? aligned(o, 16) : aligned(o, 8));
-    if (path >= 2 && !can_chunked)
+    // fp32 q/k/v: the chunked forward on fp32 MFMA (plain forward only)
+    const bool can_f32 = !in_bf16 && !g && pm::chunked_supported(D, H) && aligned(q, 16) && aligned(k, 16) &&
+                         aligned(v, 16) && (out_dtype == PM_DTYPE_F32 ? aligned(o, 4) : aligned(o, 2));
+    if (path >= 2 && !can_chunked && !can_f32)
         return fail(PM_E_UNSUPPORTED,
-                    "chunked kernel needs bf16 inputs, D in {64, 128} and 16-byte aligned "
-                    "q/k/v/o (got in_dtype %d, D %d)",
+                    "chunked kernel needs bf16 (or, for the plain forward, fp32) inputs, D in {64, 128} "
+                    "and 16-byte aligned q/k/v (got in_dtype %d, D %d)",
                     in_dtype, D);
+    if (want_chunked && can_f32) {
+        const size_t need = pm::chunked_f32_ws_bytes(varlen, n_seq, varlen ? total_T : T, H);
+        if (workspace && ws_bytes >= need && aligned(workspace, 16)) {
+            pm::ChunkedF32Args a{static_cast<const float*>(q), static_cast<const float*>(k),
+                                 static_cast<const float*>(v), beta, s0, o, s_out, cu, n_seq,
+                                 varlen ? total_T : T, H, D, out_dtype == PM_DTYPE_BF16, g_tile};
+            hipError_t e = pm::launch_chunked_f32(a, workspace, st);
+            return e == hipSuccess ? 0 : hip_fail(e, "fp32 chunked forward launch");
+        }
+        if (path >= 2)
+            return fail(PM_E_WORKSPACE, "the fp32 chunked forward needs a 16-byte aligned workspace of %zu bytes "
+                        "(got %zu)", need, workspace ? ws_bytes : static_cast<size_t>(0));
+    }
     if (want_chunked && can_chunked) {
         pm::ChunkedArgs a{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                           static_cast<const uint16_t*>(v), beta, s0, o, s_out, cu, n_seq,
@@ -238,6 +254,17 @@ size_t bwd_ws_bytes(int B, int T, int H, int D, int in_dtype) {
     return sizeof(float) * pm::bwd_workspace_floats(n_pairs, T, D);
 }
 
+// The forward's workspace: the split form's T blocks (bf16 inputs, where split_chosen), or
+// the fp32 chunked forward's (T'')^T and P^T (fp32 inputs); 0 where the call runs neither.
+size_t fwd_ws_bytes(bool varlen, int n_seq, int T, int H, int D, int in_dtype) {
+    if (n_seq < 0 || T < 0 || H < 0 || !pm::chunked_supported(D, H) || g_path == 1) return 0;
+    const long n_pairs = static_cast<long>(n_seq) * H;
+    if (n_pairs > (1L << 30)) return 0;
+    if (in_dtype == PM_DTYPE_F32) return pm::chunked_f32_ws_bytes(varlen, n_seq, T, H);
+    if (in_dtype != PM_DTYPE_BF16 || !split_chosen(g_path, D, n_pairs)) return 0;
+    return pm::chunked_split_ws_bytes(varlen, n_seq, T, H);
+}
+
 }  // namespace
 
 extern "C" {
@@ -247,18 +274,11 @@ int pm_abi_version(void) { return PM_DELTA_ABI_VERSION; }
 const char* pm_last_error(void) { return g_err; }
 
 size_t pm_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype) {
-    if (B < 0 || T < 0 || H < 0 || in_dtype != PM_DTYPE_BF16 || !pm::chunked_supported(D, H)) return 0;
-    const long n_pairs = static_cast<long>(B) * H;
-    if (n_pairs > (1L << 30) || g_path == 1 || !split_chosen(g_path, D, n_pairs)) return 0;
-    return pm::chunked_split_ws_bytes(false, B, T, H);
+    return fwd_ws_bytes(false, B, T, H, D, in_dtype);
 }
 
 size_t pm_delta_varlen_workspace_bytes(int n_seqs, int total_T, int H, int D, int in_dtype) {
-    if (n_seqs < 0 || total_T < 0 || H < 0 || in_dtype != PM_DTYPE_BF16 || !pm::chunked_supported(D, H))
-        return 0;
-    const long n_pairs = static_cast<long>(n_seqs) * H;
-    if (n_pairs > (1L << 30) || g_path == 1 || !split_chosen(g_path, D, n_pairs)) return 0;
-    return pm::chunked_split_ws_bytes(true, n_seqs, total_T, H);
+    return fwd_ws_bytes(true, n_seqs, total_T, H, D, in_dtype);
 }
 
 size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype) {

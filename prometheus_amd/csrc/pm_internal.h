@@ -79,6 +79,27 @@ hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st);
 // Same algebra as the single-stage kernel, rounded differently (bf16 parity).
 size_t chunked_split_ws_bytes(bool varlen, int n_seq, int T, int H);
 hipError_t launch_chunked_split(const ChunkedArgs& a, int dv, void* t_ws, hipStream_t st);
+// Chunked forward for fp32 q/k/v on fp32 MFMA (delta_chunked_f32.hip), D in {64, 128},
+// plain (no norm, no gates): a parallel pass writes every 16-token chunk's (T'')^T and
+// P^T into `ws` (chunked_f32_ws_bytes bytes, 16-byte aligned), then the recurrence runs
+// on them.  fp32 arithmetic throughout.
+struct ChunkedF32Args {
+    const float* q;
+    const float* k;
+    const float* v;
+    const float* beta;
+    const float* s0;  // nullable
+    void* o;
+    float* s_out;
+    const int32_t* cu_seqlens;  // nullable
+    int n_seq;                  // B, or n_seqs in varlen mode
+    int T, H, D;                // varlen: T = packed token count
+    bool out_bf16;
+    int dv_tile;  // 0 = automatic
+};
+size_t chunked_f32_ws_bytes(bool varlen, int n_seq, int T, int H);
+int chunked_f32_pick_tile(int D, long n_pairs, int requested);
+hipError_t launch_chunked_f32(const ChunkedF32Args& a, void* ws, hipStream_t st);
 // The same kernel writing, instead of O and the final state, the state at
 // the start of every chunk as bf16 rows of S^T (fixed-length batches only):
 // s_hist holds n_seq*H x ceil(T/64) x D x D values.

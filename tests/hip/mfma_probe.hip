@@ -5,7 +5,8 @@
 //   16x16x32: A lane l -> row l%16, B lane l -> column l%16, lane group
 //             g = l/16 slot s <-> contraction index 4g+s (s<4), 16+4g+(s-4);
 //   16x16x16: same with slot s <-> 4g+s;
-//   both:     accumulator lane l, element i -> C[4(l/16)+i][l%16].
+//   both:     accumulator lane l, element i -> C[4(l/16)+i][l%16];
+//   16x16x4 fp32: A lane l -> A[l%16][l/16], B lane l -> B[l/16][l%16], accumulator alike.
 // The host compares C with a NumPy product; any wrong assumption shows.
 //
 // dpp_probe runs the DPP lane reductions of pm_common.h / pm_rec.h on one
@@ -45,6 +46,21 @@ __global__ void probe16(const uint16_t* A, const uint16_t* B, float* C) {
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
     acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
     for (int i = 0; i < 4; ++i) C[(4 * g + i) * 16 + r] = acc[i];
+}
+
+// 16x16x4 fp32 (the fp32 chunked forward): A lane l -> A[l%16][l/16], B lane l ->
+// B[l/16][l%16], accumulator as above.
+__global__ void probe4f32(const float* A, const float* B, float* C) {
+    const int l = threadIdx.x, r = l % 16, g = l / 16;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[r * 4 + g], B[g * 16 + r], acc, 0, 0, 0);
+    for (int i = 0; i < 4; ++i) C[(4 * g + i) * 16 + r] = acc[i];
+}
+
+extern "C" int mfma_probe_f32(const float* a, const float* b, float* c) {
+    hipLaunchKernelGGL(probe4f32, dim3(1), dim3(64), 0, 0, a, b, c);
+    if (hipGetLastError() != hipSuccess) return 1;
+    return hipDeviceSynchronize() == hipSuccess ? 0 : 2;
 }
 
 extern "C" int mfma_probe(const uint16_t* a32, const uint16_t* b32, float* c32,

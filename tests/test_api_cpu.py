@@ -272,8 +272,12 @@ def test_forward_workspace_sizes_and_checks():
     assert lib.pm_delta_workspace_bytes(1, 32768, 32, 128, bf16) == 32 * 512 * per  # cfg3: 16-col tiles
     assert lib.pm_delta_workspace_bytes(1, 130, 2, 64, bf16) == 2 * 3 * per
     assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, bf16) == 0  # cfg1: 32-col tiles
-    assert lib.pm_delta_workspace_bytes(1, 4096, 16, 128, f32) == 0
     assert lib.pm_delta_workspace_bytes(1, 4096, 16, 256, bf16) == 0
+    # fp32 q/k/v at D in {64, 128}: the fp32 chunked forward's 2 KiB per (b, h) and 16-token chunk
+    assert lib.pm_delta_workspace_bytes(1, 4096, 16, 128, f32) == 16 * 256 * 2048
+    assert lib.pm_delta_workspace_bytes(2, 17, 3, 64, f32) == 6 * 2 * 2048
+    assert lib.pm_delta_workspace_bytes(2, 17, 3, 48, f32) == 0  # per-token kernel
+    assert lib.pm_delta_varlen_workspace_bytes(3, 100, 2, 128, f32) == 2 * (7 + 3) * 2048
     # varlen: H x (ceil(total / 64) + n_seqs) slots
     assert lib.pm_delta_varlen_workspace_bytes(3, 1000, 4, 128, bf16) == 4 * (16 + 3) * per
     assert lib.pm_delta_varlen_workspace_bytes(8, 16384, 16, 128, bf16) == 0  # cfg2: 32-col tiles
@@ -292,6 +296,17 @@ def test_forward_workspace_sizes_and_checks():
     old = _native.set_path(1)
     try:
         assert lib.pm_delta_workspace_bytes(1, 32768, 32, 128, bf16) == 0
+        assert lib.pm_delta_workspace_bytes(1, 4096, 16, 128, f32) == 0
+    finally:
+        _native.set_path(old)
+    old = _native.set_path(2)
+    try:
+        # path 2 with fp32 inputs: the fp32 chunked forward, which needs its workspace
+        p = ctypes.c_void_p(256)
+        rc = lib.pm_delta_fwd(p, p, p, p, None, p, p, 1, 64, 1, 128, f32, f32, 64, None, 0, None)
+        assert rc == _native.E_WORKSPACE and b"fp32 chunked" in lib.pm_last_error()
+        rc = lib.pm_delta_fwd(p, p, p, p, None, p, p, 1, 64, 1, 48, f32, f32, 64, None, 0, None)
+        assert rc == _native.E_UNSUPPORTED
     finally:
         _native.set_path(old)
     old = _native.set_tile(32)

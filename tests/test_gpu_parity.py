@@ -94,6 +94,20 @@ def test_mfma_layout_probe():
     np.testing.assert_allclose(_np(c16), e16, rtol=1e-5, atol=1e-5)
 
 
+def test_mfma_f32_layout_probe():
+    """v_mfma_f32_16x16x4f32's lane layout, which the fp32 chunked forward assumes."""
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(__file__), "hip", "libmfma_probe.so"))
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal((16, 4)).astype(np.float32)
+    b = rng.standard_normal((4, 16)).astype(np.float32)
+    c = torch.zeros((16, 16), dtype=torch.float32, device="cuda")
+    da, db = _dev(a), _dev(b)
+    torch.cuda.synchronize()
+    assert lib.mfma_probe_f32(ctypes.c_void_p(da.data_ptr()), ctypes.c_void_p(db.data_ptr()),
+                              ctypes.c_void_p(c.data_ptr())) == 0
+    np.testing.assert_allclose(_np(c), a.astype(np.float64) @ b, rtol=1e-6, atol=1e-6)
+
+
 def test_dpp_lane_reductions_probe():
     """The DPP reductions the kernels use (gate scan, row and wave sums, lane-group
     sums), on one wave: against NumPy, and every lane of a group with the same bits."""

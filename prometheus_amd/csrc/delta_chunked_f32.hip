@@ -18,21 +18,24 @@
 //     register v of X's or U's accumulator is the B operand, and the A operand M[r][4 g
 //     + v] is register v of the accumulator of M^T.
 //
-// K7p (prep, one wave per (sequence, head, chunk), all chunks at once): G = K K^T and
-// P^T = K Q^T from K and Q rows read straight into operand registers, N = -A and N^T
-// from G (which is symmetric), and T^T = ((I+N)(I+N^2)(I+N^4)(I+N^8))^T (N is strictly
-// lower triangular, so N^16 = 0) as products of accumulators with transposed
-// accumulators.  It writes (T'')^T and (lower_incl P)^T as accumulator registers, 1 KiB
-// each per chunk: the A operands of U = T'' X and of P U, lane-linear.
+// K7p (prep, one wave per (sequence, head, chunk), all chunks at once): G = K K^T from K
+// rows read straight into operand registers, N = -A and N^T from G (which is symmetric),
+// and T^T = ((I+N)(I+N^2)(I+N^4)(I+N^8))^T (N is strictly lower triangular, so N^16 = 0)
+// as products of accumulators with transposed accumulators.  It writes (T'')^T as
+// accumulator registers, 1 KiB per chunk: the A operand of U = T'' X, lane-linear.
 //
 // K7 (recurrence): one workgroup per (sequence, head, d_v tile of DV columns) with DV/16
 // chain waves and as many output waves.  Chain wave w owns the S columns col0 + 16 w +
 // [0, 16) as D/16 accumulator tiles and runs chunk i (X, U, S: 68 MFMAs at D = 128),
 // handing S_i (before its update) and U_i to output wave w through LDS; output wave w
-// runs chunk i - 1 (Y = Q S, O = Y + P U) and stores O.  HBM -> LDS copies
-// (buffer_load ... lds) run two chunks ahead: the output waves copy K and Q rows and
-// P^T, the chain waves their V columns and (wave 0) T''^T.  One LDS-only barrier per
-// chunk.
+// runs chunk i - 1 (Y = Q S, P^T = K Q^T, O = Y + P U: 68 MFMAs at D = 128, as many as
+// the chain's) and stores O.  Products of one accumulator are spread over several
+// accumulators (a dependent MFMA waits for its predecessor's result), summed at the end.
+// HBM -> LDS copies (buffer_load ... lds) run two chunks ahead: the output waves copy K
+// and Q rows, the chain waves their V columns and (wave 0) T''^T.  One LDS-only barrier
+// per chunk.
+
+#include <type_traits>
 
 #include "pm_cdna4.h"
 #include "pm_internal.h"
@@ -41,17 +44,19 @@ namespace pm {
 namespace {
 
 constexpr int kC16 = 16;          // tokens per chunk
-constexpr int kWsFloats = 512;    // workspace floats per chunk: (T'')^T, then P^T
+constexpr int kWsFloats = 256;    // workspace floats per chunk: (T'')^T
 
 __device__ __forceinline__ f32x4_t mfma4(float a, float b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
-// Left * Right over a 16-token contraction, given the accumulators of Left^T and Right.
-__device__ __forceinline__ f32x4_t mm16(f32x4_t lt, f32x4_t r) {
-    f32x4_t a = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int v = 0; v < 4; ++v) a = mfma4(lt[v], r[v], a);
-    return a;
+// Left * Right over a 16-token contraction, given the accumulators of Left^T and Right
+// (plus c), in two accumulators.
+__device__ __forceinline__ f32x4_t mm16(f32x4_t lt, f32x4_t r, f32x4_t c = f32x4_t{0.f, 0.f, 0.f, 0.f}) {
+    const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t a0 = mfma4(lt[0], r[0], c), a1 = mfma4(lt[1], r[1], z);
+    a0 = mfma4(lt[2], r[2], a0);
+    a1 = mfma4(lt[3], r[3], a1);
+    return a0 + a1;
 }
 
 // Workspace slots (16-token chunks), as the split form's: fixed length, row = pair, slot
@@ -72,8 +77,7 @@ __device__ __forceinline__ int f32_chunk(int t, int p) {
 
 // ---------------------------------------------------------------- K7p
 template <int D>
-__global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __restrict__ q,
-                                                             const float* __restrict__ k,
+__global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __restrict__ k,
                                                              const float* __restrict__ beta,
                                                              const int32_t* __restrict__ cu_seqlens,
                                                              int n_seq, int T, int H, int n_slot, long n_items,
@@ -114,15 +118,14 @@ __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __rest
     const size_t tstride = static_cast<size_t>(H) * D;
     const size_t row0 = static_cast<size_t>(tok0 + base) * tstride + static_cast<size_t>(h) * D;
     const unsigned nb = static_cast<unsigned>(((clen - 1) * tstride + D) * 4);
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(k + row0, nb), rq = make_rsrc(q + row0, nb);
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(k + row0, nb);
     const __amdgpu_buffer_rsrc_t rb =
         make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4));
-    f32x4_t kf[NJ], qf[NJ];
+    f32x4_t kf[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const unsigned vo = static_cast<unsigned>((r * tstride + 16 * j + 4 * g) * 4);
         kf[j] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 0, 0));
-        qf[j] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rq, vo, 0, 0));
     }
     const float bc = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, static_cast<unsigned>(r * H * 4), 0, 0));
     f32x4_t bt;
@@ -130,23 +133,14 @@ __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __rest
     for (int v = 0; v < 4; ++v)
         bt[v] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, static_cast<unsigned>((4 * g + v) * H * 4), 0, 0));
 
-    // G = K K^T and P^T = K Q^T (two accumulators each, summed at the end)
+    // G = K K^T (one accumulator per step of a tile, summed at the end)
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-    f32x4_t g0 = zero, g1 = zero, p0 = zero, p1 = zero;
+    f32x4_t ga[4] = {zero, zero, zero, zero};
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            if (j & 1) {
-                g1 = mfma4(kf[j][v], kf[j][v], g1);
-                p1 = mfma4(kf[j][v], qf[j][v], p1);
-            } else {
-                g0 = mfma4(kf[j][v], kf[j][v], g0);
-                p0 = mfma4(kf[j][v], qf[j][v], p0);
-            }
-        }
-    }
-    const f32x4_t G = g0 + g1, Pt = p0 + p1;
+        for (int v = 0; v < 4; ++v) ga[v] = mfma4(kf[j][v], kf[j][v], ga[v]);
+    const f32x4_t G = (ga[0] + ga[1]) + (ga[2] + ga[3]);
     // N[i][j] = -beta_i G[i][j] (i > j), N^T[i][j] = -beta_j G[i][j] (j > i); i = 4 g + v, j = r
     f32x4_t N, Nt, eye;
 #pragma unroll
@@ -162,15 +156,10 @@ __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __rest
     const f32x4_t F1t = mm16(eye + N2, eye + Nt);   // ((I+N)(I+N^2))^T
     const f32x4_t F2t = mm16(eye + N4, F1t);        // (... (I+N^4))^T
     const f32x4_t Tt = mm16(eye + N8, F2t);         // T^T
-    f32x4_t tw, pw;
+    f32x4_t tw;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        tw[v] = -bt[v] * Tt[v];                     // (T'')^T[i][j] = -beta_i T[j][i]
-        pw[v] = (4 * g + v <= r) ? Pt[v] : 0.f;     // P^T[i][j] = P[j][i], kept for i <= j
-    }
-    float* out = ws + (static_cast<size_t>(row) * n_slot + slot) * kWsFloats + lane * 4;
-    *reinterpret_cast<f32x4_t*>(out) = tw;
-    *reinterpret_cast<f32x4_t*>(out + 256) = pw;
+    for (int v = 0; v < 4; ++v) tw[v] = -bt[v] * Tt[v];  // (T'')^T[i][j] = -beta_i T[j][i]
+    *reinterpret_cast<f32x4_t*>(ws + (static_cast<size_t>(row) * n_slot + slot) * kWsFloats + lane * 4) = tw;
 }
 
 // ---------------------------------------------------------------- K7
@@ -180,24 +169,23 @@ struct F32Geo {
     static constexpr int NT = D / 16;              // S accumulator tiles per chain wave
     static constexpr int NI = kC16 * D * 4 / 1024; // 1 KiB copies per K or Q tile
     static constexpr int NB = 4;                   // rotating chunk buffers
-    // one chunk buffer: K rows, Q rows, P^T, (T'')^T, V columns of each chain wave
+    // one chunk buffer: K rows, Q rows, (T'')^T, V columns of each chain wave
     static constexpr int B_K = 0;
     static constexpr int B_Q = B_K + kC16 * D * 4;
-    static constexpr int B_P = B_Q + kC16 * D * 4;
-    static constexpr int B_T = B_P + 1024;
+    static constexpr int B_T = B_Q + kC16 * D * 4;
     static constexpr int B_V = B_T + 1024;
     static constexpr int BUF = B_V + NCW * 1024;
     static constexpr int OFF_S = NB * BUF;                     // 2 slots x NCW x NT KiB: S_i
     static constexpr int OFF_U = OFF_S + 2 * NCW * NT * 1024;  // 2 slots x NCW KiB: U_i
-    static constexpr int BYTES = OFF_U + 2 * NCW * 1024;
-    // copies per chunk: output wave 0 (K, P^T and, with one output wave, Q), output wave 1
-    // (Q); chain wave 0 (V, T''), chain wave 1 (V)
-    static constexpr int NCP_O0 = NI + 1 + (NCW == 1 ? NI : 0);
-    static constexpr int NCP_O1 = NI;
+    static constexpr int OFF_P = OFF_U + 2 * NCW * 1024;       // 2 slots x 1 KiB: P^T of a chunk
+    static constexpr int BYTES = OFF_P + 2 * 1024;
+    // the last output wave (the copy wave) issues every copy of a chunk: K and Q rows,
+    // (T'')^T and the V columns of each chain wave
+    static constexpr int NCP = 2 * NI + 1 + NCW;
     static constexpr int NST = 4;  // O stores per output wave per chunk
     static_assert(D == 64 || D == 128, "D");
     static_assert(DV == 16 || DV == 32, "DV");
-    static_assert(BYTES <= 160 * 1024 && NCP_O0 + NST <= 63, "LDS / vmcnt");
+    static_assert(BYTES <= 160 * 1024 && NCP + NST <= 63, "LDS / vmcnt");
 };
 
 template <int D, int DV, bool OUT_BF16>
@@ -238,13 +226,17 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
     const int r = lane & 15, g = lane >> 4;
     const bool chain = w < NCW;
     const int cw = chain ? w : w - NCW;  // the 16 columns this wave works on
+    const bool p_wave = w == NCW;         // builds P^T for every output wave
+    const bool copy_wave = w == 2 * NCW - 1;
     const size_t tstride = static_cast<size_t>(H) * D;
     const size_t sbase = static_cast<size_t>(pair) * D * D;
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    auto fence = []() __attribute__((always_inline)) { __builtin_amdgcn_sched_barrier(0); };
 
     auto buf = [&](int c) { return smem + (c % G::NB) * G::BUF; };
     auto sslot = [&](int c, int which) { return smem + G::OFF_S + ((c & 1) * NCW + which) * NT * 1024; };
     auto uslot = [&](int c, int which) { return smem + G::OFF_U + ((c & 1) * NCW + which) * 1024; };
+    auto pslot = [&](int c) { return smem + G::OFF_P + (c & 1) * 1024; };
     auto ld4 = [&](const unsigned char* p) { return *reinterpret_cast<const f32x4_t*>(p); };
     auto st4 = [&](unsigned char* p, f32x4_t x) { *reinterpret_cast<f32x4_t*>(p) = x; };
 
@@ -264,53 +256,41 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
             dma16_asm(rs, d0 + 1024 * i, static_cast<unsigned>(t * tstride * 4 + 16 * p));
         }
     };
-    auto copy_ws = [&](int c, int part, unsigned char* dst) __attribute__((always_inline)) {
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(
-            ws + (static_cast<size_t>(ws_row) * n_slot + ws_slot0 + c) * kWsFloats + 256 * part, 1024);
+    auto copy_ws = [&](int c, unsigned char* dst) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rs =
+            make_rsrc(ws + (static_cast<size_t>(ws_row) * n_slot + ws_slot0 + c) * kWsFloats, 1024);
         dma16_asm(rs, uniform_ptr(dst), static_cast<unsigned>(16 * lane));
     };
-    auto copy_v = [&](int c, unsigned char* dst) __attribute__((always_inline)) {
-        const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(v, c, 16, col0 + 16 * cw);
+    auto copy_v = [&](int c, int j, unsigned char* dst) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(v, c, 16, col0 + 16 * j);
         const int t = lane >> 2, p = lane & 3;
         dma16_asm(rs, uniform_ptr(dst), static_cast<unsigned>(t * tstride * 4 + 16 * p));
     };
-    // this wave's copies of chunk c
+    // the copy wave's copies of chunk c
     auto copies = [&](int c) __attribute__((always_inline)) {
         unsigned char* b = buf(c);
-        if (chain) {
-            copy_v(c, b + G::B_V + 1024 * cw);
-            if (cw == 0) copy_ws(c, 0, b + G::B_T);
-        } else if (cw == 0) {
-            copy_tile(k, c, b + G::B_K);
-            copy_ws(c, 1, b + G::B_P);
-            if (NCW == 1) copy_tile(q, c, b + G::B_Q);
-        } else {
-            copy_tile(q, c, b + G::B_Q);
-        }
+        copy_tile(k, c, b + G::B_K);
+        copy_tile(q, c, b + G::B_Q);
+        copy_ws(c, b + G::B_T);
+#pragma unroll
+        for (int j = 0; j < NCW; ++j) copy_v(c, j, b + G::B_V + 1024 * j);
     };
-    // wait until chunk c's copies (issued before `extra` later operations) have landed
-    auto wait_own = [&](int extra_stores, bool extra_copies) __attribute__((always_inline)) {
-        if (chain) {
-            if (!extra_copies) wait_vm_n<0>();
-            else if (cw == 0) wait_vm_n<2>();
-            else wait_vm_n<1>();
-        } else if (cw == 0) {
-            if (extra_copies && extra_stores) wait_vm_n<G::NCP_O0 + G::NST>();
-            else if (extra_copies) wait_vm_n<G::NCP_O0>();
-            else if (extra_stores) wait_vm_n<G::NST>();
-            else wait_vm_n<0>();
-        } else {
-            if (extra_copies && extra_stores) wait_vm_n<G::NCP_O1 + G::NST>();
-            else if (extra_copies) wait_vm_n<G::NCP_O1>();
-            else if (extra_stores) wait_vm_n<G::NST>();
-            else wait_vm_n<0>();
-        }
+    // the copy wave: wait until the next chunk's copies have landed, with the operations
+    // issued after them (this and the last iteration's O stores, the copies of the chunk
+    // after next) possibly in flight
+    auto wait_next = [&](bool extra_stores, bool extra_copies) __attribute__((always_inline)) {
+        if (extra_copies && extra_stores) wait_vm_n<G::NCP + G::NST>();
+        else if (extra_copies) wait_vm_n<G::NCP>();
+        else if (extra_stores) wait_vm_n<G::NST>();
+        else wait_vm_n<0>();
     };
 
     if (n_chunks > 0) {
-        copies(0);
-        if (n_chunks > 1) copies(1);
-        wait_own(0, n_chunks > 1);
+        if (copy_wave) {
+            copies(0);
+            if (n_chunks > 1) copies(1);
+            wait_next(false, n_chunks > 1);
+        }
         lds_barrier();  // B0
     }
 
@@ -323,45 +303,65 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 S[m][e] = s0 ? s0[sbase + static_cast<size_t>(16 * m + 4 * g + e) * D + ecol] : 0.f;
-        for (int i = 0; i < n_chunks; ++i) {
-            const bool cp = i + 2 < n_chunks;
-            if (cp) copies(i + 2);
-            const unsigned char* b = buf(i);
-            const float* Kf = reinterpret_cast<const float*>(b + G::B_K);
+        // s_waitcnt vmcnt(0) as the intrinsic, which the compiler's wait insertion sees: with
+        // the S0 loads settled here it puts no wait for them inside the loop, where a
+        // vmcnt(0) would also wait for the copies of two chunks ahead
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        // Iteration i (after barrier B_i) finishes chunk i - 1 (S += K^T U, its K^T operands
+        // read before the barrier) and runs chunk i up to U, so the state update of one chunk
+        // and X of the next run back to back on the MFMA pipe; the LDS reads of each phase
+        // are issued ahead of it, in groups fenced by sched_barrier (left to itself the
+        // compiler reads each operand right before its MFMA and waits out the LDS latency).
+        float kt[4][NT];  // K^T operand of chunk i - 1: K[4 g + e][16 m + r]
+        f32x4_t Up = zero;
+        for (int i = 0; i <= n_chunks; ++i) {
+            const bool run = i < n_chunks;
+            const unsigned char* b = buf(run ? i : 0);
             const float* Vf = reinterpret_cast<const float*>(b + G::B_V + 1024 * cw);
-            // X = K S - V (two accumulators over alternate tiles)
-            f32x4_t x0, x1 = zero;
+            f32x4_t kf[NT], xa[4] = {zero, zero, zero, zero}, tt = zero, vr = zero;
+            if (run) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) x0[e] = -Vf[(4 * g + e) * 16 + r];
+                for (int m = 0; m < NT; ++m) kf[m] = ld4(b + G::B_K + 16 * f32_chunk<D>(r, 4 * m + g));
 #pragma unroll
-            for (int m = 0; m < NT; ++m) {
-                const f32x4_t kf = ld4(b + G::B_K + 16 * f32_chunk<D>(r, 4 * m + g));
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (m & 1) x1 = mfma4(kf[e], S[m][e], x1);
-                    else x0 = mfma4(kf[e], S[m][e], x0);
-                }
+                for (int e = 0; e < 4; ++e) vr[e] = Vf[(4 * g + e) * 16 + r];
+                tt = ld4(b + G::B_T + 16 * lane);
             }
-            const f32x4_t X = x0 + x1;
+            fence();
+            // S += K^T U of chunk i - 1 (consecutive MFMAs go to different tiles)
+            if (i > 0) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int m = 0; m < NT; ++m) S[m] = mfma4(kt[e][m], Up[e], S[m]);
+            }
+            if (!run) break;
+            fence();
+            xa[0] = -vr;  // (negated only here: a use right after the read would wait for it)
+            // X = K S - V (accumulator e takes the steps (m, e))
+#pragma unroll
+            for (int m = 0; m < NT; ++m)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xa[e] = mfma4(kf[m][e], S[m][e], xa[e]);
+            const f32x4_t X = (xa[0] + xa[1]) + (xa[2] + xa[3]);
             // U = T'' X
-            const f32x4_t tt = ld4(b + G::B_T + 16 * lane);
-            const f32x4_t U = mm16(tt, X);
+            Up = mm16(tt, X);
             // hand S_i and U_i to the output wave
             unsigned char* ss = sslot(i, cw);
 #pragma unroll
             for (int m = 0; m < NT; ++m) st4(ss + 1024 * m + 16 * lane, S[m]);
-            st4(uslot(i, cw) + 16 * lane, U);
-            // S += K^T U: A operand K[4 g + e][16 m + r]
+            st4(uslot(i, cw) + 16 * lane, Up);
+            // K^T operand of chunk i, for the next iteration's state update
+            const float* Kf = reinterpret_cast<const float*>(b + G::B_K);
 #pragma unroll
-            for (int m = 0; m < NT; ++m) {
+            for (int e = 0; e < 4; ++e)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
+                for (int m = 0; m < NT; ++m) {
                     const int t = 4 * g + e, d = 16 * m + r;
-                    const float kt = Kf[4 * f32_chunk<D>(t, d >> 2) + (d & 3)];
-                    S[m] = mfma4(kt, U[e], S[m]);
+                    kt[e][m] = Kf[4 * f32_chunk<D>(t, d >> 2) + (d & 3)];
                 }
-            }
-            if (i + 1 < n_chunks) wait_own(0, cp);
+            // lgkmcnt(0) as the intrinsic, so that the compiler knows kt has landed and puts
+            // no wait for it after the barrier (where it would also wait for the new reads)
+            __builtin_amdgcn_s_waitcnt(0xC07F);
             lds_barrier();
         }
 #pragma unroll
@@ -369,32 +369,67 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
 #pragma unroll
             for (int e = 0; e < 4; ++e) s_out[sbase + static_cast<size_t>(16 * m + 4 * g + e) * D + ecol] = S[m][e];
     } else if (n_chunks > 0) {
-        // ============ output wave: O of chunk i - 1 for the columns of chain wave cw ============
+        // ============ output waves: O of chunk i - 1 for the columns of chain wave cw ============
+        // Iteration i: the P wave builds P^T of chunk i (for the next iteration, into LDS);
+        // every output wave forms Y = Q S and O = Y + P U of chunk i - 1 and stores O; the
+        // copy wave issues chunk i + 2's copies.
         constexpr int ES = OUT_BF16 ? 2 : 4;
         for (int i = 0; i <= n_chunks; ++i) {
-            const bool cp = i + 2 < n_chunks;
+            const bool cp = copy_wave && i + 2 < n_chunks;
             if (cp) copies(i + 2);
             const bool st = i >= 1;
-            if (st) {
-                const int c = i - 1;
-                const unsigned char* b = buf(c);
-                const unsigned char* ss = sslot(c, cw);
-                f32x4_t y0 = zero, y1 = zero;
+            const bool pp = p_wave && i < n_chunks;
+            // accumulator e takes the steps (m, e); each tile's operand reads are issued two
+            // tiles ahead.  One straight-line body per combination of the two products.
+            f32x4_t ya[4] = {zero, zero, zero, zero}, pa[4] = {zero, zero, zero, zero};
+            const unsigned char* by = buf(st ? i - 1 : 0);
+            const unsigned char* bp = buf(i);
+            const unsigned char* ss = sslot(st ? i - 1 : 0, cw);
+            auto products = [&](auto ST, auto PP) __attribute__((always_inline)) {
+                constexpr bool DO_Y = decltype(ST)::value, DO_P = decltype(PP)::value;
+                f32x4_t qy[NT], sc[NT], qp[NT], kp[NT];
+                auto rd = [&](int m) __attribute__((always_inline)) {
+                    if constexpr (DO_Y) {
+                        qy[m] = ld4(by + G::B_Q + 16 * f32_chunk<D>(r, 4 * m + g));
+                        sc[m] = ld4(ss + 1024 * m + 16 * lane);
+                    }
+                    if constexpr (DO_P) {
+                        qp[m] = ld4(bp + G::B_Q + 16 * f32_chunk<D>(r, 4 * m + g));
+                        kp[m] = ld4(bp + G::B_K + 16 * f32_chunk<D>(r, 4 * m + g));
+                    }
+                };
+                rd(0);
+                rd(1);
+                fence();
 #pragma unroll
                 for (int m = 0; m < NT; ++m) {
-                    const f32x4_t qf = ld4(b + G::B_Q + 16 * f32_chunk<D>(r, 4 * m + g));
-                    const f32x4_t sc = ld4(ss + 1024 * m + 16 * lane);
+                    if (m + 2 < NT) rd(m + 2);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        if (m & 1) y1 = mfma4(qf[e], sc[e], y1);
-                        else y0 = mfma4(qf[e], sc[e], y0);
+                        if constexpr (DO_Y) ya[e] = mfma4(qy[m][e], sc[m][e], ya[e]);
+                        if constexpr (DO_P) pa[e] = mfma4(kp[m][e], qp[m][e], pa[e]);
                     }
+                    fence();
                 }
-                const f32x4_t pt = ld4(b + G::B_P + 16 * lane);
-                const f32x4_t u = ld4(uslot(c, cw) + 16 * lane);
-                f32x4_t O = y0 + y1;
+            };
+            using T_ = std::true_type;
+            using F_ = std::false_type;
+            if (st && pp) products(T_{}, T_{});
+            else if (st) products(T_{}, F_{});
+            else if (pp) products(F_{}, T_{});
+            if (pp) {
+                // P^T[i][j] = P[j][i] = q_j . k_i, kept for i <= j (lower_incl P)
+                const f32x4_t pq = (pa[0] + pa[1]) + (pa[2] + pa[3]);
+                f32x4_t pt;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) O = mfma4(pt[e], u[e], O);
+                for (int e = 0; e < 4; ++e) pt[e] = (4 * g + e <= r) ? pq[e] : 0.f;
+                st4(pslot(i) + 16 * lane, pt);
+            }
+            if (st) {
+                const int c = i - 1;
+                const f32x4_t pt = ld4(pslot(c) + 16 * lane);
+                const f32x4_t u = ld4(uslot(c, cw) + 16 * lane);
+                const f32x4_t O = mm16(pt, u, (ya[0] + ya[1]) + (ya[2] + ya[3]));
                 // lane (g, r) holds O[4 g + e][16 cw + r]; rows past the end are dropped by
                 // the range-checked stores
                 const int clen = min(kC16, len - c * kC16);
@@ -412,7 +447,7 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
                 }
             }
             if (i < n_chunks) {
-                if (i + 1 < n_chunks) wait_own(st, cp);
+                if (copy_wave && i + 1 < n_chunks) wait_next(st, cp);
                 lds_barrier();
             }
         }
@@ -441,7 +476,7 @@ hipError_t launch_f32_t(const ChunkedF32Args& a, float* ws, hipStream_t st) {
     const float *q = a.q, *k = a.k, *v = a.v;
     if (n_items > 0) {
         hipLaunchKernelGGL(delta_f32_prep_kernel<D>, dim3(static_cast<unsigned>((n_items + 3) / 4)), dim3(256), 0,
-                           st, q, k, a.beta, a.cu_seqlens, a.n_seq, a.T, a.H, n_slot, n_items, ws);
+                           st, k, a.beta, a.cu_seqlens, a.n_seq, a.T, a.H, n_slot, n_items, ws);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -274,10 +274,10 @@ def test_forward_workspace_sizes_and_checks():
     assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, bf16) == 0  # cfg1: 32-col tiles
     assert lib.pm_delta_workspace_bytes(1, 4096, 16, 256, bf16) == 0
     # fp32 q/k/v at D in {64, 128}: the fp32 chunked forward's 2 KiB per (b, h) and 16-token chunk
-    assert lib.pm_delta_workspace_bytes(1, 4096, 16, 128, f32) == 16 * 256 * 2048
-    assert lib.pm_delta_workspace_bytes(2, 17, 3, 64, f32) == 6 * 2 * 2048
+    assert lib.pm_delta_workspace_bytes(1, 4096, 16, 128, f32) == 16 * 256 * 1024
+    assert lib.pm_delta_workspace_bytes(2, 17, 3, 64, f32) == 6 * 2 * 1024
     assert lib.pm_delta_workspace_bytes(2, 17, 3, 48, f32) == 0  # per-token kernel
-    assert lib.pm_delta_varlen_workspace_bytes(3, 100, 2, 128, f32) == 2 * (7 + 3) * 2048
+    assert lib.pm_delta_varlen_workspace_bytes(3, 100, 2, 128, f32) == 2 * (7 + 3) * 1024
     # varlen: H x (ceil(total / 64) + n_seqs) slots
     assert lib.pm_delta_varlen_workspace_bytes(3, 1000, 4, 128, bf16) == 4 * (16 + 3) * per
     assert lib.pm_delta_varlen_workspace_bytes(8, 16384, 16, 128, bf16) == 0  # cfg2: 32-col tiles

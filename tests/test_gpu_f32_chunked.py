@@ -137,7 +137,7 @@ def test_f32_chunked_graph_replay_is_bitwise():
     _, (q, k, v, b, s0) = _case((B, T, H, D), seed=12, s0_std=0.02)
     lib = _native.lib()
     nb = lib.pm_delta_workspace_bytes(B, T, H, D, _native.DTYPE_F32)
-    assert nb == B * H * (T // 16) * 2048
+    assert nb == B * H * (T // 16) * 1024
     ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
     o = torch.empty((B, T, H, D), device="cuda")
     s = torch.empty((B, H, D, D), device="cuda")

@@ -79,7 +79,12 @@ extern "C" {
  * {64, 128} when B*H*(D/32) < 256 (the chunked kernel's 16-column tiles),
  * where the split form is the faster one.  Without the workspace the
  * single-stage chunked kernel runs, which needs none; the two agree within
- * the bf16 parity bound.  The library never allocates.
+ * the bf16 parity bound.  fp32 inputs at D in {64, 128} (16-byte aligned
+ * q, k, v) run the chunked forward on fp32 MFMA, whose parallel pass writes
+ * every 16-token chunk's (-T diag(beta))^T into the workspace (1 KiB per
+ * (b, h) and chunk); without the workspace they run the per-token fp32
+ * kernel.  Both are fp32 arithmetic (fp32 parity).  The library never
+ * allocates.
  */
 int pm_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
                  const float* s0, void* o, float* s_out, int B, int T, int H, int D,
@@ -171,15 +176,17 @@ int pm_linear_attention(const void* q, const void* k, const void* v, const float
                         void* stream);
 
 /*
- * Workspace bytes pm_delta_fwd uses for the split form of the chunked
- * kernel (6 KiB per (b, h) and 64-token chunk); 0 when the call, under the
- * calling thread's pm_delta_set_path / pm_delta_set_tile setting, would not
- * run the split form.  No reference counterpart: the reference's scan keeps
- * no per-chunk state (kernels/__init__.py:421-458).
+ * Workspace bytes pm_delta_fwd uses: the split form of the bf16 chunked
+ * kernel (6 KiB per (b, h) and 64-token chunk) or the fp32 chunked forward
+ * (1 KiB per (b, h) and 16-token chunk); 0 when the call, under the calling
+ * thread's pm_delta_set_path / pm_delta_set_tile setting, would use neither.
+ * No reference counterpart: the reference's scan keeps no per-chunk state
+ * (kernels/__init__.py:421-458).
  */
 size_t pm_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype);
-/* The same for pm_delta_fwd_varlen (6 KiB per head per slot, with
- * ceil(total_T / 64) + n_seqs slots). */
+/* The same for pm_delta_fwd_varlen (per head: 6 KiB per slot, with
+ * ceil(total_T / 64) + n_seqs slots; fp32: 1 KiB per slot, with
+ * ceil(total_T / 16) + n_seqs slots). */
 size_t pm_delta_varlen_workspace_bytes(int n_seqs, int total_T, int H, int D, int in_dtype);
 
 /*
@@ -248,10 +255,12 @@ int pm_abi_version(void);
  * pm_linear_attention, for tests and benchmarks: 0 = automatic (chunked MFMA
  * kernel where the shape and dtype allow, else the per-token kernel; the
  * plain forward in split form where that is faster and a workspace is
+ * given; fp32 inputs on the fp32 chunked forward where a workspace is
  * given), 1 = always the per-token kernel, 2 = chunked kernel required
- * (PM_E_UNSUPPORTED when it cannot serve the call), single-stage form, 3 = as
- * 2, with the plain forward always in split form (PM_E_WORKSPACE without a
- * workspace of pm_delta_workspace_bytes bytes).  The previous value is
+ * (PM_E_UNSUPPORTED when it cannot serve the call; for fp32 inputs the fp32
+ * chunked forward, PM_E_WORKSPACE without its workspace), single-stage form,
+ * 3 = as 2, with the plain bf16 forward always in split form (PM_E_WORKSPACE
+ * without a workspace of pm_delta_workspace_bytes bytes).  The previous value is
  * returned.  The setting is per calling thread: a
  * workspace-size query and the call it sizes, made on one thread, always see
  * the same setting.

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 7
+#define PM_DELTA_ABI_VERSION 8
 
 /* element types */
 #define PM_DTYPE_F32 0

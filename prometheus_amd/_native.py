@@ -18,7 +18,7 @@ import torch  # noqa: F401  (see module docstring: must precede CDLL)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpmdelta.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256

@@ -422,9 +422,9 @@ def main():
                              "decode_over_rmw": decode["roofline"]["achieved"] / rmw_gbs}
     del buf
 
-    # the model's linear attention (pm_linear_attention: q/k L2-normalised inside the
-    # kernel, beta = 1) at the cfg1 shape: bf16 q/k/v on the chunked kernel, and fp32
-    # (the reference model's dtype) on the per-token kernel
+    # the model's linear attention (pm_linear_attention_ws: q/k L2-normalised inside the
+    # kernel, beta = 1) at the cfg1 shape: bf16 q/k/v on the chunked kernel, fp32 (the
+    # reference model's dtype) on the fp32 chunked forward, with the per-token kernel beside
     model_la = None
     if args.model_calls > 0:
         model_la = {"workload": "cfg1 shape, model.linear_attention (beta 1, L2-normalised q/k)"}
@@ -434,26 +434,23 @@ def main():
         for name, dt, code, s_in in (("bf16", torch.bfloat16, _native.DTYPE_BF16, 2),
                                      ("fp32", torch.float32, _native.DTYPE_F32, 4)):
             qm, km, vm = (torch.randn((B, T, H, D), generator=g, device=dev).to(dt) for _ in range(3))
+            nbl = lib.pm_linear_attention_workspace_bytes(B, T, H, D, code)
+            wsl = torch.empty(nbl, dtype=torch.uint8, device=dev) if nbl else None
 
-            def la():
-                rc = lib.pm_linear_attention(qm.data_ptr(), km.data_ptr(), vm.data_ptr(), None,
-                                             om.data_ptr(), sm.data_ptr(), B, T, H, D, code,
-                                             _native.DTYPE_F32, stream.cuda_stream)
+            def la(i, ws=wsl, nb=nbl):
+                rc = lib.pm_linear_attention_ws(qm.data_ptr(), km.data_ptr(), vm.data_ptr(), None,
+                                                om.data_ptr(), sm.data_ptr(), B, T, H, D, code,
+                                                _native.DTYPE_F32, None if ws is None else ws.data_ptr(), nb,
+                                                stream.cuda_stream)
                 _native.check(rc)
 
-            la()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            calls = args.model_calls * (10 if name == "bf16" else 1)
-            e0.record(stream)
-            for _ in range(calls):
-                la()
-            e1.record(stream)
-            torch.cuda.synchronize()
-            la_ms = e0.elapsed_time(e1) / calls
+            la(0)
+            calls = args.model_calls * (10 if name == "bf16" else 5)
+            la_ms = time_launches(stream, la, calls)
             lb = fwd_bytes(B, T, H, D, s_in=s_in, s_out=4) - 4 * B * T * H  # no beta array
             model_la[name] = {
-                "kernel": "chunked MFMA, norms folded in" if name == "bf16" else "per-token fp32",
+                "kernel": "chunked MFMA, norms folded in" if name == "bf16"
+                          else "fp32 chunked forward on fp32 MFMA, norms folded in",
                 "calls": calls,
                 "ms_per_call": la_ms,
                 "tokens_per_s": tokens / (la_ms * 1e-3),
@@ -461,7 +458,11 @@ def main():
                              "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": lb / (la_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
             }
-            del qm, km, vm
+            if name == "fp32":
+                la(0, None, 0)
+                model_la[name]["per_token_ms_per_call"] = time_launches(
+                    stream, lambda i: la(i, None, 0), args.model_calls * 2)
+            del qm, km, vm, wsl
         del om, sm
 
     # the same cfg1 forward with fp32 q/k/v (the reference's dtype): the per-token kernel

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 8
+#define PM_DELTA_ABI_VERSION 9
 
 /* element types */
 #define PM_DTYPE_F32 0
@@ -174,6 +174,21 @@ int pm_delta_step_slots(float* pool, const int32_t* slots, int n_slots, const vo
 int pm_linear_attention(const void* q, const void* k, const void* v, const float* s0, void* o,
                         float* s_out, int B, int T, int H, int D, int in_dtype, int out_dtype,
                         void* stream);
+
+/*
+ * pm_linear_attention with a workspace: fp32 q/k/v at D in {64, 128}
+ * (16-byte aligned) run the fp32 chunked forward on fp32 MFMA in its
+ * normalised mode when workspace holds pm_linear_attention_workspace_bytes
+ * bytes (16-byte aligned); without it, the per-token kernel.  Everything
+ * else as pm_linear_attention (same replaced interface, model/__init__.py:
+ * 393-432; the workspace has no reference counterpart).
+ */
+int pm_linear_attention_ws(const void* q, const void* k, const void* v, const float* s0, void* o,
+                           float* s_out, int B, int T, int H, int D, int in_dtype, int out_dtype,
+                           void* workspace, size_t ws_bytes, void* stream);
+/* Workspace bytes pm_linear_attention_ws uses (1088 bytes per (b, h) and
+ * 16-token chunk for fp32 inputs at D in {64, 128}; otherwise 0). */
+size_t pm_linear_attention_workspace_bytes(int B, int T, int H, int D, int in_dtype);
 
 /*
  * Workspace bytes pm_delta_fwd uses: the split form of the bf16 chunked

@@ -18,7 +18,7 @@ import torch  # noqa: F401  (see module docstring: must precede CDLL)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpmdelta.so")
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256
@@ -36,6 +36,8 @@ EXPORTS = (
     "pm_gated_delta_fwd",
     "pm_gated_delta_step",
     "pm_linear_attention",
+    "pm_linear_attention_ws",
+    "pm_linear_attention_workspace_bytes",
     "pm_delta_workspace_bytes",
     "pm_delta_varlen_workspace_bytes",
     "pm_delta_bwd",
@@ -89,6 +91,10 @@ def lib() -> ctypes.CDLL:
         L.pm_delta_step_slots.restype = i
         L.pm_linear_attention.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, i, i, vp]
         L.pm_linear_attention.restype = i
+        L.pm_linear_attention_ws.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, i, i, vp, sz, vp]
+        L.pm_linear_attention_ws.restype = i
+        L.pm_linear_attention_workspace_bytes.argtypes = [i] * 5
+        L.pm_linear_attention_workspace_bytes.restype = sz
         L.pm_delta_workspace_bytes.argtypes = [i, i, i, i, i]
         L.pm_delta_workspace_bytes.restype = sz
         L.pm_delta_varlen_workspace_bytes.argtypes = [i, i, i, i, i]

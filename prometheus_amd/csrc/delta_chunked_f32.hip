@@ -44,7 +44,9 @@ namespace pm {
 namespace {
 
 constexpr int kC16 = 16;          // tokens per chunk
-constexpr int kWsFloats = 256;    // workspace floats per chunk: (T'')^T
+// workspace floats per chunk: (T'')^T, then (normalised mode) the 16 keys' 1 / max(||k||, 1e-6)
+template <bool NORM>
+constexpr int ws_floats() { return NORM ? 256 + 16 : 256; }
 
 __device__ __forceinline__ f32x4_t mfma4(float a, float b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -76,7 +78,7 @@ __device__ __forceinline__ int f32_chunk(int t, int p) {
 }
 
 // ---------------------------------------------------------------- K7p
-template <int D>
+template <int D, bool NORM>
 __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __restrict__ k,
                                                              const float* __restrict__ beta,
                                                              const int32_t* __restrict__ cu_seqlens,
@@ -119,19 +121,36 @@ __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __rest
     const size_t row0 = static_cast<size_t>(tok0 + base) * tstride + static_cast<size_t>(h) * D;
     const unsigned nb = static_cast<unsigned>(((clen - 1) * tstride + D) * 4);
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(k + row0, nb);
-    const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4));
     f32x4_t kf[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const unsigned vo = static_cast<unsigned>((r * tstride + 16 * j + 4 * g) * 4);
         kf[j] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 0, 0));
     }
-    const float bc = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, static_cast<unsigned>(r * H * 4), 0, 0));
-    f32x4_t bt;
+    // beta of this lane's column token r (bc) and of its accumulator rows 4 g + v (bt); in the
+    // normalised mode beta = 1 and sk / s4 are the keys' 1 / max(||k||, 1e-6) instead
+    float bc = 1.f, sk = 1.f;
+    f32x4_t bt = {1.f, 1.f, 1.f, 1.f}, s4 = {1.f, 1.f, 1.f, 1.f};
+    if constexpr (NORM) {
+        float ss = 0.f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-        bt[v] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, static_cast<unsigned>((4 * g + v) * H * 4), 0, 0));
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) ss = fmaf(kf[j][v], kf[j][v], ss);
+        ss += __shfl_xor(ss, 16);  // row r's four slices (every lane of the row gets equal bits)
+        ss += __shfl_xor(ss, 32);
+        sk = 1.f / fmaxf(sqrtf(ss), 1e-6f);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) s4[v] = __shfl(sk, 4 * g + v);
+    } else {
+        const __amdgpu_buffer_rsrc_t rb =
+            make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4));
+        bc = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, static_cast<unsigned>(r * H * 4), 0, 0));
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            bt[v] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rb, static_cast<unsigned>((4 * g + v) * H * 4), 0, 0));
+    }
 
     // G = K K^T (one accumulator per step of a tile, summed at the end)
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
@@ -140,7 +159,8 @@ __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __rest
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int v = 0; v < 4; ++v) ga[v] = mfma4(kf[j][v], kf[j][v], ga[v]);
-    const f32x4_t G = (ga[0] + ga[1]) + (ga[2] + ga[3]);
+    f32x4_t G = (ga[0] + ga[1]) + (ga[2] + ga[3]);
+    if constexpr (NORM) G = G * s4 * sk;  // Gram matrix of the normalised keys
     // N[i][j] = -beta_i G[i][j] (i > j), N^T[i][j] = -beta_j G[i][j] (j > i); i = 4 g + v, j = r
     f32x4_t N, Nt, eye;
 #pragma unroll
@@ -159,11 +179,15 @@ __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __rest
     f32x4_t tw;
 #pragma unroll
     for (int v = 0; v < 4; ++v) tw[v] = -bt[v] * Tt[v];  // (T'')^T[i][j] = -beta_i T[j][i]
-    *reinterpret_cast<f32x4_t*>(ws + (static_cast<size_t>(row) * n_slot + slot) * kWsFloats + lane * 4) = tw;
+    float* out = ws + (static_cast<size_t>(row) * n_slot + slot) * ws_floats<NORM>();
+    *reinterpret_cast<f32x4_t*>(out + lane * 4) = tw;
+    if constexpr (NORM) {
+        if (g == 0) out[256 + r] = sk;
+    }
 }
 
 // ---------------------------------------------------------------- K7
-template <int D, int DV>
+template <int D, int DV, bool NORM>
 struct F32Geo {
     static constexpr int NCW = DV / 16;            // chain waves 0 .. NCW-1, output waves NCW ..
     static constexpr int NT = D / 16;              // S accumulator tiles per chain wave
@@ -173,29 +197,31 @@ struct F32Geo {
     static constexpr int B_K = 0;
     static constexpr int B_Q = B_K + kC16 * D * 4;
     static constexpr int B_T = B_Q + kC16 * D * 4;
-    static constexpr int B_V = B_T + 1024;
+    static constexpr int B_V = B_T + (NORM ? 2048 : 1024);  // (T'')^T, then the keys' scales
     static constexpr int BUF = B_V + NCW * 1024;
     static constexpr int OFF_S = NB * BUF;                     // 2 slots x NCW x NT KiB: S_i
     static constexpr int OFF_U = OFF_S + 2 * NCW * NT * 1024;  // 2 slots x NCW KiB: U_i
-    static constexpr int OFF_P = OFF_U + 2 * NCW * 1024;       // 2 slots x 1 KiB: P^T of a chunk
-    static constexpr int BYTES = OFF_P + 2 * 1024;
+    static constexpr int PSLOT = NORM ? 1024 + 64 : 1024;      // P^T, then the queries' scales
+    static constexpr int OFF_P = OFF_U + 2 * NCW * 1024;       // 2 slots: P^T of a chunk
+    static constexpr int BYTES = OFF_P + 2 * PSLOT;
     // the last output wave (the copy wave) issues every copy of a chunk: K and Q rows,
     // (T'')^T and the V columns of each chain wave
-    static constexpr int NCP = 2 * NI + 1 + NCW;
+    static constexpr int NCP = 2 * NI + 1 + NCW + (NORM ? 1 : 0);
     static constexpr int NST = 4;  // O stores per output wave per chunk
     static_assert(D == 64 || D == 128, "D");
     static_assert(DV == 16 || DV == 32, "DV");
     static_assert(BYTES <= 160 * 1024 && NCP + NST <= 63, "LDS / vmcnt");
 };
 
-template <int D, int DV, bool OUT_BF16>
+template <int D, int DV, bool OUT_BF16, bool NORM>
 __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ s0, void* __restrict__ o_out, float* __restrict__ s_out,
     const int32_t* __restrict__ cu_seqlens, const float* __restrict__ ws, int n_pairs, int T, int H,
     int n_tiles, int n_slot) {
-    using G = F32Geo<D, DV>;
+    using G = F32Geo<D, DV, NORM>;
     constexpr int NCW = G::NCW, NT = G::NT;
+    constexpr int WSF = ws_floats<NORM>();
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
     // XCD-aware placement: the n_tiles workgroups of a pair share bid % 8
@@ -236,7 +262,7 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
     auto buf = [&](int c) { return smem + (c % G::NB) * G::BUF; };
     auto sslot = [&](int c, int which) { return smem + G::OFF_S + ((c & 1) * NCW + which) * NT * 1024; };
     auto uslot = [&](int c, int which) { return smem + G::OFF_U + ((c & 1) * NCW + which) * 1024; };
-    auto pslot = [&](int c) { return smem + G::OFF_P + (c & 1) * 1024; };
+    auto pslot = [&](int c) { return smem + G::OFF_P + (c & 1) * G::PSLOT; };
     auto ld4 = [&](const unsigned char* p) { return *reinterpret_cast<const f32x4_t*>(p); };
     auto st4 = [&](unsigned char* p, f32x4_t x) { *reinterpret_cast<f32x4_t*>(p) = x; };
 
@@ -257,9 +283,10 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
         }
     };
     auto copy_ws = [&](int c, unsigned char* dst) __attribute__((always_inline)) {
-        const __amdgpu_buffer_rsrc_t rs =
-            make_rsrc(ws + (static_cast<size_t>(ws_row) * n_slot + ws_slot0 + c) * kWsFloats, 1024);
-        dma16_asm(rs, uniform_ptr(dst), static_cast<unsigned>(16 * lane));
+        const float* src = ws + (static_cast<size_t>(ws_row) * n_slot + ws_slot0 + c) * WSF;
+        dma16_asm(make_rsrc(src, 1024), uniform_ptr(dst), static_cast<unsigned>(16 * lane));
+        // the keys' scales: 64 bytes (lanes past them read zeros)
+        if constexpr (NORM) dma16_asm(make_rsrc(src + 256, 64), uniform_ptr(dst + 1024), static_cast<unsigned>(16 * lane));
     };
     auto copy_v = [&](int c, int j, unsigned char* dst) __attribute__((always_inline)) {
         const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(v, c, 16, col0 + 16 * j);
@@ -336,15 +363,22 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
             }
             if (!run) break;
             fence();
-            xa[0] = -vr;  // (negated only here: a use right after the read would wait for it)
+            if constexpr (!NORM) xa[0] = -vr;  // (negated only here: a use right after the read would wait for it)
             // X = K S - V (accumulator e takes the steps (m, e))
 #pragma unroll
             for (int m = 0; m < NT; ++m)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) xa[e] = mfma4(kf[m][e], S[m][e], xa[e]);
-            const f32x4_t X = (xa[0] + xa[1]) + (xa[2] + xa[3]);
-            // U = T'' X
+            f32x4_t X = (xa[0] + xa[1]) + (xa[2] + xa[3]);
+            // normalised mode: X = diag(s) K S - V with s the keys' scales (rows 4 g + e)
+            f32x4_t skc = {1.f, 1.f, 1.f, 1.f};
+            if constexpr (NORM) {
+                skc = ld4(b + G::B_T + 1024 + 16 * g);
+                X = X * skc - vr;
+            }
+            // U = T'' X (normalised mode: the state update and P U take diag(s) U)
             Up = mm16(tt, X);
+            if constexpr (NORM) Up = Up * skc;
             // hand S_i and U_i to the output wave
             unsigned char* ss = sslot(i, cw);
 #pragma unroll
@@ -382,6 +416,7 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
             // accumulator e takes the steps (m, e); each tile's operand reads are issued two
             // tiles ahead.  One straight-line body per combination of the two products.
             f32x4_t ya[4] = {zero, zero, zero, zero}, pa[4] = {zero, zero, zero, zero};
+            float qss = 0.f;  // normalised mode: this lane's part of ||q_r||^2 of chunk i
             const unsigned char* by = buf(st ? i - 1 : 0);
             const unsigned char* bp = buf(i);
             const unsigned char* ss = sslot(st ? i - 1 : 0, cw);
@@ -408,6 +443,7 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
                     for (int e = 0; e < 4; ++e) {
                         if constexpr (DO_Y) ya[e] = mfma4(qy[m][e], sc[m][e], ya[e]);
                         if constexpr (DO_P) pa[e] = mfma4(kp[m][e], qp[m][e], pa[e]);
+                        if constexpr (DO_P && NORM) qss = fmaf(qp[m][e], qp[m][e], qss);
                     }
                     fence();
                 }
@@ -424,12 +460,21 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
 #pragma unroll
                 for (int e = 0; e < 4; ++e) pt[e] = (4 * g + e <= r) ? pq[e] : 0.f;
                 st4(pslot(i) + 16 * lane, pt);
+                if constexpr (NORM) {
+                    // the queries' scales 1 / max(||q||, 1e-6) of chunk i, from the Q operands
+                    // just used (a row's four slices are lanes r, r + 16, r + 32, r + 48)
+                    float ss = qss;
+                    ss += __shfl_xor(ss, 16);
+                    ss += __shfl_xor(ss, 32);
+                    if (g == 0) reinterpret_cast<float*>(pslot(i) + 1024)[r] = 1.f / fmaxf(sqrtf(ss), 1e-6f);
+                }
             }
             if (st) {
                 const int c = i - 1;
                 const f32x4_t pt = ld4(pslot(c) + 16 * lane);
                 const f32x4_t u = ld4(uslot(c, cw) + 16 * lane);
-                const f32x4_t O = mm16(pt, u, (ya[0] + ya[1]) + (ya[2] + ya[3]));
+                f32x4_t O = mm16(pt, u, (ya[0] + ya[1]) + (ya[2] + ya[3]));
+                if constexpr (NORM) O = O * ld4(pslot(c) + 1024 + 16 * g);  // rows scaled by the queries' scales
                 // lane (g, r) holds O[4 g + e][16 cw + r]; rows past the end are dropped by
                 // the range-checked stores
                 const int clen = min(kC16, len - c * kC16);
@@ -454,34 +499,36 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
     }
 }
 
-template <typename K>
-hipError_t set_lds_f32(K kern, int bytes) {
+// The dynamic-LDS limit is a per-device function attribute, set once per device for each
+// kernel (KERN: one static flag array per kernel, not per signature).
+template <auto KERN>
+hipError_t set_lds_f32(int bytes) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     static bool done[64] = {};
     if (dev >= 0 && dev < 64 && done[dev]) return hipSuccess;
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(KERN), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (e == hipSuccess && dev >= 0 && dev < 64) done[dev] = true;
     return e;
 }
 
-template <int D, int DV, bool OB>
+template <int D, int DV, bool OB, bool NORM>
 hipError_t launch_f32_t(const ChunkedF32Args& a, float* ws, hipStream_t st) {
-    using G = F32Geo<D, DV>;
+    using G = F32Geo<D, DV, NORM>;
     const bool varlen = a.cu_seqlens != nullptr;
     const int n_pairs = a.n_seq * a.H;
     const int n_slot = f32_n_slot(varlen, a.T, a.n_seq);
     const long n_items = static_cast<long>(varlen ? a.H : n_pairs) * n_slot;
     const float *q = a.q, *k = a.k, *v = a.v;
     if (n_items > 0) {
-        hipLaunchKernelGGL(delta_f32_prep_kernel<D>, dim3(static_cast<unsigned>((n_items + 3) / 4)), dim3(256), 0,
+        hipLaunchKernelGGL((delta_f32_prep_kernel<D, NORM>), dim3(static_cast<unsigned>((n_items + 3) / 4)), dim3(256), 0,
                            st, k, a.beta, a.cu_seqlens, a.n_seq, a.T, a.H, n_slot, n_items, ws);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    auto kern = delta_f32_kernel<D, DV, OB>;
-    hipError_t e = set_lds_f32(kern, G::BYTES);
+    auto kern = delta_f32_kernel<D, DV, OB, NORM>;
+    hipError_t e = set_lds_f32<delta_f32_kernel<D, DV, OB, NORM>>(G::BYTES);
     if (e != hipSuccess) return e;
     const int n_tiles = D / DV;
     const int slots = (n_pairs + 7) / 8;
@@ -490,16 +537,20 @@ hipError_t launch_f32_t(const ChunkedF32Args& a, float* ws, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <int D, int DV, bool NORM>
+hipError_t launch_f32_n(const ChunkedF32Args& a, float* ws, hipStream_t st) {
+    return a.out_bf16 ? launch_f32_t<D, DV, true, NORM>(a, ws, st) : launch_f32_t<D, DV, false, NORM>(a, ws, st);
+}
 template <int D, int DV>
 hipError_t launch_f32_dv(const ChunkedF32Args& a, float* ws, hipStream_t st) {
-    return a.out_bf16 ? launch_f32_t<D, DV, true>(a, ws, st) : launch_f32_t<D, DV, false>(a, ws, st);
+    return a.norm ? launch_f32_n<D, DV, true>(a, ws, st) : launch_f32_n<D, DV, false>(a, ws, st);
 }
 
 }  // namespace
 
-size_t chunked_f32_ws_bytes(bool varlen, int n_seq, int T, int H) {
+size_t chunked_f32_ws_bytes(bool varlen, int n_seq, int T, int H, bool norm) {
     const long rows = varlen ? H : static_cast<long>(n_seq) * H;
-    return static_cast<size_t>(rows) * f32_n_slot(varlen, T, n_seq) * kWsFloats * 4;
+    return static_cast<size_t>(rows) * f32_n_slot(varlen, T, n_seq) * (norm ? ws_floats<true>() : ws_floats<false>()) * 4;
 }
 
 int chunked_f32_pick_tile(int D, long n_pairs, int requested) {

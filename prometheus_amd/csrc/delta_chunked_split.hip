@@ -605,14 +605,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
-template <typename K>
-hipError_t set_lds_once(K kern, int bytes) {
+// The dynamic-LDS limit is a per-device function attribute, set once per device for each
+// kernel (KERN: one static flag array per kernel, not per signature).
+template <auto KERN>
+hipError_t set_lds_once(int bytes) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     static bool done[64] = {};
     if (dev >= 0 && dev < 64 && done[dev]) return hipSuccess;
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(KERN), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (e == hipSuccess && dev >= 0 && dev < 64) done[dev] = true;
     return e;
 }
@@ -629,7 +631,7 @@ hipError_t launch_split_t(const ChunkedArgs& a, uint16_t* tws, hipStream_t st) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     auto kern = delta_chunked_split_kernel<D, DV, OB>;
-    if ((e = set_lds_once(kern, G::BYTES)) != hipSuccess) return e;
+    if ((e = set_lds_once<delta_chunked_split_kernel<D, DV, OB>>(G::BYTES)) != hipSuccess) return e;
     const int n_tiles = D / DV;
     const int slots = (n_pairs + 7) / 8;
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(slots * 8 * n_tiles)), dim3(256), G::BYTES, st, a.q, a.k,

@@ -430,9 +430,22 @@ int pm_delta_step_slots(float* pool, const int32_t* slots, int n_slots, const vo
     return e == hipSuccess ? 0 : hip_fail(e, "slot decode step launch");
 }
 
+size_t pm_linear_attention_workspace_bytes(int B, int T, int H, int D, int in_dtype) {
+    if (B < 0 || T < 0 || H < 0 || in_dtype != PM_DTYPE_F32 || !pm::chunked_supported(D, H) || g_path == 1)
+        return 0;
+    if (static_cast<long>(B) * H > (1L << 30)) return 0;
+    return pm::chunked_f32_ws_bytes(false, B, T, H, true);
+}
+
 int pm_linear_attention(const void* q, const void* k, const void* v, const float* s0, void* o,
                         float* s_out, int B, int T, int H, int D, int in_dtype, int out_dtype,
                         void* stream) {
+    return pm_linear_attention_ws(q, k, v, s0, o, s_out, B, T, H, D, in_dtype, out_dtype, nullptr, 0, stream);
+}
+
+int pm_linear_attention_ws(const void* q, const void* k, const void* v, const float* s0, void* o,
+                           float* s_out, int B, int T, int H, int D, int in_dtype, int out_dtype,
+                           void* workspace, size_t ws_bytes, void* stream) {
     g_err[0] = '\0';
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (B < 0 || T < 0 || H < 0)
@@ -459,10 +472,13 @@ int pm_linear_attention(const void* q, const void* k, const void* v, const float
     const bool can_chunked = in_dtype == PM_DTYPE_BF16 && pm::chunked_supported(D, H) &&
                              aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
                              (out_dtype == PM_DTYPE_F32 ? aligned(o, 16) : aligned(o, 8));
-    if (path >= 2 && !can_chunked)
+    // fp32 q/k/v: the fp32 chunked forward in its normalised mode, with the workspace
+    const bool can_f32 = in_dtype == PM_DTYPE_F32 && pm::chunked_supported(D, H) && aligned(q, 16) &&
+                         aligned(k, 16) && aligned(v, 16) && (out_dtype == PM_DTYPE_F32 ? aligned(o, 4) : aligned(o, 2));
+    if (path >= 2 && !can_chunked && !can_f32)
         return fail(PM_E_UNSUPPORTED,
-                    "chunked kernel needs bf16 inputs, D in {64, 128} and 16-byte aligned "
-                    "q/k/v/o (got in_dtype %d, D %d)",
+                    "chunked kernel needs bf16 or fp32 inputs, D in {64, 128} and 16-byte aligned "
+                    "q/k/v (got in_dtype %d, D %d)",
                     in_dtype, D);
     if (path != 1 && can_chunked) {
         pm::ChunkedArgs a{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
@@ -470,6 +486,20 @@ int pm_linear_attention(const void* q, const void* k, const void* v, const float
                           out_dtype == PM_DTYPE_BF16, g_tile, true};
         hipError_t e = pm::launch_chunked(a, st);
         return e == hipSuccess ? 0 : hip_fail(e, "chunked linear attention launch");
+    }
+    if (path != 1 && can_f32) {
+        const size_t need = pm::chunked_f32_ws_bytes(false, B, T, H, true);
+        if (workspace && ws_bytes >= need && aligned(workspace, 16)) {
+            pm::ChunkedF32Args a{static_cast<const float*>(q), static_cast<const float*>(k),
+                                 static_cast<const float*>(v), nullptr, s0, o, s_out, nullptr, B, T, H, D,
+                                 out_dtype == PM_DTYPE_BF16, g_tile};
+            a.norm = true;
+            hipError_t e = pm::launch_chunked_f32(a, workspace, st);
+            return e == hipSuccess ? 0 : hip_fail(e, "fp32 chunked linear attention launch");
+        }
+        if (path >= 2)
+            return fail(PM_E_WORKSPACE, "the fp32 chunked linear attention needs a 16-byte aligned workspace of "
+                        "%zu bytes (got %zu)", need, workspace ? ws_bytes : static_cast<size_t>(0));
     }
     pm::RecurrentArgs a{q, k, v, nullptr, s0, o, s_out, nullptr, static_cast<int>(n_pairs), T, H, D,
                         in_dtype == PM_DTYPE_BF16, out_dtype == PM_DTYPE_BF16, true};

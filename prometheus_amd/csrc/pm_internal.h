@@ -96,8 +96,11 @@ struct ChunkedF32Args {
     int T, H, D;                // varlen: T = packed token count
     bool out_bf16;
     int dv_tile;  // 0 = automatic
+    // The model's linear attention: beta = 1 (beta unused), q and k divided by
+    // max(||.||, 1e-6) per token inside the kernels.
+    bool norm = false;
 };
-size_t chunked_f32_ws_bytes(bool varlen, int n_seq, int T, int H);
+size_t chunked_f32_ws_bytes(bool varlen, int n_seq, int T, int H, bool norm = false);
 int chunked_f32_pick_tile(int D, long n_pairs, int requested);
 hipError_t launch_chunked_f32(const ChunkedF32Args& a, void* ws, hipStream_t st);
 // The same kernel writing, instead of O and the final state, the state at

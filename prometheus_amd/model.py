@@ -60,9 +60,12 @@ def _run_linear_attention(qd, kd, vd, sd, cdt, device):
     batch, seq, heads, dim = qd.shape
     o = torch.empty(qd.shape, dtype=torch.float32, device=device)
     s_out = torch.empty((batch, heads, dim, dim), dtype=torch.float32, device=device)
-    rc = _native.lib().pm_linear_attention(
+    lib = _native.lib()
+    nbytes = lib.pm_linear_attention_workspace_bytes(batch, seq, heads, dim, _code(cdt))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+    rc = lib.pm_linear_attention_ws(
         _ptr(qd), _ptr(kd), _ptr(vd), _ptr(sd), _ptr(o), _ptr(s_out),
-        batch, seq, heads, dim, _code(cdt), _native.DTYPE_F32, _stream(device),
+        batch, seq, heads, dim, _code(cdt), _native.DTYPE_F32, _ptr(ws), nbytes, _stream(device),
     )
     _native.check(rc)
     return o, s_out

@@ -159,6 +159,46 @@ def test_chunked_kernel_large_zero_rows_and_repeatable():
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
+@pytest.mark.parametrize("shape", [(1, 1, 1, 64), (2, 77, 3, 64), (1, 200, 2, 128), (2, 64, 1, 128)])
+@pytest.mark.parametrize("state", [False, True])
+def test_fp32_chunked_kernel_against_oracle(shape, state):
+    """fp32 q/k/v, D in {64, 128}: the fp32 chunked forward in its normalised mode
+    (fp32 MFMA), at the fp32 bounds."""
+    rng = np.random.default_rng(100 + sum(shape) + state)
+    q, k, v = (_rand(rng, shape) for _ in range(3))
+    s0 = (_rand(rng, (shape[0], shape[2], shape[3], shape[3])) * 0.05) if state else None
+    lib = _native.lib()
+    assert lib.pm_linear_attention_workspace_bytes(shape[0], shape[1], shape[2], shape[3],
+                                                   _native.DTYPE_F32) > 0
+    qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, k, v))
+    out, st = model.linear_attention(qd, kd, vd, state=None if s0 is None else torch.from_numpy(s0).cuda())
+    out_r, st_r = mref.linear_attention(q, k, v, s0, dtype=np.float64)
+    assert_f32_parity(out.cpu().numpy(), out_r, f"{shape} out")
+    assert_f32_parity(st.cpu().numpy(), st_r, f"{shape} state")
+
+
+def test_fp32_chunked_kernel_large_zero_rows_and_repeatable():
+    """(2, 1000, 4, 128) fp32 against the per-token kernel, with zero and tiny q/k
+    rows (the eps guard), and bitwise repeatable."""
+    rng = np.random.default_rng(14)
+    shape = (2, 1000, 4, 128)
+    q, k, v = (torch.from_numpy(_rand(rng, shape)).cuda() for _ in range(3))
+    q[0, 10, 1] = 0
+    k[1, 500, 2] = 0
+    k[0, 65, 0] = 1e-9
+    a = model.linear_attention(q, k, v)
+    old = _native.set_path(1)
+    try:
+        exact = model.linear_attention(q, k, v)
+    finally:
+        _native.set_path(old)
+    for x, e, n in zip(a, exact, ("out", "state")):
+        assert_f32_parity(x.cpu().numpy(), e.cpu().numpy(), n)
+    assert torch.all(a[0][0, 10, 1] == 0)
+    b = model.linear_attention(q, k, v)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
 def test_empty_sequence_passes_state_through():
     s0 = np.random.default_rng(13).standard_normal((2, 3, 8, 8)).astype(np.float32)
     z = np.zeros((2, 0, 3, 8), np.float32)

@@ -24,7 +24,7 @@
 //   3. bwd_rev_kernel walks the chunks backwards per (b, h, 32 columns of
 //      d_v) carrying G in fp32 MFMA accumulators (the columns of G are
 //      independent) in two waves, while two more waves copy the next chunk;
-//      it writes G_c (bf16, rows of G^T), W (bf16, rows of W^T), dV and
+//      it writes G_c and W (bf16, in the packed order below), dV and
 //      finally dS_0;
 //   4. bwd_grad_kernel, all chunks in parallel (one persistent workgroup
 //      per CU, the next chunk's inputs fetched during the last phase): dQ,
@@ -85,6 +85,39 @@ __device__ __forceinline__ int swz(int r, int c) {
     return r * RL + 8 * ((c >> 3) ^ kq_f<RL>(r)) + (c & 7);
 }
 __device__ __forceinline__ bf16x8_t as_b(u32x4_t x) { return __builtin_bit_cast(bf16x8_t, x); }
+
+// Packed order of a chunk's W and G in the workspace (written by the reverse sweep in its
+// accumulator layout, so each store instruction covers one contiguous block).  Block
+// (jt, x) holds column tile jt (columns j = 16 jt + l16) and contraction block x; the piece
+// of lane (g, l16) goes to slot w_slot / g_slot, a bijection on 0..63 chosen so that the
+// gradient kernel's transposing reads hit every LDS bank once:
+//   W (x = m):  4-element pieces W[16m + 4g .. +4][16jt + l16], blocks of 256 elements;
+//   G (x = kb): 8-element pieces G[32kb + 8g .. +8][16jt + l16], blocks of 512 elements.
+__device__ __forceinline__ int w_slot(int g, int l16) { return 16 * g + (l16 ^ (4 * (g >> 1))); }
+__device__ __forceinline__ int g_slot(int g, int l16) { return 16 * g + (l16 ^ (4 * (g & 1))); }
+// From the packed W: lane (g, l16) gets W[16m + l16][32kb + 8g + i], i < 8 (two transposing
+// reads; valid after lds_wait_all + tie).
+__device__ __forceinline__ u32x4_t w_col_issue(const uint16_t* Wp, int kb, int m, int lane) {
+    const int g = lane >> 4, jp = (lane >> 2) & 3, cc = lane & 3;
+    const int ja = 32 * kb + 8 * g + jp, jb = ja + 4;
+    const u32x2_t lo = lds_tr16_issue<0>(lds_addr(Wp + (((ja >> 4) * 4 + m) * 64 + w_slot(cc, ja & 15)) * 4));
+    const u32x2_t hi = lds_tr16_issue<0>(lds_addr(Wp + (((jb >> 4) * 4 + m) * 64 + w_slot(cc, jb & 15)) * 4));
+    const u32x4_t v = {lo.x, lo.y, hi.x, hi.y};
+    return v;
+}
+// From the packed G: lane (g, l16) gets G[16dt + l16][32kb + 8g + i], i < 8.
+template <int D>
+__device__ __forceinline__ u32x4_t g_col_issue(const uint16_t* Gp, int kb, int dt, int lane) {
+    const int g = lane >> 4, jp = (lane >> 2) & 3, cc = lane & 3;
+    const int ja = 32 * kb + 8 * g + jp, jb = ja + 4;
+    const int d = 16 * dt + 4 * cc;
+    const int e = ((d >> 5) * 64) * 8 + 4 * ((d >> 2) & 1);  // contraction block and half piece
+    const int gg = (d & 31) >> 3;
+    const u32x2_t lo = lds_tr16_issue<0>(lds_addr(Gp + (ja >> 4) * (D / 32) * 512 + e + g_slot(gg, ja & 15) * 8));
+    const u32x2_t hi = lds_tr16_issue<0>(lds_addr(Gp + (jb >> 4) * (D / 32) * 512 + e + g_slot(gg, jb & 15) * 8));
+    const u32x4_t v = {lo.x, lo.y, hi.x, hi.y};
+    return v;
+}
 
 // Copy n_instr KiB of a tile of rows of RL bf16 (rows src_row_bytes apart
 // in the buffer) into a swizzled LDS tile; instruction ii (taken by wave
@@ -249,6 +282,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // chunk into LDS and wait for it, so no wave waits on the others' stores
     const bool chain = w < 2;
     const int j = tile * G::NC + 16 * (w & 1) + l16;  // this lane's column of G (chain waves)
+    const int jt = j >> 4;                             // its 16-column tile
     const size_t tstride = static_cast<size_t>(H) * D;
     const size_t sbase = static_cast<size_t>(pair) * D * D;
 
@@ -305,9 +339,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     // One LDS-only barrier per chunk: by then the loaders have waited for the copies of the
     // chunk the chain takes next, and the chain's stores need not complete.  The loaders
-    // keep the chunk after that in flight: a loader wave issues nothing but these copies,
-    // so waiting until G::COPIES (+1 for the beta copy) are outstanding completes exactly
-    // the older chunk's.
+    // keep the chunk after that in flight: a loader wave issues only these copies and,
+    // before them, its dV stores, so waiting until G::COPIES (+1 for the beta copy) are
+    // outstanding completes at least the older chunk's copies (loads complete in order).
     auto wait_older = [&] {
         if (w == 3)
             __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(G::COPIES + 1) : "memory");
@@ -327,9 +361,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         lds_barrier();
     }
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    // Stores that scatter over many rows stall a chain wave while the loaders' copies are in
+    // flight.  So G and W go out in packed order (one contiguous block per instruction), W
+    // at the start of the next iteration next to G; and dV, whose rows are 64 bytes per
+    // chain wave, is staged in the chunk's dO space (dead once the chain has its dO
+    // operands; each wave overwrites only the bytes of its own dO columns) and stored by the
+    // loader waves in whole 128-byte rows in the next iteration, before that buffer is
+    // refilled.
+    u32x2_t w_pend[4];
+    uint16_t* wp_pend = nullptr;
+    auto store_w = [&] {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) *reinterpret_cast<u32x2_t*>(wp_pend + m * 256) = w_pend[m];
+    };
+    // dV of chunk cc from its staging tile (rows of 32 fp32 in the dO tile's order) to gv;
+    // rows past the chunk's end fall outside the buffer range and are dropped (offsets
+    // fit 32 bits since H D <= 2^23)
+    auto store_dv = [&](int cc) {
+        const int cb = cc * kC, cl = min(kC, T - cb);
+        const __amdgpu_buffer_rsrc_t rv =
+            make_rsrc(gv + (tok0 + cb) * tstride + static_cast<size_t>(h) * D + col0,
+                      static_cast<unsigned>(((cl - 1) * tstride + G::NC) * 4));
+        const float* Ds = reinterpret_cast<const float*>(buf(cc) + G::DO);
+#pragma unroll
+        for (int ii = w - 2; ii < kC * G::NC * 4 / 1024; ii += 2) {
+            const int r = 8 * ii + (lane >> 3), p = lane & 7;
+            const u32x4_t x = *reinterpret_cast<const u32x4_t*>(Ds + r * G::NC + 4 * (p ^ fdo(r)));
+            __builtin_amdgcn_raw_buffer_store_b128(x, rv, static_cast<unsigned>((r * tstride + 4 * p) * 4), 0, 0);
+        }
+    };
     for (int c = n_ch - 1; c >= 0; --c) {
         if (!chain) {
             if (c > 0) {  // make chunk c - 1 ready; put c - 2 in flight
+                if (c < n_ch - 1) store_dv(c + 1);  // staged in the last iteration; c + 1 and c - 2 share a buffer
                 if (c >= 2) {
                     issue(c - 2);
                     wait_older();
@@ -337,6 +401,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     wait_copies();
                 }
                 lds_barrier();
+            } else if (n_ch > 1) {
+                store_dv(1);
             }
             continue;
         }
@@ -348,15 +414,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const float* Bs = reinterpret_cast<const float*>(b + G::BS);
         const float* Ds = reinterpret_cast<const float*>(b + G::DO);
         const int base = c * kC, clen = min(kC, T - base);
-        // G_c: the gradient of the state at the end of chunk c, as rows of G^T (Gb[kb] holds
-        // G[32kb + 8g .. +8][j])
+        // G_c, the gradient of the state at the end of chunk c, in packed order (Gb[kb] holds
+        // G[32kb + 8g .. +8][j], j in column tile jt)
         {
-            uint16_t* hp = g_hist + (static_cast<size_t>(pair) * n_ch + c) * D * D + static_cast<size_t>(j) * D;
+            uint16_t* hp = g_hist + (static_cast<size_t>(pair) * n_ch + c) * D * D + static_cast<size_t>(jt) * D * 16 +
+                           g_slot(lg, l16) * 8;
 #pragma unroll
-            for (int kb = 0; kb < D / 32; ++kb)
-                *reinterpret_cast<bf16x8_t*>(hp + 32 * kb + 8 * lg) = Gb[kb];
+            for (int kb = 0; kb < D / 32; ++kb) *reinterpret_cast<bf16x8_t*>(hp + kb * 512) = Gb[kb];
         }
+        if (c < n_ch - 1) store_w();
         const bf16x8_t d0 = do_op(Ds, 0), d1 = do_op(Ds, 1);
+        // beta of tokens 16m + 4g + [0, 4) (the state update) and 16m + l16 (dV), read now so
+        // that the stores below wait on no LDS read
+        f32x4_t bq[4];
+        float bt[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            bq[m] = *reinterpret_cast<const f32x4_t*>(Bs + 16 * m + 4 * lg);
+            bt[m] = Bs[16 * m + l16];
+        }
         // Y = K G + P^T dO
         f32x4_t Y[4];
 #pragma unroll
@@ -405,16 +481,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         WT[3] = mfma32(Yb1, packed_a(TTp, qblk_u(3, 1), lane), zero);
         // W^T rows (bf16) for the gradient kernel; the state update takes -beta W
         f32x4_t NBW[4];
-        uint16_t* wp = w_hist + (static_cast<size_t>(pair) * n_ch + c) * D * kC + static_cast<size_t>(j) * kC;
-        const size_t vcol = static_cast<size_t>(h) * D + tile * G::NC + 16 * (w & 1) + 4 * lg;
+        float* Dst = reinterpret_cast<float*>(b + G::DO);  // dV staging (the chain's own dO columns)
+        wp_pend = w_hist + (static_cast<size_t>(pair) * n_ch + c) * D * kC + static_cast<size_t>(jt) * 4 * 256 +
+                  w_slot(lg, l16) * 4;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            const int t0 = 16 * m + 4 * lg;
-            NBW[m] = -(*reinterpret_cast<const f32x4_t*>(Bs + t0) * W[m]);
-            *reinterpret_cast<u32x2_t*>(wp + t0) = cvt4(W[m]);
+            NBW[m] = -(bq[m] * W[m]);
+            w_pend[m] = cvt4(W[m]);
             const int t = 16 * m + l16;
-            if (t < clen)
-                *reinterpret_cast<f32x4_t*>(gv + (tok0 + base + t) * tstride + vcol) = Bs[t] * WT[m];
+            *reinterpret_cast<f32x4_t*>(Dst + t * G::NC + 4 * ((4 * (w & 1) + lg) ^ fdo(t))) = bt[m] * WT[m];
         }
         // G -= K^T diag(beta) W (Q^T dO was added above)
         const bf16x8_t nb0 = acc_to_b(NBW[0], NBW[1]), nb1 = acc_to_b(NBW[2], NBW[3]);
@@ -436,6 +511,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int kb = 0; kb < D / 32; ++kb) Gb[kb] = acc_to_b(Gm[2 * kb], Gm[2 * kb + 1]);
         if (c > 0) lds_barrier();
     }
+    if (n_ch > 0) {
+        lds_barrier();  // chunk 0's dV is staged
+        if (chain)
+            store_w();
+        else
+            store_dv(0);
+    }
     if (chain) {
 #pragma unroll
         for (int md = 0; md < D / 16; ++md)
@@ -455,9 +537,9 @@ struct GradGeo {
     static constexpr int VS = QS + kC * D * 2;     // V  [t][j], later U^T [j][t]
     static constexpr int DO = VS + kC * D * 2;     // dO [t][j] (bf16)
     static constexpr int ST = DO + kC * D * 2;     // S^T [j][d]
-    static constexpr int GT = ST + D * D * 2;      // G^T [j][d], later dP^T, (beta dA)^T [s][t]
+    static constexpr int GT = ST + D * D * 2;      // G (packed), later dP^T, (beta dA)^T [s][t]
     static constexpr int GT_BYTES = D * D * 2 > 4 * kC * kC ? D * D * 2 : 4 * kC * kC;
-    static constexpr int WT = GT + GT_BYTES;       // W^T [j][t]
+    static constexpr int WT = GT + GT_BYTES;       // W (packed)
     static constexpr int TP = WT + D * kC * 2;     // packed T
     static constexpr int BS = TP + kPacked * 2;    // beta
     static constexpr int DB = BS + kC * 4;         // dbeta partial sums [2][4][kC]
@@ -542,8 +624,7 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         const unsigned rb = static_cast<unsigned>(tstride * 2);
         copy_rows<D>(make_rsrc(v + r.row0, n_kq), smem + G::VS, kC * D * 2 / 1024, rb, w, 4, lane);
         copy_rows<D>(make_rsrc(s_hist + r.cidx * D * D, D * D * 2), smem + G::ST, D * D * 2 / 1024, D * 2, w, 4, lane);
-        copy_rows<kC>(make_rsrc(w_hist + r.cidx * D * kC, D * kC * 2), smem + G::WT, D * kC * 2 / 1024, kC * 2, w, 4,
-                      lane);
+        copy_flat(make_rsrc(w_hist + r.cidx * D * kC, D * kC * 2), smem + G::WT, D * kC * 2 / 1024, w, 4, lane);
         copy_flat(make_rsrc(tp_ws + r.cidx * 3 * kPacked, kPacked * 2), smem + G::TP, kPacked * 2 / 1024, w, 4, lane);
     };
     // the inputs phase 3 reads: K, Q, G^T, beta
@@ -552,7 +633,7 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         const unsigned rb = static_cast<unsigned>(tstride * 2);
         copy_rows<D>(make_rsrc(k + r.row0, n_kq), smem + G::KS, kC * D * 2 / 1024, rb, w, 4, lane);
         copy_rows<D>(make_rsrc(q + r.row0, n_kq), smem + G::QS, kC * D * 2 / 1024, rb, w, 4, lane);
-        copy_rows<D>(make_rsrc(g_hist + r.cidx * D * D, D * D * 2), smem + G::GT, D * D * 2 / 1024, D * 2, w, 4, lane);
+        copy_flat(make_rsrc(g_hist + r.cidx * D * D, D * D * 2), smem + G::GT, D * D * 2 / 1024, w, 4, lane);
         if (w == 3)
             copy_to_lds(make_rsrc(beta + (r.tok0 + r.base) * H + r.h, static_cast<unsigned>(((r.clen - 1) * H + 1) * 4)),
                         smem + G::BS, 4, static_cast<unsigned>(lane * H * 4));
@@ -598,7 +679,7 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
             for (int m = 0; m < 4; ++m) dbp[m] = zero;
 #pragma unroll
             for (int jj = 0; jj < JW; ++jj) {
-                const int jt = JW * w + jj, jcol = 16 * jt + l16;
+                const int jt = JW * w + jj;
                 u32x2_t vv0 = lds_acc_issue<D>(Vs, 0, 16 * jt, lane), vv1 = lds_acc_issue<D>(Vs, 16, 16 * jt, lane);
                 u32x2_t vv2 = lds_acc_issue<D>(Vs, 32, 16 * jt, lane), vv3 = lds_acc_issue<D>(Vs, 48, 16 * jt, lane);
                 lds_wait(vv0, vv1, vv2, vv3);
@@ -608,7 +689,7 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
                 for (int m = 0; m < 4; ++m) {
                     const int t0 = 16 * m + 4 * lg;
                     const f32x4_t rp = widen4(vv[m]) - X[m][jj];  // V - K S
-                    const f32x4_t wv = widen4(*reinterpret_cast<const u32x2_t*>(Wt + swz<kC>(jcol, t0)));
+                    const f32x4_t wv = widen4(*reinterpret_cast<const u32x2_t*>(Wt + ((jt * 4 + m) * 64 + w_slot(lg, l16)) * 4));
                     dbp[m] += wv * rp;
                     R[m] = *reinterpret_cast<const f32x4_t*>(Bs + t0) * rp;
                 }
@@ -669,13 +750,13 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 fu[m] = lds_col_issue<kC>(Ut, 32 * kb, 16 * m, lane);
-                fw[m] = lds_col_issue<kC>(Wt, 32 * kb, 16 * m, lane);
+                fw[m] = w_col_issue(Wt, kb, m, lane);
             }
             u32x4_t fst[JW], fgt[JW];
 #pragma unroll
             for (int dd = 0; dd < JW; ++dd) {
                 fst[dd] = lds_col_issue<D>(St, 32 * kb, 16 * (JW * w + dd), lane);
-                fgt[dd] = lds_col_issue<D>(Gt, 32 * kb, 16 * (JW * w + dd), lane);
+                fgt[dd] = g_col_issue<D>(Gt, kb, JW * w + dd, lane);
             }
             bf16x8_t fdo[4];
 #pragma unroll

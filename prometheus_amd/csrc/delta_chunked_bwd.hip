@@ -580,8 +580,9 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
     float* db2 = db1 + 4 * kC;                             // [wave][t]: sum_s dA (k_t . k_s)
 
     // Persistent: workgroup b takes chunks b, b + gridDim.x, ...  Phase 3 reads only K, Q,
-    // G^T's space (dP^T, dA^T) and beta, so the next chunk's V, S^T, W^T, T and dO are
-    // fetched while it runs, and only K, Q, G^T and beta are copied between chunks.
+    // G's space (dP^T, dA^T) and beta, so the next chunk's V, S^T, W, T and dO are fetched
+    // while it runs; Q and G, first read in phase 2, are fetched while phase 1 runs; only
+    // K and beta are copied between chunks.
     struct Ref {
         long tok0;
         int h, base, clen;
@@ -627,23 +628,29 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         copy_flat(make_rsrc(w_hist + r.cidx * D * kC, D * kC * 2), smem + G::WT, D * kC * 2 / 1024, w, 4, lane);
         copy_flat(make_rsrc(tp_ws + r.cidx * 3 * kPacked, kPacked * 2), smem + G::TP, kPacked * 2 / 1024, w, 4, lane);
     };
-    // the inputs phase 3 reads: K, Q, G^T, beta
-    auto copy_b = [&](const Ref& r) {
+    // K and beta (read from phase 1 on), copied between chunks
+    auto copy_k = [&](const Ref& r) {
         const unsigned n_kq = static_cast<unsigned>(((r.clen - 1) * tstride + D) * 2);
         const unsigned rb = static_cast<unsigned>(tstride * 2);
         copy_rows<D>(make_rsrc(k + r.row0, n_kq), smem + G::KS, kC * D * 2 / 1024, rb, w, 4, lane);
-        copy_rows<D>(make_rsrc(q + r.row0, n_kq), smem + G::QS, kC * D * 2 / 1024, rb, w, 4, lane);
-        copy_flat(make_rsrc(g_hist + r.cidx * D * D, D * D * 2), smem + G::GT, D * D * 2 / 1024, w, 4, lane);
         if (w == 3)
             copy_to_lds(make_rsrc(beta + (r.tok0 + r.base) * H + r.h, static_cast<unsigned>(((r.clen - 1) * H + 1) * 4)),
                         smem + G::BS, 4, static_cast<unsigned>(lane * H * 4));
+    };
+    // Q and G (read from phase 2 on, into space phase 3 of the chunk before read last),
+    // copied while phase 1 runs
+    auto copy_qg = [&](const Ref& r) {
+        const unsigned n_kq = static_cast<unsigned>(((r.clen - 1) * tstride + D) * 2);
+        const unsigned rb = static_cast<unsigned>(tstride * 2);
+        copy_flat(make_rsrc(g_hist + r.cidx * D * D, D * D * 2), smem + G::GT, D * D * 2 / 1024, w, 4, lane);
+        copy_rows<D>(make_rsrc(q + r.row0, n_kq), smem + G::QS, kC * D * 2 / 1024, rb, w, 4, lane);
     };
 
     int idx = blockIdx.x;
     if (idx >= n_total) return;  // whole workgroup, before any barrier
     Ref cur = ref_of(idx);
     load_do(cur);
-    copy_b(cur);
+    copy_k(cur);
     copy_a(cur);
     store_do();
     wait_copies();
@@ -653,6 +660,7 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         const int h = cur.h, base = cur.base, clen = cur.clen;
         const size_t row0 = cur.row0;
         const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+        copy_qg(cur);
 
         // ---- phase 1: R' = V - K S and U = T diag(beta) R' for this wave's columns ----
         f32x4_t U[4][JW];
@@ -709,6 +717,7 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
                 if (l16 == 0) *reinterpret_cast<f32x4_t*>(db1 + w * kC + 16 * m + 4 * lg) = dbp[m];
             }
         }
+        wait_copies();    // Q and G (no other copy or store is in flight)
         __syncthreads();  // V is dead: its space takes U^T
 #pragma unroll
         for (int m = 0; m < 4; ++m)
@@ -945,7 +954,7 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         }
         if (!more) break;
         __syncthreads();  // phase 3's reads of K, Q, dP^T, dA^T, beta and the dbeta sums are done
-        copy_b(nxt);
+        copy_k(nxt);
         store_do();
         wait_copies();
         __syncthreads();

@@ -83,10 +83,15 @@ struct Geo {
     // GATED: one 64-float scratch per producer for the scanned gates, after RN
     static constexpr int GS = BYTES_NORM;
     static constexpr int BYTES_GATED = BYTES_NORM + 2 * 256;
+    // bf16 O with two chain waves (DV = 32): O staged per chunk parity as rows of DV bf16,
+    // after every mode's own layout (see flush_o)
+    static constexpr int OB = BYTES_GATED;
+    static constexpr int OB_BYTES = kC * DV * 2;
+    static constexpr int BYTES_STAGED = OB + 2 * OB_BYTES;
     static_assert(D == 64 || D == 128, "D");
     static_assert(DV == 16 || DV == 32, "DV");
     static_assert(NI_V >= 1 && RAW % 16 == 0, "RAW layout");
-    static_assert(BYTES <= 160 * 1024, "LDS budget");
+    static_assert(BYTES_STAGED <= 160 * 1024, "LDS budget");
 };
 
 // HIST: the backward's state recompute.  Instead of O and the final state,
@@ -507,6 +512,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int kb = 0; kb < D / 32; ++kb) Sb[kb] = acc_to_b(S[2 * kb], S[2 * kb + 1]);
 
+    // bf16 O staging (two chain waves).  A chain wave holds 16 columns of O, 32 bytes of
+    // each token row, and storing them straight from the accumulators scatters every store
+    // instruction over 16 rows.  Instead the chain waves write their O tiles into the
+    // staging rows of the chunk's parity, and the loader, two iterations later, stores whole
+    // 64-byte rows (16 bytes per lane).  16-byte unit u of row r sits at u ^ ((r >> 2) & 3):
+    // the accumulator writes (16 rows, 8 bytes each) and the row reads are conflict-free.
+    // (With fp32 O, 64 bytes per row per wave, staging measured no faster.)
+    constexpr bool STAGE = OUT_BF16 && G::NCW == 2 && !HIST;
+    constexpr int ORB = DV * 2;  // bytes per staged row
+    constexpr int OUPR = ORB / 16;
+    auto ostg_f = [](int r) { return (r >> 2) & 3; };
+    auto obuf = [&](int c) { return smem + G::OB + (c & 1) * G::OB_BYTES; };
+    auto flush_o = [&](int cc) {
+        const int cb = cc * kC, cl = min(kC, len - cb);
+        // rows past the sequence's end fall outside the buffer range and are dropped
+        const __amdgpu_buffer_rsrc_t ro =
+            make_rsrc(static_cast<uint16_t*>(o_out) + (tok0 + cb) * tstride + static_cast<size_t>(h) * D + col0,
+                      static_cast<unsigned>(((cl - 1) * tstride + DV) * 2));
+        const unsigned char* ob = obuf(cc);
+#pragma unroll
+        for (int i = 0; i < kC * ORB / 1024; ++i) {
+            const int r = i * (1024 / ORB) + lane / OUPR, p = lane % OUPR;
+            const u32x4_t x = *reinterpret_cast<const u32x4_t*>(ob + r * ORB + 16 * (p ^ ostg_f(r)));
+            __builtin_amdgcn_raw_buffer_store_b128(x, ro, static_cast<unsigned>(r * tstride * 2 + 16 * p), 0, 0);
+        }
+    };
+
     auto run_chunk = [&](int c) {
         unsigned char* rb = raw(c);
         const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + G::R_KS);
@@ -621,10 +653,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int kb = 0; kb < D / 32; ++kb) Sb[kb] = acc_to_b(S[2 * kb], S[2 * kb + 1]);
         const int ocol = col0 + 16 * w + 4 * lg;
+        if constexpr (STAGE) {
+            unsigned char* ob = obuf(c);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const int t = 16 * m + l16;
+                const u32x2_t x = {pack_rne(O[m].x, O[m].y), pack_rne(O[m].z, O[m].w)};
+                *reinterpret_cast<u32x2_t*>(ob + t * ORB + 16 * ((2 * w + (lg >> 1)) ^ ostg_f(t)) + 8 * (lg & 1)) = x;
+            }
+        }
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int t = 16 * m + l16;
-            if (!HIST && t < clen) {
+            if (!HIST && !STAGE && t < clen) {
                 const size_t a = (tok0 + base + t) * tstride + static_cast<size_t>(h) * D + ocol;
                 if constexpr (OUT_BF16) {
                     const u32x2_t ob = {pack_rne(O[m].x, O[m].y), pack_rne(O[m].z, O[m].w)};
@@ -641,7 +682,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // the producers build chunk i's T and P from RAW[i%3] into TP[i%2], and the
     // chain runs chunk i-1 from RAW[(i-1)%3] and TP[(i-1)%2].  Barrier i+1
     // publishes all three, and frees RAW[(i-1)%3] and TP[(i-1)%2] for reuse.
-    // Every role passes the same n_chunks + 1 barriers.
+    // Every role passes the same n_chunks + 1 barriers (+ 1 when bf16 O is staged).
     if (n_chunks > 0) {
         if (chain) {
             lds_barrier();  // chunk 0 copied
@@ -650,6 +691,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 run_chunk(c);
                 if (c + 1 < n_chunks) lds_barrier();
             }
+            if constexpr (STAGE) lds_barrier();
         } else {
             const bool loader = pw == G::LOADER;
             if (loader) {
@@ -659,6 +701,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             lds_barrier();
             for (int c = 0; c < n_chunks; ++c) {
                 if (loader && c + 1 < n_chunks) issue_copies(c + 1);
+                if (STAGE && loader && c >= 2) flush_o(c - 2);  // staged in iteration c - 1
                 if (pw == 0) {
                     build_t(c);
                 } else if (pw == 1 && !HIST) {  // HIST computes no O, so no P
@@ -666,6 +709,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 }
                 if (loader) wait_copies();
                 lds_barrier();
+            }
+            if constexpr (STAGE) {
+                if (loader && n_chunks >= 2) flush_o(n_chunks - 2);
+                lds_barrier();  // the chain has staged the last chunk
+                if (loader) flush_o(n_chunks - 1);
             }
         }
     }
@@ -685,7 +733,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 template <int D, int DV, bool OB, bool HIST, bool NORM = false, bool GATED = false>
 hipError_t launch_t(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
     using G = Geo<D, DV, GATED>;
-    constexpr int kBytes = GATED ? G::BYTES_GATED : NORM ? G::BYTES_NORM : G::BYTES;
+    constexpr int kBytes = (OB && G::NCW == 2 && !HIST) ? G::BYTES_STAGED
+                           : GATED                    ? G::BYTES_GATED
+                           : NORM                     ? G::BYTES_NORM
+                                                      : G::BYTES;
     auto kern = delta_chunked_kernel<D, DV, OB, HIST, NORM, GATED>;
     // the dynamic-LDS limit is a per-device function attribute
     int dev = 0;

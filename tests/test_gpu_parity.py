@@ -324,6 +324,24 @@ def test_chunked_bf16_output_mode():
     np.testing.assert_array_equal(_np(o16.float()), _np(o32.to(torch.bfloat16).float()))
 
 
+@pytest.mark.parametrize("tile", [16, 32])
+def test_chunked_bf16_output_tiles_ragged_and_varlen(tile):
+    # 32-column tiles stage bf16 O in LDS and store whole rows from the loader wave;
+    # 16-column tiles store from the chain wave: both round the fp32 result once
+    _, (q, k, v, b, s0) = _bf16_case((2, 200, 2, 128), seed=18, s0_std=0.02)
+    with _path(2, tile):
+        o32, s32 = kernels.chunked_delta_rule(q, k, v, b, s0)
+        o16, s16 = kernels.chunked_delta_rule(q, k, v, b, s0, out_dtype=torch.bfloat16)
+    np.testing.assert_array_equal(_np(s16), _np(s32))
+    np.testing.assert_array_equal(_np(o16.float()), _np(o32.to(torch.bfloat16).float()))
+    _, (qv, kv, vv, bv), cu = _varlen_case(700, 2, 128, seed=19, lo=1, hi=300)
+    with _path(2, tile):
+        ov32, sv32 = kernels.chunked_delta_rule_varlen(qv, kv, vv, bv, cu)
+        ov16, sv16 = kernels.chunked_delta_rule_varlen(qv, kv, vv, bv, cu, out_dtype=torch.bfloat16)
+    np.testing.assert_array_equal(_np(sv16), _np(sv32))
+    np.testing.assert_array_equal(_np(ov16.float()), _np(ov32.to(torch.bfloat16).float()))
+
+
 def test_chunked_state_carry_is_bitwise_at_chunk_boundaries():
     _, (q, k, v, b, s0) = _bf16_case((2, 640, 2, 128), seed=9, s0_std=0.02)
     of, sf = kernels.chunked_delta_rule(q, k, v, b, s0)

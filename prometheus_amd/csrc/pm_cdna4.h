@@ -206,6 +206,12 @@ __device__ __forceinline__ void lds_barrier() {
 }
 // Wait for this wave's outstanding buffer loads (and so its LDS copies).
 __device__ __forceinline__ void wait_copies() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Cache-policy operand of the raw buffer intrinsics for a nontemporal (streaming)
+// access on gfx950 ("nt"), the form __builtin_nontemporal_store gives plain stores.
+// Outputs written once and not read back by the same kernel go out this way: at the
+// cfg1 forward the chunked kernel took 122 us with default-policy O stores and 96 us
+// with nontemporal ones.
+constexpr int kNT = 2;
 // Wait until at most N vector-memory operations of this wave are outstanding
 // (they complete in issue order).
 template <int N>

@@ -224,9 +224,11 @@ def main():
                          "executed_over_algorithmic": mc.get("executed_over_algorithmic")}
 
     def time_fwd(out_code, out_t, calls=20, ws=None):
-        q, k, v, beta = sets[0]
+        n = [0]
 
-        def f():
+        def f():  # the two input sets alternate, as in the headline loop
+            q, k, v, beta = sets[n[0] % 2]
+            n[0] += 1
             rc = lib.pm_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), None,
                                   out_t.data_ptr(), s.data_ptr(), B, T, H, D, _native.DTYPE_BF16,
                                   out_code, CHUNK, None if ws is None else ws.data_ptr(),
@@ -469,13 +471,14 @@ def main():
     # the same cfg1 forward with fp32 q/k/v (the reference's dtype): the per-token kernel
     fp32_fwd = None
     if args.model_calls > 0:
-        q, k, v, beta = (x.float() for x in sets[0])
+        fsets = [tuple(x.float() for x in st_) for st_ in sets]  # both input sets, alternating
         of = torch.empty((B, T, H, D), device=dev)
         sf = torch.empty((B, H, D, D), device=dev)
         nbf = lib.pm_delta_workspace_bytes(B, T, H, D, _native.DTYPE_F32)
         wsf = torch.empty(nbf, dtype=torch.uint8, device=dev) if nbf else None
 
-        def ffwd(ws):
+        def ffwd(ws, i=0):
+            q, k, v, beta = fsets[i % 2]
             rc = lib.pm_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), None,
                                   of.data_ptr(), sf.data_ptr(), B, T, H, D, _native.DTYPE_F32,
                                   _native.DTYPE_F32, CHUNK, None if ws is None else ws.data_ptr(),
@@ -484,7 +487,7 @@ def main():
 
         def time_ffwd(ws, calls):
             ffwd(ws)
-            return time_launches(stream, lambda i: ffwd(ws), calls)
+            return time_launches(stream, lambda i: ffwd(ws, i), calls)
 
         calls = args.model_calls * 5
         f_ms = time_ffwd(wsf, calls)  # the default: the fp32 chunked forward on fp32 MFMA
@@ -515,19 +518,19 @@ def main():
                              "frac": rflop / (r_ms * 1e-3) / 1e12 / FP32_VALU_PEAK_TFLOPS},
             },
         }
-        del q, k, v, beta, of, sf, wsf
+        del fsets, of, sf, wsf
 
     # the gated delta rule at cfg1 (pm_gated_delta_fwd): cfg1's inputs plus log-gates
     # -0.1 |N(0, 1)| per token and head, on the chunked kernel
     gated = None
     if args.gated_calls > 0:
-        q, k, v, beta = sets[0]
         g.manual_seed(8)
         gates = -0.1 * torch.randn((B, T, H), generator=g, device=dev).abs()
         og = torch.empty((B, T, H, D), device=dev)
         sg = torch.empty((B, H, D, D), device=dev)
 
-        def gfwd():
+        def gfwd(i=0):  # the two input sets alternate, as in the headline loop
+            q, k, v, beta = sets[i % 2]
             rc = lib.pm_gated_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
                                         gates.data_ptr(), None, og.data_ptr(), sg.data_ptr(), B, T, H,
                                         D, _native.DTYPE_BF16, _native.DTYPE_F32, stream.cuda_stream)
@@ -537,8 +540,8 @@ def main():
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for _ in range(args.gated_calls):
-            gfwd()
+        for i in range(args.gated_calls):
+            gfwd(i)
         e1.record(stream)
         torch.cuda.synchronize()
         g_ms = e0.elapsed_time(e1) / args.gated_calls

@@ -76,9 +76,8 @@ extern "C" {
  * parallel pass builds every chunk's T diag(beta), T = (I + A)^-1, into the
  * workspace and the chunk recurrence loads it instead of building it.  By
  * default (pm_delta_set_path(0)) that is the case for bf16 inputs at D in
- * {64, 128}, where the split form is the faster one, except when
- * pm_delta_set_tile(32) forces 32-column tiles on a grid that does not
- * fill the GPU (B*H*(D/32) < 256).  Without the workspace the
+ * {64, 128} when B*H*(D/32) < 256 (the chunked kernel's 16-column tiles),
+ * where the split form is the faster one.  Without the workspace the
  * single-stage chunked kernel runs, which needs none; the two agree within
  * the bf16 parity bound.  fp32 inputs at D in {64, 128} (16-byte aligned
  * q, k, v) run the chunked forward on fp32 MFMA, whose parallel pass writes

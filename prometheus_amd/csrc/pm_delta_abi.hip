@@ -112,14 +112,12 @@ int hip_fail(hipError_t e, const char* what) {
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// The split form of the chunked forward runs under path 3, and by default (path 0) except
-// where 32-column tiles are forced on fewer (b, h) pairs than fill the GPU.  Measured with
-// nontemporal O stores (µs, single-stage / split): cfg1 96-104 / 92-97, 16-column tiles
-// 5-28 % faster split, cfg3 with forced 32-column tiles 768 / 841.
+// The split form of the chunked forward runs under path 3, and by default (path 0) where
+// the chunked kernel takes 16-column tiles: fewer (b, h) pairs than fill the GPU with
+// 32-column tiles.  There its lighter memory traffic per CU wins (measured 5-25 % faster);
+// with 32-column tiles on every CU the single-stage kernel is faster.
 bool split_chosen(int path, int D, long n_pairs) {
-    if (path == 3) return true;
-    if (path != 0) return false;
-    return pm::chunked_pick_tile(D, n_pairs, g_tile) == 16 || n_pairs * (D / 32) >= 256;
+    return path == 3 || (path == 0 && pm::chunked_pick_tile(D, n_pairs, g_tile) == 16);
 }
 
 int check_dtypes(int in_dtype, int out_dtype) {

@@ -260,19 +260,18 @@ def test_abi_argument_validation_without_gpu():
     assert h(None, dummy, dummy, dummy, dummy, dummy, 2, 2, 8, 0, None) == _native.E_NULL
     assert h(dummy, dummy, dummy, dummy, dummy, dummy, 2, 2, 0, 0, None) == _native.E_SHAPE
     assert h(dummy, dummy, dummy, dummy, dummy, dummy, 2, 2, 8, 3, None) == _native.E_DTYPE
-    assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, 2) == 0  # no such dtype
+    assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, 1) == 0
 
 
 def test_forward_workspace_sizes_and_checks():
     """The split form's T workspace (6 KiB per (b, h) and chunk) is asked for exactly where
-    the forward would run that form: by default unless 32-column tiles are forced on a
-    grid that does not fill the GPU, always under path 3."""
+    the forward would run that form: 16-column tiles by default, always under path 3."""
     lib = _native.lib()
     bf16, f32 = _native.DTYPE_BF16, _native.DTYPE_F32
     per = 6 * 1024
     assert lib.pm_delta_workspace_bytes(1, 32768, 32, 128, bf16) == 32 * 512 * per  # cfg3: 16-col tiles
     assert lib.pm_delta_workspace_bytes(1, 130, 2, 64, bf16) == 2 * 3 * per
-    assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, bf16) == 64 * 64 * per  # cfg1: 32-col tiles
+    assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, bf16) == 0  # cfg1: 32-col tiles
     assert lib.pm_delta_workspace_bytes(1, 4096, 16, 256, bf16) == 0
     # fp32 q/k/v at D in {64, 128}: the fp32 chunked forward's 2 KiB per (b, h) and 16-token chunk
     assert lib.pm_delta_workspace_bytes(1, 4096, 16, 128, f32) == 16 * 256 * 1024
@@ -281,7 +280,7 @@ def test_forward_workspace_sizes_and_checks():
     assert lib.pm_delta_varlen_workspace_bytes(3, 100, 2, 128, f32) == 2 * (7 + 3) * 1024
     # varlen: H x (ceil(total / 64) + n_seqs) slots
     assert lib.pm_delta_varlen_workspace_bytes(3, 1000, 4, 128, bf16) == 4 * (16 + 3) * per
-    assert lib.pm_delta_varlen_workspace_bytes(8, 16384, 16, 128, bf16) == 16 * (256 + 8) * per  # cfg2
+    assert lib.pm_delta_varlen_workspace_bytes(8, 16384, 16, 128, bf16) == 0  # cfg2: 32-col tiles
     old = _native.set_path(3)
     try:
         assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, bf16) == 64 * 64 * per
@@ -312,8 +311,7 @@ def test_forward_workspace_sizes_and_checks():
         _native.set_path(old)
     old = _native.set_tile(32)
     try:
-        assert lib.pm_delta_workspace_bytes(1, 32768, 32, 128, bf16) == 0  # 128 workgroups
-        assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, bf16) == 64 * 64 * per
+        assert lib.pm_delta_workspace_bytes(1, 32768, 32, 128, bf16) == 0
     finally:
         _native.set_tile(old)
 

@@ -431,8 +431,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
         }
         for (int idx = tid; idx < nst * NC; idx += NT) {
             const int j = idx / NC, c = idx % NC;
-            if (col0 + c < D)
-                __builtin_nontemporal_store(sov[idx], gv + (static_cast<size_t>(tok0 + lo + j) * H + h) * D + col0 + c);
+            if (col0 + c < D) gv[(static_cast<size_t>(tok0 + lo + j) * H + h) * D + col0 + c] = sov[idx];
         }
         for (int j = wave; j < nst; j += NWV) {
             float sum = 0.f;

@@ -535,7 +535,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int i = 0; i < kC * ORB / 1024; ++i) {
             const int r = i * (1024 / ORB) + lane / OUPR, p = lane % OUPR;
             const u32x4_t x = *reinterpret_cast<const u32x4_t*>(ob + r * ORB + 16 * (p ^ ostg_f(r)));
-            __builtin_amdgcn_raw_buffer_store_b128(x, ro, static_cast<unsigned>(r * tstride * 2 + 16 * p), 0, kNT);
+            __builtin_amdgcn_raw_buffer_store_b128(x, ro, static_cast<unsigned>(r * tstride * 2 + 16 * p), 0, 0);
         }
     };
 
@@ -669,9 +669,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 const size_t a = (tok0 + base + t) * tstride + static_cast<size_t>(h) * D + ocol;
                 if constexpr (OUT_BF16) {
                     const u32x2_t ob = {pack_rne(O[m].x, O[m].y), pack_rne(O[m].z, O[m].w)};
-                    __builtin_nontemporal_store(ob, reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(o_out) + a));
+                    *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(o_out) + a) = ob;
                 } else {
-                    __builtin_nontemporal_store(O[m], reinterpret_cast<f32x4_t*>(static_cast<float*>(o_out) + a));
+                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(o_out) + a) = O[m];
                 }
             }
         }

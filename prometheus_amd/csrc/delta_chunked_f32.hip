@@ -486,9 +486,9 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
                 for (int e = 0; e < 4; ++e) {
                     const unsigned off = static_cast<unsigned>(((4 * g + e) * tstride + r) * ES);
                     if constexpr (OUT_BF16)
-                        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(O[e]), ro, off, 0, kNT);
+                        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(O[e]), ro, off, 0, 0);
                     else
-                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(O[e]), ro, off, 0, kNT);
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(O[e]), ro, off, 0, 0);
                 }
             }
             if (i < n_chunks) {

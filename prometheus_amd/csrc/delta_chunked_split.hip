@@ -510,9 +510,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     const unsigned off = static_cast<unsigned>(((16 * m + l16) * tstride + 16 * cw + 4 * lg) * ES);
                     if constexpr (OUT_BF16) {
                         const u32x2_t ob = {pack_rne(O[m].x, O[m].y), pack_rne(O[m].z, O[m].w)};
-                        __builtin_amdgcn_raw_buffer_store_b64(ob, ro, off, 0, kNT);
+                        __builtin_amdgcn_raw_buffer_store_b64(ob, ro, off, 0, 0);
                     } else {
-                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, O[m]), ro, off, 0, kNT);
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, O[m]), ro, off, 0, 0);
                     }
                 }
             }

@@ -229,7 +229,7 @@ __global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
         for (int s = 0; s < NPV; ++s) {
             const int idx = s * NT + tid;
             const int j = idx / CW, e2 = c * CW + idx % CW;
-            if (j < nst && e2 < D) __builtin_nontemporal_store(from_f32<OutT>(so[idx]), o + row(t0 + j) + e2);
+            if (j < nst && e2 < D) o[row(t0 + j) + e2] = from_f32<OutT>(so[idx]);
         }
     };
 

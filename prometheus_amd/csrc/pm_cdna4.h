@@ -206,13 +206,6 @@ __device__ __forceinline__ void lds_barrier() {
 }
 // Wait for this wave's outstanding buffer loads (and so its LDS copies).
 __device__ __forceinline__ void wait_copies() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-// Cache-policy operand of the raw buffer intrinsics for a nontemporal (streaming)
-// access on gfx950 ("nt"), the form __builtin_nontemporal_store gives plain stores.
-// The forward kernels' outputs (written once, not read back) go out this way, so that
-// they do not evict inputs from the last-level cache: at the cfg1 forward, with the same
-// q/k/v on every call, the chunked kernel took 96 us instead of 121; with fresh inputs
-// on every call (nothing to keep) it is 117-119 us either way.
-constexpr int kNT = 2;
 // Wait until at most N vector-memory operations of this wave are outstanding
 // (they complete in issue order).
 template <int N>

@@ -19,7 +19,7 @@
 // its start state S and end gradient G are known.  Four launches:
 //   1. the forward kernel in its state-history mode writes every chunk's S
 //      (bf16, as rows of S^T);
-//   2. bwd_prep_kernel, one wave per chunk: T (the forward's builder), and
+//   2. bwd_prep_kernel, one workgroup per chunk: T (the forward's builder), and
 //      T^T and P^T, in packed MFMA operand order;
 //   3. bwd_rev_kernel walks the chunks backwards per (b, h, 32 columns of
 //      d_v) carrying G in fp32 MFMA accumulators (the columns of G are
@@ -139,7 +139,7 @@ __device__ __forceinline__ void copy_flat(__amdgpu_buffer_rsrc_t rs, unsigned ch
 }
 
 // ---------------------------------------------------------------------------
-// 2. prep: packed T, T^T and P^T of one chunk (one wave)
+// 2. prep: packed T, T^T and P^T of one chunk (one workgroup of four waves)
 // ---------------------------------------------------------------------------
 template <int D>
 struct PrepGeo {
@@ -150,42 +150,81 @@ struct PrepGeo {
     static constexpr int BYTES = TP + kPacked * 2;
 };
 
+// The four waves copy K, Q and beta; then wave 0 builds T (K1's builder) while waves
+// 1-3 form the P^T blocks; after a barrier all four gather T^T from the packed T.
+// (One wave per chunk, four chunks per CU by LDS, took 45 us at cfg1.)
 template <int D>
-__global__ __launch_bounds__(64) void bwd_prep_kernel(const uint16_t* __restrict__ q,
-                                                      const uint16_t* __restrict__ k,
-                                                      const float* __restrict__ beta,
-                                                      uint16_t* __restrict__ tp_ws, int T, int H,
-                                                      int n_ch) {
+__global__ __launch_bounds__(256) void bwd_prep_kernel(const uint16_t* __restrict__ q,
+                                                       const uint16_t* __restrict__ k,
+                                                       const float* __restrict__ beta,
+                                                       uint16_t* __restrict__ tp_ws, int T, int H,
+                                                       int n_ch) {
     using G = PrepGeo<D>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int pair = blockIdx.x / n_ch, c = blockIdx.x % n_ch;
     const int seq = pair / H, h = pair % H;
-    const int lane = threadIdx.x, l16 = lane & 15, lg = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = static_cast<int>(uniform(static_cast<unsigned>(tid >> 6)));
+    const int l16 = lane & 15, lg = lane >> 4;
     const int base = c * kC, clen = min(kC, T - base);
     const size_t tstride = static_cast<size_t>(H) * D;
     const size_t row0 = (static_cast<size_t>(seq) * T + base) * tstride + static_cast<size_t>(h) * D;
     const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
     const unsigned n_b = static_cast<unsigned>(((clen - 1) * H + 1) * 4);
     copy_rows<D>(make_rsrc(k + row0, n_kq), smem + G::KS, kC * D * 2 / 1024,
-                 static_cast<unsigned>(tstride * 2), 0, 1, lane);
+                 static_cast<unsigned>(tstride * 2), w, 4, lane);
     copy_rows<D>(make_rsrc(q + row0, n_kq), smem + G::QS, kC * D * 2 / 1024,
-                 static_cast<unsigned>(tstride * 2), 0, 1, lane);
-    copy_to_lds(make_rsrc(beta + (static_cast<size_t>(seq) * T + base) * H + h, n_b), smem + G::BS, 4,
-                static_cast<unsigned>(lane * H * 4));
+                 static_cast<unsigned>(tstride * 2), w, 4, lane);
+    if (w == 3)
+        copy_to_lds(make_rsrc(beta + (static_cast<size_t>(seq) * T + base) * H + h, n_b), smem + G::BS, 4,
+                    static_cast<unsigned>(lane * H * 4));
     wait_copies();
     __syncthreads();
 
     uint16_t* Tp = reinterpret_cast<uint16_t*>(smem + G::TP);
-    build_t_packed<D, G::KS, G::BS>(smem, Tp, lane);
-    __syncthreads();
-
     uint16_t* out = tp_ws + (static_cast<size_t>(pair) * n_ch + c) * 3 * kPacked;
-    // packed T as built
+    if (w == 0) {
+        build_t_packed<D, G::KS, G::BS>(smem, Tp, lane);
+        // packed T as built (a wave's LDS accesses complete in order)
 #pragma unroll
-    for (int x = 0; x < 6; ++x)
-        *reinterpret_cast<u32x4_t*>(out + x * 512 + lane * 8) =
-            *reinterpret_cast<const u32x4_t*>(Tp + x * 512 + lane * 8);
-    // packed T^T: lane (g, l16), slot x of block (m, kb) = T[32kb + o(g, x)][16m + l16]
+        for (int x = 0; x < 6; ++x)
+            *reinterpret_cast<u32x4_t*>(out + x * 512 + lane * 8) =
+                *reinterpret_cast<const u32x4_t*>(Tp + x * 512 + lane * 8);
+    } else {
+        // packed P^T: the accumulator tile of Q_j K_i^T (lane: P[16j + 4g + r][16i + l16])
+        // is block (i, j) of P^T in the form the packed store takes; the ten blocks i <= j,
+        // numbered row by row, go to waves 1-3 by number mod 3
+        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(smem + G::KS);
+        const uint16_t* Qs = reinterpret_cast<const uint16_t*>(smem + G::QS);
+        uint16_t* pt = out + 2 * kPacked;
+        const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+        int idx = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int j = i; j < 4; ++j, ++idx) {
+                if (idx % 3 != w - 1) continue;
+                f32x4_t acc = zero;
+#pragma unroll
+                for (int kb = 0; kb < D / 32; ++kb)
+                    acc = mfma32(lds_op_kq<D>(Qs, 16 * j + l16, kb, lg), lds_op_kq<D>(Ks, 16 * i + l16, kb, lg), acc);
+                if (i == j) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[r] = (4 * lg + r >= l16) ? acc[r] : 0.f;
+                }
+                *reinterpret_cast<u32x2_t*>(pt + qblk_u(i, j >> 1) * 512 + lane * 8 + 4 * (j & 1)) = cvt4(acc);
+            }
+        }
+        if (w == 1) {
+            const u32x2_t z2 = {0u, 0u};
+            *reinterpret_cast<u32x2_t*>(pt + qblk_u(1, 0) * 512 + lane * 8) = z2;  // t < 16 <= s
+            *reinterpret_cast<u32x2_t*>(pt + qblk_u(3, 1) * 512 + lane * 8) = z2;  // t < 48 <= s
+        }
+    }
+    __syncthreads();  // the packed T is in LDS
+
+    // packed T^T: lane (g, l16), slot x of block (m, kb) = T[32kb + o(g, x)][16m + l16];
+    // wave w takes blocks w and w + 4
     auto t_at = [&](int i, int kk) -> uint16_t {  // T[i][kk] from the packed T (0 above the diagonal)
         if (kk > i) return 0;
         const int gg = (kk & 15) >> 2, x = (kk & 3) + 4 * ((kk >> 4) & 1);
@@ -194,6 +233,7 @@ __global__ __launch_bounds__(64) void bwd_prep_kernel(const uint16_t* __restrict
     const int mk[6][2] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}, {2, 1}, {3, 1}};
 #pragma unroll
     for (int b = 0; b < 6; ++b) {
+        if ((b & 3) != w) continue;
         const int m = mk[b][0], kb = mk[b][1];
         const int s = 16 * m + l16;
         unsigned wds[4];
@@ -205,30 +245,6 @@ __global__ __launch_bounds__(64) void bwd_prep_kernel(const uint16_t* __restrict
         const u32x4_t v = {wds[0], wds[1], wds[2], wds[3]};
         *reinterpret_cast<u32x4_t*>(out + kPacked + qblk_u(m, kb) * 512 + lane * 8) = v;
     }
-    // packed P^T: the accumulator tile of Q_j K_i^T (lane: P[16j + 4g + r][16i + l16])
-    // is block (i, j) of P^T in the form the packed store takes
-    const uint16_t* Ks = reinterpret_cast<const uint16_t*>(smem + G::KS);
-    const uint16_t* Qs = reinterpret_cast<const uint16_t*>(smem + G::QS);
-    uint16_t* pt = out + 2 * kPacked;
-    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = i; j < 4; ++j) {
-            f32x4_t acc = zero;
-#pragma unroll
-            for (int kb = 0; kb < D / 32; ++kb)
-                acc = mfma32(lds_op_kq<D>(Qs, 16 * j + l16, kb, lg), lds_op_kq<D>(Ks, 16 * i + l16, kb, lg), acc);
-            if (i == j) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[r] = (4 * lg + r >= l16) ? acc[r] : 0.f;
-            }
-            *reinterpret_cast<u32x2_t*>(pt + qblk_u(i, j >> 1) * 512 + lane * 8 + 4 * (j & 1)) = cvt4(acc);
-        }
-    }
-    const u32x2_t z2 = {0u, 0u};
-    *reinterpret_cast<u32x2_t*>(pt + qblk_u(1, 0) * 512 + lane * 8) = z2;  // t < 16 <= s
-    *reinterpret_cast<u32x2_t*>(pt + qblk_u(3, 1) * 512 + lane * 8) = z2;  // t < 48 <= s
 }
 
 // ---------------------------------------------------------------------------
@@ -989,7 +1005,7 @@ hipError_t launch_d(const BwdArgs& a, hipStream_t st) {
         ChunkedArgs f{q, k, v, a.beta, a.s0, nullptr, nullptr, nullptr, a.n_pairs / a.H, a.T, a.H, D, false, 0};
         if ((e = launch_chunked_states(f, s_hist, st)) != hipSuccess) return e;
         if ((e = set_lds(bwd_prep_kernel<D>, PrepGeo<D>::BYTES)) != hipSuccess) return e;
-        hipLaunchKernelGGL(bwd_prep_kernel<D>, dim3(static_cast<unsigned>(a.n_pairs) * n_ch), dim3(64),
+        hipLaunchKernelGGL(bwd_prep_kernel<D>, dim3(static_cast<unsigned>(a.n_pairs) * n_ch), dim3(256),
                            PrepGeo<D>::BYTES, st, q, k, a.beta, tp, a.T, a.H, n_ch);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }

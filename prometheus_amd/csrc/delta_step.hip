@@ -6,7 +6,8 @@
 // in once and out once with 128-bit non-temporal accesses and every column
 // of S stays in VGPRs between the two reductions (k^T S, then q^T S').
 //
-// Mapping (D=128): one 256-thread workgroup per (b, h).  Thread t owns
+// Mapping (D=128): one 256-thread workgroup per (b, h), on a (H, B) grid so that no
+// division is needed to find b.  Thread t owns
 // columns 4*(t % 32) .. +3 and rows (t / 32) + 8*i, i < 16, so each wave
 // instruction reads or writes two whole 512-byte rows (1 KiB contiguous).
 // Column partial sums are reduced across the row groups of a wave with
@@ -34,7 +35,7 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
                                                          const float* __restrict__ beta,
                                                          float* __restrict__ o,
                                                          const int32_t* __restrict__ slots,
-                                                         int H, int n_slots,
+                                                         int b0, int n_slots,
                                                          const float* __restrict__ gate) {
     constexpr int NT = 256;
     constexpr int CG = D / 4;      // column groups of 4
@@ -46,14 +47,24 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
     __shared__ float sk[D], sq[D], sv[D];
     __shared__ f32x4 red[2][NW][CG];
 
-    const int pair = blockIdx.x;
+    const int H = static_cast<int>(gridDim.x), bi = b0 + static_cast<int>(blockIdx.y);
+    const int pair = bi * H + static_cast<int>(blockIdx.x);
     const int t = threadIdx.x;
     const int cg = t % CG, rg = t / CG;
     const int lane = t & 63, w = t >> 6;
 
+    // the token's q, k, v and beta do not depend on the slot: their loads go out first
+    InT kq = InT(), qq = InT(), vq = InT();
+    if (t < D) {
+        const size_t a = static_cast<size_t>(pair) * D + t;
+        kq = k[a];
+        qq = q[a];
+        vq = v[a];
+    }
+    const float b = beta[pair];
     size_t state = pair;
     if (slots) {
-        const int slot = slots[pair / H];
+        const int slot = slots[bi];
         if (slot < 0 || slot >= n_slots) {
             if (t < CG) {
                 const f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -61,7 +72,7 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
             }
             return;
         }
-        state = static_cast<size_t>(slot) * H + pair % H;
+        state = static_cast<size_t>(slot) * H + blockIdx.x;
     }
     f32x4* sp = reinterpret_cast<f32x4*>(s + state * D * D);
     f32x4 S[RPT];
@@ -70,12 +81,10 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
         S[i] = __builtin_nontemporal_load(sp + (rg + RG * i) * CG + cg);
 
     if (t < D) {
-        const size_t a = static_cast<size_t>(pair) * D + t;
-        sk[t] = to_f32(k[a]);
-        sq[t] = to_f32(q[a]);
-        sv[t] = to_f32(v[a]);
+        sk[t] = to_f32(kq);
+        sq[t] = to_f32(qq);
+        sv[t] = to_f32(vq);
     }
-    const float b = beta[pair];
     __syncthreads();
 
     f32x4 kp = {0.f, 0.f, 0.f, 0.f};
@@ -128,16 +137,23 @@ bool step_supported(int D) { return D == 32 || D == 64 || D == 128; }
 
 template <int D, bool GATED>
 static hipError_t launch_step_g(const StepArgs& a, hipStream_t st) {
-    if (a.in_bf16) {
-        hipLaunchKernelGGL((delta_step_kernel<D, uint16_t, GATED>), dim3(a.n_pairs), dim3(256), 0, st,
-                           a.s, static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.k),
-                           static_cast<const uint16_t*>(a.v), a.beta, a.o, a.slots, a.H, a.n_slots, a.g);
-    } else {
-        hipLaunchKernelGGL((delta_step_kernel<D, float, GATED>), dim3(a.n_pairs), dim3(256), 0, st, a.s,
-                           static_cast<const float*>(a.q), static_cast<const float*>(a.k),
-                           static_cast<const float*>(a.v), a.beta, a.o, a.slots, a.H, a.n_slots, a.g);
+    // grid (H, rows of b), at most 65535 rows per launch
+    const int n_b = a.n_pairs / a.H;
+    for (int b0 = 0; b0 < n_b; b0 += 65535) {
+        const dim3 grid(static_cast<unsigned>(a.H), static_cast<unsigned>(min(65535, n_b - b0)));
+        if (a.in_bf16) {
+            hipLaunchKernelGGL((delta_step_kernel<D, uint16_t, GATED>), grid, dim3(256), 0, st, a.s,
+                               static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.k),
+                               static_cast<const uint16_t*>(a.v), a.beta, a.o, a.slots, b0, a.n_slots, a.g);
+        } else {
+            hipLaunchKernelGGL((delta_step_kernel<D, float, GATED>), grid, dim3(256), 0, st, a.s,
+                               static_cast<const float*>(a.q), static_cast<const float*>(a.k),
+                               static_cast<const float*>(a.v), a.beta, a.o, a.slots, b0, a.n_slots, a.g);
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 template <int D>

@@ -228,6 +228,7 @@ int step(float* s_inout, const void* q, const void* k, const void* v, const floa
     if (pm::step_supported(D) && aligned(s_inout, 16) && aligned(o, 16)) {
         pm::StepArgs a{s_inout, q, k, v, beta, o, static_cast<int>(n_pairs), D,
                        in_dtype == PM_DTYPE_BF16};
+        a.H = H;
         a.g = g;
         hipError_t e = pm::launch_step(a, st);
         return e == hipSuccess ? 0 : hip_fail(e, "decode step launch");

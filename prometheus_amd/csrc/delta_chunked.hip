@@ -88,10 +88,16 @@ struct Geo {
     static constexpr int OB = BYTES_GATED;
     static constexpr int OB_BYTES = kC * DV * 2;
     static constexpr int BYTES_STAGED = OB + 2 * OB_BYTES;
+    // HIST (the backward's state history): chunk buffers without Q, six of them (two
+    // chunks in each of three pipeline stages), then four 6 KiB T slots
+    static constexpr int H_VS = kC * D * 2;
+    static constexpr int H_BS = H_VS + kC * DV * 2;
+    static constexpr int RAWH = H_BS + kC * 4;
+    static constexpr int BYTES_HIST = 6 * RAWH + 4 * 6 * 1024;
     static_assert(D == 64 || D == 128, "D");
     static_assert(DV == 16 || DV == 32, "DV");
     static_assert(NI_V >= 1 && RAW % 16 == 0, "RAW layout");
-    static_assert(BYTES_STAGED <= 160 * 1024, "LDS budget");
+    static_assert(BYTES_STAGED <= 160 * 1024 && BYTES_HIST <= 160 * 1024, "LDS budget");
 };
 
 // HIST: the backward's state recompute.  Instead of O and the final state,
@@ -163,9 +169,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const size_t sbase = static_cast<size_t>(pair) * D * D;
     const size_t tstride = static_cast<size_t>(H) * D;  // elements between tokens
 
-    auto raw = [&](int c) { return smem + (c % G::NRAW) * G::RAW; };
+    // chunk buffers and their fields; HIST has its own (no Q, two chunks per stage)
+    constexpr int R_KS = HIST ? 0 : G::R_KS;
+    constexpr int R_VS = HIST ? G::H_VS : G::R_VS;
+    constexpr int R_BS = HIST ? G::H_BS : G::R_BS;
+    auto raw = [&](int c) { return HIST ? smem + (c % 6) * G::RAWH : smem + (c % G::NRAW) * G::RAW; };
     auto tpb = [&](int c) {
-        return reinterpret_cast<uint16_t*>(smem + G::NRAW * G::RAW + (c & 1) * G::TP);
+        return reinterpret_cast<uint16_t*>(HIST ? smem + 6 * G::RAWH + (c & 3) * 6 * 1024
+                                                : smem + G::NRAW * G::RAW + (c & 1) * G::TP);
     };
     auto rnb = [&](int c) { return reinterpret_cast<float*>(smem + G::RN + (c & 1) * 512); };
     // GATED: producer pw's scanned gates, written and read back by that wave only
@@ -174,7 +185,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // ---------------- loader: chunk c's K, Q, V tile and beta, HBM -> LDS ----------------
     // Copy instruction i, lane L fills LDS bytes [1024 i + 16 L, +16) of the tile: row r,
     // stored chunk p, i.e. logical chunk p ^ f(r) of token row r.
-    auto issue_copies = [&](int c) {
+    auto issue_copies = [&](int c) __attribute__((always_inline)) {
         const int base = c * kC;
         const int clen = min(kC, len - base);
         const size_t row0 = static_cast<size_t>(tok0 + base) * tstride + static_cast<size_t>(h) * D;
@@ -192,7 +203,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const int pos = 512 * i + 8 * lane;  // element position in the tile
             const int r = pos / D, p = (pos % D) / 8;
             const unsigned vo = static_cast<unsigned>(r * tstride * 2) + 16u * (p ^ kq_f<D>(r));
-            copy_to_lds(rk, rbuf + G::R_KS + 1024 * i, 16, vo);
+            copy_to_lds(rk, rbuf + R_KS + 1024 * i, 16, vo);
             if constexpr (!HIST) copy_to_lds(rq, rbuf + G::R_QS + 1024 * i, 16, vo);  // HIST: no O
         }
 #pragma unroll
@@ -200,9 +211,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const int pos = 512 * i + 8 * lane;
             const int r = pos / DV, p = (pos % DV) / 8;
             const unsigned vo = static_cast<unsigned>(r * tstride * 2) + 16u * (p ^ v_f<DV>(r));
-            copy_to_lds(rv, rbuf + G::R_VS + 1024 * i, 16, vo);
+            copy_to_lds(rv, rbuf + R_VS + 1024 * i, 16, vo);
         }
-        if constexpr (!NORM) copy_to_lds(rb, rbuf + G::R_BS, 4, static_cast<unsigned>(lane * H * 4));
+        if constexpr (!NORM) copy_to_lds(rb, rbuf + R_BS, 4, static_cast<unsigned>(lane * H * 4));
         if constexpr (GATED)
             copy_to_lds(make_rsrc(gate + (tok0 + base) * H + h, n_b), rbuf + G::R_GS, 4,
                         static_cast<unsigned>(lane * H * 4));
@@ -228,8 +239,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // ---------------- producer 0: T = (I + A)^-1 in packed operand order ----------------
     auto build_t = [&](int c) {
         unsigned char* rb = raw(c);
-        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + G::R_KS);
-        const float* Bs = reinterpret_cast<const float*>(rb + G::R_BS);
+        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + R_KS);
+        const float* Bs = reinterpret_cast<const float*>(rb + R_BS);
         uint16_t* Tp = tpb(c);
         const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
         // G = K K^T: diagonal tiles gd[b] and upper tiles gu(k, i), k < i
@@ -541,10 +552,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     auto run_chunk = [&](int c) {
         unsigned char* rb = raw(c);
-        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + G::R_KS);
-        const uint16_t* Qs = reinterpret_cast<const uint16_t*>(rb + G::R_QS);
-        const uint16_t* Vs = reinterpret_cast<const uint16_t*>(rb + G::R_VS);
-        const float* Bs = reinterpret_cast<const float*>(rb + G::R_BS);
+        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + R_KS);
+        const uint16_t* Qs = reinterpret_cast<const uint16_t*>(rb + G::R_QS);  // (not in HIST)
+        const uint16_t* Vs = reinterpret_cast<const uint16_t*>(rb + R_VS);
+        const float* Bs = reinterpret_cast<const float*>(rb + R_BS);
         const uint16_t* Tp = tpb(c);
         const uint16_t* Pp = Tp + 6 * 512;
         const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
@@ -683,7 +694,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // chain runs chunk i-1 from RAW[(i-1)%3] and TP[(i-1)%2].  Barrier i+1
     // publishes all three, and frees RAW[(i-1)%3] and TP[(i-1)%2] for reuse.
     // Every role passes the same n_chunks + 1 barriers (+ 1 when bf16 O is staged).
-    if (n_chunks > 0) {
+    if (HIST && n_chunks > 0) {
+        // HIST builds no P, and the T build is the longest role: two chunks per barrier,
+        // producers 0 and 1 each building one of a pair's T while the loader copies the
+        // next pair and the chain runs the previous one (six chunk buffers, four T slots).
+        const int n_pr = (n_chunks + 1) / 2;
+        if (chain) {
+            lds_barrier();  // pair 0 copied
+            lds_barrier();  // pair 0's T built
+            for (int c = 0; c < n_chunks; ++c) {  // (one call site, so that it stays inline)
+                run_chunk(c);
+                if ((c & 1) && c + 1 < n_chunks) lds_barrier();  // after each pair but the last
+            }
+        } else {
+            const bool loader = pw == G::LOADER;
+            auto copy_pair = [&](int j) __attribute__((always_inline)) {
+                issue_copies(2 * j);
+                if (2 * j + 1 < n_chunks) issue_copies(2 * j + 1);
+            };
+            if (loader) {
+                copy_pair(0);
+                wait_copies();
+            }
+            lds_barrier();
+            for (int j = 0; j < n_pr; ++j) {
+                if (loader && j + 1 < n_pr) copy_pair(j + 1);
+                if (pw < 2 && 2 * j + pw < n_chunks) build_t(2 * j + pw);
+                if (loader) wait_copies();
+                lds_barrier();
+            }
+        }
+    } else if (n_chunks > 0) {
         if (chain) {
             lds_barrier();  // chunk 0 copied
             lds_barrier();  // chunk 0's T and P built
@@ -733,7 +774,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 template <int D, int DV, bool OB, bool HIST, bool NORM = false, bool GATED = false>
 hipError_t launch_t(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
     using G = Geo<D, DV, GATED>;
-    constexpr int kBytes = (OB && G::NCW == 2 && !HIST) ? G::BYTES_STAGED
+    constexpr int kBytes = HIST                       ? G::BYTES_HIST
+                           : (OB && G::NCW == 2)      ? G::BYTES_STAGED
                            : GATED                    ? G::BYTES_GATED
                            : NORM                     ? G::BYTES_NORM
                                                       : G::BYTES;

@@ -363,6 +363,11 @@ def test_state_cache_bookkeeping_without_gpu():
         cache.free([3])  # never allocated
     with pytest.raises(ValueError):
         cache.reset([4])  # outside the pool
+    # the lowest free slots come first, whatever the order they were freed in
+    big = serving.LinearStateCache(1, 8, 1, 8, device="cpu")
+    assert big.alloc(6) == [0, 1, 2, 3, 4, 5]
+    big.free([4, 1, 3])
+    assert big.alloc(2) == [1, 3] and big.alloc(2) == [4, 6]
     with pytest.raises(RuntimeError):  # computing needs the GPU: no host fallback
         cache.decode(0, None, None, None, None, None)
 

@@ -679,6 +679,23 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         copy_qg(cur);
 
         // ---- phase 1: R' = V - K S and U = T diag(beta) R' for this wave's columns ----
+        // The lower 16x16 tiles (m, st), m >= st, numbered 0..9 row by row, go to waves by
+        // number mod 4 (wave w takes tiles w, w + 4, w + 8): KK = K K^T here in phase 1, from
+        // the K operands X = K S reads anyway; dP = dO U^T and dA = -W U^T in phase 2.
+        constexpr int kTiles = 3;
+        auto tile_m = [](int idx) { return idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0; };
+        auto tile_s = [&](int idx) { const int m = tile_m(idx); return idx - m * (m + 1) / 2; };
+        const int nt = w < 2 ? 3 : 2;
+        int tm[kTiles], ts[kTiles];
+#pragma unroll
+        for (int x = 0; x < kTiles; ++x) {
+            const int idx = min(w + 4 * x, 9);
+            tm[x] = tile_m(idx);
+            ts[x] = tile_s(idx);
+        }
+        f32x4_t KK[kTiles];
+#pragma unroll
+        for (int x = 0; x < kTiles; ++x) KK[x] = zero;
         f32x4_t U[4][JW];
         {
             f32x4_t X[4][JW];
@@ -697,6 +714,19 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
                 for (int m = 0; m < 4; ++m)
 #pragma unroll
                     for (int jj = 0; jj < JW; ++jj) X[m][jj] = mfma32(fk[m], fs[jj], X[m][jj]);
+#pragma unroll
+                for (int x = 0; x < kTiles; ++x) {
+                    if (x < nt) {
+                        // rows tm[x] and ts[x] of K without dynamic register indexing
+                        bf16x8_t ka = fk[0], kc = fk[0];
+#pragma unroll
+                        for (int m = 1; m < 4; ++m) {
+                            if (tm[x] == m) ka = fk[m];
+                            if (ts[x] == m) kc = fk[m];
+                        }
+                        KK[x] = mfma32(ka, kc, KK[x]);
+                    }
+                }
             }
             f32x4_t dbp[4];
 #pragma unroll
@@ -743,9 +773,8 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         __syncthreads();
 
         // ---- phase 2: products contracting over the d_v index j ----
-        // dQ1 = dO S^T, dKa = U G^T, dKb = W S^T for this wave's d tiles; the lower
-        // 16x16 tiles (m, st), m >= st, numbered 0..9 row by row, go to waves by number mod 4:
-        // dP = dO U^T, dA = -W U^T, KK = K K^T.
+        // dQ1 = dO S^T, dKa = U G^T, dKb = W S^T for this wave's d tiles; dP = dO U^T and
+        // dA = -W U^T for its lower tiles.
         f32x4_t dQ[4][JW], dKa[4][JW], dKb[4][JW];
 #pragma unroll
         for (int m = 0; m < 4; ++m)
@@ -755,20 +784,9 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
                 dKa[m][dd] = zero;
                 dKb[m][dd] = zero;
             }
-        constexpr int kTiles = 3;  // wave w takes lower tiles w, w + 4, w + 8
-        auto tile_m = [](int idx) { return idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0; };
-        auto tile_s = [&](int idx) { const int m = tile_m(idx); return idx - m * (m + 1) / 2; };
-        const int nt = w < 2 ? 3 : 2;
-        int tm[kTiles], ts[kTiles];
+        f32x4_t dP[kTiles], dA[kTiles];
 #pragma unroll
-        for (int x = 0; x < kTiles; ++x) {
-            const int idx = min(w + 4 * x, 9);
-            tm[x] = tile_m(idx);
-            ts[x] = tile_s(idx);
-        }
-        f32x4_t dP[kTiles], dA[kTiles], KK[kTiles];
-#pragma unroll
-        for (int x = 0; x < kTiles; ++x) dP[x] = dA[x] = KK[x] = zero;
+        for (int x = 0; x < kTiles; ++x) dP[x] = dA[x] = zero;
 #pragma unroll
         for (int kb = 0; kb < D / 32; ++kb) {
             u32x4_t fu[4], fw[4];
@@ -823,14 +841,6 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
                     dP[x] = mfma32(ado, as_b(bu), dP[x]);
                     dA[x] = mfma32(as_b(aw), as_b(bu), dA[x]);
                 }
-            }
-        }
-#pragma unroll
-        for (int x = 0; x < kTiles; ++x) {
-            if (x < nt) {
-#pragma unroll
-                for (int kb = 0; kb < D / 32; ++kb)
-                    KK[x] = mfma32(lds_op_kq<D>(Ks, 16 * tm[x] + l16, kb, lg), lds_op_kq<D>(Ks, 16 * ts[x] + l16, kb, lg), KK[x]);
             }
         }
         // masks, dbeta second term, beta dA

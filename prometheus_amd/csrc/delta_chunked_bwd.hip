@@ -429,7 +429,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const uint16_t* PTp = reinterpret_cast<const uint16_t*>(b + G::PT);
         const float* Bs = reinterpret_cast<const float*>(b + G::BS);
         const float* Ds = reinterpret_cast<const float*>(b + G::DO);
-        const int base = c * kC, clen = min(kC, T - base);
         // G_c, the gradient of the state at the end of chunk c, in packed order (Gb[kb] holds
         // G[32kb + 8g .. +8][j], j in column tile jt)
         {

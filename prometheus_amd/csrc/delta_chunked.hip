@@ -561,12 +561,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
         const int base = c * kC;
         const int clen = min(kC, len - base);
+        // HIST: the state at the chunk's start, rounded to bf16 here, goes out once the
+        // state update below is issued (stores issued here, among the loader's copies of
+        // the next pair, stall the chain longer)
+        u32x2_t hv[HIST ? D / 16 : 1] = {};
         if constexpr (HIST) {
-            uint16_t* hp = s_hist + (static_cast<size_t>(pair) * n_chunks + c) * D * D +
-                           static_cast<size_t>(ecol) * D;
 #pragma unroll
-            for (int md = 0; md < D / 16; ++md)
-                *reinterpret_cast<u32x2_t*>(hp + s_row_d(md, 4 * lg)) = cvt4(S[md]);
+            for (int md = 0; md < D / 16; ++md) hv[md] = cvt4(S[md]);
         }
         // X = K S (token rows) and Y^T = S^T Q^T (column rows: lane holds 4 columns of a token)
         f32x4_t X[4], Y[4];
@@ -645,6 +646,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 S[4 * h4 + x] = mfma32(__builtin_bit_cast(bf16x8_t, f0[x]), Us0, S[4 * h4 + x]);
                 S[4 * h4 + x] = mfma32(__builtin_bit_cast(bf16x8_t, f1[x]), Us1, S[4 * h4 + x]);
             }
+        }
+        if constexpr (HIST) {
+            uint16_t* hp = s_hist + (static_cast<size_t>(pair) * n_chunks + c) * D * D +
+                           static_cast<size_t>(ecol) * D;
+#pragma unroll
+            for (int md = 0; md < D / 16; ++md) *reinterpret_cast<u32x2_t*>(hp + s_row_d(md, 4 * lg)) = hv[md];
         }
         // O^T = Y^T + U^T P^T (U tiles as the A operand give U^T; the packed P rows are the
         // B operand P^T); lane (g, l16) holds O[16m+l16][4g..4g+3] of its 16 columns

@@ -27,8 +27,8 @@
 //      it writes G_c and W (bf16, in the packed order below), dV and
 //      finally dS_0;
 //   4. bwd_grad_kernel, all chunks in parallel (one persistent workgroup
-//      per CU, the next chunk's inputs fetched during the last phase): dQ,
-//      dK and dbeta from S_c, G_c, W and the chunk's q/k/v/beta.
+//      per CU, the next chunk's inputs fetched during the last two phases):
+//      dQ, dK and dbeta from S_c, G_c, W and the chunk's q/k/v/beta.
 // Numerics as in the forward: bf16 operands, fp32 accumulation; G and the
 // outputs stay fp32.
 //
@@ -558,7 +558,8 @@ struct GradGeo {
     static constexpr int TP = WT + D * kC * 2;     // packed T
     static constexpr int BS = TP + kPacked * 2;    // beta
     static constexpr int DB = BS + kC * 4;         // dbeta partial sums [2][4][kC]
-    static constexpr int BYTES = DB + 2 * 4 * kC * 4;
+    static constexpr int BS2 = DB + 2 * 4 * kC * 4;  // beta of every other chunk
+    static constexpr int BYTES = BS2 + kC * 4;
     static constexpr int JW = D / 64;              // 16-column tiles per wave
     static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
@@ -579,6 +580,9 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
     const int l16 = lane & 15, lg = lane >> 4;
     const size_t tstride = static_cast<size_t>(H) * D;
 
+    // beta alternates between two buffers by chunk, so the next chunk's is copied while
+    // phase 3 still reads the current one
+    int par = 0;
     uint16_t* Ks = reinterpret_cast<uint16_t*>(smem + G::KS);
     uint16_t* Qs = reinterpret_cast<uint16_t*>(smem + G::QS);
     uint16_t* Vs = reinterpret_cast<uint16_t*>(smem + G::VS);
@@ -591,13 +595,21 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
     uint16_t* Wt = reinterpret_cast<uint16_t*>(smem + G::WT);
     const uint16_t* Tp = reinterpret_cast<const uint16_t*>(smem + G::TP);
     const float* Bs = reinterpret_cast<const float*>(smem + G::BS);
+    auto set_par = [&](int p) {
+        par = p;
+        Bs = reinterpret_cast<const float*>(smem + (p ? G::BS2 : G::BS));
+    };
     float* db1 = reinterpret_cast<float*>(smem + G::DB);  // [wave][t]: W . (V - K S)
     float* db2 = db1 + 4 * kC;                             // [wave][t]: sum_s dA (k_t . k_s)
 
-    // Persistent: workgroup b takes chunks b, b + gridDim.x, ...  Phase 3 reads only K, Q,
-    // G's space (dP^T, dA^T) and beta, so the next chunk's V, S^T, W, T and dO are fetched
-    // while it runs; Q and G, first read in phase 2, are fetched while phase 1 runs; only
-    // K and beta are copied between chunks.
+    // Persistent: workgroup b takes chunks b, b + gridDim.x, ...  Memory stays busy through
+    // all three phases:
+    //   * phase 1: this chunk's G and Q, and the previous chunk's dQ/dK stores;
+    //   * phase 2 (reads U^T, W, S^T, G, dO): the next chunk's K, beta, T and dO (phase 1
+    //     read K and T last; phase 3's K operands are taken into registers before it);
+    //   * phase 3 (reads K's registers, Q, dP^T, dA^T, beta): the next chunk's V, S^T, W.
+    // The one barrier between chunks waits for LDS traffic only, so the dQ/dK stores run
+    // on into the next chunk.
     struct Ref {
         long tok0;
         int h, base, clen;
@@ -634,26 +646,29 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
             *reinterpret_cast<u32x2_t*>(DOs + swz<D>(t, d)) = cvt4(xdo[i]);
         }
     };
-    // the inputs phase 3 does not read: V (later U^T), S^T, W^T, T
+    // the inputs phase 3 does not read: V (later U^T), S^T, W^T
     auto copy_a = [&](const Ref& r) {
         const unsigned n_kq = static_cast<unsigned>(((r.clen - 1) * tstride + D) * 2);
         const unsigned rb = static_cast<unsigned>(tstride * 2);
         copy_rows<D>(make_rsrc(v + r.row0, n_kq), smem + G::VS, kC * D * 2 / 1024, rb, w, 4, lane);
         copy_rows<D>(make_rsrc(s_hist + r.cidx * D * D, D * D * 2), smem + G::ST, D * D * 2 / 1024, D * 2, w, 4, lane);
         copy_flat(make_rsrc(w_hist + r.cidx * D * kC, D * kC * 2), smem + G::WT, D * kC * 2 / 1024, w, 4, lane);
+    };
+    auto copy_t = [&](const Ref& r) {
         copy_flat(make_rsrc(tp_ws + r.cidx * 3 * kPacked, kPacked * 2), smem + G::TP, kPacked * 2 / 1024, w, 4, lane);
     };
-    // K and beta (read from phase 1 on), copied between chunks
-    auto copy_k = [&](const Ref& r) {
+    // K and beta, copied while phase 2 runs: K over the K that phase 1 read last, beta into
+    // the other buffer (phase 3 still reads the current one)
+    auto copy_k = [&](const Ref& r, int p) {
         const unsigned n_kq = static_cast<unsigned>(((r.clen - 1) * tstride + D) * 2);
         const unsigned rb = static_cast<unsigned>(tstride * 2);
         copy_rows<D>(make_rsrc(k + r.row0, n_kq), smem + G::KS, kC * D * 2 / 1024, rb, w, 4, lane);
         if (w == 3)
             copy_to_lds(make_rsrc(beta + (r.tok0 + r.base) * H + r.h, static_cast<unsigned>(((r.clen - 1) * H + 1) * 4)),
-                        smem + G::BS, 4, static_cast<unsigned>(lane * H * 4));
+                        smem + (p ? G::BS2 : G::BS), 4, static_cast<unsigned>(lane * H * 4));
     };
-    // Q and G (read from phase 2 on, into space phase 3 of the chunk before read last),
-    // copied while phase 1 runs
+    // G (read in phase 2) and Q (read in phase 3), into space phase 3 of the chunk before
+    // read last, copied while phase 1 runs
     auto copy_qg = [&](const Ref& r) {
         const unsigned n_kq = static_cast<unsigned>(((r.clen - 1) * tstride + D) * 2);
         const unsigned rb = static_cast<unsigned>(tstride * 2);
@@ -665,8 +680,9 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
     if (idx >= n_total) return;  // whole workgroup, before any barrier
     Ref cur = ref_of(idx);
     load_do(cur);
-    copy_k(cur);
+    copy_k(cur, 0);
     copy_a(cur);
+    copy_t(cur);
     store_do();
     wait_copies();
     __syncthreads();
@@ -762,14 +778,36 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
                 if (l16 == 0) *reinterpret_cast<f32x4_t*>(db1 + w * kC + 16 * m + 4 * lg) = dbp[m];
             }
         }
-        wait_copies();    // Q and G (no other copy or store is in flight)
-        __syncthreads();  // V is dead: its space takes U^T
+        // phase 3's K operands, taken into registers now: the next chunk's K lands over
+        // them while phase 2 runs
+        u32x4_t fkc[2][JW];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int dd = 0; dd < JW; ++dd) fkc[kb][dd] = lds_col_issue<D>(Ks, 32 * kb, 16 * (JW * w + dd), lane);
+        lds_wait_all();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int dd = 0; dd < JW; ++dd) tie(fkc[kb][dd]);
+        wait_copies();    // Q and G (and the previous chunk's dQ/dK stores)
+        __syncthreads();  // V is dead: its space takes U^T; K and T are free
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int jj = 0; jj < JW; ++jj)
                 *reinterpret_cast<u32x2_t*>(Ut + swz<kC>(16 * (JW * w + jj) + l16, 16 * m + 4 * lg)) = cvt4(U[m][jj]);
         __syncthreads();
+        // the next chunk's K, beta, T and dO, fetched while phase 2 runs
+        const int nidx = idx + static_cast<int>(gridDim.x);
+        const bool more = nidx < n_total;
+        Ref nxt{};
+        if (more) {
+            nxt = ref_of(nidx);
+            load_do(nxt);
+            copy_k(nxt, par ^ 1);
+            copy_t(nxt);
+        }
 
         // ---- phase 2: products contracting over the d_v index j ----
         // dQ1 = dO S^T, dKa = U G^T, dKb = W S^T for this wave's d tiles; dP = dO U^T and
@@ -896,15 +934,8 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         }
         __syncthreads();
 
-        // the next chunk's V, S^T, W^T, T and dO, into space phase 3 does not read
-        const int nidx = idx + static_cast<int>(gridDim.x);
-        const bool more = nidx < n_total;
-        Ref nxt{};
-        if (more) {
-            nxt = ref_of(nidx);
-            load_do(nxt);
-            copy_a(nxt);
-        }
+        // the next chunk's V, S^T and W^T, into space phase 3 does not read
+        if (more) copy_a(nxt);
 
         // ---- phase 3: products contracting over tokens ----
         // dQ += dP K;  dKc = dP^T Q + (beta dA)^T K + (beta dA) K
@@ -915,12 +946,9 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
             for (int dd = 0; dd < JW; ++dd) dKc[m][dd] = zero;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-            u32x4_t fkc[JW], fqc[JW], fpc[4], fac[4];
+            u32x4_t fqc[JW], fpc[4], fac[4];
 #pragma unroll
-            for (int dd = 0; dd < JW; ++dd) {
-                fkc[dd] = lds_col_issue<D>(Ks, 32 * kb, 16 * (JW * w + dd), lane);
-                fqc[dd] = lds_col_issue<D>(Qs, 32 * kb, 16 * (JW * w + dd), lane);
-            }
+            for (int dd = 0; dd < JW; ++dd) fqc[dd] = lds_col_issue<D>(Qs, 32 * kb, 16 * (JW * w + dd), lane);
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 fpc[m] = lds_col_issue<kC>(dPt, 32 * kb, 16 * m, lane);
@@ -934,10 +962,7 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
             }
             lds_wait_all();
 #pragma unroll
-            for (int dd = 0; dd < JW; ++dd) {
-                tie(fkc[dd]);
-                tie(fqc[dd]);
-            }
+            for (int dd = 0; dd < JW; ++dd) tie(fqc[dd]);
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 tie(fpc[m]);
@@ -947,44 +972,57 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
             for (int m = 0; m < 4; ++m)
 #pragma unroll
                 for (int dd = 0; dd < JW; ++dd) {
-                    dQ[m][dd] = mfma32(as_b(fkc[dd]), as_b(fpc[m]), dQ[m][dd]);
+                    dQ[m][dd] = mfma32(as_b(fkc[kb][dd]), as_b(fpc[m]), dQ[m][dd]);
                     dKc[m][dd] = mfma32(as_b(fqc[dd]), fpr[m], dKc[m][dd]);
-                    dKc[m][dd] = mfma32(as_b(fkc[dd]), far[m], dKc[m][dd]);
-                    dKc[m][dd] = mfma32(as_b(fkc[dd]), as_b(fac[m]), dKc[m][dd]);
+                    dKc[m][dd] = mfma32(as_b(fkc[kb][dd]), far[m], dKc[m][dd]);
+                    dKc[m][dd] = mfma32(as_b(fkc[kb][dd]), as_b(fac[m]), dKc[m][dd]);
                 }
         }
-        // outputs: lane (g, l16) holds d = 16 dt + 4g + [0, 4) of token 16m + l16 (16-byte stores)
+        // outputs: lane (g, l16) holds d = 16 dt + 4g + [0, 4) of token 16m + l16 (16-byte
+        // stores).  Range-checked buffer stores (rows past the chunk's end are dropped), so
+        // every wave issues exactly kStores of them whatever the chunk's length.
+        constexpr int kStores = 2 * 4 * JW;
+        {
+            const unsigned nb = static_cast<unsigned>(((clen - 1) * tstride + D) * 4);
+            const __amdgpu_buffer_rsrc_t rq = make_rsrc(gq + row0, nb), rk = make_rsrc(gk + row0, nb);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int t = 16 * m + l16;
-            const float bt = Bs[t];
+            for (int m = 0; m < 4; ++m) {
+                const int t = 16 * m + l16;
+                const float bt = Bs[t];
 #pragma unroll
-            for (int dd = 0; dd < JW; ++dd) {
-                const int d0 = 16 * (JW * w + dd) + 4 * lg;
-                const f32x4_t kk = dKa[m][dd] - bt * dKb[m][dd] + dKc[m][dd];
-                if (t < clen) {
-                    const size_t a = row0 + t * tstride + d0;
-                    *reinterpret_cast<f32x4_t*>(gq + a) = dQ[m][dd];
-                    *reinterpret_cast<f32x4_t*>(gk + a) = kk;
+                for (int dd = 0; dd < JW; ++dd) {
+                    const int d0 = 16 * (JW * w + dd) + 4 * lg;
+                    const f32x4_t kk = dKa[m][dd] - bt * dKb[m][dd] + dKc[m][dd];
+                    const unsigned off = static_cast<unsigned>((t * tstride + d0) * 4);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, dQ[m][dd]), rq, off, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, kk), rk, off, 0, 0);
                 }
             }
         }
-        if (tid < clen) {
-            float s = 0.f;
+        auto store_gbeta = [&]() {
+            if (tid < clen) {
+                float s = 0.f;
 #pragma unroll
-            for (int x = 0; x < 4; ++x) s += db1[x * kC + tid];
+                for (int x = 0; x < 4; ++x) s += db1[x * kC + tid];
 #pragma unroll
-            for (int x = 0; x < 4; ++x) s += db2[x * kC + tid];
-            gbeta[(tok0 + base + tid) * H + h] = s;
+                for (int x = 0; x < 4; ++x) s += db2[x * kC + tid];
+                gbeta[(tok0 + base + tid) * H + h] = s;
+            }
+        };
+        if (!more) {
+            store_gbeta();
+            break;
         }
-        if (!more) break;
-        __syncthreads();  // phase 3's reads of K, Q, dP^T, dA^T, beta and the dbeta sums are done
-        copy_k(nxt);
-        store_do();
-        wait_copies();
-        __syncthreads();
+        // No barrier before these: phase 3 reads neither dO's space nor the next chunk's
+        // copies, and the dbeta sums were complete at the barrier before phase 3.  The
+        // dQ/dK stores stay in flight into the next chunk.
+        store_do();            // waits for this wave's dO loads only
+        wait_vm_n<kStores>();  // and its copies, issued before the stores
+        store_gbeta();
+        lds_barrier();         // every wave's copies have landed; db1/db2 and dO are free
         idx = nidx;
         cur = nxt;
+        set_par(par ^ 1);
     }
 }
 

@@ -22,10 +22,11 @@
 //     O = Q S + P U, S += K^T U;
 //   * producer 0 builds chunk c's T and producer 1 chunk c's P, in
 //     registers, into LDS in MFMA operand order;
-//   * the last producer also issues chunk c+1's HBM -> LDS copies
-//     (buffer_load ... lds: no registers, no LDS write instructions).
-// K, Q, V and beta stay in LDS exactly as in HBM (token rows), in three
-// rotating buffers; the K^T and V operands the chain needs come from the
+//   * the last producer also issues the HBM -> LDS copies (buffer_load ...
+//     lds: no registers, no LDS write instructions): chunk c+1's Q and V,
+//     and chunk c+2's K and beta.
+// K, Q, V and beta stay in LDS exactly as in HBM (token rows), K and beta in
+// four rotating buffers, Q and V in three; the K^T and V operands the chain needs come from the
 // same token rows through the gfx950 LDS transpose read
 // (ds_read_b64_tr_b16).  Rows past the end of a sequence are read as
 // zeros by the buffer range check.  The workgroups of one (sequence,
@@ -65,17 +66,18 @@ struct Geo {
     static constexpr int LOADER = NPW - 1;     // producer that issues the HBM -> LDS copies
     static constexpr int NI_KQ = kC * D * 2 / 1024;   // 1 KiB copy instructions per K or Q tile
     static constexpr int NI_V = kC * DV * 2 / 1024;   // ... per V tile
-    // one RAW buffer: Ks, Qs, Vs (bf16 token rows, swizzled), Bs (fp32)
-    static constexpr int R_KS = 0;
-    static constexpr int R_QS = R_KS + kC * D * 2;
-    static constexpr int R_VS = R_QS + kC * D * 2;
-    static constexpr int R_BS = R_VS + kC * DV * 2;
-    static constexpr int R_GS = R_BS + kC * 4;  // GATED: the chunk's log-gates (fp32)
-    static constexpr int RAW = R_GS + (GATED ? kC * 4 : 0);
-    static constexpr int NRAW = 3;
+    // Chunk buffers (bf16 token rows, swizzled; fp32 beta and gates), in two rings:
+    // K, beta and the gates four deep (K is copied two chunks ahead), Q and V three deep
+    static constexpr int K_BS = kC * D * 2;
+    static constexpr int K_GS = K_BS + kC * 4;
+    static constexpr int KB = K_GS + (GATED ? kC * 4 : 0);
+    static constexpr int Q_VS = kC * D * 2;
+    static constexpr int QB = Q_VS + kC * DV * 2;
+    static constexpr int NKB = 4, NQB = 3;
+    static constexpr int RINGS = NKB * KB + NQB * QB;
     // one TP buffer: T and P, 6 operand blocks of 1 KiB each
     static constexpr int TP = 2 * 6 * 1024;
-    static constexpr int BYTES = NRAW * RAW + 2 * TP;
+    static constexpr int BYTES = RINGS + 2 * TP;
     // NORM / GATED modes: per chunk parity, 128 floats handed from the producers to the
     // chain after the TP buffers (NORM: 1/||k_t||, 1/||q_t||; GATED: e^(G_t), e^(G_C - G_t))
     static constexpr int RN = BYTES;
@@ -96,7 +98,7 @@ struct Geo {
     static constexpr int BYTES_HIST = 6 * RAWH + 4 * 6 * 1024;
     static_assert(D == 64 || D == 128, "D");
     static_assert(DV == 16 || DV == 32, "DV");
-    static_assert(NI_V >= 1 && RAW % 16 == 0, "RAW layout");
+    static_assert(NI_V >= 1 && KB % 16 == 0 && QB % 16 == 0 && RAWH % 16 == 0, "chunk buffer layout");
     static_assert(BYTES_STAGED <= 160 * 1024 && BYTES_HIST <= 160 * 1024, "LDS budget");
 };
 
@@ -169,23 +171,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const size_t sbase = static_cast<size_t>(pair) * D * D;
     const size_t tstride = static_cast<size_t>(H) * D;  // elements between tokens
 
-    // chunk buffers and their fields; HIST has its own (no Q, two chunks per stage)
-    constexpr int R_KS = HIST ? 0 : G::R_KS;
-    constexpr int R_VS = HIST ? G::H_VS : G::R_VS;
-    constexpr int R_BS = HIST ? G::H_BS : G::R_BS;
-    auto raw = [&](int c) { return HIST ? smem + (c % 6) * G::RAWH : smem + (c % G::NRAW) * G::RAW; };
+    // chunk c's fields: HIST has one ring of its own (no Q, two chunks per stage)
+    constexpr int R_KS = 0, R_VS = G::H_VS, R_BS = G::H_BS;
+    auto raw = [&](int c) { return smem + (c % 6) * G::RAWH; };
+    // With bf16 O staged, K goes one chunk ahead (see the loader), so its ring is three
+    // deep and everything after the rings sits one K buffer lower (SH bytes)
+    constexpr bool STAGED = OUT_BF16 && G::NCW == 2 && !HIST;
+    constexpr int NKB = STAGED ? 3 : G::NKB, SH = STAGED ? G::KB : 0;
+    auto ks_of = [&](int c) { return HIST ? raw(c) + R_KS : smem + (c % NKB) * G::KB; };
+    auto bs_of = [&](int c) { return HIST ? raw(c) + R_BS : smem + (c % NKB) * G::KB + G::K_BS; };
+    auto gs_of = [&](int c) { return smem + (c % NKB) * G::KB + G::K_GS; };
+    auto qs_of = [&](int c) { return smem + NKB * G::KB + (c % G::NQB) * G::QB; };
+    auto vs_of = [&](int c) { return HIST ? raw(c) + R_VS : smem + NKB * G::KB + (c % G::NQB) * G::QB + G::Q_VS; };
     auto tpb = [&](int c) {
         return reinterpret_cast<uint16_t*>(HIST ? smem + 6 * G::RAWH + (c & 3) * 6 * 1024
-                                                : smem + G::NRAW * G::RAW + (c & 1) * G::TP);
+                                                : smem + G::RINGS - SH + (c & 1) * G::TP);
     };
-    auto rnb = [&](int c) { return reinterpret_cast<float*>(smem + G::RN + (c & 1) * 512); };
+    auto rnb = [&](int c) { return reinterpret_cast<float*>(smem + G::RN - SH + (c & 1) * 512); };
     // GATED: producer pw's scanned gates, written and read back by that wave only
-    auto gsb = [&](int p) { return reinterpret_cast<float*>(smem + G::GS + p * 256); };
+    auto gsb = [&](int p) { return reinterpret_cast<float*>(smem + G::GS - SH + p * 256); };
 
     // ---------------- loader: chunk c's K, Q, V tile and beta, HBM -> LDS ----------------
+    // (the K part: K, beta and gates; the QV part: Q and V)
     // Copy instruction i, lane L fills LDS bytes [1024 i + 16 L, +16) of the tile: row r,
     // stored chunk p, i.e. logical chunk p ^ f(r) of token row r.
-    auto issue_copies = [&](int c) __attribute__((always_inline)) {
+    auto issue_part = [&](int c, bool kpart, bool qvpart) __attribute__((always_inline)) {
         const int base = c * kC;
         const int clen = min(kC, len - base);
         const size_t row0 = static_cast<size_t>(tok0 + base) * tstride + static_cast<size_t>(h) * D;
@@ -197,31 +207,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const __amdgpu_buffer_rsrc_t rq = make_rsrc(q + row0, n_kq);
         const __amdgpu_buffer_rsrc_t rv = make_rsrc(v + row0 + col0, n_v);
         const __amdgpu_buffer_rsrc_t rb = make_rsrc(NORM ? beta : beta + (tok0 + base) * H + h, NORM ? 0u : n_b);
-        unsigned char* rbuf = uniform_ptr(raw(c));
+        // K and Q rows interleaved when both parts go out together (measured faster for
+        // the staged bf16 O mode, which copies whole chunks one ahead)
+        unsigned char* kbuf = uniform_ptr(ks_of(c));
+        unsigned char* qbuf = uniform_ptr(qs_of(c));
+        if (kpart || (qvpart && !HIST)) {
 #pragma unroll
-        for (int i = 0; i < G::NI_KQ; ++i) {
-            const int pos = 512 * i + 8 * lane;  // element position in the tile
-            const int r = pos / D, p = (pos % D) / 8;
-            const unsigned vo = static_cast<unsigned>(r * tstride * 2) + 16u * (p ^ kq_f<D>(r));
-            copy_to_lds(rk, rbuf + R_KS + 1024 * i, 16, vo);
-            if constexpr (!HIST) copy_to_lds(rq, rbuf + G::R_QS + 1024 * i, 16, vo);  // HIST: no O
+            for (int i = 0; i < G::NI_KQ; ++i) {
+                const int pos = 512 * i + 8 * lane;  // element position in the tile
+                const int r = pos / D, p = (pos % D) / 8;
+                const unsigned vo = static_cast<unsigned>(r * tstride * 2) + 16u * (p ^ kq_f<D>(r));
+                if (kpart) copy_to_lds(rk, kbuf + 1024 * i, 16, vo);
+                if (!HIST && qvpart) copy_to_lds(rq, qbuf + 1024 * i, 16, vo);  // HIST: no O
+            }
         }
+        if (qvpart) {
+            unsigned char* vbuf = uniform_ptr(vs_of(c));
 #pragma unroll
-        for (int i = 0; i < G::NI_V; ++i) {
-            const int pos = 512 * i + 8 * lane;
-            const int r = pos / DV, p = (pos % DV) / 8;
-            const unsigned vo = static_cast<unsigned>(r * tstride * 2) + 16u * (p ^ v_f<DV>(r));
-            copy_to_lds(rv, rbuf + R_VS + 1024 * i, 16, vo);
+            for (int i = 0; i < G::NI_V; ++i) {
+                const int pos = 512 * i + 8 * lane;
+                const int r = pos / DV, p = (pos % DV) / 8;
+                const unsigned vo = static_cast<unsigned>(r * tstride * 2) + 16u * (p ^ v_f<DV>(r));
+                copy_to_lds(rv, vbuf + 1024 * i, 16, vo);
+            }
         }
-        if constexpr (!NORM) copy_to_lds(rb, rbuf + R_BS, 4, static_cast<unsigned>(lane * H * 4));
-        if constexpr (GATED)
-            copy_to_lds(make_rsrc(gate + (tok0 + base) * H + h, n_b), rbuf + G::R_GS, 4,
-                        static_cast<unsigned>(lane * H * 4));
+        if (kpart) {
+            if constexpr (!NORM) copy_to_lds(rb, uniform_ptr(bs_of(c)), 4, static_cast<unsigned>(lane * H * 4));
+            if constexpr (GATED)
+                copy_to_lds(make_rsrc(gate + (tok0 + base) * H + h, n_b), uniform_ptr(gs_of(c)), 4,
+                            static_cast<unsigned>(lane * H * 4));
+        }
     };
+    auto issue_copies = [&](int c) __attribute__((always_inline)) { issue_part(c, true, true); };
+    // VMEM instructions of one K-part copy (K rows, beta, gates)
+    constexpr int kNK = G::NI_KQ + (NORM ? 0 : 1) + (GATED ? 1 : 0);
     // GATED: inclusive scan of the chunk's log-gates (rows past the end read 0), in the
     // base-2 domain: lane t gets G_t * log2(e), so that every decay is one v_exp_f32 (2^x)
-    auto gate_scan = [&](const unsigned char* rb) {
-        return wave_prefix_sum(reinterpret_cast<const float*>(rb + G::R_GS)[lane] * 1.44269504088896341f);
+    auto gate_scan = [&](const unsigned char* gs) {
+        return wave_prefix_sum(reinterpret_cast<const float*>(gs)[lane] * 1.44269504088896341f);
     };
     // GATED: the scanned gates of token 16b + l16 (col) and of tokens 16b + 4lg + [0, 4)
     // (row), through this producer's LDS scratch (one write, eight reads; a wave's LDS
@@ -238,9 +261,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     // ---------------- producer 0: T = (I + A)^-1 in packed operand order ----------------
     auto build_t = [&](int c) {
-        unsigned char* rb = raw(c);
-        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + R_KS);
-        const float* Bs = reinterpret_cast<const float*>(rb + R_BS);
+        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(ks_of(c));
+        const float* Bs = reinterpret_cast<const float*>(bs_of(c));
         uint16_t* Tp = tpb(c);
         const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
         // G = K K^T: diagonal tiles gd[b] and upper tiles gu(k, i), k < i
@@ -302,7 +324,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         float gcol[4];
         f32x4_t grow[4];
         if constexpr (GATED) {
-            const float gsc = gate_scan(rb);
+            const float gsc = gate_scan(gs_of(c));
             gate_bcast(gsc, gcol, grow);
             float* gh = rnb(c);
             gh[lane] = exp2_hw(gsc);
@@ -440,9 +462,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     // ---------------- producer 1: P = lower_incl_diag(Q K^T) in packed operand order ----------------
     auto build_p = [&](int c) {
-        unsigned char* rb = raw(c);
-        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + G::R_KS);
-        const uint16_t* Qs = reinterpret_cast<const uint16_t*>(rb + G::R_QS);
+        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(ks_of(c));
+        const uint16_t* Qs = reinterpret_cast<const uint16_t*>(qs_of(c));
         uint16_t* Pp = tpb(c) + 6 * 512;
         const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
         f32x4_t p[10];
@@ -482,7 +503,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
         float pgc[4];    // GATED: G_{16i + l16}
         f32x4_t pgr[4];  // GATED: G_{16j + 4lg + r}
-        if constexpr (GATED) gate_bcast(gate_scan(rb), pgc, pgr);
+        if constexpr (GATED) gate_bcast(gate_scan(gs_of(c)), pgc, pgr);
         int x = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -530,11 +551,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // 64-byte rows (16 bytes per lane).  16-byte unit u of row r sits at u ^ ((r >> 2) & 3):
     // the accumulator writes (16 rows, 8 bytes each) and the row reads are conflict-free.
     // (With fp32 O, 64 bytes per row per wave, staging measured no faster.)
-    constexpr bool STAGE = OUT_BF16 && G::NCW == 2 && !HIST;
+    constexpr bool STAGE = STAGED;
     constexpr int ORB = DV * 2;  // bytes per staged row
     constexpr int OUPR = ORB / 16;
     auto ostg_f = [](int r) { return (r >> 2) & 3; };
-    auto obuf = [&](int c) { return smem + G::OB + (c & 1) * G::OB_BYTES; };
+    auto obuf = [&](int c) { return smem + G::OB - SH + (c & 1) * G::OB_BYTES; };
     auto flush_o = [&](int cc) {
         const int cb = cc * kC, cl = min(kC, len - cb);
         // rows past the sequence's end fall outside the buffer range and are dropped
@@ -551,11 +572,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     };
 
     auto run_chunk = [&](int c) {
-        unsigned char* rb = raw(c);
-        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + R_KS);
-        const uint16_t* Qs = reinterpret_cast<const uint16_t*>(rb + G::R_QS);  // (not in HIST)
-        const uint16_t* Vs = reinterpret_cast<const uint16_t*>(rb + R_VS);
-        const float* Bs = reinterpret_cast<const float*>(rb + R_BS);
+        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(ks_of(c));
+        const uint16_t* Qs = reinterpret_cast<const uint16_t*>(qs_of(c));  // (not in HIST)
+        const uint16_t* Vs = reinterpret_cast<const uint16_t*>(vs_of(c));
+        const float* Bs = reinterpret_cast<const float*>(bs_of(c));
         const uint16_t* Tp = tpb(c);
         const uint16_t* Pp = Tp + 6 * 512;
         const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
@@ -696,10 +716,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     };
 
     // ---------------- pipeline: one barrier per chunk ----------------
-    // Between barriers i and i+1: the loader copies chunk i+1 into RAW[(i+1)%3],
-    // the producers build chunk i's T and P from RAW[i%3] into TP[i%2], and the
-    // chain runs chunk i-1 from RAW[(i-1)%3] and TP[(i-1)%2].  Barrier i+1
-    // publishes all three, and frees RAW[(i-1)%3] and TP[(i-1)%2] for reuse.
+    // Between barriers i and i+1: the loader copies chunk i+1's Q and V and chunk
+    // i+2's K part, the producers build chunk i's T and P into TP[i%2], and the
+    // chain runs chunk i-1 with TP[(i-1)%2].  Barrier i+1 publishes all three
+    // (chunk i+2's K part may still be in flight: it is waited for at barrier i+2),
+    // and frees chunk i-1's buffers and TP[(i-1)%2] for reuse.
     // Every role passes the same n_chunks + 1 barriers (+ 1 when bf16 O is staged).
     if (HIST && n_chunks > 0) {
         // HIST builds no P, and the T build is the longest role: two chunks per barrier,
@@ -742,20 +763,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             if constexpr (STAGE) lds_barrier();
         } else {
             const bool loader = pw == G::LOADER;
+            // Q and V go one chunk ahead, K (with beta and gates) two: each iteration waits
+            // for everything but the newest K part.  With bf16 O staged, the loader also
+            // stores O, and K one chunk ahead measured faster (K2 false).
+            constexpr bool K2 = !STAGE;
             if (loader) {
-                issue_copies(0);
-                wait_copies();
+                issue_part(0, true, true);
+                if (K2 && 1 < n_chunks) {
+                    issue_part(1, true, false);
+                    wait_vm_n<kNK>();
+                } else {
+                    wait_copies();
+                }
             }
             lds_barrier();
             for (int c = 0; c < n_chunks; ++c) {
-                if (loader && c + 1 < n_chunks) issue_copies(c + 1);
+                if (loader && c + 1 < n_chunks) issue_part(c + 1, !K2, true);
                 if (STAGE && loader && c >= 2) flush_o(c - 2);  // staged in iteration c - 1
+                if (K2 && loader && c + 2 < n_chunks) issue_part(c + 2, true, false);
                 if (pw == 0) {
                     build_t(c);
                 } else if (pw == 1 && !HIST) {  // HIST computes no O, so no P
                     build_p(c);
                 }
-                if (loader) wait_copies();
+                if (loader) {
+                    if (K2 && c + 2 < n_chunks)
+                        wait_vm_n<kNK>();
+                    else
+                        wait_copies();
+                }
                 lds_barrier();
             }
             if constexpr (STAGE) {
@@ -782,7 +818,7 @@ template <int D, int DV, bool OB, bool HIST, bool NORM = false, bool GATED = fal
 hipError_t launch_t(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
     using G = Geo<D, DV, GATED>;
     constexpr int kBytes = HIST                       ? G::BYTES_HIST
-                           : (OB && G::NCW == 2)      ? G::BYTES_STAGED
+                           : (OB && G::NCW == 2)      ? G::BYTES_STAGED - G::KB  // K ring three deep
                            : GATED                    ? G::BYTES_GATED
                            : NORM                     ? G::BYTES_NORM
                                                       : G::BYTES;

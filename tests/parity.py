@@ -1,11 +1,24 @@
 """Parity criteria shared by the tests (tolerances from BASELINE.json north_star).
 
 fp32 inputs: rel-L2 <= 1e-5 and max-abs <= 1e-4 against the fp32/fp64
-reference recurrence. The max-abs bound is scaled by max(1, max|ref|): the
-reference tests' unnormalised keys make the recurrence grow (|1 - beta
-||k||^2| > 1), and one case (tests/test_kernels.py:1537-1548's rng(50),
+reference recurrence, both exactly as written (``assert_f32_parity``).
+Every test on the benchmark distribution (q, k L2-normalised per token,
+v ~ N(0, 1), beta = sigmoid(N(0, 1))) uses this gate, unscaled.
+
+One family of inputs gets a max-abs bound scaled by max(1, max|ref|)
+(``assert_f32_parity(..., scaled=True)``): the reference tests' own
+unnormalised keys (tests/test_kernels.py:77-82, reproduced by
+``synth.reference_test_inputs``). There |1 - beta ||k||^2| > 1, the
+recurrence grows, and one case (tests/test_kernels.py:1537-1548's rng(50),
 outputs up to ~6e3) carries fp32 rounding of ~1e-3 in absolute terms even
-between two fp32 evaluations of the same formula.
+between two fp32 evaluations of the same formula. rel-L2 stays unscaled
+there too.
+
+Gradients (the backward's gq, gk, gv, gbeta, gstate) also use the scaled
+max-abs bound: the north star's gate speaks of the forward's outputs and
+final state, and gradient entries are sums over T and D whose magnitude
+grows with both (gbeta sums D products per token, gstate sums over T), so
+their fp32 rounding grows with them. rel-L2 <= 1e-5 is enforced unscaled.
 
 bf16 inputs: rel-L2 <= 2e-2 against the fp32 reference on the same
 (bf16-rounded) inputs.
@@ -28,14 +41,17 @@ def rel_l2(got, exp) -> float:
     return num if den == 0.0 else num / den
 
 
-def assert_f32_parity(got, exp, what: str = "") -> None:
+def assert_f32_parity(got, exp, what: str = "", scaled: bool = False) -> None:
+    """rel-L2 <= 1e-5 and max-abs <= 1e-4; ``scaled`` (unnormalised-key cases only)
+    multiplies the max-abs bound by max(1, max|exp|)."""
     got = np.asarray(got, dtype=np.float64)
     exp = np.asarray(exp, dtype=np.float64)
     assert got.shape == exp.shape, f"{what}: shape {got.shape} != {exp.shape}"
     if exp.size == 0:
         return
+    assert np.all(np.isfinite(got)), f"{what}: non-finite values"
     r = rel_l2(got, exp)
-    scale = max(1.0, float(np.abs(exp).max()))
+    scale = max(1.0, float(np.abs(exp).max())) if scaled else 1.0
     m = float(np.abs(got - exp).max())
     assert r <= F32_REL_L2, f"{what}: rel-L2 {r:.3e} > {F32_REL_L2}"
     assert m <= F32_MAX_ABS * scale, f"{what}: max-abs {m:.3e} > {F32_MAX_ABS} * {scale:.3g}"

@@ -51,7 +51,7 @@ def _check(got, exp, what):
     for name, g, e in zip(NAMES, got, exp):
         g = _np(g)
         assert g.dtype == np.float32, f"{what} {name}"
-        assert_f32_parity(g, e, f"{what} {name}")
+        assert_f32_parity(g, e, f"{what} {name}", scaled=True)
 
 
 def test_reference_cases_with_random_cotangents():

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 9
+#define PM_DELTA_ABI_VERSION 10
 
 /* element types */
 #define PM_DTYPE_F32 0
@@ -105,6 +105,23 @@ int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float
                         const float* s0, void* o, float* s_out, int H, int D,
                         int in_dtype, int out_dtype, int chunk, void* workspace,
                         size_t ws_bytes, void* stream);
+
+/*
+ * Device-side check of a packed batch's offsets, for callers whose cu_seqlens
+ * already live on the device: no host copy and no synchronisation, so it can
+ * be captured in a graph with the forward it guards.  One small kernel on
+ * `stream` ORs into *flag (a device int32 the caller owns and reads when it
+ * chooses):
+ *   1: cu_seqlens[0] != 0            2: cu_seqlens[n_seqs] != total_T
+ *   4: a decreasing pair             8: an offset outside [0, total_T]
+ * pm_delta_fwd_varlen itself clamps every segment into [0, total_T], so bad
+ * offsets never reach outside the buffers; this entry point reports them.
+ * No reference counterpart: the reference has no packed batch, and its
+ * callers' offsets would be host values checked in Python
+ * (kernels/__init__.py:308-338 is where the reference validates shapes).
+ */
+int pm_varlen_check(const int32_t* cu_seqlens, int n_seqs, int total_T, int32_t* flag,
+                    void* stream);
 
 /*
  * One recurrent decode step for B*H sequences, state updated in place.

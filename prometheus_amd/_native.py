@@ -18,7 +18,7 @@ import torch  # noqa: F401  (see module docstring: must precede CDLL)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpmdelta.so")
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256
@@ -47,6 +47,7 @@ EXPORTS = (
     "pm_abi_version",
     "pm_delta_set_path",
     "pm_delta_set_tile",
+    "pm_varlen_check",
 )
 
 _lib = None
@@ -113,6 +114,8 @@ def lib() -> ctypes.CDLL:
         L.pm_delta_set_path.restype = i
         L.pm_delta_set_tile.argtypes = [i]
         L.pm_delta_set_tile.restype = i
+        L.pm_varlen_check.argtypes = [vp, i, i, vp, vp]
+        L.pm_varlen_check.restype = i
         got = L.pm_abi_version()
         if got != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH}: ABI version {got}, expected {ABI_VERSION}")
@@ -140,3 +143,31 @@ def set_tile(dv_tile: int) -> int:
     if old < 0:
         check(old)
     return old
+
+
+def knobs() -> tuple[int, int]:
+    """The calling thread's (path, tile) selection.  Both knobs are per thread in the
+    library, so code that launches on another thread (torch autograd runs a CUDA
+    backward on its device thread) carries them over with ``use_knobs``."""
+    path = set_path(0)
+    set_path(path)
+    tile = set_tile(0)
+    set_tile(tile)
+    return path, tile
+
+
+class use_knobs:
+    """Context manager: this thread's path and tile set to ``(path, tile)`` inside the
+    block, restored after it."""
+
+    def __init__(self, path: int, tile: int):
+        self.path, self.tile = int(path), int(tile)
+
+    def __enter__(self):
+        self.old = (set_path(self.path), set_tile(self.tile))
+        return self
+
+    def __exit__(self, *exc):
+        set_path(self.old[0])
+        set_tile(self.old[1])
+        return False

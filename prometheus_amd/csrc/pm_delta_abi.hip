@@ -47,6 +47,33 @@ hipError_t launch_fill_zero(float* p, size_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Offsets of a packed batch checked on the device: one workgroup ORs what it finds into
+// *flag (bit 1: cu[0] != 0; 2: cu[n] != total; 4: a decreasing pair; 8: an offset outside
+// [0, total]).  The workgroup combines its lanes' bits in LDS and one lane updates the
+// flag, so the word is read and written by a single thread of a single launch.
+__global__ __launch_bounds__(256) void varlen_check_kernel(const int32_t* __restrict__ cu, int n_seqs,
+                                                           int total, int32_t* __restrict__ flag) {
+    __shared__ int found;
+    if (threadIdx.x == 0) found = 0;
+    __syncthreads();
+    int bits = 0;
+    for (int i = threadIdx.x; i <= n_seqs; i += blockDim.x) {
+        const int a = cu[i];
+        if (a < 0 || a > total) bits |= 8;
+        if (i == 0 && a != 0) bits |= 1;
+        if (i == n_seqs && a != total) bits |= 2;
+        if (i < n_seqs && cu[i + 1] < a) bits |= 4;
+    }
+    if (bits) atomicOr(&found, bits);
+    __syncthreads();
+    if (threadIdx.x == 0 && found) flag[0] |= found;
+}
+
+hipError_t launch_varlen_check(const int32_t* cu, int n_seqs, int total, int32_t* flag, hipStream_t st) {
+    hipLaunchKernelGGL(varlen_check_kernel, dim3(1), dim3(256), 0, st, cu, n_seqs, total, flag);
+    return hipGetLastError();
+}
+
 hipError_t launch_copy_f32(float* dst, const float* src, size_t n, hipStream_t st) {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(copy_f32_kernel, dim3(grid_for(n)), dim3(256), 0, st, dst, src, n);
@@ -405,6 +432,17 @@ int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float
         return fail(PM_E_ALIGN, "cu_seqlens must be 4-byte aligned");
     return forward(q, k, v, beta, s0, o, s_out, cu_seqlens, n_seqs, 0, total_T, H, D, in_dtype,
                    out_dtype, chunk, static_cast<hipStream_t>(stream), nullptr, workspace, ws_bytes);
+}
+
+int pm_varlen_check(const int32_t* cu_seqlens, int n_seqs, int total_T, int32_t* flag, void* stream) {
+    g_err[0] = '\0';
+    if (n_seqs < 0 || total_T < 0)
+        return fail(PM_E_SHAPE, "n_seqs and total_T must be >= 0 (got %d, %d)", n_seqs, total_T);
+    if (!cu_seqlens || !flag) return fail(PM_E_NULL, "cu_seqlens and flag must be non-NULL");
+    if (!aligned(cu_seqlens, 4) || !aligned(flag, 4))
+        return fail(PM_E_ALIGN, "cu_seqlens and flag must be 4-byte aligned");
+    hipError_t e = pm::launch_varlen_check(cu_seqlens, n_seqs, total_T, flag, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? 0 : hip_fail(e, "cu_seqlens check launch");
 }
 
 int pm_delta_step_slots(float* pool, const int32_t* slots, int n_slots, const void* q,

@@ -150,5 +150,7 @@ hipError_t launch_bwd_chunked(const BwdArgs& a, hipStream_t st);
 // Zero fill (used instead of hipMemsetAsync so callers may graph-capture).
 hipError_t launch_fill_zero(float* p, size_t n, hipStream_t st);
 hipError_t launch_copy_f32(float* dst, const float* src, size_t n, hipStream_t st);
+// One workgroup checks a packed batch's offsets and ORs error bits into *flag.
+hipError_t launch_varlen_check(const int32_t* cu, int n_seqs, int total, int32_t* flag, hipStream_t st);
 
 }  // namespace pm

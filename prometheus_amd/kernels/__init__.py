@@ -247,13 +247,17 @@ class _ChunkedDeltaRule(torch.autograd.Function):
         ctx.chunk = chunk
         ctx.like = [(x.dtype, x.device) if isinstance(x, torch.Tensor) else None
                     for x in (q, k, v, beta, state)]
+        # the library's kernel knobs are per thread and autograd may run the backward on
+        # another thread: the backward runs under the forward caller's selection
+        ctx.knobs = _native.knobs()
         return call.out(o), call.out(s)
 
     @staticmethod
     def backward(ctx, go, gs):
         qd, kd, vd, bd, sd = ctx.saved_tensors
         res = _DeltaResidual(q=qd, k=kd, v=vd, beta=bd, state0=sd, chunk=ctx.chunk)
-        grads = chunked_delta_rule_bwd(res, (go, gs))
+        with _native.use_knobs(*ctx.knobs):
+            grads = chunked_delta_rule_bwd(res, (go, gs))
         out = []
         for g, like, need in zip(grads, ctx.like, ctx.needs_input_grad[:5]):
             out.append(g.to(device=like[1], dtype=like[0]) if (like is not None and need) else None)
@@ -364,6 +368,42 @@ def _validate_cu(cu_host: np.ndarray, total: int) -> None:
         raise KernelError("cu_seqlens must be non-decreasing")
 
 
+# Per-device flag words of the device-side cu_seqlens check (pm_varlen_check).
+_VARLEN_FLAGS: dict = {}
+_VARLEN_BITS = {1: "cu_seqlens[0] != 0", 2: "cu_seqlens[-1] != N", 4: "decreasing offsets",
+                8: "an offset outside [0, N]"}
+
+
+def _varlen_flag(device) -> torch.Tensor:
+    flag = _VARLEN_FLAGS.get(device)
+    if flag is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise KernelError("the device-side cu_seqlens check keeps one flag word per device: run "
+                              "check_varlen(device) (or one varlen call) there before capturing a graph")
+        flag = torch.zeros(1, dtype=torch.int32, device=device)
+        _VARLEN_FLAGS[device] = flag
+    return flag
+
+
+def check_varlen(device=None) -> None:
+    """Surface what the device-side checks of ``chunked_delta_rule_varlen`` found.
+
+    A ``cu_seqlens`` tensor already on the GPU is checked by a kernel on the call's
+    stream (no host copy, no synchronisation; graph-capturable), which records any
+    malformed offsets in a per-device flag word. This synchronises with the device,
+    clears the flag and raises ``KernelError`` naming what was found since the last
+    check. (The forward kernels clamp every segment into [0, N] themselves, so bad
+    offsets never reach outside the buffers.)
+    """
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    flag = _varlen_flag(dev)
+    bits = int(flag.item())
+    if bits:
+        flag.zero_()
+        found = ", ".join(msg for b, msg in _VARLEN_BITS.items() if bits & b)
+        raise KernelError(f"a device cu_seqlens passed to chunked_delta_rule_varlen was malformed: {found}")
+
+
 def chunked_delta_rule_varlen(q, k, v, beta, cu_seqlens, state=None, config=None, *,
                               out_dtype=None):
     """Packed batch of independent sequences, state reset at every boundary.
@@ -373,7 +413,16 @@ def chunked_delta_rule_varlen(q, k, v, beta, cu_seqlens, state=None, config=None
     state: None (zeros) or (n_seqs, H, D, D) initial states.
     Returns ``(output, final_states)`` with output shaped like q and
     final_states (n_seqs, H, D, D) fp32. Each segment equals a B=1
-    ``chunked_delta_rule`` call on that segment alone, bit for bit.
+    ``chunked_delta_rule`` call on that segment alone, bit for bit, when both
+    calls run the same kernel form (``pm_delta_set_path`` 1, 2 or 3; the default
+    picks the form from a call's (sequence, head) count, and two forms agree within
+    the bf16 bound).
+
+    ``cu_seqlens`` on the host (NumPy, a CPU tensor) is validated here before any
+    device work. A GPU tensor (int32, or int64 converted on the device) is never
+    copied to the host: a kernel on the call's stream checks it and records what it
+    finds for ``check_varlen`` to report, so the call stays free of synchronisation
+    and can be captured in a graph.
     """
     cfg = LinearAttnConfig() if config is None else config
     chunk = _check_chunk(cfg)
@@ -391,17 +440,27 @@ def chunked_delta_rule_varlen(q, k, v, beta, cu_seqlens, state=None, config=None
         raise KernelError(f"beta shape {bs} != {(n_tok, heads)}")
     if dim > _native.MAX_D:
         raise KernelError(f"head dimension {dim} exceeds the supported maximum {_native.MAX_D}")
-    if isinstance(cu_seqlens, torch.Tensor):
-        cu_host = cu_seqlens.detach().cpu().numpy()
+    cu_on_dev = isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.device.type == "cuda"
+    if cu_on_dev:
+        if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 1:
+            raise KernelError("cu_seqlens must be a 1-D array of n_seqs + 1 offsets")
+        if cu_seqlens.dtype not in (torch.int32, torch.int64):
+            raise KernelError(f"cu_seqlens must be an integer array, got {cu_seqlens.dtype}")
+        if n_tok >= 2**31:
+            raise KernelError("cu_seqlens exceeds int32")
+        n_seqs = cu_seqlens.numel() - 1
     else:
-        cu_host = np.asarray(cu_seqlens)
-    if not np.issubdtype(cu_host.dtype, np.integer):
-        raise KernelError(f"cu_seqlens must be an integer array, got {cu_host.dtype}")
-    cu_host = cu_host.astype(np.int64)
-    _validate_cu(cu_host, n_tok)
-    if cu_host[-1] >= 2**31:
-        raise KernelError("cu_seqlens exceeds int32")
-    n_seqs = cu_host.size - 1
+        if isinstance(cu_seqlens, torch.Tensor):
+            cu_host = cu_seqlens.detach().numpy()
+        else:
+            cu_host = np.asarray(cu_seqlens)
+        if not np.issubdtype(cu_host.dtype, np.integer):
+            raise KernelError(f"cu_seqlens must be an integer array, got {cu_host.dtype}")
+        cu_host = cu_host.astype(np.int64)
+        _validate_cu(cu_host, n_tok)
+        if cu_host[-1] >= 2**31:
+            raise KernelError("cu_seqlens exceeds int32")
+        n_seqs = cu_host.size - 1
     if state is not None and _shape(state) != (n_seqs, heads, dim, dim):
         raise KernelError(f"state shape {_shape(state)} != {(n_seqs, heads, dim, dim)}")
 
@@ -416,7 +475,13 @@ def chunked_delta_rule_varlen(q, k, v, beta, cu_seqlens, state=None, config=None
         vd = call.dev(v, cdt).reshape(n_tok, heads, dim)
         bd = call.dev(beta, torch.float32).reshape(n_tok, heads)
         sd = call.dev(state, torch.float32)
-        cu = torch.from_numpy(cu_host.astype(np.int32)).to(call.device)
+        if cu_on_dev:
+            cu = cu_seqlens.to(torch.int32).contiguous()
+            _native.check(_native.lib().pm_varlen_check(_ptr(cu), n_seqs, n_tok,
+                                                        _varlen_flag(call.device).data_ptr(),
+                                                        _stream(call.device)))
+        else:
+            cu = torch.from_numpy(cu_host.astype(np.int32)).to(call.device)
         o = torch.empty((n_tok, heads, dim), dtype=odt, device=call.device)
         s_out = torch.empty((n_seqs, heads, dim, dim), dtype=torch.float32, device=call.device)
         nbytes = _native.lib().pm_delta_varlen_workspace_bytes(n_seqs, n_tok, heads, dim, _code(cdt))
@@ -562,6 +627,7 @@ __all__ = [
     "chunked_delta_rule_fwd",
     "chunked_delta_rule_bwd",
     "chunked_delta_rule_varlen",
+    "check_varlen",
     "delta_rule_step",
     "chunked_gated_delta_rule",
     "gated_delta_rule_step",

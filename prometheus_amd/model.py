@@ -82,6 +82,9 @@ class _LinearAttention(torch.autograd.Function):
         o, s_out = _run_linear_attention(qd, kd, vd, sd, cdt, qd.device)
         ctx.save_for_backward(qd, kd, vd, sd)
         ctx.cdt = cdt
+        # the library's kernel knobs are per thread and autograd may run the backward on
+        # another thread: the backward runs under the forward caller's selection
+        ctx.knobs = _native.knobs()
         return o, s_out
 
     @staticmethod
@@ -96,7 +99,8 @@ class _LinearAttention(torch.autograd.Function):
             (qd.shape[0], qd.shape[2], qd.shape[3], qd.shape[3]), dtype=torch.float32, device=qd.device)
         res = _DeltaResidual(q=qn.detach().to(ctx.cdt), k=kn.detach().to(ctx.cdt), v=vd, beta=ones,
                              state0=s0, chunk=64)
-        gqn, gkn, gv, _, gs0 = chunked_delta_rule_bwd(res, (go, gs))
+        with _native.use_knobs(*ctx.knobs):
+            gqn, gkn, gv, _, gs0 = chunked_delta_rule_bwd(res, (go, gs))
         gq, gk = torch.autograd.grad((qn, kn), (qf, kf), (gqn, gkn))
         need = ctx.needs_input_grad
         return (gq.to(qd.dtype) if need[0] else None, gk.to(kd.dtype) if need[1] else None,

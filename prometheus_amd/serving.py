@@ -13,6 +13,10 @@ host memory. ``LinearStateCache`` is that pool on one GPU:
 * ``alloc`` / ``free`` / ``reset``: slot bookkeeping on the host;
 * ``prefill``: runs a prompt through the forward (the chunked MFMA kernel for
   bf16 with D in {64, 128}), starting from and ending in the requests' slots;
+  with the slots and ``cu_seqlens`` as GPU tensors it never synchronises with
+  the host, so it can be captured in a HIP graph (an out-of-range device slot
+  computes from a zero state into a spare slot past the pool's end, leaves the
+  pool untouched, and is reported by ``check_slots``);
 * ``decode``: one token per request, in place, through ``pm_delta_step_slots``
   (allocation-free with ``out=``, no host synchronisation, so it can be
   captured in a HIP graph with a fixed slot tensor whose contents change
@@ -41,8 +45,11 @@ class LinearStateCache:
         if device is None:
             device = torch.device("cuda", torch.cuda.current_device())
         self.n_layers, self.n_slots, self.heads, self.dim = n_layers, n_slots, heads, dim
-        self.pool = torch.zeros((n_layers, n_slots, heads, dim, dim), dtype=torch.float32,
-                                device=device)
+        # one spare slot past the end: out-of-range device slot indices land there
+        self._pool = torch.zeros((n_layers, n_slots + 1, heads, dim, dim), dtype=torch.float32,
+                                 device=device)
+        self.pool = self._pool[:, :n_slots]
+        self._bad_slot = torch.zeros(1, dtype=torch.int32, device=device)
         # a min-heap: alloc hands out the lowest free slots, so that a batch admitted in
         # order decodes through an increasing slot table, which walks the pool in address
         # order (at cfg4, 0.71 of HBM against 0.69 for a random table)
@@ -73,7 +80,7 @@ class LinearStateCache:
 
     def reset(self, slots) -> None:
         idx = self._index(slots)
-        self.pool[:, idx] = 0.0
+        self._pool[:, idx] = 0.0
 
     # ---- compute ----
     def prefill(self, layer: int, slots, q, k, v, beta, cu_seqlens=None, config=None):
@@ -81,18 +88,28 @@ class LinearStateCache:
 
         Fixed length: q, k, v ``(n, T, H, D)``, beta ``(n, T, H)``, one request per
         row. Packed: q, k, v ``(1, N, H, D)`` with ``cu_seqlens`` ``(n + 1,)``.
-        Returns the output ``(.., H, D)`` fp32.
+        Returns the output ``(.., H, D)`` fp32. ``slots`` may be a list of ints or a
+        GPU int tensor; with GPU ``slots`` and ``cu_seqlens`` nothing here waits for
+        the device (see ``check_slots`` and ``kernels.check_varlen``).
         """
         self._check_layer(layer)
         idx = self._index(slots)
         self._check_cuda(q, k, v, beta)
-        s0 = self.pool[layer, idx]  # gathered copy (n, H, D, D)
+        self._pool[layer, self.n_slots].zero_()  # the spare slot: a fresh state
+        s0 = self._pool[layer, idx]  # gathered copy (n, H, D, D)
         if cu_seqlens is None:
             o, s = kernels.chunked_delta_rule(q, k, v, beta, s0, config)
         else:
             o, s = kernels.chunked_delta_rule_varlen(q, k, v, beta, cu_seqlens, s0, config)
-        self.pool[layer, idx] = s
+        self._pool[layer, idx] = s
         return o
+
+    def check_slots(self) -> None:
+        """Raise ``ValueError`` if a GPU slot tensor given to ``prefill`` or ``reset`` since
+        the last check held an index outside ``[0, n_slots)`` (synchronises; clears)."""
+        if int(self._bad_slot.item()):
+            self._bad_slot.zero_()
+            raise ValueError(f"a device slot index was outside [0, {self.n_slots})")
 
     def decode(self, layer: int, slots: torch.Tensor, q, k, v, beta, out=None):
         """One token per request: q, k, v ``(B, H, D)``, beta ``(B, H)``, ``slots``
@@ -131,7 +148,7 @@ class LinearStateCache:
         idx = self._index(slots)
         host = torch.empty((self.n_layers, len(idx), self.heads, self.dim, self.dim),
                            dtype=torch.float32, pin_memory=True)
-        host.copy_(self.pool[:, idx])
+        host.copy_(self._pool[:, idx])
         return host
 
     def swap_in(self, slots, saved: torch.Tensor) -> None:
@@ -139,7 +156,7 @@ class LinearStateCache:
         want = (self.n_layers, len(idx), self.heads, self.dim, self.dim)
         if tuple(saved.shape) != want:
             raise ValueError(f"saved states {tuple(saved.shape)} != {want}")
-        self.pool[:, idx] = saved.to(self.pool.device, dtype=torch.float32)
+        self._pool[:, idx] = saved.to(self._pool.device, dtype=torch.float32)
 
     # ---- helpers ----
     def _ids(self, slots) -> list[int]:
@@ -150,7 +167,17 @@ class LinearStateCache:
         return ids
 
     def _index(self, slots) -> torch.Tensor:
-        return torch.tensor(self._ids(slots), dtype=torch.long, device=self.pool.device)
+        if isinstance(slots, torch.Tensor) and slots.device.type == "cuda":
+            # checked on the device: an index outside [0, n_slots) becomes the spare slot
+            if slots.dim() != 1 or slots.dtype not in (torch.int32, torch.int64):
+                raise ValueError("a GPU slot tensor must be 1-D int32 or int64")
+            if slots.device != self._pool.device:
+                raise ValueError("slots must be on the pool's device")
+            idx = slots.long()
+            bad = (idx < 0) | (idx >= self.n_slots)
+            self._bad_slot.bitwise_or_(bad.any().to(torch.int32))
+            return torch.where(bad, torch.full_like(idx, self.n_slots), idx)
+        return torch.tensor(self._ids(slots), dtype=torch.long, device=self._pool.device)
 
     def _check_layer(self, layer: int) -> None:
         if not 0 <= layer < self.n_layers:

@@ -470,3 +470,26 @@ def test_noalloc_backward_rejects_sizes_beyond_its_scratch():
     assert L.pm_delta_bwd_noalloc(*ptrs, 1, 8, 1, 8, 7, None) == _native.E_DTYPE
     # nothing to do: B*H == 0 returns before any device work
     assert L.pm_delta_bwd_noalloc(*([None] * 12), 0, 8, 1, 8, _native.DTYPE_F32, None) == 0
+
+
+def test_knobs_read_and_scoped_set():
+    """knobs() reads this thread's (path, tile) without changing them; use_knobs sets both
+    for a block and restores them, also when the block raises; another thread keeps its own."""
+    import threading
+
+    base = _native.knobs()
+    assert _native.knobs() == base
+    with _native.use_knobs(2, 16):
+        assert _native.knobs() == (2, 16)
+        seen = []
+        t = threading.Thread(target=lambda: seen.append(_native.knobs()))
+        t.start()
+        t.join()
+        assert seen == [(0, 0)]  # a fresh thread starts at the defaults
+    assert _native.knobs() == base
+    try:
+        with _native.use_knobs(1, 32):
+            raise KeyError("inside")
+    except KeyError:
+        pass
+    assert _native.knobs() == base

@@ -22,7 +22,7 @@ import pytest
 import torch
 
 from oracle import delta_oracle as ref
-from prometheus_amd import kernels, model, synth
+from prometheus_amd import _native, kernels, model, synth
 from tests.parity import assert_bf16_parity, assert_f32_parity
 
 pytestmark = pytest.mark.gpu
@@ -139,6 +139,37 @@ def test_autograd_bf16_chunked_kernel():
     exp = ref.delta_vjp(x.q, x.k, x.v, x.beta, _np(go), _np(gs), x.s0)
     for name, got, e in zip(("gq", "gk", "gv", "gbeta", "gstate"), direct, exp):
         assert_bf16_parity(_np(got), e, f"bf16 autograd {name}")
+
+
+def test_autograd_backward_runs_under_the_callers_path():
+    """The path and tile knobs are per thread, and torch autograd runs a CUDA backward on
+    its device thread: the backward must still run the kernels the caller selected. With
+    path 1 (per-token kernels) around the forward, the gradients are the per-token fp32
+    backward's bits, not the chunked bf16 backward's (which differ from them)."""
+    x = synth.fwd_inputs((1, 100, 2, 128), seed=17, dtype="bf16", s0_std=0.02)
+
+    def bf(bits):
+        return torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda().requires_grad_(True)
+
+    q, k, v = bf(x.q_bits), bf(x.k_bits), bf(x.v_bits)
+    beta, s0 = _leaf(x.beta), _leaf(x.s0)
+    rng = np.random.default_rng(18)
+    go = torch.from_numpy(rng.standard_normal(q.shape).astype(np.float32)).cuda()
+    gs = torch.from_numpy(rng.standard_normal(x.s0.shape).astype(np.float32) * 0.05).cuda()
+    res = kernels._DeltaResidual(q=q.detach(), k=k.detach(), v=v.detach(), beta=beta.detach(),
+                                 state0=s0.detach(), chunk=64)
+    chunked = kernels.chunked_delta_rule_bwd(res, (go, gs))
+    old = _native.set_path(1)
+    try:
+        per_token = kernels.chunked_delta_rule_bwd(res, (go, gs))
+        y, ns = kernels.chunked_delta_rule(q, k, v, beta, s0)
+        grads = torch.autograd.grad((y, ns), (q, k, v, beta, s0), (go, gs))
+        assert _native.knobs()[0] == 1
+    finally:
+        _native.set_path(old)
+    assert not torch.equal(chunked[1], per_token[1]), "the two backwards should round differently"
+    for got, d in zip(grads, per_token):
+        assert torch.equal(got, d.to(got.dtype))
 
 
 # ---------------------------------------------------------------------------

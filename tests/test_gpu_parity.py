@@ -437,8 +437,11 @@ def _varlen_case(total, heads, dim, seed, lo=64, hi=4096):
     return x, dev, cu
 
 
-@pytest.mark.parametrize("path", [0, 1])
+@pytest.mark.parametrize("path", [0, 1, 2, 3])
 def test_varlen_segments_bitwise_equal_standalone(path):
+    """With the kernel form fixed (path 1 per-token, 2 single-stage chunked, 3 split form),
+    each varlen segment equals its standalone call bit for bit. At H = 2 the default path
+    takes the split form for both calls, so path 0 is bitwise here too."""
     x, (q, k, v, b), cu = _varlen_case(3000, 2, 128, seed=12, lo=1, hi=700)
     cu = np.concatenate([cu[:2], cu[1:2], cu[2:]]).astype(np.int32)  # add an empty segment
     with _path(path):
@@ -450,6 +453,30 @@ def test_varlen_segments_bitwise_equal_standalone(path):
                                                 b[None, a:z])
             assert torch.equal(out[a:z], oi[0]), f"segment {i} [{a}, {z})"
             assert torch.equal(st[i], si[0]), f"segment {i} state"
+
+
+def test_cfg2_default_path_segments_vs_standalone():
+    """cfg2 (10 sequences x 16 heads) under the default path. The form is chosen per call
+    from its (sequence, head) count: the varlen call (160 pairs, 32-column tiles) runs the
+    single-stage kernel, while each standalone segment (16 pairs) runs the split form.
+    The two forms round differently, so the segments agree within the bf16 bound, not
+    bitwise; with the single-stage form forced (path 2) they agree bit for bit."""
+    c = synth.CONFIGS[2]
+    x, (q, k, v, b), cu = _varlen_case(c["total"], c["H"], c["D"], seed=2, lo=c["lo"], hi=c["hi"])
+    cu_d = torch.from_numpy(cu).cuda()
+    out0, st0 = kernels.chunked_delta_rule_varlen(q, k, v, b, cu_d)
+    with _path(2):
+        out2, st2 = kernels.chunked_delta_rule_varlen(q, k, v, b, cu_d)
+    assert torch.equal(out0, out2) and torch.equal(st0, st2), "default varlen call is the single-stage form"
+    for i in range(cu.size - 1):
+        a, z = int(cu[i]), int(cu[i + 1])
+        seg = (q[None, a:z], k[None, a:z], v[None, a:z], b[None, a:z])
+        oi, si = kernels.chunked_delta_rule(*seg)
+        assert_bf16_parity(_np(oi[0]), _np(out0[a:z]), f"segment {i} O, default path")
+        assert_bf16_parity(_np(si[0]), _np(st0[i]), f"segment {i} S, default path")
+        with _path(2):
+            oi2, si2 = kernels.chunked_delta_rule(*seg)
+        assert torch.equal(oi2[0], out2[a:z]) and torch.equal(si2[0], st2[i]), f"segment {i}, path 2"
 
 
 def test_cfg2_varlen_vs_c_oracle():

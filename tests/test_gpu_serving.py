@@ -178,3 +178,81 @@ def test_graph_captured_decode_replays():
         torch.cuda.synchronize()
         assert torch.equal(got_out, want), rep
         assert torch.equal(got_pool, cache.pool), rep
+
+
+def test_graph_captured_packed_prefill_replays():
+    """prefill with GPU slots and GPU cu_seqlens under HIP graph capture: nothing in it
+    synchronises with the host (the offsets are checked on the device), and every replay,
+    with new tokens, offsets and slots written in place between replays, equals the eager
+    prefill of the same inputs bit for bit (outputs and the whole pool)."""
+    rng = np.random.default_rng(51)
+    h, d, n_slots, n_tok = 2, 128, 8, 400
+    cache = serving.LinearStateCache(1, n_slots, h, d)
+    cache.pool.copy_(torch.from_numpy(rng.standard_normal(cache.pool.shape).astype(np.float32) * 0.02))
+    slots = torch.tensor([1, 4, 6], dtype=torch.int64, device="cuda")
+    cu = torch.tensor([0, 150, 151, n_tok], dtype=torch.int32, device="cuda")
+
+    def tokens(seed):
+        x = synth.fwd_inputs((1, n_tok, h, d), seed=seed, dtype="bf16")
+        bf = lambda b: torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(torch.bfloat16).cuda()
+        return bf(x.q_bits), bf(x.k_bits), bf(x.v_bits), torch.from_numpy(x.beta).cuda()
+
+    q, k, v, beta = tokens(51)
+    kernels.check_varlen()  # the device flag word exists before capture
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        cache.prefill(0, slots, q, k, v, beta, cu_seqlens=cu)  # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        o_graph = cache.prefill(0, slots, q, k, v, beta, cu_seqlens=cu)
+    for rep in range(4):
+        nq, nk, nv, nb = tokens(60 + rep)
+        q.copy_(nq), k.copy_(nk), v.copy_(nv), beta.copy_(nb)
+        a = int(rng.integers(0, n_tok))
+        z = int(rng.integers(a, n_tok + 1))
+        cu.copy_(torch.tensor([0, a, z, n_tok], dtype=torch.int32))
+        slots.copy_(torch.from_numpy(rng.permutation(n_slots)[:3].astype(np.int64)))
+        pool_before = cache.pool.clone()
+        graph.replay()
+        torch.cuda.synchronize()
+        got_o, got_pool = o_graph.clone(), cache.pool.clone()
+        cache.pool.copy_(pool_before)
+        want = cache.prefill(0, slots, q, k, v, beta, cu_seqlens=cu)
+        torch.cuda.synchronize()
+        assert torch.equal(got_o, want), rep
+        assert torch.equal(got_pool, cache.pool), rep
+    kernels.check_varlen()
+    cache.check_slots()
+
+
+def test_device_offsets_and_slots_are_checked_lazily():
+    """A malformed GPU cu_seqlens is reported by check_varlen (then cleared); an out-of-range
+    GPU slot computes into the spare slot, leaves every pool slot but the valid ones
+    untouched, and is reported by check_slots."""
+    rng = np.random.default_rng(52)
+    h, d, n_slots, n_tok = 2, 64, 6, 200
+    cache = serving.LinearStateCache(1, n_slots, h, d)
+    cache.pool.copy_(torch.from_numpy(rng.standard_normal(cache.pool.shape).astype(np.float32) * 0.02))
+    x = synth.fwd_inputs((1, n_tok, h, d), seed=52, dtype="bf16")
+    bf = lambda b: torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(torch.bfloat16).cuda()
+    q, k, v, beta = bf(x.q_bits), bf(x.k_bits), bf(x.v_bits), torch.from_numpy(x.beta).cuda()
+    kernels.check_varlen()
+    cache.check_slots()
+    for bad, what in (([0, 120, 80, n_tok], "decreasing"), ([5, 80, 120, n_tok], r"cu_seqlens\[0\]"),
+                      ([0, 80, 120, n_tok - 1], r"cu_seqlens\[-1\]"), ([0, -3, 120, n_tok], "outside")):
+        cache.prefill(0, [0, 1, 2], q, k, v, beta,
+                      cu_seqlens=torch.tensor(bad, dtype=torch.int32, device="cuda"))
+        with pytest.raises(kernels.KernelError, match=what):
+            kernels.check_varlen()
+        kernels.check_varlen()  # cleared
+    good = torch.tensor([0, 70, 71, n_tok], dtype=torch.int32, device="cuda")
+    before = cache.pool.clone()
+    cache.prefill(0, torch.tensor([3, 99, 5], device="cuda"), q, k, v, beta, cu_seqlens=good)
+    with pytest.raises(ValueError, match="outside"):
+        cache.check_slots()
+    cache.check_slots()  # cleared
+    changed = {i for i in range(n_slots) if not torch.equal(before[0, i], cache.pool[0, i])}
+    assert changed == {3, 5}

@@ -173,6 +173,34 @@ __device__ __forceinline__ void zero_upper_half(uint16_t* buf, int q, int lane) 
     *reinterpret_cast<u32x2_t*>(buf + q * 512 + lane * 8 + 4) = z;
 }
 
+// I + X in bf16 operand form for a strictly lower X (or its transpose) held as a 16x16
+// accumulator tile converted with cvt4 (lane (g, l16) holds rows 4g + [0, 4) of column
+// l16; halves (r0, r1) and (r2, r3)).  X's diagonal entries are exact zeros (+0 or -0),
+// so cvt4(X + I) equals cvt4(X) with the diagonal halves replaced by bf16 1.0 (0x3F80):
+// two bit operations per word instead of four adds and two conversions.
+struct EyeBits {
+    u32x2_t one;   // 0x3F80 in the halves on the diagonal
+    u32x2_t keep;  // 0xFFFF in the halves off the diagonal
+};
+__device__ __forceinline__ EyeBits eye_bits(int lane) {
+    const int r = (lane & 15) - 4 * (lane >> 4);  // the component on the diagonal, if in [0, 4)
+    EyeBits e = {{0u, 0u}, {~0u, ~0u}};
+    if (r >= 0 && r < 4) {
+        const int sh = 16 * (r & 1);
+        if (r < 2) {
+            e.one.x = 0x3F80u << sh;
+            e.keep.x = ~(0xFFFFu << sh);
+        } else {
+            e.one.y = 0x3F80u << sh;
+            e.keep.y = ~(0xFFFFu << sh);
+        }
+    }
+    return e;
+}
+// (Plain C on purpose: these words feed MFMA operands, and hipcc inserts the wait states
+// between a VALU write and an MFMA read only for instructions it generated itself.)
+__device__ __forceinline__ u32x2_t with_eye(u32x2_t x, const EyeBits& e) { return (x & e.keep) | e.one; }
+
 // Wave-uniform values made visibly uniform (SGPRs), so that buffer
 // descriptors and role branches are scalar rather than per-lane.
 __device__ __forceinline__ unsigned uniform(unsigned x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -256,9 +284,7 @@ __device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const f
         gu[4] = mfma32(f[1][kb], f[3][kb], gu[4]);  // (1,3)
         gu[5] = mfma32(f[2][kb], f[3][kb], gu[5]);  // (2,3)
     }
-    f32x4_t eye;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) eye[r] = (4 * lg + r == l16) ? 1.f : 0.f;
+    const EyeBits eyeb = eye_bits(lane);
     // diagonal inverses D_b = (I+N)(I+N^2)(I+N^4)(I+N^8), N = -L_b (dd = D_b, ddt = D_b^T),
     // one level at a time over the four independent blocks
     u32x2_t cn[4], cnt[4];
@@ -285,16 +311,12 @@ __device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const f
     for (int b = 0; b < 4; ++b) {
         cn2[b] = cvt4(n2[b]);
         cn2t[b] = cvt4(n2t[b]);
-        ci2[b] = cvt4(n2[b] + eye);
+        ci2[b] = with_eye(cn2[b], eyeb);
     }
     f32x4_t n4[4], n4t[4], ft[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-        // cet = (I + N)^T as an accumulator, rebuilt from cnt's source values
-        f32x4_t nt;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) nt[r] = (l16 > 4 * lg + r) ? -bc[b] * gd[b][r] : 0.f;
-        cet[b] = cvt4(nt + eye);
+        cet[b] = with_eye(cnt[b], eyeb);  // (I + N)^T
         n4[b] = mfma16(cn2t[b], cn2[b], zero);
         n4t[b] = mfma16(cn2[b], cn2t[b], zero);
         ft[b] = mfma16(ci2[b], cet[b], zero);       // ((I+N)(I+N^2))^T
@@ -304,7 +326,7 @@ __device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const f
     for (int b = 0; b < 4; ++b) {
         cn4[b] = cvt4(n4[b]);
         cn4t[b] = cvt4(n4t[b]);
-        ci4[b] = cvt4(n4[b] + eye);
+        ci4[b] = with_eye(cn4[b], eyeb);
         cft[b] = cvt4(ft[b]);
     }
     f32x4_t n8[4], f2t[4];
@@ -316,36 +338,39 @@ __device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const f
     f32x4_t dd[4], ddt[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-        const u32x2_t ci8 = cvt4(n8[b] + eye), cf2t = cvt4(f2t[b]);
+        const u32x2_t ci8 = with_eye(cvt4(n8[b]), eyeb), cf2t = cvt4(f2t[b]);
         dd[b] = mfma16(cf2t, ci8, zero);            // ...(I+N^8)
         ddt[b] = mfma16(ci8, cf2t, zero);
     }
-    // A_ik as an A operand: upper tile (k, i) of K K^T, rows scaled by beta_{16i+l16}
-    auto a_op = [&](int x, int i) { return cvt4(bc[i] * gu[x]); };
+    // -A_ik as an A operand: upper tile (k, i) of K K^T, rows scaled by -beta_{16i+l16} (the
+    // minus folded in here, so that every product below comes out with T's sign; rounding
+    // to nearest is symmetric, so negating an operand negates the rounded result exactly)
+    auto a_op = [&](int x, int i) { return cvt4(-bc[i] * gu[x]); };
     const u32x2_t cd0 = cvt4(dd[0]), cd1 = cvt4(dd[1]), cd2 = cvt4(dd[2]);
     const u32x2_t cdt1 = cvt4(ddt[1]), cdt2 = cvt4(ddt[2]), cdt3 = cvt4(ddt[3]);
     const u32x2_t a10 = a_op(0, 1), a20 = a_op(1, 2), a21 = a_op(2, 2);
     const u32x2_t a30 = a_op(3, 3), a31 = a_op(4, 3), a32 = a_op(5, 3);
-    // T_ij = -D_i Z_ij with Z_ij = sum_k A_ik T_kj; cdt_i is D_i as an A operand and
-    // D_i^T as a B operand, so -mfma(Z, cdt_i) is T_ij^T (what the packed store takes)
+    // T_ij = D_i Z_ij with Z_ij = -sum_k A_ik T_kj (the a_op operands carry the minus);
+    // cdt_i is D_i as an A operand and D_i^T as a B operand, so mfma(Z, cdt_i) is T_ij^T
+    // (what the packed store takes)
     // level 1
     const u32x2_t z10 = cvt4(mfma16(a10, cd0, zero));
     const u32x2_t z21 = cvt4(mfma16(a21, cd1, zero));
     const u32x2_t z32 = cvt4(mfma16(a32, cd2, zero));
-    const u32x2_t cx10 = cvt4(-mfma16(cdt1, z10, zero));
-    const u32x2_t cx21 = cvt4(-mfma16(cdt2, z21, zero));
-    tb[1] = -mfma16(z10, cdt1, zero);  // (1,0)
-    tb[4] = -mfma16(z21, cdt2, zero);  // (2,1)
-    tb[8] = -mfma16(z32, cdt3, zero);  // (3,2)
+    const u32x2_t cx10 = cvt4(mfma16(cdt1, z10, zero));
+    const u32x2_t cx21 = cvt4(mfma16(cdt2, z21, zero));
+    tb[1] = mfma16(z10, cdt1, zero);  // (1,0)
+    tb[4] = mfma16(z21, cdt2, zero);  // (2,1)
+    tb[8] = mfma16(z32, cdt3, zero);  // (3,2)
     // level 2
     const u32x2_t z20 = cvt4(mfma16(a21, cx10, mfma16(a20, cd0, zero)));
     const u32x2_t z31 = cvt4(mfma16(a32, cx21, mfma16(a31, cd1, zero)));
-    const u32x2_t cx20 = cvt4(-mfma16(cdt2, z20, zero));
-    tb[3] = -mfma16(z20, cdt2, zero);  // (2,0)
-    tb[7] = -mfma16(z31, cdt3, zero);  // (3,1)
+    const u32x2_t cx20 = cvt4(mfma16(cdt2, z20, zero));
+    tb[3] = mfma16(z20, cdt2, zero);  // (2,0)
+    tb[7] = mfma16(z31, cdt3, zero);  // (3,1)
     // level 3
     const u32x2_t z30 = cvt4(mfma16(a32, cx20, mfma16(a31, cx10, mfma16(a30, cd0, zero))));
-    tb[6] = -mfma16(z30, cdt3, zero);  // (3,0)
+    tb[6] = mfma16(z30, cdt3, zero);  // (3,0)
     tb[0] = ddt[0];
     tb[2] = ddt[1];
     tb[5] = ddt[2];

@@ -127,6 +127,110 @@ def time_launches(stream, fn, n):
     return e0.elapsed_time(e1) / n
 
 
+def _time_calls(torch, stream, f, calls):
+    """Mean ms per call over `calls` back-to-back calls (one event pair), after 2 untimed."""
+    for i in range(2):
+        f(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(calls):
+        f(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / calls
+
+
+def _roofline(nbytes, ms):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}
+
+
+def time_cfg3(torch, lib, _native, dev, stream, calls=8):
+    """cfg3, the long-context single-GPU share: B1 H32 T32768 D128 bf16 with S0 ~ N(0, 0.02).
+    The default path (with the workspace the Python layer passes) and the single-stage
+    kernel forced (path 2); two input sets alternate."""
+    B, T, H, D = 1, 32768, 32, 128
+    print(f"[bench] cfg3 B{B} T{T} H{H} D{D}", file=sys.stderr, flush=True)
+    sets = [make_inputs(torch, B, T, H, D, seed, dev) for seed in (31, 32)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(33)
+    s0 = (torch.randn((B, H, D, D), generator=g, device=dev) * 0.02).contiguous()
+    o = torch.empty((B, T, H, D), dtype=torch.float32, device=dev)
+    s = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+    nws = lib.pm_delta_workspace_bytes(B, T, H, D, _native.DTYPE_BF16)
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+
+    def f(i, use_ws=True):
+        q, k, v, beta = sets[i % 2]
+        rc = lib.pm_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), s0.data_ptr(),
+                              o.data_ptr(), s.data_ptr(), B, T, H, D, _native.DTYPE_BF16, _native.DTYPE_F32,
+                              CHUNK, ws.data_ptr() if use_ws and nws else None, nws if use_ws else 0,
+                              stream.cuda_stream)
+        _native.check(rc)
+
+    ms_default = _time_calls(torch, stream, f, calls)
+    old = _native.set_path(2)
+    try:
+        ms_single = _time_calls(torch, stream, lambda i: f(i, False), calls)
+    finally:
+        _native.set_path(old)
+    nb = fwd_bytes(B, T, H, D, s0=True)
+    tile = 16 if B * H * (D // 32) < 256 else 32  # the chunked kernel's d_v tile rule
+    return {
+        "workload": "cfg3 forward: B1 H32 T32768 D128 bf16, S0 ~ N(0, 0.02), fp32 O and S",
+        "calls": calls,
+        "kernel_us": ms_default * 1e3,
+        "path": "split form (T by a parallel pass into the workspace, then the recurrence)" if nws
+                else "single-stage chunked kernel",
+        "d_v_tile": tile,
+        "tokens_per_s": B * T / (ms_default * 1e-3),
+        "algorithmic_bytes": nb,
+        "roofline": _roofline(nb, ms_default),
+        "single_stage": {"kernel_us": ms_single * 1e3, "roofline": _roofline(nb, ms_single)},
+    }
+
+
+def time_cfg2(torch, lib, _native, synth, dev, stream, calls=10):
+    """cfg2, the packed variable-length batch: 16384 tokens, H16 D128 bf16, lengths drawn
+    from U[64, 4096] (seed 2) and concatenated through cu_seqlens (on the device)."""
+    c = synth.CONFIGS[2]
+    N, H, D = c["total"], c["H"], c["D"]
+    lens = synth.varlen_lengths(N, c["lo"], c["hi"], seed=2)
+    cu = torch.from_numpy(synth.cu_seqlens(lens)).to(dev)
+    n_seqs = len(lens)
+    print(f"[bench] cfg2 varlen N{N} H{H} D{D}, {n_seqs} sequences", file=sys.stderr, flush=True)
+    sets = [make_inputs(torch, 1, N, H, D, seed, dev) for seed in (21, 22)]
+    o = torch.empty((1, N, H, D), dtype=torch.float32, device=dev)
+    s = torch.empty((n_seqs, H, D, D), dtype=torch.float32, device=dev)
+    nws = lib.pm_delta_varlen_workspace_bytes(n_seqs, N, H, D, _native.DTYPE_BF16)
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+
+    def f(i):
+        q, k, v, beta = sets[i % 2]
+        rc = lib.pm_delta_fwd_varlen(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), cu.data_ptr(),
+                                     n_seqs, N, None, o.data_ptr(), s.data_ptr(), H, D, _native.DTYPE_BF16,
+                                     _native.DTYPE_F32, CHUNK, ws.data_ptr() if nws else None, nws,
+                                     stream.cuda_stream)
+        _native.check(rc)
+
+    ms = _time_calls(torch, stream, f, calls)
+    E = N * H * D
+    nb = 3 * E * 2 + 4 * N * H + 4 * E + 4 * n_seqs * H * D * D + 4 * (n_seqs + 1)
+    return {
+        "workload": f"cfg2 varlen forward: {N} packed tokens, H16 D128 bf16, {n_seqs} sequences "
+                    f"(lengths U[64, 4096], seed 2), cu_seqlens int32 on the device",
+        "calls": calls,
+        "kernel_us": ms * 1e3,
+        "path": "split form" if nws else "single-stage chunked kernel",
+        "lengths": [int(x) for x in lens],
+        "longest": int(max(lens)),
+        "tokens_per_s": N / (ms * 1e-3),
+        "algorithmic_bytes": nb,
+        "roofline": _roofline(nb, ms),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -140,6 +244,8 @@ def main():
     ap.add_argument("--bwd-steps", type=int, default=3,
                     help="timed calls of the backward at cfg1 (0 skips it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-long-configs", dest="long_configs", action="store_false",
+                    help="skip the cfg3 (B1 H32 T32768, S0) and cfg2 (varlen) forward legs")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_cfg1.json"),
                     help="JSON with measured HBM bytes per launch (from rocprofv3 --pmc)")
     ap.add_argument("--mfma-counters", default=os.path.join(ROOT, "profiles", "mfma_cfg1.json"),
@@ -246,13 +352,23 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / calls
 
-    # the opt-in bf16 output (out_dtype=bf16): 273.7 MB instead of 340.8 MB per call
+    # the opt-in bf16 output (out_dtype=bf16): 273.7 MB instead of 340.8 MB per call. The
+    # shader clock of these boxes depends on the power the work draws and drifts between
+    # runs, so bf16 O is timed in rounds interleaved with fp32 O calls (medians over rounds)
     o16 = torch.empty((B, T, H, D), dtype=torch.bfloat16, device=dev)
-    b16_ms = time_fwd(_native.DTYPE_BF16, o16)
+    rounds_16, rounds_32 = [], []
+    for _ in range(5):
+        rounds_32.append(time_fwd(_native.DTYPE_F32, o, calls=10))
+        rounds_16.append(time_fwd(_native.DTYPE_BF16, o16, calls=10))
+    b16_ms = float(np.median(rounds_16))
+    f32_ms_interleaved = float(np.median(rounds_32))
     b16_bytes = fwd_bytes(B, T, H, D, s_out=2)
     bf16_out = {
         "workload": "cfg1 forward, bf16 O (pm_delta_fwd out_dtype bf16)",
+        "timing": "5 rounds of 10 calls, each round right after 10 fp32-O calls; medians",
         "kernel_us": b16_ms * 1e3,
+        "fp32_out_kernel_us_same_rounds": f32_ms_interleaved * 1e3,
+        "bf16_over_fp32": b16_ms / f32_ms_interleaved,
         "tokens_per_s": tokens / (b16_ms * 1e-3),
         "algorithmic_bytes": b16_bytes,
         "roofline": {"bound": "hbm", "achieved": b16_bytes / (b16_ms * 1e-3) / 1e9,
@@ -276,6 +392,10 @@ def main():
     split_form = {"workload": "cfg1 forward, chunked kernel in split form (path 3, prep + recurrence)",
                   "kernel_us": split_ms * 1e3,
                   "roofline_frac": nbytes / (split_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    cfg3 = cfg2 = None
+    if args.long_configs:
+        cfg3 = time_cfg3(torch, lib, _native, dev, stream)
+        cfg2 = time_cfg2(torch, lib, _native, synth, dev, stream)
     launch(last)  # the output the parity check reads
     torch.cuda.synchronize()
 
@@ -678,6 +798,8 @@ def main():
         "decode": decode,
         "bf16_out": bf16_out,
         "split_form": split_form,
+        "cfg3": cfg3,
+        "cfg2": cfg2,
         "model_linear_attention": model_la,
         "fp32_forward": fp32_fwd,
         "gated": gated,

@@ -140,11 +140,13 @@ int hip_fail(hipError_t e, const char* what) {
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // The split form of the chunked forward runs under path 3, and by default (path 0) where
-// the chunked kernel takes 16-column tiles: fewer (b, h) pairs than fill the GPU with
-// 32-column tiles.  There its lighter memory traffic per CU wins (measured 5-25 % faster);
-// with 32-column tiles on every CU the single-stage kernel is faster.
+// even 16-column tiles leave CUs idle: fewer than 256 workgroups of the single-stage
+// kernel (n_pairs * D / 16 < 256).  There its fully parallel T pass and lighter recurrence
+// win (measured 9-32 % faster); from 256 workgroups on, the single-stage kernel is faster
+// or level (cfg3, 256 workgroups: 656 against 706 us).
 bool split_chosen(int path, int D, long n_pairs) {
-    return path == 3 || (path == 0 && pm::chunked_pick_tile(D, n_pairs, g_tile) == 16);
+    return path == 3 || (path == 0 && pm::chunked_pick_tile(D, n_pairs, g_tile) == 16 &&
+                         n_pairs * (D / 16) < 256);
 }
 
 int check_dtypes(int in_dtype, int out_dtype) {

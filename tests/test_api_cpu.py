@@ -265,11 +265,15 @@ def test_abi_argument_validation_without_gpu():
 
 def test_forward_workspace_sizes_and_checks():
     """The split form's T workspace (6 KiB per (b, h) and chunk) is asked for exactly where
-    the forward would run that form: 16-column tiles by default, always under path 3."""
+    the forward would run that form: by default where even 16-column tiles give fewer than
+    256 workgroups (pairs * D / 16 < 256), always under path 3."""
     lib = _native.lib()
     bf16, f32 = _native.DTYPE_BF16, _native.DTYPE_F32
     per = 6 * 1024
-    assert lib.pm_delta_workspace_bytes(1, 32768, 32, 128, bf16) == 32 * 512 * per  # cfg3: 16-col tiles
+    assert lib.pm_delta_workspace_bytes(1, 32768, 32, 128, bf16) == 0  # cfg3: 256 workgroups
+    assert lib.pm_delta_workspace_bytes(1, 32768, 31, 128, bf16) == 31 * 512 * per  # 248
+    assert lib.pm_delta_workspace_bytes(1, 4096, 16, 128, bf16) == 16 * 64 * per
+    assert lib.pm_delta_workspace_bytes(4, 4096, 16, 64, bf16) == 0  # 256 workgroups at D = 64
     assert lib.pm_delta_workspace_bytes(1, 130, 2, 64, bf16) == 2 * 3 * per
     assert lib.pm_delta_workspace_bytes(4, 4096, 16, 128, bf16) == 0  # cfg1: 32-col tiles
     assert lib.pm_delta_workspace_bytes(1, 4096, 16, 256, bf16) == 0

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 10
+#define PM_DELTA_ABI_VERSION 11
 
 /* element types */
 #define PM_DTYPE_F32 0
@@ -257,6 +257,30 @@ int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
 /* Workspace bytes pm_delta_bwd needs for these shapes and in_dtype under the
  * current path setting (0 for invalid shapes, dtypes or D > 256). */
 size_t pm_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype);
+
+/*
+ * Reverse mode of pm_gated_delta_fwd (the gated delta rule, alpha = exp(g)
+ * per token and head).  No reference counterpart: the reference's model
+ * names the variant (spec/03-model.md:12) and has no code for it
+ * (PROGRESS.md:109); every primitive on its path has a VJP
+ * (kernels/__init__.py:591-658), and this is that VJP for the gated forward.
+ * Arguments as pm_delta_bwd, plus g (B, T, H) fp32, the forward's log-gates,
+ * and gg (B, T, H) fp32, dL/dg.  With P_t = alpha_t S_{t-1}, per token in
+ * reverse: y = P_t w, dL/dg_t = <G - beta_t k_t w^T, P_t>, G <- alpha_t (G -
+ * beta_t k_t w^T), the other gradients as pm_delta_bwd's.  Runs the
+ * per-token fp32 kernels (any D <= 256, fp32 or bf16 q/k/v); each 8-token
+ * checkpoint block is recomputed forward from its start state, never walked
+ * back (which would divide by alpha).  Path 2 (chunked backward required)
+ * returns PM_E_UNSUPPORTED.  workspace: pm_gated_delta_bwd_workspace_bytes.
+ */
+int pm_gated_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
+                       const float* g, const float* s0, const float* go, const float* gs, float* gq,
+                       float* gk, float* gv, float* gbeta, float* gg, float* gs0, int B, int T,
+                       int H, int D, int in_dtype, void* workspace, size_t ws_bytes, void* stream);
+
+/* Workspace bytes pm_gated_delta_bwd needs (0 for invalid shapes, dtypes or D > 256):
+ * pm_delta_bwd's per-token workspace plus, for D > 32, the partial sums of gg. */
+size_t pm_gated_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype);
 
 /*
  * pm_delta_bwd without a caller workspace and without any allocation.

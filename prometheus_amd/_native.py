@@ -18,7 +18,7 @@ import torch  # noqa: F401  (see module docstring: must precede CDLL)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpmdelta.so")
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256
@@ -48,6 +48,8 @@ EXPORTS = (
     "pm_delta_set_path",
     "pm_delta_set_tile",
     "pm_varlen_check",
+    "pm_gated_delta_bwd",
+    "pm_gated_delta_bwd_workspace_bytes",
 )
 
 _lib = None
@@ -116,6 +118,10 @@ def lib() -> ctypes.CDLL:
         L.pm_delta_set_tile.restype = i
         L.pm_varlen_check.argtypes = [vp, i, i, vp, vp]
         L.pm_varlen_check.restype = i
+        L.pm_gated_delta_bwd.argtypes = [vp] * 14 + [i] * 5 + [vp, sz, vp]
+        L.pm_gated_delta_bwd.restype = i
+        L.pm_gated_delta_bwd_workspace_bytes.argtypes = [i] * 5
+        L.pm_gated_delta_bwd_workspace_bytes.restype = sz
         got = L.pm_abi_version()
         if got != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH}: ABI version {got}, expected {ABI_VERSION}")

@@ -87,11 +87,11 @@ static BwdGeo bwd_geo(int D) {
 // of its column, DPP column sums, tokens staged 16 at a time with the next block's
 // loads in flight), writing u_t = v_t - S_{t-1}^T k_t per token (through LDS, one
 // block later) and S after every kCk-th token and after the last.
-template <int RPT, int RS, typename InT>
+template <int RPT, int RS, typename InT, bool GATED>
 __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
     const InT* __restrict__ k, const InT* __restrict__ v, const float* __restrict__ beta,
-    const float* __restrict__ s0, float* __restrict__ u_ws, float* __restrict__ ck_ws, int pair0,
-    int n_pairs, int ncg, int T, int H, int D, int vec) {
+    const float* __restrict__ gate, const float* __restrict__ s0, float* __restrict__ u_ws,
+    float* __restrict__ ck_ws, int pair0, int n_pairs, int ncg, int T, int H, int D, int vec) {
     using G = RecGeo<RPT, RS>;
     constexpr int CW = G::CW, DP = G::DP, SL = G::SL, DPL = G::DPL;
     constexpr int KB = kRecSteps, NT = kRecThreads;
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
 
     Raw4<InT> pk[NPF];
     InT pv[NPV];
-    float pb = 0.f;
+    float pb = 0.f, pg = 0.f;
     auto prefetch = [&](int t0, int nst) {
 #pragma unroll
         for (int s = 0; s < NPF; ++s) {
@@ -147,11 +147,12 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
             pv[s] = (j < nst && e2 < D) ? v[row(t0 + j) + e2] : InT(0);
         }
         if (tid < KB) pb = tid < nst ? beta[static_cast<size_t>(tok0 + t0 + tid) * H + h] : 0.f;
+        if (GATED && tid < KB) pg = tid < nst ? gate[static_cast<size_t>(tok0 + t0 + tid) * H + h] : 0.f;
     };
     auto stage = [&](float* buf) {
         float* sk = buf;
         float* sv = sk + KB * DPL;
-        float* sb = sv + 2 * KB * CW;
+        float* sb = sv + 2 * KB * CW;  // beta, then (GATED) alpha = exp(g)
 #pragma unroll
         for (int s = 0; s < NPF; ++s) {
             const int grp = s * NT + tid;
@@ -166,6 +167,7 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
 #pragma unroll
         for (int s = 0; s < NPV; ++s) sv[s * NT + tid] = to_f32(pv[s]);
         if (tid < KB) sb[tid] = pb;
+        if (GATED && tid < KB) sb[KB + tid] = expf(pg);
     };
     auto checkpoint = [&](int t) {
         float* cp = ck_p + static_cast<size_t>(t / kCk) * D * D;
@@ -191,11 +193,13 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
                 kk[4 * i] = t.x, kk[4 * i + 1] = t.y, kk[4 * i + 2] = t.z, kk[4 * i + 3] = t.w;
             }
             const float ks = col_sum<RS>(row_dot<RPT>(kk, S));
-            const float u = sv[j * CW + el] - ks;
+            // GATED: the decayed state P = alpha S enters both the prediction and the update
+            const float a = GATED ? sb[KB + j] : 1.f;
+            const float u = sv[j * CW + el] - (GATED ? a * ks : ks);
             su[j * CW + el] = u;  // the RS lanes of a column store the same bits
             const float bu = sb[j] * u;
 #pragma unroll
-            for (int i = 0; i < RPT; ++i) S[i] = fmaf(kk[i], bu, S[i]);
+            for (int i = 0; i < RPT; ++i) S[i] = fmaf(kk[i], bu, GATED ? a * S[i] : S[i]);
             // t0 is a multiple of kCk
             if ((j + 1) % kCk == 0 || t0 + j + 1 == len) checkpoint(t0 + j);
         };
@@ -235,11 +239,11 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
     }
 }
 
-template <int RPT, int RS, typename InT>
+template <int RPT, int RS, typename InT, bool GATED>
 static hipError_t launch_ckpt_t(const BwdArgs& a, float* u_ws, float* ck_ws, hipStream_t st) {
     using G = RecGeo<RPT, RS>;
     constexpr size_t kBytes = 2 * sizeof(float) * (kRecSteps * G::DPL + 2 * kRecSteps * G::CW + 4 * kRecSteps);
-    auto kern = delta_bwd_ckpt_kernel<RPT, RS, InT>;
+    auto kern = delta_bwd_ckpt_kernel<RPT, RS, InT, GATED>;
     if (kBytes > 64 * 1024) {
         // the dynamic-LDS limit is a per-device function attribute
         int dev = 0;
@@ -262,7 +266,7 @@ static hipError_t launch_ckpt_t(const BwdArgs& a, float* u_ws, float* ck_ws, hip
         const long np = a.n_pairs - p0 < per ? a.n_pairs - p0 : per;
         const dim3 grid(static_cast<unsigned>((np + 7) / 8 * 8 * ncg));
         hipLaunchKernelGGL(kern, grid, dim3(kRecThreads), kBytes, st, static_cast<const InT*>(a.k),
-                           static_cast<const InT*>(a.v), a.beta, a.s0, u_ws, ck_ws, static_cast<int>(p0),
+                           static_cast<const InT*>(a.v), a.beta, a.g, a.s0, u_ws, ck_ws, static_cast<int>(p0),
                            a.n_pairs, ncg, a.T, a.H, a.D, vec);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -272,17 +276,17 @@ static hipError_t launch_ckpt_t(const BwdArgs& a, float* u_ws, float* ck_ws, hip
 
 // RPT 8 and RS the smallest power of two with 8 RS >= D for D <= 128; RPT 16 and RS 16
 // above (the per-token forward's geometry).
-template <typename InT>
+template <typename InT, bool GATED>
 static hipError_t launch_ckpt(const BwdArgs& a, float* u_ws, float* ck_ws, hipStream_t st) {
-    if (a.D > 128) return launch_ckpt_t<16, 16, InT>(a, u_ws, ck_ws, st);
+    if (a.D > 128) return launch_ckpt_t<16, 16, InT, GATED>(a, u_ws, ck_ws, st);
     int rs = 1;
     while (8 * rs < a.D) rs <<= 1;
     switch (rs) {
-        case 1: return launch_ckpt_t<8, 1, InT>(a, u_ws, ck_ws, st);
-        case 2: return launch_ckpt_t<8, 2, InT>(a, u_ws, ck_ws, st);
-        case 4: return launch_ckpt_t<8, 4, InT>(a, u_ws, ck_ws, st);
-        case 8: return launch_ckpt_t<8, 8, InT>(a, u_ws, ck_ws, st);
-        default: return launch_ckpt_t<8, 16, InT>(a, u_ws, ck_ws, st);
+        case 1: return launch_ckpt_t<8, 1, InT, GATED>(a, u_ws, ck_ws, st);
+        case 2: return launch_ckpt_t<8, 2, InT, GATED>(a, u_ws, ck_ws, st);
+        case 4: return launch_ckpt_t<8, 4, InT, GATED>(a, u_ws, ck_ws, st);
+        case 8: return launch_ckpt_t<8, 8, InT, GATED>(a, u_ws, ck_ws, st);
+        default: return launch_ckpt_t<8, 16, InT, GATED>(a, u_ws, ck_ws, st);
     }
 }
 
@@ -306,13 +310,22 @@ __device__ __forceinline__ float slice_dot(const float (&a)[kRpt], const float (
 // when n_tiles == 1, else this tile's slot of the partial-sum buffers.
 // RSC row slices per column (column layout), RSR column slices per row (row layout), NCT
 // the tile width the geometry is sized for (the fewest threads a launch has is NCT RSC).
-template <typename InT, int RSC, int RSR, int NCT>
+//
+// GATED (log-gates g, alpha = exp(g)): with P_t = alpha_t S_{t-1} the step is
+// S_t = P_t + beta_t k_t u_t^T, and per token in reverse
+//   y = P_t w,   dL/dg_t = <G_P, P_t> with G_P = G - beta_t k_t w^T,   G <- alpha_t G_P.
+// Walking S back would divide by alpha (unbounded error for strong decay), so each
+// checkpoint block is first recomputed forward from its start state (the previous
+// block's end, or S0), its states before every token kept in registers, and the
+// reverse walk reads them.
+template <typename InT, int RSC, int RSR, int NCT, bool GATED>
 __global__ __launch_bounds__(512) void delta_bwd_kernel(
     const InT* __restrict__ q, const InT* __restrict__ k, const float* __restrict__ beta,
+    const float* __restrict__ gate, const float* __restrict__ s0,
     const float* __restrict__ go, const float* __restrict__ gs, const float* __restrict__ u_ws,
     const float* __restrict__ ck_ws, float* __restrict__ gq, float* __restrict__ gk,
-    float* __restrict__ gv, float* __restrict__ gb, float* __restrict__ gs0, int T, int H, int D,
-    int NC, int n_tiles, size_t part_stride_e, size_t part_stride_b) {
+    float* __restrict__ gv, float* __restrict__ gb, float* __restrict__ gg, float* __restrict__ gs0,
+    int T, int H, int D, int NC, int n_tiles, size_t part_stride_e, size_t part_stride_b) {
     extern __shared__ float lds[];
     constexpr int DP = RSC * kRpt;   // padded rows (column layout)
     constexpr int CP = RSR * kRpt;   // padded tile columns (row layout)
@@ -322,11 +335,12 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
     // per-thread staging slots, for the fewest threads a launch of this geometry has
     constexpr int NTMIN = NCT * RSC < 64 ? 64 : NCT * RSC;
     constexpr int MK = (KB * DP + NTMIN - 1) / NTMIN, MG = (KB * CP + NTMIN - 1) / NTMIN;
-    constexpr int SB = 2 * KB * DPL + 2 * KB * CPL + KB;  // one staging buffer
+    constexpr int SB = 2 * KB * DPL + 2 * KB * CPL + 2 * KB;  // one staging buffer
     const int NT = blockDim.x, NWV = NT / 64;
     // outputs of a block, written out one block later: by block parity,
     // [KB][D] gbeta terms k[d] x[d], [KB][D] gq, [KB][D] gk, [KB][NC] gv
-    const int OB = 3 * KB * D + KB * NC;
+    // (GATED: then [KB][D] gate terms, summed over d when written out)
+    const int OB = (GATED ? 4 : 3) * KB * D + KB * NC;
     float* sw = lds + 2 * SB;           // [2][CPL]       w, by token parity
     float* so0 = sw + 2 * CPL;          // [2][OB]
 
@@ -347,6 +361,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
     float* gq_t = gq + tile * part_stride_e;
     float* gk_t = gk + tile * part_stride_e;
     float* gb_t = gb + tile * part_stride_b;
+    float* gg_t = GATED ? gg + tile * part_stride_b : nullptr;
 
     // w's padding entries (tile columns past NC or D) are read as zeros, never written
     for (int x = tid; x < 2 * CPL; x += NT) sw[x] = 0.f;
@@ -362,7 +377,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
 
     // ---- one checkpoint block's inputs, loaded a block ahead into registers ----
     InT pk[MK], pq[MK];
-    float pg[MG], pu[MG], ps[kRpt], pb = 0.f;
+    float pg[MG], pu[MG], ps[kRpt], pb = 0.f, pa = 0.f;
     auto prefetch = [&](int blk) {
         const int lo = blk * kCk, nst = min(T, lo + kCk) - lo;
 #pragma unroll
@@ -383,11 +398,16 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
             pu[s] = ok ? u_p[static_cast<size_t>(lo + j) * D + col0 + c] : 0.f;
         }
         if (tid < KB) pb = tid < nst ? beta[static_cast<size_t>(tok0 + lo + tid) * H + h] : 0.f;
-        const float* cp = ck_p + static_cast<size_t>(blk) * D * D;
+        if (GATED && tid < KB) pa = tid < nst ? gate[static_cast<size_t>(tok0 + lo + tid) * H + h] : 0.f;
+        // the block's end state, walked back (GATED: its start state, recomputed forward)
+        const float* cp = !GATED      ? ck_p + static_cast<size_t>(blk) * D * D
+                          : blk > 0   ? ck_p + static_cast<size_t>(blk - 1) * D * D
+                          : s0        ? s0 + sbase
+                                      : nullptr;
 #pragma unroll
         for (int i = 0; i < kRpt; ++i) {
             const int c = rr * kRpt + i;
-            ps[i] = (ok_r && c < NC && col0 + c < D) ? cp[static_cast<size_t>(d) * D + col0 + c] : 0.f;
+            ps[i] = (cp && ok_r && c < NC && col0 + c < D) ? cp[static_cast<size_t>(d) * D + col0 + c] : 0.f;
         }
     };
     auto stage = [&](float* buf) {
@@ -415,6 +435,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
             }
         }
         if (tid < KB) sb[tid] = pb;
+        if (GATED && tid < KB) sb[KB + tid] = expf(pa);
 #pragma unroll
         for (int i = 0; i < kRpt; ++i) Sr[i] = ps[i];
     };
@@ -439,6 +460,15 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
             sum = wave_sum_row3(sum);
             if (lane == 63) gb_t[static_cast<size_t>(tok0 + lo + j) * H + h] = sum;
         }
+        if constexpr (GATED) {
+            const float* sog = sov + KB * NC;
+            for (int j = wave; j < nst; j += NWV) {
+                float sum = 0.f;
+                for (int x = lane; x < D; x += 64) sum += sog[j * D + x];
+                sum = wave_sum_row3(sum);
+                if (lane == 63) gg_t[static_cast<size_t>(tok0 + lo + j) * H + h] = sum;
+            }
+        }
     };
 
     if (n_ck > 0) prefetch(n_ck - 1);
@@ -457,10 +487,29 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
         const float* sg = sq + KB * DPL;
         const float* su = sg + KB * CPL;
         const float* sb = su + KB * CPL;
-        float* sgb = so0 + (it & 1) * OB;  // gbeta terms, then gq, gk, gv
+        float* sgb = so0 + (it & 1) * OB;  // gbeta terms, then gq, gk, gv (GATED: gate terms)
         float* soq = sgb + KB * D;
         float* sok = soq + KB * D;
         float* sov = sok + KB * D;
+        float* sog = sov + KB * NC;
+        // GATED: the block recomputed forward from its start state; Sh[j] = S before token lo + j
+        float Sh[GATED ? KB : 1][kRpt];
+        if constexpr (GATED) {
+            const float* sa = sb + KB;
+#pragma unroll
+            for (int j = 0; j < KB; ++j) {
+                if (j < nst) {
+                    float ur[kRpt];
+                    load_slice(su + j * CPL + rr * kSl, ur);
+                    const float a = sa[j], bkd = sb[j] * (ok_r ? sk[j * DPL + spad(d)] : 0.f);
+#pragma unroll
+                    for (int i = 0; i < kRpt; ++i) {
+                        Sh[j][i] = Sr[i];
+                        Sr[i] = fmaf(bkd, ur[i], a * Sr[i]);
+                    }
+                }
+            }
+        }
         {
             // a token's operands; the next token's are loaded while this one finishes
             float b, ge, kd, qd, kc[kRpt], qc[kRpt], gr[kRpt], ur[kRpt];
@@ -475,7 +524,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 qd = ok_r ? sq[j * DPL + spad(d)] : 0.f;  // q[d]
             };
             if (nst > 0) load_tok(nst - 1);
-            for (int j = nst - 1; j >= 0; --j) {
+            auto step = [&](int j) __attribute__((always_inline)) {
                 const int t = lo + j;
                 // G += q go^T (both layouts); S_t go over the tile's columns (row layout)
 #pragma unroll
@@ -496,10 +545,11 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                     sov[j * NC + e] = b * wp;
                 }
                 if (rr == 0 && ok_r) soq[j * D + d] = gqp;
-                // S_{t-1} = S_t - b k u^T (row layout)
+                // S_{t-1} = S_t - b k u^T (row layout); GATED: the recomputed S_{t-1}
                 const float bkd = b * kd;
+                const float at = GATED ? sb[KB + j] : 1.f;
 #pragma unroll
-                for (int i = 0; i < kRpt; ++i) Sr[i] = fmaf(-bkd, ur[i], Sr[i]);
+                for (int i = 0; i < kRpt; ++i) Sr[i] = GATED ? Sh[GATED ? j : 0][i] : fmaf(-bkd, ur[i], Sr[i]);
                 // what the rest of this token needs from its operands
                 const float bt = b, kdt = kd;
                 float bk[kRpt];
@@ -509,7 +559,8 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 float wr[kRpt];
                 load_slice(swp + rr * kSl, wr);  // w[col0 + rr*R + i]
                 if (j > 0) load_tok(j - 1);
-                const float yp = col_sum<RSR>(slice_dot(wr, Sr));
+                // y = P w with P = alpha S_{t-1}
+                const float yp = (GATED ? at : 1.f) * col_sum<RSR>(slice_dot(wr, Sr));
                 if (rr == 0 && ok_r) {
                     sok[j * D + d] = bt * (xp - yp);
                     sgb[j * D + d] = kdt * xp;  // gbeta = k . x, summed when written out
@@ -520,6 +571,25 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                     Gc[i] = fmaf(bk[i], wp, Gc[i]);
                     Gr[i] = fmaf(-bkd, wr[i], Gr[i]);
                 }
+                if constexpr (GATED) {
+                    // dL/dg_t = <G_P, alpha S_{t-1}> (row d's share; summed over d when written
+                    // out), then G <- alpha G_P
+                    const float gp = col_sum<RSR>(slice_dot(Gr, Sr));
+                    if (rr == 0 && ok_r) sog[j * D + d] = at * gp;
+#pragma unroll
+                    for (int i = 0; i < kRpt; ++i) {
+                        Gc[i] *= at;
+                        Gr[i] *= at;
+                    }
+                }
+            };
+            if constexpr (GATED) {
+                // unrolled, so that the recomputed states Sh[j] stay in registers
+#pragma unroll
+                for (int j = KB - 1; j >= 0; --j)
+                    if (j < nst) step(j);
+            } else {
+                for (int j = nst - 1; j >= 0; --j) step(j);
             }
         }
     }
@@ -582,16 +652,16 @@ static hipError_t launch_reduce(float* out, const float* part, size_t n, size_t 
     return hipGetLastError();
 }
 
-size_t bwd_workspace_floats(long n_pairs, int T, int D) {
+size_t bwd_workspace_floats(long n_pairs, int T, int D, bool gated) {
     const BwdGeo g = bwd_geo(D);
     const long n_ck = (T + kCk - 1) / kCk;
     const size_t e = static_cast<size_t>(n_pairs) * T * D, bt = static_cast<size_t>(n_pairs) * T;
     size_t f = e + static_cast<size_t>(n_pairs) * n_ck * D * D;
-    if (g.n_tiles > 1) f += static_cast<size_t>(g.n_tiles) * (2 * e + bt);
+    if (g.n_tiles > 1) f += static_cast<size_t>(g.n_tiles) * (2 * e + (gated ? 2 : 1) * bt);
     return f;
 }
 
-template <typename InT>
+template <typename InT, bool GATED>
 static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
     const BwdGeo g = bwd_geo(a.D);
     const size_t e = static_cast<size_t>(a.n_pairs) * a.T * a.D;
@@ -602,37 +672,39 @@ static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
     float* part = ck_ws + static_cast<size_t>(a.n_pairs) * n_ck * a.D * a.D;
     const unsigned grid = static_cast<unsigned>(a.n_pairs) * g.n_tiles;
 
-    hipError_t err = launch_ckpt<InT>(a, u_ws, ck_ws, st);
+    hipError_t err = launch_ckpt<InT, GATED>(a, u_ws, ck_ws, st);
     if (err != hipSuccess) return err;
 
     const bool split = g.n_tiles > 1;
     float* gq = split ? part : a.gq;
     float* gk = split ? part + static_cast<size_t>(g.n_tiles) * e : a.gk;
     float* gb = split ? part + static_cast<size_t>(2 * g.n_tiles) * e : a.gbeta;
+    float* gg = !GATED ? nullptr : split ? part + static_cast<size_t>(2 * g.n_tiles) * e + g.n_tiles * bt : a.gg;
     const int dp = g.rsc * kSl, cp = g.rsr * kSl;
-    const size_t lds_b = sizeof(float) * (2 * (2 * kBwdSteps * dp + 2 * kBwdSteps * cp + kBwdSteps) +
-                                          2 * cp + 2 * (3 * kBwdSteps * a.D + kBwdSteps * g.nc));
+    constexpr int NO = GATED ? 4 : 3;  // [KB][D] output arrays per block
+    const size_t lds_b = sizeof(float) * (2 * (2 * kBwdSteps * dp + 2 * kBwdSteps * cp + 2 * kBwdSteps) +
+                                          2 * cp + 2 * (NO * kBwdSteps * a.D + kBwdSteps * g.nc));
     // with kRpt 8 and tiles of min(D, 32) columns, RSR = min(RSC, 4) for every D <= 128;
     // above, 16-column tiles: RSC 32, RSR 2
     const bool wide = a.D > 128;
     if (wide ? (g.rsc != 32 || g.rsr != 2 || g.nc != kTileColsWide)
              : (g.rsr != (g.rsc < 4 ? g.rsc : 4) || g.rsc > 16))
         return hipErrorInvalidValue;
-    auto kern = delta_bwd_kernel<InT, 16, 4, kTileCols>;
+    auto kern = delta_bwd_kernel<InT, 16, 4, kTileCols, GATED>;
     switch (g.rsc) {
-        case 1: kern = delta_bwd_kernel<InT, 1, 1, kTileCols>; break;
-        case 2: kern = delta_bwd_kernel<InT, 2, 2, kTileCols>; break;
-        case 4: kern = delta_bwd_kernel<InT, 4, 4, kTileCols>; break;
-        case 8: kern = delta_bwd_kernel<InT, 8, 4, kTileCols>; break;
-        case 32: kern = delta_bwd_kernel<InT, 32, 2, kTileColsWide>; break;
+        case 1: kern = delta_bwd_kernel<InT, 1, 1, kTileCols, GATED>; break;
+        case 2: kern = delta_bwd_kernel<InT, 2, 2, kTileCols, GATED>; break;
+        case 4: kern = delta_bwd_kernel<InT, 4, 4, kTileCols, GATED>; break;
+        case 8: kern = delta_bwd_kernel<InT, 8, 4, kTileCols, GATED>; break;
+        case 32: kern = delta_bwd_kernel<InT, 32, 2, kTileColsWide, GATED>; break;
         default: break;
     }
     if (wide) {
         // the dynamic-LDS limit is a per-device function attribute: set it once, to what
         // the largest D (256) of this kernel needs
         const int dp_w = 32 * kSl, cp_w = 2 * kSl;
-        const size_t lds_max = sizeof(float) * (2 * (2 * kBwdSteps * dp_w + 2 * kBwdSteps * cp_w + kBwdSteps) +
-                                                2 * cp_w + 2 * (3 * kBwdSteps * 256 + kBwdSteps * kTileColsWide));
+        const size_t lds_max = sizeof(float) * (2 * (2 * kBwdSteps * dp_w + 2 * kBwdSteps * cp_w + 2 * kBwdSteps) +
+                                                2 * cp_w + 2 * (NO * kBwdSteps * 256 + kBwdSteps * kTileColsWide));
         if (lds_b > lds_max) return hipErrorInvalidValue;
         int dev = 0;
         if ((err = hipGetDevice(&dev)) != hipSuccess) return err;
@@ -646,18 +718,21 @@ static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
         }
     }
     hipLaunchKernelGGL(kern, dim3(grid), dim3(g.threads), lds_b, st, static_cast<const InT*>(a.q),
-                       static_cast<const InT*>(a.k), a.beta, a.go, a.gs, u_ws, ck_ws, gq, gk, a.gv, gb,
-                       a.gs0, a.T, a.H, a.D, g.nc, g.n_tiles, split ? e : 0, split ? bt : 0);
+                       static_cast<const InT*>(a.k), a.beta, a.g, a.s0, a.go, a.gs, u_ws, ck_ws, gq, gk,
+                       a.gv, gb, gg, a.gs0, a.T, a.H, a.D, g.nc, g.n_tiles, split ? e : 0, split ? bt : 0);
     err = hipGetLastError();
     if (err != hipSuccess || !split) return err;
     if ((err = launch_reduce(a.gq, gq, e, e, g.n_tiles, st)) != hipSuccess) return err;
     if ((err = launch_reduce(a.gk, gk, e, e, g.n_tiles, st)) != hipSuccess) return err;
+    if (GATED && (err = launch_reduce(a.gg, gg, bt, bt, g.n_tiles, st)) != hipSuccess) return err;
     return launch_reduce(a.gbeta, gb, bt, bt, g.n_tiles, st);
 }
 
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t st) {
     if (a.n_pairs == 0) return hipSuccess;
-    return a.in_bf16 ? launch_bwd_in<uint16_t>(a, st) : launch_bwd_in<float>(a, st);
+    if (a.g)
+        return a.in_bf16 ? launch_bwd_in<uint16_t, true>(a, st) : launch_bwd_in<float, true>(a, st);
+    return a.in_bf16 ? launch_bwd_in<uint16_t, false>(a, st) : launch_bwd_in<float, false>(a, st);
 }
 
 }  // namespace pm

@@ -278,10 +278,60 @@ bool bwd_chunked(int H, int D, int in_dtype) {
     return g_path != 1 && in_dtype == PM_DTYPE_BF16 && pm::chunked_bwd_supported(D, H);
 }
 
-size_t bwd_ws_bytes(int B, int T, int H, int D, int in_dtype) {
+size_t bwd_ws_bytes(int B, int T, int H, int D, int in_dtype, bool gated = false) {
     const long n_pairs = static_cast<long>(B) * H;
-    if (bwd_chunked(H, D, in_dtype)) return pm::chunked_bwd_ws(n_pairs, T, D).bytes;
-    return sizeof(float) * pm::bwd_workspace_floats(n_pairs, T, D);
+    if (!gated && bwd_chunked(H, D, in_dtype)) return pm::chunked_bwd_ws(n_pairs, T, D).bytes;
+    return sizeof(float) * pm::bwd_workspace_floats(n_pairs, T, D, gated);
+}
+
+// Common backward dispatch; g != NULL: the gated variant (per-token kernels, gg out).
+int backward(const void* q, const void* k, const void* v, const float* beta, const float* g,
+             const float* s0, const float* go, const float* gs, float* gq, float* gk, float* gv,
+             float* gbeta, float* gg, float* gs0, int B, int T, int H, int D, int in_dtype,
+             void* workspace, size_t ws_bytes, void* stream) {
+    if (B < 0 || T < 0 || H < 0)
+        return fail(PM_E_SHAPE, "B, T, H must be >= 0 (got %d, %d, %d)", B, T, H);
+    if (D < 1 || D > pm::kBwdMaxD)
+        return fail(PM_E_SHAPE, "backward D must be in [1, %d] (got %d)", pm::kBwdMaxD, D);
+    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16)
+        return fail(PM_E_DTYPE, "in_dtype %d is not PM_DTYPE_F32 or PM_DTYPE_BF16", in_dtype);
+    const long n_pairs = static_cast<long>(B) * H;
+    const long n_tok = static_cast<long>(B) * T;
+    if (n_pairs == 0) return 0;
+    if (n_pairs > (1L << 30) || n_tok > (1L << 40)) return fail(PM_E_SHAPE, "problem too large");
+    if (!gs0) return fail(PM_E_NULL, "gs0 is NULL");
+    if (n_tok > 0 && (!q || !k || !v || !beta || !gq || !gk || !gv || !gbeta))
+        return fail(PM_E_NULL, "q, k, v, beta, gq, gk, gv and gbeta must be non-NULL");
+    const bool gated = g != nullptr || gg != nullptr;
+    if (gated && n_tok > 0 && (!g || !gg)) return fail(PM_E_NULL, "g and gg must be non-NULL");
+    const void* f32s[] = {beta, g, s0, go, gs, gq, gk, gv, gbeta, gg, gs0, workspace};
+    for (const void* p : f32s)
+        if (p && !aligned(p, 4)) return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
+    const bool chunked = !gated && bwd_chunked(H, D, in_dtype);
+    if (g_path >= 2 && !chunked)
+        return fail(PM_E_UNSUPPORTED,
+                    gated ? "the gated backward runs on the per-token kernels only (path 2 asks for the chunked one)"
+                          : "chunked backward needs bf16 inputs and D in {64, 128} (got in_dtype %d, D %d)",
+                    in_dtype, D);
+    if (chunked && n_tok > 0) {
+        const void* v16[] = {q, k, v, go, gq, gk, gv, workspace};
+        for (const void* p : v16)
+            if (p && !aligned(p, 16))
+                return fail(PM_E_ALIGN,
+                            "chunked backward: q, k, v, go, gq, gk, gv and workspace must be 16-byte aligned");
+    }
+    const size_t need = bwd_ws_bytes(B, T, H, D, in_dtype, gated);
+    if (need > 0 && (!workspace || ws_bytes < need))
+        return fail(PM_E_WORKSPACE, "workspace of %zu bytes needed (got %zu)", need,
+                    workspace ? ws_bytes : static_cast<size_t>(0));
+    pm::BwdArgs a{q, k, v, beta, s0, go, gs, gq, gk, gv, gbeta, gs0,
+                  static_cast<float*>(workspace), static_cast<int>(n_pairs), T, H, D,
+                  in_dtype == PM_DTYPE_BF16};
+    a.g = g;
+    a.gg = gg;
+    hipError_t e = chunked ? pm::launch_bwd_chunked(a, static_cast<hipStream_t>(stream))
+                           : pm::launch_bwd(a, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? 0 : hip_fail(e, "backward launch");
 }
 
 // The forward's workspace: the split form's T blocks (bf16 inputs, where split_chosen), or
@@ -322,44 +372,24 @@ int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
                  float* gv, float* gbeta, float* gs0, int B, int T, int H, int D, int in_dtype,
                  void* workspace, size_t ws_bytes, void* stream) {
     g_err[0] = '\0';
-    if (B < 0 || T < 0 || H < 0)
-        return fail(PM_E_SHAPE, "B, T, H must be >= 0 (got %d, %d, %d)", B, T, H);
-    if (D < 1 || D > pm::kBwdMaxD)
-        return fail(PM_E_SHAPE, "backward D must be in [1, %d] (got %d)", pm::kBwdMaxD, D);
-    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16)
-        return fail(PM_E_DTYPE, "in_dtype %d is not PM_DTYPE_F32 or PM_DTYPE_BF16", in_dtype);
-    const long n_pairs = static_cast<long>(B) * H;
-    const long n_tok = static_cast<long>(B) * T;
-    if (n_pairs == 0) return 0;
-    if (n_pairs > (1L << 30) || n_tok > (1L << 40)) return fail(PM_E_SHAPE, "problem too large");
-    if (!gs0) return fail(PM_E_NULL, "gs0 is NULL");
-    if (n_tok > 0 && (!q || !k || !v || !beta || !gq || !gk || !gv || !gbeta))
-        return fail(PM_E_NULL, "q, k, v, beta, gq, gk, gv and gbeta must be non-NULL");
-    const void* f32s[] = {beta, s0, go, gs, gq, gk, gv, gbeta, gs0, workspace};
-    for (const void* p : f32s)
-        if (p && !aligned(p, 4)) return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
-    const bool chunked = bwd_chunked(H, D, in_dtype);
-    if (g_path >= 2 && !chunked)
-        return fail(PM_E_UNSUPPORTED,
-                    "chunked backward needs bf16 inputs and D in {64, 128} (got in_dtype %d, D %d)",
-                    in_dtype, D);
-    if (chunked && n_tok > 0) {
-        const void* v16[] = {q, k, v, go, gq, gk, gv, workspace};
-        for (const void* p : v16)
-            if (p && !aligned(p, 16))
-                return fail(PM_E_ALIGN,
-                            "chunked backward: q, k, v, go, gq, gk, gv and workspace must be 16-byte aligned");
-    }
-    const size_t need = bwd_ws_bytes(B, T, H, D, in_dtype);
-    if (need > 0 && (!workspace || ws_bytes < need))
-        return fail(PM_E_WORKSPACE, "workspace of %zu bytes needed (got %zu)", need,
-                    workspace ? ws_bytes : static_cast<size_t>(0));
-    pm::BwdArgs a{q, k, v, beta, s0, go, gs, gq, gk, gv, gbeta, gs0,
-                  static_cast<float*>(workspace), static_cast<int>(n_pairs), T, H, D,
-                  in_dtype == PM_DTYPE_BF16};
-    hipError_t e = chunked ? pm::launch_bwd_chunked(a, static_cast<hipStream_t>(stream))
-                           : pm::launch_bwd(a, static_cast<hipStream_t>(stream));
-    return e == hipSuccess ? 0 : hip_fail(e, "backward launch");
+    return backward(q, k, v, beta, nullptr, s0, go, gs, gq, gk, gv, gbeta, nullptr, gs0, B, T, H, D,
+                    in_dtype, workspace, ws_bytes, stream);
+}
+
+size_t pm_gated_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype) {
+    if (B < 0 || T < 0 || H < 0 || D < 1 || D > pm::kBwdMaxD) return 0;
+    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16) return 0;
+    return bwd_ws_bytes(B, T, H, D, in_dtype, true);
+}
+
+int pm_gated_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
+                       const float* g, const float* s0, const float* go, const float* gs, float* gq,
+                       float* gk, float* gv, float* gbeta, float* gg, float* gs0, int B, int T,
+                       int H, int D, int in_dtype, void* workspace, size_t ws_bytes, void* stream) {
+    g_err[0] = '\0';
+    if (static_cast<long>(B) * T * H > 0 && (!g || !gg)) return fail(PM_E_NULL, "g and gg must be non-NULL");
+    return backward(q, k, v, beta, g, s0, go, gs, gq, gk, gv, gbeta, gg, gs0, B, T, H, D, in_dtype,
+                    workspace, ws_bytes, stream);
 }
 
 int pm_delta_bwd_noalloc(const void* q, const void* k, const void* v, const float* beta,

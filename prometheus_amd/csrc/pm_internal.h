@@ -130,9 +130,13 @@ struct BwdArgs {
     float* workspace;
     int n_pairs, T, H, D;
     bool in_bf16;
+    // gated variant (per-token fp32 kernels only): log-gates per (token, head), alpha =
+    // exp(g), and their gradient gg (B, T, H)
+    const float* g = nullptr;
+    float* gg = nullptr;
 };
 constexpr int kBwdMaxD = 256;
-size_t bwd_workspace_floats(long n_pairs, int T, int D);
+size_t bwd_workspace_floats(long n_pairs, int T, int D, bool gated = false);
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t st);
 
 // Chunked reverse mode (K6, bf16 MFMA): bf16 q/k/v and chunked_supported(D,

@@ -313,7 +313,7 @@ def chunked_delta_rule_bwd(residual: _DeltaResidual, grads):
     ``:638-653``). Returns ``(gq, gk, gv, gbeta, gstate)``, all fp32, shaped
     like ``q, k, v, beta, state0``: the gradients of the reference's
     ``_delta_vjp_np`` / ``_delta_vjp_jax`` (``:460-588``). Head dimension up
-    to 128. As in the forward, bf16 q/k/v with head dimension 64 or 128 run
+    to 256. As in the forward, bf16 q/k/v with head dimension 64 or 128 run
     the chunked backward on bf16 MFMA (bf16 parity); everything else runs the
     fp32 per-token reverse-mode kernel with state checkpoints (fp32 parity).
     Neither keeps the reference's per-token state history.
@@ -554,18 +554,21 @@ def delta_rule_step(q, k, v, beta, state):
 # ---------------------------------------------------------------------------
 
 
-def chunked_gated_delta_rule(q, k, v, beta, g, state=None, config=None, *, out_dtype=None):
-    """Gated delta rule (Gated DeltaNet) with a log-gate per token and head.
+@dataclass(frozen=True)
+class _GatedDeltaResidual:
+    """Residual of ``chunked_gated_delta_rule_fwd``: ``_DeltaResidual``'s fields plus the
+    log-gates ``g`` (the arrays the kernel consumed, not copied)."""
 
-    ``S_t = exp(g_t) (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T``,
-    ``o_t = q_t S_t``. q, k, v, beta, state and the return value as
-    ``chunked_delta_rule``; g: (batch, seq, heads) fp32 log-gates (g = 0 gives
-    ``chunked_delta_rule``). bf16 q/k/v with dim 64 or 128 run the chunked
-    MFMA kernel with the in-chunk decays folded into its tiles; other inputs
-    run the fp32 per-token kernel.
-    """
-    cfg = LinearAttnConfig() if config is None else config
-    _check_chunk(cfg)
+    q: Array
+    k: Array
+    v: Array
+    beta: Array
+    g: Array
+    state0: Array
+    chunk: int
+
+
+def _gated_forward(q, k, v, beta, g, state, out_dtype):
     batch, seq, heads, dim = _validate(q, k, v, beta, state)
     if _shape(g) != (batch, seq, heads):
         raise KernelError(f"g shape {_shape(g)} != {(batch, seq, heads)}")
@@ -585,7 +588,114 @@ def chunked_gated_delta_rule(q, k, v, beta, g, state=None, config=None, *, out_d
             batch, seq, heads, dim, _code(cdt), _code(odt), _stream(call.device),
         )
         _native.check(rc)
-    return call.out(o), call.out(s_out)
+        if sd is None:
+            sd = torch.zeros((batch, heads, dim, dim), dtype=torch.float32, device=call.device)
+    return call, (qd, kd, vd, bd, gd, sd), o, s_out
+
+
+def chunked_gated_delta_rule_bwd(residual: _GatedDeltaResidual, grads):
+    """Backward of the gated VJP pair: ``grads = (go, gs)`` as ``chunked_delta_rule_bwd``
+    (either may be None). Returns ``(gq, gk, gv, gbeta, gg, gstate)``, fp32, shaped like
+    ``q, k, v, beta, g, state0``. Runs the per-token fp32 reverse-mode kernels
+    (``pm_gated_delta_bwd``) for every dtype and head dimension up to 256: with P_t =
+    exp(g_t) S_{t-1}, dL/dg_t = <G - beta_t k_t w^T, P_t> and G <- exp(g_t) (G - beta_t
+    k_t w^T), the other gradients as in the ungated backward."""
+    go, gs = grads
+    q, k, v, beta, g, s0 = residual.q, residual.k, residual.v, residual.beta, residual.g, residual.state0
+    batch, seq, heads, dim = _validate(q, k, v, beta, s0)
+    if _shape(g) != (batch, seq, heads):
+        raise KernelError(f"g shape {_shape(g)} != {(batch, seq, heads)}")
+    if dim > _native.MAX_D_BWD:
+        raise KernelError(f"backward head dimension {dim} exceeds {_native.MAX_D_BWD}")
+    if go is not None and _shape(go) != (batch, seq, heads, dim):
+        raise KernelError(f"grad of output shape {_shape(go)} != {(batch, seq, heads, dim)}")
+    if gs is not None and _shape(gs) != (batch, heads, dim, dim):
+        raise KernelError(f"grad of state shape {_shape(gs)} != {(batch, heads, dim, dim)}")
+    call = _Call(q, k, v, beta, g, s0, go, gs)
+    cdt = _qkv_dtype(q, k, v)
+    f32 = torch.float32
+    with torch.cuda.device(call.device):
+        qd, kd, vd = call.dev(q, cdt), call.dev(k, cdt), call.dev(v, cdt)
+        bd, gd, sd = call.dev(beta, f32), call.dev(g, f32), call.dev(s0, f32)
+        god, gsd = call.dev(go, f32), call.dev(gs, f32)
+        gq = torch.empty((batch, seq, heads, dim), dtype=f32, device=call.device)
+        gk, gv = torch.empty_like(gq), torch.empty_like(gq)
+        gb = torch.empty((batch, seq, heads), dtype=f32, device=call.device)
+        gg = torch.empty_like(gb)
+        gs0 = torch.empty((batch, heads, dim, dim), dtype=f32, device=call.device)
+        L = _native.lib()
+        nbytes = L.pm_gated_delta_bwd_workspace_bytes(batch, seq, heads, dim, _code(cdt))
+        ws = torch.empty(((nbytes + 3) // 4,), dtype=f32, device=call.device) if nbytes else None
+        rc = L.pm_gated_delta_bwd(
+            _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(gd), _ptr(sd), _ptr(god), _ptr(gsd),
+            _ptr(gq), _ptr(gk), _ptr(gv), _ptr(gb), _ptr(gg), _ptr(gs0),
+            batch, seq, heads, dim, _code(cdt), _ptr(ws), nbytes, _stream(call.device),
+        )
+        _native.check(rc)
+    return tuple(call.out(x) for x in (gq, gk, gv, gb, gg, gs0))
+
+
+class _ChunkedGatedDeltaRule(torch.autograd.Function):
+    """``chunked_gated_delta_rule`` as a differentiable op: the gated forward kernel and
+    ``chunked_gated_delta_rule_bwd`` as its backward (gradients for q, k, v, beta, g and
+    the state, in each input's dtype and device)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, g, state, chunk, out_dtype):
+        call, (qd, kd, vd, bd, gd, sd), o, s = _gated_forward(q, k, v, beta, g, state, out_dtype)
+        ctx.save_for_backward(qd, kd, vd, bd, gd, sd)
+        ctx.chunk = chunk
+        ctx.like = [(x.dtype, x.device) if isinstance(x, torch.Tensor) else None
+                    for x in (q, k, v, beta, g, state)]
+        ctx.knobs = _native.knobs()
+        return call.out(o), call.out(s)
+
+    @staticmethod
+    def backward(ctx, go, gs):
+        qd, kd, vd, bd, gd, sd = ctx.saved_tensors
+        res = _GatedDeltaResidual(q=qd, k=kd, v=vd, beta=bd, g=gd, state0=sd, chunk=ctx.chunk)
+        with _native.use_knobs(*ctx.knobs):
+            grads = chunked_gated_delta_rule_bwd(res, (go, gs))
+        out = []
+        for gr, like, need in zip(grads, ctx.like, ctx.needs_input_grad[:6]):
+            out.append(gr.to(device=like[1], dtype=like[0]) if (like is not None and need) else None)
+        return (*out, None, None)
+
+
+def chunked_gated_delta_rule(q, k, v, beta, g, state=None, config=None, *, out_dtype=None):
+    """Gated delta rule (Gated DeltaNet) with a log-gate per token and head.
+
+    ``S_t = exp(g_t) (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T``,
+    ``o_t = q_t S_t``. q, k, v, beta, state and the return value as
+    ``chunked_delta_rule``; g: (batch, seq, heads) fp32 log-gates (g = 0 gives
+    ``chunked_delta_rule``). bf16 q/k/v with dim 64 or 128 run the chunked
+    MFMA kernel with the in-chunk decays folded into its tiles; other inputs
+    run the fp32 per-token kernel. Differentiable: when autograd records and a
+    torch input (the gates included) requires grad, the backward runs
+    ``chunked_gated_delta_rule_bwd``.
+    """
+    cfg = LinearAttnConfig() if config is None else config
+    chunk = _check_chunk(cfg)
+    if _wants_grad(q, k, v, beta, g, state):
+        _validate(q, k, v, beta, state)
+        return _ChunkedGatedDeltaRule.apply(q, k, v, beta, g, state, chunk, out_dtype)
+    call, _, o, s = _gated_forward(q, k, v, beta, g, state, out_dtype)
+    return call.out(o), call.out(s)
+
+
+def chunked_gated_delta_rule_fwd(q, k, v, beta, g, state, config, *, out_dtype=None):
+    """Explicit forward of the gated VJP pair: ``((output, next_state), _GatedDeltaResidual)``."""
+    chunk = _check_chunk(config)
+    call, (qd, kd, vd, bd, gd, sd), o, s = _gated_forward(q, k, v, beta, g, state, out_dtype)
+    if call.host_numpy:
+        residual = _GatedDeltaResidual(
+            q=np.asarray(q, dtype=np.float32), k=np.asarray(k, dtype=np.float32),
+            v=np.asarray(v, dtype=np.float32), beta=np.asarray(beta, dtype=np.float32),
+            g=np.asarray(g, dtype=np.float32), state0=sd.cpu().numpy(), chunk=chunk)
+    else:
+        residual = _GatedDeltaResidual(q=call.out(qd), k=call.out(kd), v=call.out(vd), beta=call.out(bd),
+                                       g=call.out(gd), state0=call.out(sd), chunk=chunk)
+    return (call.out(o), call.out(s)), residual
 
 
 def gated_delta_rule_step(q, k, v, beta, g, state):
@@ -630,5 +740,7 @@ __all__ = [
     "check_varlen",
     "delta_rule_step",
     "chunked_gated_delta_rule",
+    "chunked_gated_delta_rule_fwd",
+    "chunked_gated_delta_rule_bwd",
     "gated_delta_rule_step",
 ]

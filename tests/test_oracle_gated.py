@@ -125,3 +125,101 @@ def test_planted_mistakes_are_caught(kind):
     kk, vv, S0 = k[0, 0, 0], v[0, 0, 0], s0[0, 0]
     s1 = a * (S0 - b_ * np.outer(kk, kk @ S0)) + b_ * np.outer(kk, vv)
     assert not np.allclose(s[0, 0], s1, rtol=1e-9)
+
+
+# --- the reverse mode (gated_vjp) ---
+
+
+def _loss(q, k, v, beta, g, s0, go, gs):
+    o, s = gref.gated_delta_rule(q, k, v, beta, g, s0)
+    return float(np.sum(o * go) + np.sum(s * gs))
+
+
+def test_vjp_zero_gate_is_the_delta_rule_vjp():
+    """g = 0: the five ungated gradients are the pinned delta_vjp's."""
+    rng = np.random.default_rng(11)
+    q, k, v, beta, _, s0 = _problem(rng, (2, 9, 2, 5))
+    go = rng.standard_normal(q.shape)
+    gs = rng.standard_normal(s0.shape) * 0.1
+    got = gref.gated_vjp(q, k, v, beta, np.zeros(beta.shape), go, gs, s0)
+    want = dref.delta_vjp(q, k, v, beta, go, gs, s0)
+    for name, a, b in zip(("gq", "gk", "gv", "gbeta", "gs0"), got[:4] + got[5:], want):
+        np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12, err_msg=name)
+
+
+@pytest.mark.parametrize("gate_scale", [0.05, 0.3, 2.0])
+def test_vjp_finite_differences(gate_scale):
+    """Every gradient, g's included, against central differences of the fp64 forward
+    along random directions (strong decay at gate_scale 2: alpha down to ~0.01)."""
+    rng = np.random.default_rng(int(gate_scale * 100))
+    q, k, v, beta, g, s0 = _problem(rng, (1, 7, 2, 4), gate_scale)
+    go = rng.standard_normal(q.shape)
+    gs = rng.standard_normal(s0.shape)
+    grads = gref.gated_vjp(q, k, v, beta, g, go, gs, s0)
+    args = {"q": q, "k": k, "v": v, "beta": beta, "g": g, "s0": s0}
+    eps = 1e-6
+    for name, gx in zip(("q", "k", "v", "beta", "g", "s0"), grads):
+        d = rng.standard_normal(args[name].shape)
+        plus, minus = dict(args), dict(args)
+        plus[name], minus[name] = args[name] + eps * d, args[name] - eps * d
+        fd = (_loss(**plus, go=go, gs=gs) - _loss(**minus, go=go, gs=gs)) / (2 * eps)
+        np.testing.assert_allclose(np.sum(gx * d), fd, rtol=1e-6, atol=1e-8, err_msg=name)
+
+
+def test_vjp_pure_decay_closed_form():
+    """beta = 0, go = 0: S_T = exp(sum g) S_0, so dL/dg_t = <gs, S_T> for every t and
+    dL/dS_0 = exp(sum g) gs."""
+    rng = np.random.default_rng(12)
+    q, k, v, _, g, s0 = _problem(rng, (1, 6, 2, 3))
+    gs = rng.standard_normal(s0.shape)
+    _, _, _, _, gg, gs0 = gref.gated_vjp(q, k, v, np.zeros(g.shape), g, None, gs, s0)
+    s_t = np.exp(g.sum(axis=1))[..., None, None] * s0
+    want = np.einsum("bhde,bhde->bh", gs, s_t)
+    np.testing.assert_allclose(gg, np.repeat(want[:, None], g.shape[1], axis=1), rtol=1e-12)
+    np.testing.assert_allclose(gs0, np.exp(g.sum(axis=1))[..., None, None] * gs, rtol=1e-12)
+
+
+def test_vjp_planted_mistakes_are_caught():
+    """Restatements with a plausible mistake each (the gate gradient taken against S_{t-1}
+    instead of alpha S_{t-1}; G not scaled by alpha; the gate's gradient taken before the
+    rank-1 downdate) differ from finite differences."""
+    rng = np.random.default_rng(13)
+    q, k, v, beta, g, s0 = _problem(rng, (1, 5, 1, 4), 0.5)
+    go = rng.standard_normal(q.shape)
+    gs = rng.standard_normal(s0.shape)
+    eps = 1e-6
+    d = rng.standard_normal(g.shape)
+    fd = (_loss(q, k, v, beta, g + eps * d, s0, go, gs) - _loss(q, k, v, beta, g - eps * d, s0, go, gs)) / (2 * eps)
+
+    def mutant(kind):
+        b, t, h, dd = q.shape
+        G = gs.copy()
+        s = s0.copy()
+        hist, us = [s], []
+        for i in range(t):
+            a = np.exp(g[:, i])[..., None, None]
+            p = a * s
+            u = v[:, i] - np.einsum("bhd,bhde->bhe", k[:, i], p)
+            s = p + beta[:, i][..., None, None] * np.einsum("bhd,bhe->bhde", k[:, i], u)
+            hist.append(s)
+            us.append(u)
+        gg = np.zeros(g.shape)
+        for i in range(t - 1, -1, -1):
+            a = np.exp(g[:, i])
+            p = a[..., None, None] * hist[i]
+            G = G + np.einsum("bhd,bhe->bhde", q[:, i], go[:, i])
+            w = np.einsum("bhde,bhd->bhe", G, k[:, i])
+            if kind == "before_downdate":
+                gg[:, i] = np.einsum("bhde,bhde->bh", G, p)
+            G = G - beta[:, i][..., None, None] * np.einsum("bhd,bhe->bhde", k[:, i], w)
+            if kind == "no_alpha_in_gate":
+                gg[:, i] = np.einsum("bhde,bhde->bh", G, hist[i])
+            elif kind != "before_downdate":
+                gg[:, i] = np.einsum("bhde,bhde->bh", G, p)
+            if kind != "G_not_scaled":
+                G = a[..., None, None] * G
+        return float(np.sum(gg * d))
+
+    for kind in ("no_alpha_in_gate", "G_not_scaled", "before_downdate"):
+        assert abs(mutant(kind) - fd) > 1e-4 * max(1.0, abs(fd)), kind
+    assert abs(mutant("correct") - fd) < 1e-6 * max(1.0, abs(fd))

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 11
+#define PM_DELTA_ABI_VERSION 12
 
 /* element types */
 #define PM_DTYPE_F32 0
@@ -156,6 +156,31 @@ int pm_gated_delta_fwd(const void* q, const void* k, const void* v, const float*
 int pm_gated_delta_step(float* s_inout, const void* q, const void* k, const void* v,
                         const float* beta, const float* g, float* o, int B, int H, int D,
                         int in_dtype, void* stream);
+
+/*
+ * The delta rule with a decay per key channel (KDA, Kimi Delta Attention; the
+ * reference's model names the "Gated DeltaNet / KDA family",
+ * spec/03-model.md:12 and kernels/__init__.py:6, and has code for neither
+ * gate).  No reference counterpart:
+ *   S_t = (I - beta_t k_t k_t^T) Diag(alpha_t) S_{t-1} + beta_t k_t v_t^T,  o_t = q_t S_t,
+ * alpha_t = exp(g_t) with g (B, T, H, D) fp32 (one log-gate per key channel,
+ * i.e. per row of S), NULL only when B*T*H == 0.  With g constant along D
+ * this is pm_gated_delta_fwd.  Runs the fp32 per-token kernel for every
+ * in_dtype and D <= 256 (row d of S is decayed by alpha_t[d] before the
+ * token's dot products); path 2 (chunked kernel required) returns
+ * PM_E_UNSUPPORTED.  Everything else as pm_delta_fwd.
+ */
+int pm_kda_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
+                     const float* g, const float* s0, void* o, float* s_out, int B, int T, int H,
+                     int D, int in_dtype, int out_dtype, void* stream);
+
+/*
+ * One KDA step: S' = (I - beta k k^T) Diag(exp(g)) S + beta k v^T, o = q S',
+ * g (B, H, D) fp32; otherwise as pm_delta_step.
+ */
+int pm_kda_delta_step(float* s_inout, const void* q, const void* k, const void* v,
+                      const float* beta, const float* g, float* o, int B, int H, int D,
+                      int in_dtype, void* stream);
 
 /*
  * Decode step over a serving-side state cache (no reference counterpart in

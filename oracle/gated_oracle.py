@@ -131,3 +131,64 @@ def gated_vjp(q, k, v, beta, g, go, gs, state=None, dtype=np.float64):
         gg[:, i] = np.einsum("bhde,bhde->bh", G, p)
         G = a[..., None, None] * G
     return gq, gk, gv, gbeta, gg, G
+
+
+# --- KDA: a log-gate per key channel (Kimi Delta Attention) ---
+
+
+def kda_delta_rule(q, k, v, beta, g, state=None, dtype=np.float64):
+    """Per-token recurrence with a decay per key channel: g (B, T, H, D) log-gates,
+    alpha_t = exp(g_t) a d_k-vector, and (Kimi Linear's KDA, the reference's "KDA
+    family" of spec/03-model.md:12)
+
+        S_t = (I - beta_t k_t k_t^T) Diag(alpha_t) S_{t-1} + beta_t k_t v_t^T,   o_t = q_t S_t
+
+    With g constant along d it is ``gated_delta_rule`` (Diag(alpha) = alpha I commutes)."""
+    q, k, v, beta, g = (np.asarray(x, dtype=dtype) for x in (q, k, v, beta, g))
+    b, t, h, d = q.shape
+    s = np.zeros((b, h, d, d), dtype=dtype) if state is None else np.array(state, dtype=dtype)
+    out = np.zeros((b, t, h, d), dtype=dtype)
+    for i in range(t):
+        kt, vt, qt = k[:, i], v[:, i], q[:, i]
+        bt = beta[:, i][..., None, None]
+        s = np.exp(g[:, i])[..., None] * s  # rows (key channels) decay
+        ks = np.einsum("bhd,bhde->bhe", kt, s)
+        s = s - bt * np.einsum("bhd,bhe->bhde", kt, ks) + bt * np.einsum("bhd,bhe->bhde", kt, vt)
+        out[:, i] = np.einsum("bhd,bhde->bhe", qt, s)
+    return out, s
+
+
+def kda_wy_chunked(q, k, v, beta, g, state=None, chunk=16, dtype=np.float64):
+    """The chunked (WY/UT) form of ``kda_delta_rule``, independent of the loop above.
+
+    Per chunk, with G_t the cumulative log-gates inside the chunk (a d_k-vector per token),
+    K^ = K * exp(G) and K~ = K * exp(-G) (row-wise), Q^ = Q * exp(G):
+        A = strict_lower(diag(beta) K^ K~^T),  U = (I + A)^-1 diag(beta) (V - K^ S)
+        O = Q^ S + lower_incl(Q^ K~^T) U,      S <- Diag(exp(G_C)) S + (K * exp(G_C - G))^T U
+    (exp(-G) grows along the chunk, so the chunk is kept short for the test inputs.)"""
+    q, k, v, beta, g = (np.asarray(x, dtype=dtype) for x in (q, k, v, beta, g))
+    b, t, h, d = q.shape
+    s_all = np.zeros((b, h, d, d), dtype=dtype) if state is None else np.array(state, dtype=dtype)
+    out = np.zeros((b, t, h, d), dtype=dtype)
+    for bi in range(b):
+        for hi in range(h):
+            s = s_all[bi, hi]
+            for c0 in range(0, t, chunk):
+                sl = slice(c0, min(t, c0 + chunk))
+                K, Q, V = k[bi, sl, hi], q[bi, sl, hi], v[bi, sl, hi]
+                be, G = beta[bi, sl, hi], np.cumsum(g[bi, sl, hi], axis=0)
+                n = K.shape[0]
+                Kh, Kt, Qh = K * np.exp(G), K * np.exp(-G), Q * np.exp(G)
+                A = np.tril(be[:, None] * (Kh @ Kt.T), -1)
+                U = np.linalg.solve(np.eye(n) + A, be[:, None] * (V - Kh @ s))
+                out[bi, sl, hi] = Qh @ s + np.tril(Qh @ Kt.T) @ U
+                s = np.exp(G[-1])[:, None] * s + (K * np.exp(G[-1] - G)).T @ U
+            s_all[bi, hi] = s
+    return out, s_all
+
+
+def kda_step(s, q, k, v, beta, g):
+    """One KDA token for (B, H, D) inputs, beta (B, H), g (B, H, D); returns (o, new state)."""
+    o, s1 = kda_delta_rule(np.asarray(q)[:, None], np.asarray(k)[:, None], np.asarray(v)[:, None],
+                           np.asarray(beta)[:, None], np.asarray(g)[:, None], s)
+    return o[:, 0], s1

@@ -18,7 +18,7 @@ import torch  # noqa: F401  (see module docstring: must precede CDLL)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpmdelta.so")
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256
@@ -50,6 +50,8 @@ EXPORTS = (
     "pm_varlen_check",
     "pm_gated_delta_bwd",
     "pm_gated_delta_bwd_workspace_bytes",
+    "pm_kda_delta_fwd",
+    "pm_kda_delta_step",
 )
 
 _lib = None
@@ -90,6 +92,10 @@ def lib() -> ctypes.CDLL:
         L.pm_gated_delta_fwd.restype = i
         L.pm_gated_delta_step.argtypes = [vp] * 7 + [i] * 4 + [vp]
         L.pm_gated_delta_step.restype = i
+        L.pm_kda_delta_fwd.argtypes = [vp] * 8 + [i] * 6 + [vp]
+        L.pm_kda_delta_fwd.restype = i
+        L.pm_kda_delta_step.argtypes = [vp] * 7 + [i] * 4 + [vp]
+        L.pm_kda_delta_step.restype = i
         L.pm_delta_step_slots.argtypes = [vp, vp, i, vp, vp, vp, vp, vp, i, i, i, i, vp]
         L.pm_delta_step_slots.restype = i
         L.pm_linear_attention.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, i, i, vp]

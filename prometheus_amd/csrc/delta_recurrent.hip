@@ -40,6 +40,14 @@
 //   S_t = alpha_t (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T,
 // i.e. u = beta (v - alpha k^T S), S = alpha S + k u^T.  With g = 0, alpha = 1
 // and the arithmetic is exactly the ungated step.
+//
+// Per-channel variant (KDA: log-gates g per token, head and key channel,
+// alpha_t = exp(g_t) a d_k-vector):
+//   S_t = (I - beta_t k_t k_t^T) Diag(alpha_t) S_{t-1} + beta_t k_t v_t^T.
+// Row d of S is the key channel d, so a thread scales its RPT rows by their
+// own alpha before the token's dot products, and the rest is the ungated step
+// on the decayed state.  The alpha rows are staged like the k rows (one more
+// [16][DPL] array per buffer, after the per-token scalars).
 
 #include "pm_common.h"
 #include "pm_internal.h"
@@ -49,7 +57,8 @@ namespace pm {
 
 // One (sequence, head) column group per workgroup; blockIdx = (slot * ncg + c) * 8 + x
 // for pair = pair0 + slot * 8 + x and column group c.
-template <int RPT, int RS, bool GATED, typename InT, typename OutT>
+// GM: 0 no gate, 1 a log-gate per (token, head), 2 one per (token, head, key channel).
+template <int RPT, int RS, int GM, typename InT, typename OutT>
 __global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
     const InT* __restrict__ q, const InT* __restrict__ k, const InT* __restrict__ v,
     const float* __restrict__ beta, const float* s0, OutT* __restrict__ o, float* s_out,
@@ -58,6 +67,8 @@ __global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
     using G = RecGeo<RPT, RS>;
     constexpr int CW = G::CW, DP = G::DP, SL = G::SL, DPL = G::DPL;
     constexpr int KB = kRecSteps, NT = kRecThreads;
+    constexpr bool GATED = GM == 1, CHAN = GM == 2;
+    constexpr int BUFX = G::BUF + (CHAN ? KB * DPL : 0);  // floats of one staging buffer
     constexpr int NG = KB * DP / 4;           // 4-element groups in a staged q or k block
     constexpr int NPF = (NG + NT - 1) / NT;   // groups per thread
     constexpr int NPV = KB * CW / NT;         // staged v elements per thread (16 / RS)
@@ -100,6 +111,7 @@ __global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
 
     // ---- prefetch registers for one block ----
     Raw4<InT> pk[NPF], pq[NPF];
+    Raw4<float> pa[CHAN ? NPF : 1];
     InT pv[NPV];
     float pb = 0.f, pg = 0.f;
     auto prefetch = [&](int t0, int nst) {
@@ -115,6 +127,7 @@ __global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
             }
             pk[s].load(k + a, n, vec);
             pq[s].load(q + a, n, vec);
+            if constexpr (CHAN) pa[s].load(gate + a, n, vec);
         }
 #pragma unroll
         for (int s = 0; s < NPV; ++s) {
@@ -167,6 +180,13 @@ __global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
                 const int pos = j * DPL + (d / RPT) * SL + d % RPT;
                 *reinterpret_cast<float4*>(sk + pos) = make_float4(xk[0], xk[1], xk[2], xk[3]);
                 *reinterpret_cast<float4*>(sq + pos) = make_float4(xq[0], xq[1], xq[2], xq[3]);
+                if constexpr (CHAN) {
+                    float xa[4];
+                    pa[s].get(xa, true);
+                    // past the row end g = 0: alpha 1 on rows of S that stay zero
+                    *reinterpret_cast<float4*>(buf + G::BUF + pos) =
+                        make_float4(expf(xa[0]), expf(xa[1]), expf(xa[2]), expf(xa[3]));
+                }
                 if (d == 0) sc[4 * j + 1] = qk;
             }
         }
@@ -194,6 +214,15 @@ __global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
                 const float4 t = kp[i], w = qp[i];
                 kk[4 * i] = t.x, kk[4 * i + 1] = t.y, kk[4 * i + 2] = t.z, kk[4 * i + 3] = t.w;
                 qq[4 * i] = w.x, qq[4 * i + 1] = w.y, qq[4 * i + 2] = w.z, qq[4 * i + 3] = w.w;
+            }
+            if constexpr (CHAN) {
+                // decay each row by its channel's alpha first: S <- Diag(alpha) S
+                const float4* ap = reinterpret_cast<const float4*>(buf + G::BUF + j * DPL + r * SL);
+#pragma unroll
+                for (int i = 0; i < RPT / 4; ++i) {
+                    const float4 t = ap[i];
+                    S[4 * i] *= t.x, S[4 * i + 1] *= t.y, S[4 * i + 2] *= t.z, S[4 * i + 3] *= t.w;
+                }
             }
             float ks, qs;
             row_dot2<RPT>(kk, qq, S, ks, qs);
@@ -236,19 +265,19 @@ __global__ __launch_bounds__(kRecThreads) void delta_recurrent_kernel(
     const int nblk = (len + KB - 1) / KB;
     if (nblk > 0) prefetch(0, min(KB, len));
     for (int b = 0; b < nblk; ++b) {
-        float* buf = lds + (b & 1) * G::BUF;
+        float* buf = lds + (b & 1) * BUFX;
         const int t0 = b * KB, nst = min(KB, len - t0);
         // buf was last read by block b - 2's token loop, before the previous barrier
         stage(buf);
         __syncthreads();
         if (b + 1 < nblk) prefetch(t0 + KB, min(KB, len - t0 - KB));
-        if (b > 0) store_o(lds + ((b - 1) & 1) * G::BUF, t0 - KB, KB);
+        if (b > 0) store_o(lds + ((b - 1) & 1) * BUFX, t0 - KB, KB);
         tokens(buf, nst);
     }
     if (nblk > 0) {
         __syncthreads();
         const int t0 = (nblk - 1) * KB;
-        store_o(lds + ((nblk - 1) & 1) * G::BUF, t0, len - t0);
+        store_o(lds + ((nblk - 1) & 1) * BUFX, t0, len - t0);
     }
 
     if (col_ok) {
@@ -272,11 +301,13 @@ static void recurrent_geometry(int D, int* rpt, int* rs) {
 
 static bool is_aligned(const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
 
-template <int RPT, int RS, bool GATED, typename InT, typename OutT>
+template <int RPT, int RS, int GM, typename InT, typename OutT>
 static hipError_t launch_rec_t(const RecurrentArgs& a, hipStream_t st) {
     using G = RecGeo<RPT, RS>;
-    auto kern = delta_recurrent_kernel<RPT, RS, GATED, InT, OutT>;
-    if (G::BYTES > 64 * 1024) {
+    auto kern = delta_recurrent_kernel<RPT, RS, GM, InT, OutT>;
+    // the per-channel gate stages one more [kRecSteps][DPL] array per buffer
+    constexpr size_t BYTES = G::BYTES + (GM == 2 ? 2 * sizeof(float) * kRecSteps * G::DPL : 0);
+    if (BYTES > 64 * 1024) {
         // the dynamic-LDS limit is a per-device function attribute
         int dev = 0;
         hipError_t e = hipGetDevice(&dev);
@@ -284,7 +315,7 @@ static hipError_t launch_rec_t(const RecurrentArgs& a, hipStream_t st) {
         static bool attr_set[64] = {};
         if (dev < 0 || dev >= 64 || !attr_set[dev]) {
             e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(G::BYTES));
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(BYTES));
             if (e != hipSuccess) return e;
             if (dev >= 0 && dev < 64) attr_set[dev] = true;
         }
@@ -292,16 +323,17 @@ static hipError_t launch_rec_t(const RecurrentArgs& a, hipStream_t st) {
     const int ncg = (a.D + G::CW - 1) / G::CW;
     // 16-byte (fp32) or 8-byte (bf16) row loads when every q/k row group is aligned
     const size_t vb = sizeof(InT) * 4;
-    const int vec = (a.D % 4 == 0) && is_aligned(a.q, vb) && is_aligned(a.k, vb);
+    const int vec = (a.D % 4 == 0) && is_aligned(a.q, vb) && is_aligned(a.k, vb) &&
+                    (GM != 2 || is_aligned(a.gk, 16));
     // at most 2^22 workgroups (2^30 work-items) per launch
     const long per = ((1L << 22) / (8L * ncg)) * 8;
     for (long p0 = 0; p0 < a.n_pairs; p0 += per) {
         const long np = a.n_pairs - p0 < per ? a.n_pairs - p0 : per;
         const dim3 grid(static_cast<unsigned>((np + 7) / 8 * 8 * ncg));
-        hipLaunchKernelGGL(kern, grid, dim3(kRecThreads), G::BYTES, st, static_cast<const InT*>(a.q),
+        hipLaunchKernelGGL(kern, grid, dim3(kRecThreads), BYTES, st, static_cast<const InT*>(a.q),
                            static_cast<const InT*>(a.k), static_cast<const InT*>(a.v), a.beta, a.s0,
                            static_cast<OutT*>(a.o), a.s_out, a.cu_seqlens, static_cast<int>(p0), a.n_pairs,
-                           ncg, a.T, a.H, a.D, a.l2norm ? 1 : 0, vec, a.g);
+                           ncg, a.T, a.H, a.D, a.l2norm ? 1 : 0, vec, GM == 2 ? a.gk : a.g);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -310,7 +342,8 @@ static hipError_t launch_rec_t(const RecurrentArgs& a, hipStream_t st) {
 
 template <int RPT, int RS, typename InT, typename OutT>
 static hipError_t launch_rec_g(const RecurrentArgs& a, hipStream_t st) {
-    return a.g ? launch_rec_t<RPT, RS, true, InT, OutT>(a, st) : launch_rec_t<RPT, RS, false, InT, OutT>(a, st);
+    if (a.gk) return launch_rec_t<RPT, RS, 2, InT, OutT>(a, st);
+    return a.g ? launch_rec_t<RPT, RS, 1, InT, OutT>(a, st) : launch_rec_t<RPT, RS, 0, InT, OutT>(a, st);
 }
 
 template <typename InT, typename OutT>

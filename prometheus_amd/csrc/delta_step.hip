@@ -26,8 +26,10 @@ namespace pm {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// GATED: S' = alpha (S - beta k (k^T S)) + beta k v^T with alpha = exp(g[b, h]).
-template <int D, typename InT, bool GATED>
+// GM 1 (gated): S' = alpha (S - beta k (k^T S)) + beta k v^T with alpha = exp(g[b, h]).
+// GM 2 (per-channel, KDA): S is first decayed row by row, S <- Diag(exp(g[b, h, :])) S,
+// and the ungated step runs on the decayed state.
+template <int D, typename InT, int GM>
 __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
                                                          const InT* __restrict__ q,
                                                          const InT* __restrict__ k,
@@ -44,7 +46,8 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
     constexpr int NW = NT / 64;    // waves
     static_assert(CG <= 64 && RPT >= 1, "unsupported D");
 
-    __shared__ float sk[D], sq[D], sv[D];
+    constexpr bool GATED = GM == 1, CHAN = GM == 2;
+    __shared__ float sk[D], sq[D], sv[D], sa[CHAN ? D : 1];
     __shared__ f32x4 red[2][NW][CG];
 
     const int H = static_cast<int>(gridDim.x), bi = b0 + static_cast<int>(blockIdx.y);
@@ -55,11 +58,13 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
 
     // the token's q, k, v and beta do not depend on the slot: their loads go out first
     InT kq = InT(), qq = InT(), vq = InT();
+    float gq = 0.f;
     if (t < D) {
         const size_t a = static_cast<size_t>(pair) * D + t;
         kq = k[a];
         qq = q[a];
         vq = v[a];
+        if constexpr (CHAN) gq = gate[a];
     }
     const float b = beta[pair];
     size_t state = pair;
@@ -84,8 +89,13 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
         sk[t] = to_f32(kq);
         sq[t] = to_f32(qq);
         sv[t] = to_f32(vq);
+        if constexpr (CHAN) sa[t] = expf(gq);
     }
     __syncthreads();
+    if constexpr (CHAN) {
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) S[i] *= sa[rg + RG * i];
+    }
 
     f32x4 kp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -135,20 +145,22 @@ __global__ __launch_bounds__(256) void delta_step_kernel(float* __restrict__ s,
 
 bool step_supported(int D) { return D == 32 || D == 64 || D == 128; }
 
-template <int D, bool GATED>
+template <int D, int GM>
 static hipError_t launch_step_g(const StepArgs& a, hipStream_t st) {
     // grid (H, rows of b), at most 65535 rows per launch
     const int n_b = a.n_pairs / a.H;
     for (int b0 = 0; b0 < n_b; b0 += 65535) {
         const dim3 grid(static_cast<unsigned>(a.H), static_cast<unsigned>(min(65535, n_b - b0)));
         if (a.in_bf16) {
-            hipLaunchKernelGGL((delta_step_kernel<D, uint16_t, GATED>), grid, dim3(256), 0, st, a.s,
+            hipLaunchKernelGGL((delta_step_kernel<D, uint16_t, GM>), grid, dim3(256), 0, st, a.s,
                                static_cast<const uint16_t*>(a.q), static_cast<const uint16_t*>(a.k),
-                               static_cast<const uint16_t*>(a.v), a.beta, a.o, a.slots, b0, a.n_slots, a.g);
+                               static_cast<const uint16_t*>(a.v), a.beta, a.o, a.slots, b0, a.n_slots,
+                               GM == 2 ? a.gk : a.g);
         } else {
-            hipLaunchKernelGGL((delta_step_kernel<D, float, GATED>), grid, dim3(256), 0, st, a.s,
+            hipLaunchKernelGGL((delta_step_kernel<D, float, GM>), grid, dim3(256), 0, st, a.s,
                                static_cast<const float*>(a.q), static_cast<const float*>(a.k),
-                               static_cast<const float*>(a.v), a.beta, a.o, a.slots, b0, a.n_slots, a.g);
+                               static_cast<const float*>(a.v), a.beta, a.o, a.slots, b0, a.n_slots,
+                               GM == 2 ? a.gk : a.g);
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -158,7 +170,8 @@ static hipError_t launch_step_g(const StepArgs& a, hipStream_t st) {
 
 template <int D>
 static hipError_t launch_step_d(const StepArgs& a, hipStream_t st) {
-    return a.g ? launch_step_g<D, true>(a, st) : launch_step_g<D, false>(a, st);
+    if (a.gk) return launch_step_g<D, 2>(a, st);
+    return a.g ? launch_step_g<D, 1>(a, st) : launch_step_g<D, 0>(a, st);
 }
 
 hipError_t launch_step(const StepArgs& a, hipStream_t st) {

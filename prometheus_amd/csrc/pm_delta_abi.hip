@@ -161,7 +161,8 @@ int check_dtypes(int in_dtype, int out_dtype) {
 int forward(const void* q, const void* k, const void* v, const float* beta, const float* s0,
             void* o, float* s_out, const int32_t* cu, int n_seq, int T, int total_T, int H,
             int D, int in_dtype, int out_dtype, int chunk, hipStream_t st,
-            const float* g = nullptr, void* workspace = nullptr, size_t ws_bytes = 0) {
+            const float* g = nullptr, void* workspace = nullptr, size_t ws_bytes = 0,
+            const float* gk = nullptr) {
     const bool varlen = cu != nullptr;
     const long n_pairs = static_cast<long>(n_seq) * H;
     const long n_tok = varlen ? static_cast<long>(total_T) : static_cast<long>(n_seq) * T;
@@ -185,11 +186,15 @@ int forward(const void* q, const void* k, const void* v, const float* beta, cons
     const int path = g_path;
     const bool in_bf16 = in_dtype == PM_DTYPE_BF16;
     const bool want_chunked = path != 1;
-    const bool can_chunked = in_bf16 && pm::chunked_supported(D, H) && aligned(q, 16) &&
+    // per-channel gates (gk): the per-token kernel only
+    if (gk && path >= 2)
+        return fail(PM_E_UNSUPPORTED, "the per-channel gated forward runs on the per-token kernel only "
+                    "(path %d asks for the chunked one)", path);
+    const bool can_chunked = !gk && in_bf16 && pm::chunked_supported(D, H) && aligned(q, 16) &&
                              aligned(k, 16) && aligned(v, 16) &&
                              (out_dtype == PM_DTYPE_F32 ? aligned(o, 16) : aligned(o, 8));
     // fp32 q/k/v: the chunked forward on fp32 MFMA (plain forward only)
-    const bool can_f32 = !in_bf16 && !g && pm::chunked_supported(D, H) && aligned(q, 16) && aligned(k, 16) &&
+    const bool can_f32 = !in_bf16 && !g && !gk && pm::chunked_supported(D, H) && aligned(q, 16) && aligned(k, 16) &&
                          aligned(v, 16) && (out_dtype == PM_DTYPE_F32 ? aligned(o, 4) : aligned(o, 2));
     if (path >= 2 && !can_chunked && !can_f32)
         return fail(PM_E_UNSUPPORTED,
@@ -235,13 +240,15 @@ int forward(const void* q, const void* k, const void* v, const float* beta, cons
                         varlen ? total_T : T, H, D,
                         in_bf16, out_dtype == PM_DTYPE_BF16};
     a.g = g;
+    a.gk = gk;
     hipError_t e = pm::launch_recurrent(a, st);
     return e == hipSuccess ? 0 : hip_fail(e, "recurrent forward launch");
 }
 
-// The decode step, plain (g == NULL) or gated.
+// The decode step, plain (g == gk == NULL), gated (g) or per-channel gated (gk).
 int step(float* s_inout, const void* q, const void* k, const void* v, const float* beta,
-         const float* g, float* o, int B, int H, int D, int in_dtype, void* stream) {
+         const float* g, float* o, int B, int H, int D, int in_dtype, void* stream,
+         const float* gk = nullptr) {
     g_err[0] = '\0';
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (B < 0 || H < 0) return fail(PM_E_SHAPE, "B, H must be >= 0 (got %d, %d)", B, H);
@@ -259,6 +266,7 @@ int step(float* s_inout, const void* q, const void* k, const void* v, const floa
                        in_dtype == PM_DTYPE_BF16};
         a.H = H;
         a.g = g;
+        a.gk = gk;
         hipError_t e = pm::launch_step(a, st);
         return e == hipSuccess ? 0 : hip_fail(e, "decode step launch");
     }
@@ -268,6 +276,7 @@ int step(float* s_inout, const void* q, const void* k, const void* v, const floa
     pm::RecurrentArgs a{q, k, v, beta, s_inout, o, s_inout, nullptr, static_cast<int>(n_pairs), 1,
                         H, D, in_dtype == PM_DTYPE_BF16, false};
     a.g = g;
+    a.gk = gk;
     hipError_t e = pm::launch_recurrent(a, st);
     return e == hipSuccess ? 0 : hip_fail(e, "decode step launch");
 }
@@ -605,6 +614,30 @@ int pm_gated_delta_fwd(const void* q, const void* k, const void* v, const float*
     if (g && !aligned(g, 4)) return fail(PM_E_ALIGN, "g must be 4-byte aligned");
     return forward(q, k, v, beta, s0, o, s_out, nullptr, B, T, 0, H, D, in_dtype, out_dtype, 64,
                    static_cast<hipStream_t>(stream), g);
+}
+
+int pm_kda_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
+                     const float* g, const float* s0, void* o, float* s_out, int B, int T, int H,
+                     int D, int in_dtype, int out_dtype, void* stream) {
+    g_err[0] = '\0';
+    if (B < 0 || T < 0 || H < 0)
+        return fail(PM_E_SHAPE, "B, T, H must be >= 0 (got %d, %d, %d)", B, T, H);
+    if (D < 1 || D > PM_DELTA_MAX_D)
+        return fail(PM_E_SHAPE, "D must be in [1, %d] (got %d)", PM_DELTA_MAX_D, D);
+    if (int rc = check_dtypes(in_dtype, out_dtype)) return rc;
+    if (static_cast<long>(B) * T * H > 0 && !g) return fail(PM_E_NULL, "g is NULL");
+    if (g && !aligned(g, 4)) return fail(PM_E_ALIGN, "g must be 4-byte aligned");
+    return forward(q, k, v, beta, s0, o, s_out, nullptr, B, T, 0, H, D, in_dtype, out_dtype, 64,
+                   static_cast<hipStream_t>(stream), nullptr, nullptr, 0, g);
+}
+
+int pm_kda_delta_step(float* s_inout, const void* q, const void* k, const void* v,
+                      const float* beta, const float* g, float* o, int B, int H, int D,
+                      int in_dtype, void* stream) {
+    g_err[0] = '\0';
+    if (static_cast<long>(B) * H > 0 && !g) return fail(PM_E_NULL, "g is NULL");
+    if (g && !aligned(g, 4)) return fail(PM_E_ALIGN, "g must be 4-byte aligned");
+    return step(s_inout, q, k, v, beta, nullptr, o, B, H, D, in_dtype, stream, g);
 }
 
 }  // extern "C"

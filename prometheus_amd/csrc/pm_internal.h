@@ -24,6 +24,9 @@ struct RecurrentArgs {
     bool in_bf16, out_bf16;
     bool l2norm = false;  // q and k divided by max(||.||_2, 1e-6) per token on load
     const float* g = nullptr;  // gated variant: log-gates per (token, head), alpha = exp(g)
+    // per-channel variant (KDA; takes precedence over g): log-gates per (token, head, key
+    // channel), S <- Diag(exp(g)) S before each token; 16-byte aligned for vector loads
+    const float* gk = nullptr;
 };
 hipError_t launch_recurrent(const RecurrentArgs& a, hipStream_t st);
 
@@ -43,6 +46,7 @@ struct StepArgs {
     const int32_t* slots = nullptr;
     int H = 1, n_slots = 0;
     const float* g = nullptr;  // gated variant: log-gate per (b, h), alpha = exp(g)
+    const float* gk = nullptr; // per-channel variant (KDA): log-gates per (b, h, key channel)
 };
 bool step_supported(int D);
 hipError_t launch_step(const StepArgs& a, hipStream_t st);

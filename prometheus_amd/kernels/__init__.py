@@ -568,10 +568,11 @@ class _GatedDeltaResidual:
     chunk: int
 
 
-def _gated_forward(q, k, v, beta, g, state, out_dtype):
+def _gated_forward(q, k, v, beta, g, state, out_dtype, per_channel=False):
     batch, seq, heads, dim = _validate(q, k, v, beta, state)
-    if _shape(g) != (batch, seq, heads):
-        raise KernelError(f"g shape {_shape(g)} != {(batch, seq, heads)}")
+    gshape = (batch, seq, heads, dim) if per_channel else (batch, seq, heads)
+    if _shape(g) != gshape:
+        raise KernelError(f"g shape {_shape(g)} != {gshape}")
     odt = _out_dtype(out_dtype)
     if _on_host(q, k, v, beta, state):
         _check_beta_host(beta)
@@ -583,7 +584,8 @@ def _gated_forward(q, k, v, beta, g, state, out_dtype):
         sd = call.dev(state, torch.float32)
         o = torch.empty((batch, seq, heads, dim), dtype=odt, device=call.device)
         s_out = torch.empty((batch, heads, dim, dim), dtype=torch.float32, device=call.device)
-        rc = _native.lib().pm_gated_delta_fwd(
+        fwd = _native.lib().pm_kda_delta_fwd if per_channel else _native.lib().pm_gated_delta_fwd
+        rc = fwd(
             _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(gd), _ptr(sd), _ptr(o), _ptr(s_out),
             batch, seq, heads, dim, _code(cdt), _code(odt), _stream(call.device),
         )
@@ -698,15 +700,46 @@ def chunked_gated_delta_rule_fwd(q, k, v, beta, g, state, config, *, out_dtype=N
     return (call.out(o), call.out(s)), residual
 
 
+def chunked_kda_rule(q, k, v, beta, g, state=None, config=None, *, out_dtype=None):
+    """The delta rule with a decay per key channel (KDA, Kimi Delta Attention).
+
+    ``S_t = (I - beta_t k_t k_t^T) Diag(exp(g_t)) S_{t-1} + beta_t k_t v_t^T``,
+    ``o_t = q_t S_t``. q, k, v, beta, state and the return value as
+    ``chunked_delta_rule``; g: (batch, seq, heads, dim) fp32 log-gates, one per
+    key channel (g constant along dim gives ``chunked_gated_delta_rule``). Runs the
+    fp32 per-token kernel (``pm_kda_delta_fwd``) for every dtype and dim up to 256.
+    Forward only: a call that autograd would record raises ``KernelError``.
+    """
+    cfg = LinearAttnConfig() if config is None else config
+    _check_chunk(cfg)
+    if _wants_grad(q, k, v, beta, g, state):
+        raise KernelError("chunked_kda_rule has no backward; call it under torch.no_grad() "
+                          "or on inputs that do not require grad")
+    call, _, o, s = _gated_forward(q, k, v, beta, g, state, out_dtype, per_channel=True)
+    return call.out(o), call.out(s)
+
+
 def gated_delta_rule_step(q, k, v, beta, g, state):
     """One gated step for (B, H, D) tokens, g (B, H); ``state`` updated in place as in
     ``delta_rule_step``: ``S' = exp(g) (S - beta k (k^T S)) + beta k v^T``, ``o = q S'``."""
+    return _gated_step(q, k, v, beta, g, state, per_channel=False)
+
+
+def kda_delta_rule_step(q, k, v, beta, g, state):
+    """One KDA step for (B, H, D) tokens, g (B, H, D) log-gates per key channel;
+    ``state`` updated in place: ``S' = (I - beta k k^T) Diag(exp(g)) S + beta k v^T``,
+    ``o = q S'``."""
+    return _gated_step(q, k, v, beta, g, state, per_channel=True)
+
+
+def _gated_step(q, k, v, beta, g, state, per_channel):
     qs = _shape(q)
     if len(qs) != 3 or _shape(k) != qs or _shape(v) != qs:
         raise KernelError(f"q, k, v must all have shape (B, H, D); got {qs}")
     batch, heads, dim = qs
-    if _shape(beta) != (batch, heads) or _shape(g) != (batch, heads):
-        raise KernelError(f"beta and g must be {(batch, heads)}; got {_shape(beta)}, {_shape(g)}")
+    gshape = (batch, heads, dim) if per_channel else (batch, heads)
+    if _shape(beta) != (batch, heads) or _shape(g) != gshape:
+        raise KernelError(f"beta must be {(batch, heads)} and g {gshape}; got {_shape(beta)}, {_shape(g)}")
     if state is None or _shape(state) != (batch, heads, dim, dim):
         raise KernelError(f"state shape {_shape(state) if state is not None else None} != "
                           f"{(batch, heads, dim, dim)}")
@@ -721,9 +754,9 @@ def gated_delta_rule_step(q, k, v, beta, g, state):
         qd, kd, vd = call.dev(q, cdt), call.dev(k, cdt), call.dev(v, cdt)
         bd, gd = call.dev(beta, torch.float32), call.dev(g, torch.float32)
         o = torch.empty((batch, heads, dim), dtype=torch.float32, device=call.device)
-        rc = _native.lib().pm_gated_delta_step(_ptr(state), _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd),
-                                               _ptr(gd), _ptr(o), batch, heads, dim, _code(cdt),
-                                               _stream(call.device))
+        stepf = _native.lib().pm_kda_delta_step if per_channel else _native.lib().pm_gated_delta_step
+        rc = stepf(_ptr(state), _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(gd), _ptr(o), batch, heads,
+                   dim, _code(cdt), _stream(call.device))
         _native.check(rc)
     return call.out(o)
 
@@ -738,6 +771,8 @@ __all__ = [
     "chunked_delta_rule_bwd",
     "chunked_delta_rule_varlen",
     "check_varlen",
+    "chunked_kda_rule",
+    "kda_delta_rule_step",
     "delta_rule_step",
     "chunked_gated_delta_rule",
     "chunked_gated_delta_rule_fwd",

@@ -410,6 +410,27 @@ def test_gated_validation_without_gpu():
     assert lib.pm_gated_delta_step(p, p, p, p, p, None, p, 1, 2, 8, 0, None) == _native.E_NULL
 
 
+def test_kda_validation_without_gpu():
+    """The per-channel gates are (B, T, H, D) for the forward and (B, H, D) for the step;
+    the scalar-gate shapes are refused, as are NULL, misaligned and oversized inputs."""
+    q = np.zeros((1, 4, 2, 8), np.float32)
+    b = np.zeros((1, 4, 2), np.float32)
+    with pytest.raises(kernels.KernelError, match="g shape"):
+        kernels.chunked_kda_rule(q, q, q, b, b)
+    with pytest.raises(kernels.KernelError):
+        kernels.kda_delta_rule_step(q[:, 0], q[:, 0], q[:, 0], b[:, 0], b[:, 0],
+                                    np.zeros((1, 2, 8, 8), np.float32))
+    lib = _native.lib()
+    p = ctypes.c_void_p(256)
+    assert lib.pm_kda_delta_fwd(p, p, p, p, None, None, p, p, 1, 4, 2, 8, 0, 0, None) == _native.E_NULL
+    assert lib.pm_kda_delta_fwd(p, p, p, p, ctypes.c_void_p(2), None, p, p, 1, 4, 2, 8, 0, 0,
+                                None) == _native.E_ALIGN
+    assert lib.pm_kda_delta_fwd(p, p, p, p, p, None, p, p, 1, 4, 2, 300, 0, 0, None) == _native.E_SHAPE
+    assert lib.pm_kda_delta_fwd(p, p, p, p, p, None, p, p, 1, 4, 2, 8, 0, 7, None) == _native.E_DTYPE
+    assert lib.pm_kda_delta_step(p, p, p, p, p, None, p, 1, 2, 8, 0, None) == _native.E_NULL
+    assert lib.pm_kda_delta_step(p, p, p, p, p, p, p, 1, 2, 300, 0, None) == _native.E_SHAPE
+
+
 def test_selection_knobs_are_per_thread():
     """pm_delta_set_path / pm_delta_set_tile act on the calling thread only, so a
     workspace-size query and the call it sizes agree whatever another thread

@@ -223,3 +223,83 @@ def test_vjp_planted_mistakes_are_caught():
     for kind in ("no_alpha_in_gate", "G_not_scaled", "before_downdate"):
         assert abs(mutant(kind) - fd) > 1e-4 * max(1.0, abs(fd)), kind
     assert abs(mutant("correct") - fd) < 1e-6 * max(1.0, abs(fd))
+
+
+# --- KDA (per-channel decay) ---
+
+
+def _kda_problem(rng, shape, gate_scale=0.2):
+    q, k, v, beta, _, s0 = _problem(rng, shape)
+    g = -gate_scale * np.abs(rng.standard_normal(shape))  # a log-gate per key channel
+    return q, k, v, beta, g, s0
+
+
+def test_kda_channel_constant_gate_is_the_scalar_gate():
+    rng = np.random.default_rng(21)
+    q, k, v, beta, g, s0 = _problem(rng, (2, 9, 2, 5))
+    gch = np.repeat(g[..., None], 5, axis=-1)
+    o, s = gref.kda_delta_rule(q, k, v, beta, gch, s0)
+    o2, s2 = gref.gated_delta_rule(q, k, v, beta, g, s0)
+    np.testing.assert_allclose(o, o2, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(s, s2, rtol=1e-12, atol=1e-12)
+
+
+def test_kda_pure_decay_closed_form():
+    """beta = 0: row d of S decays by exp(sum of g[.., d]), and o_t = q_t Diag(exp G_t) S_0."""
+    rng = np.random.default_rng(22)
+    q, k, v, _, g, s0 = _kda_problem(rng, (1, 6, 2, 4))
+    o, s = gref.kda_delta_rule(q, k, v, np.zeros(g.shape[:3]), g, s0)
+    G = np.cumsum(g, axis=1)  # (B, T, H, D)
+    np.testing.assert_allclose(s, np.exp(G[:, -1])[..., None] * s0, rtol=1e-12)
+    want = np.einsum("bthd,bhde->bthe", q * np.exp(G), s0)
+    np.testing.assert_allclose(o, want, rtol=1e-12, atol=1e-14)
+
+
+def test_kda_one_token_closed_form():
+    rng = np.random.default_rng(23)
+    q, k, v, beta, g, s0 = _kda_problem(rng, (1, 1, 1, 6))
+    o, s = gref.kda_delta_rule(q, k, v, beta, g, s0)
+    a, b_ = np.exp(g[0, 0, 0]), beta[0, 0, 0]
+    kk, vv, qq, S0 = k[0, 0, 0], v[0, 0, 0], q[0, 0, 0], s0[0, 0]
+    ds = a[:, None] * S0
+    s1 = ds - b_ * np.outer(kk, kk @ ds) + b_ * np.outer(kk, vv)
+    np.testing.assert_allclose(s[0, 0], s1, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(o[0, 0, 0], qq @ s1, rtol=1e-12, atol=1e-14)
+
+
+@pytest.mark.parametrize("chunk", [1, 3, 8, 16])
+def test_kda_chunked_form_agrees(chunk):
+    rng = np.random.default_rng(24 + chunk)
+    q, k, v, beta, g, s0 = _kda_problem(rng, (2, 21, 2, 6))
+    o, s = gref.kda_delta_rule(q, k, v, beta, g, s0)
+    o2, s2 = gref.kda_wy_chunked(q, k, v, beta, g, s0, chunk=chunk)
+    np.testing.assert_allclose(o2, o, rtol=1e-9, atol=1e-10)
+    np.testing.assert_allclose(s2, s, rtol=1e-9, atol=1e-10)
+
+
+def test_kda_planted_mistakes_are_caught():
+    """Decay on the columns instead of the rows, decay after the rank-1 update, and the
+    opposite sign of the exponent each differ from the recurrence."""
+    rng = np.random.default_rng(25)
+    q, k, v, beta, g, s0 = _kda_problem(rng, (1, 8, 1, 5), 0.5)
+    o, s = gref.kda_delta_rule(q, k, v, beta, g, s0)
+
+    def mutant(kind):
+        st = s0[0, 0].copy()
+        outs = []
+        for i in range(q.shape[1]):
+            a = np.exp(-g[0, i, 0] if kind == "sign" else g[0, i, 0])
+            kk, vv, bb = k[0, i, 0], v[0, i, 0], beta[0, i, 0]
+            if kind == "columns":
+                st = st * a[None, :]
+            elif kind != "after":
+                st = a[:, None] * st
+            st = st - bb * np.outer(kk, kk @ st) + bb * np.outer(kk, vv)
+            if kind == "after":
+                st = a[:, None] * st
+            outs.append(q[0, i, 0] @ st)
+        return np.array(outs)
+
+    for kind in ("columns", "after", "sign"):
+        assert np.abs(mutant(kind) - o[0, :, 0]).max() > 1e-3, kind
+    np.testing.assert_allclose(mutant("correct"), o[0, :, 0], rtol=1e-12, atol=1e-12)

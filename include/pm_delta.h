@@ -308,6 +308,27 @@ int pm_gated_delta_bwd(const void* q, const void* k, const void* v, const float*
 size_t pm_gated_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype);
 
 /*
+ * Reverse mode of pm_kda_delta_fwd (a log-gate per key channel).  No reference
+ * counterpart (the reference names the KDA family, spec/03-model.md:12, and has no
+ * code for it).  Arguments as pm_gated_delta_bwd, with g and gg (B, T, H, D) fp32.
+ * With P_t = Diag(alpha_t) S_{t-1}, per token in reverse: y = P_t w,
+ * dL/dg_t[d] = <G_P[d, :], P_t[d, :]> with G_P = G - beta_t k_t w^T, and
+ * G <- Diag(alpha_t) G_P; the other gradients as pm_delta_bwd's.  The per-token fp32
+ * kernels (any D <= 256, fp32 or bf16 q/k/v), each 8-token checkpoint block
+ * recomputed forward from its start state.  Path 2 returns PM_E_UNSUPPORTED.
+ * workspace: pm_kda_delta_bwd_workspace_bytes.
+ */
+int pm_kda_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
+                     const float* g, const float* s0, const float* go, const float* gs, float* gq,
+                     float* gk, float* gv, float* gbeta, float* gg, float* gs0, int B, int T,
+                     int H, int D, int in_dtype, void* workspace, size_t ws_bytes, void* stream);
+
+/* Workspace bytes pm_kda_delta_bwd needs (0 for invalid shapes, dtypes or D > 256):
+ * pm_delta_bwd's per-token workspace plus, for D > 32, the partial sums of gg per
+ * column tile. */
+size_t pm_kda_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype);
+
+/*
  * pm_delta_bwd without a caller workspace and without any allocation.
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving or training loops,

@@ -192,3 +192,46 @@ def kda_step(s, q, k, v, beta, g):
     o, s1 = kda_delta_rule(np.asarray(q)[:, None], np.asarray(k)[:, None], np.asarray(v)[:, None],
                            np.asarray(beta)[:, None], np.asarray(g)[:, None], s)
     return o[:, 0], s1
+
+
+def kda_vjp(q, k, v, beta, g, go, gs, state=None, dtype=np.float64):
+    """Reverse mode of ``kda_delta_rule`` with the full state history.
+
+    With P_t = Diag(alpha_t) S_{t-1} (each key channel's row decayed) the step is
+    S_t = P_t + beta_t k_t u_t^T, u_t = v_t - P_t^T k_t, and per token in reverse
+    (G = dL/dS_t after G += q_t go_t^T) everything is ``gated_vjp``'s except the gate:
+
+        G_P = G - beta_t k_t w^T      gg_t[d] = <G_P[d, :], P_t[d, :]>      G <- Diag(alpha_t) G_P
+
+    g (B, T, H, D); returns (gq, gk, gv, gbeta, gg (B, T, H, D), gstate0). With g constant
+    along D, gg summed over D is ``gated_vjp``'s gg and the rest equals it.
+    """
+    q, k, v, beta, g = (np.asarray(x, dtype=dtype) for x in (q, k, v, beta, g))
+    b, t, h, d = q.shape
+    go = np.zeros((b, t, h, d), dtype) if go is None else np.asarray(go, dtype=dtype)
+    G = np.zeros((b, h, d, d), dtype) if gs is None else np.array(gs, dtype=dtype)
+    s = np.zeros((b, h, d, d), dtype=dtype) if state is None else np.array(state, dtype=dtype)
+    hist, us = [s], []
+    for i in range(t):
+        p = np.exp(g[:, i])[..., None] * s
+        u = v[:, i] - np.einsum("bhd,bhde->bhe", k[:, i], p)
+        s = p + beta[:, i][..., None, None] * np.einsum("bhd,bhe->bhde", k[:, i], u)
+        hist.append(s)
+        us.append(u)
+    gq, gk, gv, gg = (np.zeros((b, t, h, d), dtype) for _ in range(4))
+    gbeta = np.zeros((b, t, h), dtype)
+    for i in range(t - 1, -1, -1):
+        kt, bt, a = k[:, i], beta[:, i], np.exp(g[:, i])
+        s_t, p = hist[i + 1], a[..., None] * hist[i]
+        gq[:, i] = np.einsum("bhe,bhde->bhd", go[:, i], s_t)
+        G = G + np.einsum("bhd,bhe->bhde", q[:, i], go[:, i])
+        w = np.einsum("bhde,bhd->bhe", G, kt)
+        x = np.einsum("bhde,bhe->bhd", G, us[i])
+        y = np.einsum("bhde,bhe->bhd", p, w)
+        gv[:, i] = bt[..., None] * w
+        gbeta[:, i] = np.einsum("bhd,bhd->bh", kt, x)
+        gk[:, i] = bt[..., None] * (x - y)
+        G = G - bt[..., None, None] * np.einsum("bhd,bhe->bhde", kt, w)
+        gg[:, i] = np.einsum("bhde,bhde->bhd", G, p)
+        G = a[..., None] * G
+    return gq, gk, gv, gbeta, gg, G

@@ -52,6 +52,8 @@ EXPORTS = (
     "pm_gated_delta_bwd_workspace_bytes",
     "pm_kda_delta_fwd",
     "pm_kda_delta_step",
+    "pm_kda_delta_bwd",
+    "pm_kda_delta_bwd_workspace_bytes",
 )
 
 _lib = None
@@ -128,6 +130,10 @@ def lib() -> ctypes.CDLL:
         L.pm_gated_delta_bwd.restype = i
         L.pm_gated_delta_bwd_workspace_bytes.argtypes = [i] * 5
         L.pm_gated_delta_bwd_workspace_bytes.restype = sz
+        L.pm_kda_delta_bwd.argtypes = [vp] * 14 + [i] * 5 + [vp, sz, vp]
+        L.pm_kda_delta_bwd.restype = i
+        L.pm_kda_delta_bwd_workspace_bytes.argtypes = [i] * 5
+        L.pm_kda_delta_bwd_workspace_bytes.restype = sz
         got = L.pm_abi_version()
         if got != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH}: ABI version {got}, expected {ABI_VERSION}")

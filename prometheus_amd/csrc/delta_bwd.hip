@@ -87,7 +87,9 @@ static BwdGeo bwd_geo(int D) {
 // of its column, DPP column sums, tokens staged 16 at a time with the next block's
 // loads in flight), writing u_t = v_t - S_{t-1}^T k_t per token (through LDS, one
 // block later) and S after every kCk-th token and after the last.
-template <int RPT, int RS, typename InT, bool GATED>
+// GM: 0 ungated, 1 a log-gate per (token, head), 2 one per (token, head, key channel),
+// where P = Diag(alpha) S: each thread decays its rows before the token's dot product.
+template <int RPT, int RS, typename InT, int GM>
 __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
     const InT* __restrict__ k, const InT* __restrict__ v, const float* __restrict__ beta,
     const float* __restrict__ gate, const float* __restrict__ s0, float* __restrict__ u_ws,
@@ -96,7 +98,10 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
     constexpr int CW = G::CW, DP = G::DP, SL = G::SL, DPL = G::DPL;
     constexpr int KB = kRecSteps, NT = kRecThreads;
     constexpr int NG = KB * DP / 4, NPF = (NG + NT - 1) / NT, NPV = KB * CW / NT;
-    constexpr int BUF = KB * DPL + 2 * KB * CW + 4 * KB;  // k rows, v, u, beta
+    constexpr bool GATED = GM == 1, CHAN = GM == 2;
+    // k rows, v, u, beta (and alpha), then (CHAN) the alpha rows in the k rows' layout
+    constexpr int BUF0 = KB * DPL + 2 * KB * CW + 4 * KB;
+    constexpr int BUF = BUF0 + (CHAN ? KB * DPL : 0);
     static_assert(KB % kCk == 0, "checkpoints fall inside a staged block");
     extern __shared__ float4 lds4[];
     float* const lds = reinterpret_cast<float*>(lds4);
@@ -125,6 +130,7 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
     auto row = [&](int t) { return (static_cast<size_t>(tok0 + t) * H + h) * D; };
 
     Raw4<InT> pk[NPF];
+    Raw4<float> pa[CHAN ? NPF : 1];
     InT pv[NPV];
     float pb = 0.f, pg = 0.f;
     auto prefetch = [&](int t0, int nst) {
@@ -139,6 +145,7 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
                 a = row(t0 + j) + d;
             }
             pk[s].load(k + a, n, vec);
+            if constexpr (CHAN) pa[s].load(gate + a, n, vec);
         }
 #pragma unroll
         for (int s = 0; s < NPV; ++s) {
@@ -162,6 +169,12 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
             if (grp < NG) {
                 const int pos = j * DPL + (d / RPT) * SL + d % RPT;
                 *reinterpret_cast<float4*>(sk + pos) = make_float4(xk[0], xk[1], xk[2], xk[3]);
+                if constexpr (CHAN) {
+                    float xa[4];
+                    pa[s].get(xa, true);
+                    *reinterpret_cast<float4*>(buf + BUF0 + pos) =
+                        make_float4(expf(xa[0]), expf(xa[1]), expf(xa[2]), expf(xa[3]));
+                }
             }
         }
 #pragma unroll
@@ -191,6 +204,15 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
             for (int i = 0; i < RPT / 4; ++i) {
                 const float4 t = kp[i];
                 kk[4 * i] = t.x, kk[4 * i + 1] = t.y, kk[4 * i + 2] = t.z, kk[4 * i + 3] = t.w;
+            }
+            if constexpr (CHAN) {
+                // P = Diag(alpha) S, row by row
+                const float4* ap = reinterpret_cast<const float4*>(buf + BUF0 + j * DPL + r * SL);
+#pragma unroll
+                for (int i = 0; i < RPT / 4; ++i) {
+                    const float4 t = ap[i];
+                    S[4 * i] *= t.x, S[4 * i + 1] *= t.y, S[4 * i + 2] *= t.z, S[4 * i + 3] *= t.w;
+                }
             }
             const float ks = col_sum<RS>(row_dot<RPT>(kk, S));
             // GATED: the decayed state P = alpha S enters both the prediction and the update
@@ -239,11 +261,12 @@ __global__ __launch_bounds__(kRecThreads) void delta_bwd_ckpt_kernel(
     }
 }
 
-template <int RPT, int RS, typename InT, bool GATED>
+template <int RPT, int RS, typename InT, int GM>
 static hipError_t launch_ckpt_t(const BwdArgs& a, float* u_ws, float* ck_ws, hipStream_t st) {
     using G = RecGeo<RPT, RS>;
-    constexpr size_t kBytes = 2 * sizeof(float) * (kRecSteps * G::DPL + 2 * kRecSteps * G::CW + 4 * kRecSteps);
-    auto kern = delta_bwd_ckpt_kernel<RPT, RS, InT, GATED>;
+    constexpr size_t kBytes = 2 * sizeof(float) * ((GM == 2 ? 2 : 1) * kRecSteps * G::DPL +
+                                                   2 * kRecSteps * G::CW + 4 * kRecSteps);
+    auto kern = delta_bwd_ckpt_kernel<RPT, RS, InT, GM>;
     if (kBytes > 64 * 1024) {
         // the dynamic-LDS limit is a per-device function attribute
         int dev = 0;
@@ -259,7 +282,8 @@ static hipError_t launch_ckpt_t(const BwdArgs& a, float* u_ws, float* ck_ws, hip
     }
     const int ncg = (a.D + G::CW - 1) / G::CW;
     const size_t vb = sizeof(InT) * 4;
-    const int vec = (a.D % 4 == 0) && reinterpret_cast<uintptr_t>(a.k) % vb == 0;
+    const int vec = (a.D % 4 == 0) && reinterpret_cast<uintptr_t>(a.k) % vb == 0 &&
+                    (GM != 2 || reinterpret_cast<uintptr_t>(a.g) % 16 == 0);
     // at most 2^22 workgroups (2^30 work-items) per launch
     const long per = ((1L << 22) / (8L * ncg)) * 8;
     for (long p0 = 0; p0 < a.n_pairs; p0 += per) {
@@ -276,17 +300,17 @@ static hipError_t launch_ckpt_t(const BwdArgs& a, float* u_ws, float* ck_ws, hip
 
 // RPT 8 and RS the smallest power of two with 8 RS >= D for D <= 128; RPT 16 and RS 16
 // above (the per-token forward's geometry).
-template <typename InT, bool GATED>
+template <typename InT, int GM>
 static hipError_t launch_ckpt(const BwdArgs& a, float* u_ws, float* ck_ws, hipStream_t st) {
-    if (a.D > 128) return launch_ckpt_t<16, 16, InT, GATED>(a, u_ws, ck_ws, st);
+    if (a.D > 128) return launch_ckpt_t<16, 16, InT, GM>(a, u_ws, ck_ws, st);
     int rs = 1;
     while (8 * rs < a.D) rs <<= 1;
     switch (rs) {
-        case 1: return launch_ckpt_t<8, 1, InT, GATED>(a, u_ws, ck_ws, st);
-        case 2: return launch_ckpt_t<8, 2, InT, GATED>(a, u_ws, ck_ws, st);
-        case 4: return launch_ckpt_t<8, 4, InT, GATED>(a, u_ws, ck_ws, st);
-        case 8: return launch_ckpt_t<8, 8, InT, GATED>(a, u_ws, ck_ws, st);
-        default: return launch_ckpt_t<8, 16, InT, GATED>(a, u_ws, ck_ws, st);
+        case 1: return launch_ckpt_t<8, 1, InT, GM>(a, u_ws, ck_ws, st);
+        case 2: return launch_ckpt_t<8, 2, InT, GM>(a, u_ws, ck_ws, st);
+        case 4: return launch_ckpt_t<8, 4, InT, GM>(a, u_ws, ck_ws, st);
+        case 8: return launch_ckpt_t<8, 8, InT, GM>(a, u_ws, ck_ws, st);
+        default: return launch_ckpt_t<8, 16, InT, GM>(a, u_ws, ck_ws, st);
     }
 }
 
@@ -318,7 +342,12 @@ __device__ __forceinline__ float slice_dot(const float (&a)[kRpt], const float (
 // checkpoint block is first recomputed forward from its start state (the previous
 // block's end, or S0), its states before every token kept in registers, and the
 // reverse walk reads them.
-template <typename InT, int RSC, int RSR, int NCT, bool GATED>
+//
+// GM = 2 (a log-gate per key channel, P_t = Diag(alpha_t) S_{t-1}): the same walk with
+// row d scaled by alpha_t[d]: y_d = alpha_t[d] (S_{t-1} w)_d, dL/dg_t[d] = alpha_t[d]
+// <G_P[d, :], S_{t-1}[d, :]> (a per-row output like gk, no sum over d), and
+// G <- Diag(alpha_t) G_P (the column layout scales each of its rows by its own alpha).
+template <typename InT, int RSC, int RSR, int NCT, int GM>
 __global__ __launch_bounds__(512) void delta_bwd_kernel(
     const InT* __restrict__ q, const InT* __restrict__ k, const float* __restrict__ beta,
     const float* __restrict__ gate, const float* __restrict__ s0,
@@ -335,7 +364,10 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
     // per-thread staging slots, for the fewest threads a launch of this geometry has
     constexpr int NTMIN = NCT * RSC < 64 ? 64 : NCT * RSC;
     constexpr int MK = (KB * DP + NTMIN - 1) / NTMIN, MG = (KB * CP + NTMIN - 1) / NTMIN;
-    constexpr int SB = 2 * KB * DPL + 2 * KB * CPL + 2 * KB;  // one staging buffer
+    constexpr bool GATED = GM != 0, CHAN = GM == 2;  // GATED: any decay
+    // one staging buffer: k, q, go, u, beta and alpha, then (CHAN) the alpha rows
+    constexpr int SB0 = 2 * KB * DPL + 2 * KB * CPL + 2 * KB;
+    constexpr int SB = SB0 + (CHAN ? KB * DPL : 0);
     const int NT = blockDim.x, NWV = NT / 64;
     // outputs of a block, written out one block later: by block parity,
     // [KB][D] gbeta terms k[d] x[d], [KB][D] gq, [KB][D] gk, [KB][NC] gv
@@ -361,7 +393,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
     float* gq_t = gq + tile * part_stride_e;
     float* gk_t = gk + tile * part_stride_e;
     float* gb_t = gb + tile * part_stride_b;
-    float* gg_t = GATED ? gg + tile * part_stride_b : nullptr;
+    float* gg_t = GATED ? gg + tile * (CHAN ? part_stride_e : part_stride_b) : nullptr;
 
     // w's padding entries (tile columns past NC or D) are read as zeros, never written
     for (int x = tid; x < 2 * CPL; x += NT) sw[x] = 0.f;
@@ -377,7 +409,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
 
     // ---- one checkpoint block's inputs, loaded a block ahead into registers ----
     InT pk[MK], pq[MK];
-    float pg[MG], pu[MG], ps[kRpt], pb = 0.f, pa = 0.f;
+    float pg[MG], pu[MG], ps[kRpt], pb = 0.f, pa = 0.f, pac[CHAN ? MK : 1];
     auto prefetch = [&](int blk) {
         const int lo = blk * kCk, nst = min(T, lo + kCk) - lo;
 #pragma unroll
@@ -388,6 +420,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
             const size_t a = ok ? (static_cast<size_t>(tok0 + lo + j) * H + h) * D + x : 0;
             pk[s] = ok ? k[a] : InT(0);
             pq[s] = ok ? q[a] : InT(0);
+            if constexpr (CHAN) pac[s] = ok ? gate[a] : 0.f;
         }
 #pragma unroll
         for (int s = 0; s < MG; ++s) {
@@ -398,7 +431,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
             pu[s] = ok ? u_p[static_cast<size_t>(lo + j) * D + col0 + c] : 0.f;
         }
         if (tid < KB) pb = tid < nst ? beta[static_cast<size_t>(tok0 + lo + tid) * H + h] : 0.f;
-        if (GATED && tid < KB) pa = tid < nst ? gate[static_cast<size_t>(tok0 + lo + tid) * H + h] : 0.f;
+        if (GM == 1 && tid < KB) pa = tid < nst ? gate[static_cast<size_t>(tok0 + lo + tid) * H + h] : 0.f;
         // the block's end state, walked back (GATED: its start state, recomputed forward)
         const float* cp = !GATED      ? ck_p + static_cast<size_t>(blk) * D * D
                           : blk > 0   ? ck_p + static_cast<size_t>(blk - 1) * D * D
@@ -423,6 +456,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 const int pos = (idx / DP) * DPL + spad(idx % DP);
                 sk[pos] = to_f32(pk[s]);
                 sq[pos] = to_f32(pq[s]);
+                if constexpr (CHAN) buf[SB0 + pos] = expf(pac[s]);  // 1 past the row or block
             }
         }
 #pragma unroll
@@ -435,7 +469,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
             }
         }
         if (tid < KB) sb[tid] = pb;
-        if (GATED && tid < KB) sb[KB + tid] = expf(pa);
+        if (GM == 1 && tid < KB) sb[KB + tid] = expf(pa);
 #pragma unroll
         for (int i = 0; i < kRpt; ++i) Sr[i] = ps[i];
     };
@@ -444,11 +478,13 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
         const float* soq = so + KB * D;
         const float* sok = soq + KB * D;
         const float* sov = sok + KB * D;
+        [[maybe_unused]] const float* sog = sok + KB * D + KB * NC;  // GATED: the gate terms
         for (int idx = tid; idx < nst * D; idx += NT) {
             const int j = idx / D, x = idx % D;
             const size_t a = (static_cast<size_t>(tok0 + lo + j) * H + h) * D + x;
             gq_t[a] = soq[idx];
             gk_t[a] = sok[idx];
+            if constexpr (CHAN) gg_t[a] = sog[idx];
         }
         for (int idx = tid; idx < nst * NC; idx += NT) {
             const int j = idx / NC, c = idx % NC;
@@ -460,8 +496,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
             sum = wave_sum_row3(sum);
             if (lane == 63) gb_t[static_cast<size_t>(tok0 + lo + j) * H + h] = sum;
         }
-        if constexpr (GATED) {
-            const float* sog = sov + KB * NC;
+        if constexpr (GM == 1) {
             for (int j = wave; j < nst; j += NWV) {
                 float sum = 0.f;
                 for (int x = lane; x < D; x += 64) sum += sog[j * D + x];
@@ -492,16 +527,18 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
         float* sok = soq + KB * D;
         float* sov = sok + KB * D;
         float* sog = sov + KB * NC;
+        // CHAN: alpha of token j for row d (row layout)
+        const float* sar = buf + SB0;
+        auto alpha_row = [&](int j) { return CHAN ? (ok_r ? sar[j * DPL + spad(d)] : 1.f) : sb[KB + j]; };
         // GATED: the block recomputed forward from its start state; Sh[j] = S before token lo + j
         float Sh[GATED ? KB : 1][kRpt];
         if constexpr (GATED) {
-            const float* sa = sb + KB;
 #pragma unroll
             for (int j = 0; j < KB; ++j) {
                 if (j < nst) {
                     float ur[kRpt];
                     load_slice(su + j * CPL + rr * kSl, ur);
-                    const float a = sa[j], bkd = sb[j] * (ok_r ? sk[j * DPL + spad(d)] : 0.f);
+                    const float a = alpha_row(j), bkd = sb[j] * (ok_r ? sk[j * DPL + spad(d)] : 0.f);
 #pragma unroll
                     for (int i = 0; i < kRpt; ++i) {
                         Sh[j][i] = Sr[i];
@@ -547,7 +584,7 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                 if (rr == 0 && ok_r) soq[j * D + d] = gqp;
                 // S_{t-1} = S_t - b k u^T (row layout); GATED: the recomputed S_{t-1}
                 const float bkd = b * kd;
-                const float at = GATED ? sb[KB + j] : 1.f;
+                const float at = GATED ? alpha_row(j) : 1.f;
 #pragma unroll
                 for (int i = 0; i < kRpt; ++i) Sr[i] = GATED ? Sh[GATED ? j : 0][i] : fmaf(-bkd, ur[i], Sr[i]);
                 // what the rest of this token needs from its operands
@@ -576,10 +613,20 @@ __global__ __launch_bounds__(512) void delta_bwd_kernel(
                     // out), then G <- alpha G_P
                     const float gp = col_sum<RSR>(slice_dot(Gr, Sr));
                     if (rr == 0 && ok_r) sog[j * D + d] = at * gp;
+                    if constexpr (CHAN) {
+                        float ac[kRpt];
+                        load_slice(sar + j * DPL + rc * kSl, ac);  // alpha[rc*R + i]
 #pragma unroll
-                    for (int i = 0; i < kRpt; ++i) {
-                        Gc[i] *= at;
-                        Gr[i] *= at;
+                        for (int i = 0; i < kRpt; ++i) {
+                            Gc[i] *= ac[i];
+                            Gr[i] *= at;
+                        }
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < kRpt; ++i) {
+                            Gc[i] *= at;
+                            Gr[i] *= at;
+                        }
                     }
                 }
             };
@@ -652,17 +699,19 @@ static hipError_t launch_reduce(float* out, const float* part, size_t n, size_t 
     return hipGetLastError();
 }
 
-size_t bwd_workspace_floats(long n_pairs, int T, int D, bool gated) {
+size_t bwd_workspace_floats(long n_pairs, int T, int D, int gm) {
     const BwdGeo g = bwd_geo(D);
     const long n_ck = (T + kCk - 1) / kCk;
     const size_t e = static_cast<size_t>(n_pairs) * T * D, bt = static_cast<size_t>(n_pairs) * T;
     size_t f = e + static_cast<size_t>(n_pairs) * n_ck * D * D;
-    if (g.n_tiles > 1) f += static_cast<size_t>(g.n_tiles) * (2 * e + (gated ? 2 : 1) * bt);
+    // per tile: gq and gk partial sums, gbeta's, and gg's (per token, or per channel)
+    if (g.n_tiles > 1) f += static_cast<size_t>(g.n_tiles) * (2 * e + bt + (gm == 1 ? bt : gm == 2 ? e : 0));
     return f;
 }
 
-template <typename InT, bool GATED>
+template <typename InT, int GM>
 static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
+    constexpr bool GATED = GM != 0;
     const BwdGeo g = bwd_geo(a.D);
     const size_t e = static_cast<size_t>(a.n_pairs) * a.T * a.D;
     const size_t bt = static_cast<size_t>(a.n_pairs) * a.T;
@@ -672,7 +721,7 @@ static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
     float* part = ck_ws + static_cast<size_t>(a.n_pairs) * n_ck * a.D * a.D;
     const unsigned grid = static_cast<unsigned>(a.n_pairs) * g.n_tiles;
 
-    hipError_t err = launch_ckpt<InT, GATED>(a, u_ws, ck_ws, st);
+    hipError_t err = launch_ckpt<InT, GM>(a, u_ws, ck_ws, st);
     if (err != hipSuccess) return err;
 
     const bool split = g.n_tiles > 1;
@@ -680,36 +729,40 @@ static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
     float* gk = split ? part + static_cast<size_t>(g.n_tiles) * e : a.gk;
     float* gb = split ? part + static_cast<size_t>(2 * g.n_tiles) * e : a.gbeta;
     float* gg = !GATED ? nullptr : split ? part + static_cast<size_t>(2 * g.n_tiles) * e + g.n_tiles * bt : a.gg;
+    const size_t gg_n = GM == 2 ? e : bt;  // gg per channel or per token
     const int dp = g.rsc * kSl, cp = g.rsr * kSl;
     constexpr int NO = GATED ? 4 : 3;  // [KB][D] output arrays per block
-    const size_t lds_b = sizeof(float) * (2 * (2 * kBwdSteps * dp + 2 * kBwdSteps * cp + 2 * kBwdSteps) +
-                                          2 * cp + 2 * (NO * kBwdSteps * a.D + kBwdSteps * g.nc));
+    constexpr int NR = GM == 2 ? 3 : 2;  // [KB][DPL] arrays per staging buffer (k, q, alpha)
+    auto lds_bytes = [&](int dpx, int cpx, int nc, int D) {
+        return sizeof(float) * (2 * (NR * kBwdSteps * dpx + 2 * kBwdSteps * cpx + 2 * kBwdSteps) + 2 * cpx +
+                                2 * (NO * kBwdSteps * D + kBwdSteps * nc));
+    };
+    const size_t lds_b = lds_bytes(dp, cp, g.nc, a.D);
     // with kRpt 8 and tiles of min(D, 32) columns, RSR = min(RSC, 4) for every D <= 128;
     // above, 16-column tiles: RSC 32, RSR 2
     const bool wide = a.D > 128;
     if (wide ? (g.rsc != 32 || g.rsr != 2 || g.nc != kTileColsWide)
              : (g.rsr != (g.rsc < 4 ? g.rsc : 4) || g.rsc > 16))
         return hipErrorInvalidValue;
-    auto kern = delta_bwd_kernel<InT, 16, 4, kTileCols, GATED>;
+    auto kern = delta_bwd_kernel<InT, 16, 4, kTileCols, GM>;
+    int which = 4;  // the kernel's slot among the geometries below
     switch (g.rsc) {
-        case 1: kern = delta_bwd_kernel<InT, 1, 1, kTileCols, GATED>; break;
-        case 2: kern = delta_bwd_kernel<InT, 2, 2, kTileCols, GATED>; break;
-        case 4: kern = delta_bwd_kernel<InT, 4, 4, kTileCols, GATED>; break;
-        case 8: kern = delta_bwd_kernel<InT, 8, 4, kTileCols, GATED>; break;
-        case 32: kern = delta_bwd_kernel<InT, 32, 2, kTileColsWide, GATED>; break;
+        case 1: kern = delta_bwd_kernel<InT, 1, 1, kTileCols, GM>, which = 0; break;
+        case 2: kern = delta_bwd_kernel<InT, 2, 2, kTileCols, GM>, which = 1; break;
+        case 4: kern = delta_bwd_kernel<InT, 4, 4, kTileCols, GM>, which = 2; break;
+        case 8: kern = delta_bwd_kernel<InT, 8, 4, kTileCols, GM>, which = 3; break;
+        case 32: kern = delta_bwd_kernel<InT, 32, 2, kTileColsWide, GM>, which = 5; break;
         default: break;
     }
-    if (wide) {
-        // the dynamic-LDS limit is a per-device function attribute: set it once, to what
-        // the largest D (256) of this kernel needs
-        const int dp_w = 32 * kSl, cp_w = 2 * kSl;
-        const size_t lds_max = sizeof(float) * (2 * (2 * kBwdSteps * dp_w + 2 * kBwdSteps * cp_w + 2 * kBwdSteps) +
-                                                2 * cp_w + 2 * (NO * kBwdSteps * 256 + kBwdSteps * kTileColsWide));
+    if (lds_b > 64 * 1024) {
+        // the dynamic-LDS limit is a per-device function attribute: set it once per kernel,
+        // to what the largest D of its geometry needs (128, or 256 for the wide tiles)
+        const size_t lds_max = wide ? lds_bytes(32 * kSl, 2 * kSl, kTileColsWide, 256)
+                                    : lds_bytes(dp, cp, g.nc, 128);
         if (lds_b > lds_max) return hipErrorInvalidValue;
         int dev = 0;
         if ((err = hipGetDevice(&dev)) != hipSuccess) return err;
-        static bool attr_set[2][64] = {};
-        const int which = sizeof(InT) == 2 ? 1 : 0;
+        static bool attr_set[6][64] = {};
         if (dev < 0 || dev >= 64 || !attr_set[which][dev]) {
             err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_max));
@@ -724,15 +777,17 @@ static hipError_t launch_bwd_in(const BwdArgs& a, hipStream_t st) {
     if (err != hipSuccess || !split) return err;
     if ((err = launch_reduce(a.gq, gq, e, e, g.n_tiles, st)) != hipSuccess) return err;
     if ((err = launch_reduce(a.gk, gk, e, e, g.n_tiles, st)) != hipSuccess) return err;
-    if (GATED && (err = launch_reduce(a.gg, gg, bt, bt, g.n_tiles, st)) != hipSuccess) return err;
+    if (GATED && (err = launch_reduce(a.gg, gg, gg_n, gg_n, g.n_tiles, st)) != hipSuccess) return err;
     return launch_reduce(a.gbeta, gb, bt, bt, g.n_tiles, st);
 }
 
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t st) {
     if (a.n_pairs == 0) return hipSuccess;
+    if (a.g && a.per_channel)
+        return a.in_bf16 ? launch_bwd_in<uint16_t, 2>(a, st) : launch_bwd_in<float, 2>(a, st);
     if (a.g)
-        return a.in_bf16 ? launch_bwd_in<uint16_t, true>(a, st) : launch_bwd_in<float, true>(a, st);
-    return a.in_bf16 ? launch_bwd_in<uint16_t, false>(a, st) : launch_bwd_in<float, false>(a, st);
+        return a.in_bf16 ? launch_bwd_in<uint16_t, 1>(a, st) : launch_bwd_in<float, 1>(a, st);
+    return a.in_bf16 ? launch_bwd_in<uint16_t, 0>(a, st) : launch_bwd_in<float, 0>(a, st);
 }
 
 }  // namespace pm

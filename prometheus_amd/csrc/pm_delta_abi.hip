@@ -287,17 +287,19 @@ bool bwd_chunked(int H, int D, int in_dtype) {
     return g_path != 1 && in_dtype == PM_DTYPE_BF16 && pm::chunked_bwd_supported(D, H);
 }
 
-size_t bwd_ws_bytes(int B, int T, int H, int D, int in_dtype, bool gated = false) {
+// gm: 0 ungated, 1 gated (a log-gate per token and head), 2 per-channel gated (KDA)
+size_t bwd_ws_bytes(int B, int T, int H, int D, int in_dtype, int gm = 0) {
     const long n_pairs = static_cast<long>(B) * H;
-    if (!gated && bwd_chunked(H, D, in_dtype)) return pm::chunked_bwd_ws(n_pairs, T, D).bytes;
-    return sizeof(float) * pm::bwd_workspace_floats(n_pairs, T, D, gated);
+    if (gm == 0 && bwd_chunked(H, D, in_dtype)) return pm::chunked_bwd_ws(n_pairs, T, D).bytes;
+    return sizeof(float) * pm::bwd_workspace_floats(n_pairs, T, D, gm);
 }
 
-// Common backward dispatch; g != NULL: the gated variant (per-token kernels, gg out).
+// Common backward dispatch; g != NULL: a gated variant (per-token kernels, gg out), with
+// per_channel its KDA form (g and gg (B, T, H, D)).
 int backward(const void* q, const void* k, const void* v, const float* beta, const float* g,
              const float* s0, const float* go, const float* gs, float* gq, float* gk, float* gv,
              float* gbeta, float* gg, float* gs0, int B, int T, int H, int D, int in_dtype,
-             void* workspace, size_t ws_bytes, void* stream) {
+             void* workspace, size_t ws_bytes, void* stream, bool per_channel = false) {
     if (B < 0 || T < 0 || H < 0)
         return fail(PM_E_SHAPE, "B, T, H must be >= 0 (got %d, %d, %d)", B, T, H);
     if (D < 1 || D > pm::kBwdMaxD)
@@ -329,7 +331,7 @@ int backward(const void* q, const void* k, const void* v, const float* beta, con
                 return fail(PM_E_ALIGN,
                             "chunked backward: q, k, v, go, gq, gk, gv and workspace must be 16-byte aligned");
     }
-    const size_t need = bwd_ws_bytes(B, T, H, D, in_dtype, gated);
+    const size_t need = bwd_ws_bytes(B, T, H, D, in_dtype, !gated ? 0 : per_channel ? 2 : 1);
     if (need > 0 && (!workspace || ws_bytes < need))
         return fail(PM_E_WORKSPACE, "workspace of %zu bytes needed (got %zu)", need,
                     workspace ? ws_bytes : static_cast<size_t>(0));
@@ -338,6 +340,7 @@ int backward(const void* q, const void* k, const void* v, const float* beta, con
                   in_dtype == PM_DTYPE_BF16};
     a.g = g;
     a.gg = gg;
+    a.per_channel = per_channel;
     hipError_t e = chunked ? pm::launch_bwd_chunked(a, static_cast<hipStream_t>(stream))
                            : pm::launch_bwd(a, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? 0 : hip_fail(e, "backward launch");
@@ -388,7 +391,23 @@ int pm_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
 size_t pm_gated_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype) {
     if (B < 0 || T < 0 || H < 0 || D < 1 || D > pm::kBwdMaxD) return 0;
     if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16) return 0;
-    return bwd_ws_bytes(B, T, H, D, in_dtype, true);
+    return bwd_ws_bytes(B, T, H, D, in_dtype, 1);
+}
+
+size_t pm_kda_delta_bwd_workspace_bytes(int B, int T, int H, int D, int in_dtype) {
+    if (B < 0 || T < 0 || H < 0 || D < 1 || D > pm::kBwdMaxD) return 0;
+    if (in_dtype != PM_DTYPE_F32 && in_dtype != PM_DTYPE_BF16) return 0;
+    return bwd_ws_bytes(B, T, H, D, in_dtype, 2);
+}
+
+int pm_kda_delta_bwd(const void* q, const void* k, const void* v, const float* beta,
+                     const float* g, const float* s0, const float* go, const float* gs, float* gq,
+                     float* gk, float* gv, float* gbeta, float* gg, float* gs0, int B, int T,
+                     int H, int D, int in_dtype, void* workspace, size_t ws_bytes, void* stream) {
+    g_err[0] = '\0';
+    if (static_cast<long>(B) * T * H > 0 && (!g || !gg)) return fail(PM_E_NULL, "g and gg must be non-NULL");
+    return backward(q, k, v, beta, g, s0, go, gs, gq, gk, gv, gbeta, gg, gs0, B, T, H, D, in_dtype,
+                    workspace, ws_bytes, stream, true);
 }
 
 int pm_gated_delta_bwd(const void* q, const void* k, const void* v, const float* beta,

@@ -138,9 +138,12 @@ struct BwdArgs {
     // exp(g), and their gradient gg (B, T, H)
     const float* g = nullptr;
     float* gg = nullptr;
+    // with g: one log-gate per (token, head, key channel) (KDA), g and gg (B, T, H, D)
+    bool per_channel = false;
 };
 constexpr int kBwdMaxD = 256;
-size_t bwd_workspace_floats(long n_pairs, int T, int D, bool gated = false);
+// gm: 0 ungated, 1 gated, 2 per-channel gated
+size_t bwd_workspace_floats(long n_pairs, int T, int D, int gm = 0);
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t st);
 
 // Chunked reverse mode (K6, bf16 MFMA): bf16 q/k/v and chunked_supported(D,

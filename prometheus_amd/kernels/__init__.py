@@ -602,11 +602,24 @@ def chunked_gated_delta_rule_bwd(residual: _GatedDeltaResidual, grads):
     (``pm_gated_delta_bwd``) for every dtype and head dimension up to 256: with P_t =
     exp(g_t) S_{t-1}, dL/dg_t = <G - beta_t k_t w^T, P_t> and G <- exp(g_t) (G - beta_t
     k_t w^T), the other gradients as in the ungated backward."""
+    return _gated_bwd(residual, grads, per_channel=False)
+
+
+def chunked_kda_rule_bwd(residual: _GatedDeltaResidual, grads):
+    """Backward of ``chunked_kda_rule_fwd``: as ``chunked_gated_delta_rule_bwd`` with g
+    and gg (batch, seq, heads, dim). With P_t = Diag(exp(g_t)) S_{t-1}, dL/dg_t[d] =
+    <G_P[d, :], P_t[d, :]> (G_P = G - beta_t k_t w^T) and G <- Diag(exp(g_t)) G_P
+    (``pm_kda_delta_bwd``, the per-token fp32 kernels, head dimension up to 256)."""
+    return _gated_bwd(residual, grads, per_channel=True)
+
+
+def _gated_bwd(residual, grads, per_channel):
     go, gs = grads
     q, k, v, beta, g, s0 = residual.q, residual.k, residual.v, residual.beta, residual.g, residual.state0
     batch, seq, heads, dim = _validate(q, k, v, beta, s0)
-    if _shape(g) != (batch, seq, heads):
-        raise KernelError(f"g shape {_shape(g)} != {(batch, seq, heads)}")
+    gshape = (batch, seq, heads, dim) if per_channel else (batch, seq, heads)
+    if _shape(g) != gshape:
+        raise KernelError(f"g shape {_shape(g)} != {gshape}")
     if dim > _native.MAX_D_BWD:
         raise KernelError(f"backward head dimension {dim} exceeds {_native.MAX_D_BWD}")
     if go is not None and _shape(go) != (batch, seq, heads, dim):
@@ -623,12 +636,13 @@ def chunked_gated_delta_rule_bwd(residual: _GatedDeltaResidual, grads):
         gq = torch.empty((batch, seq, heads, dim), dtype=f32, device=call.device)
         gk, gv = torch.empty_like(gq), torch.empty_like(gq)
         gb = torch.empty((batch, seq, heads), dtype=f32, device=call.device)
-        gg = torch.empty_like(gb)
+        gg = torch.empty(gshape, dtype=f32, device=call.device)
         gs0 = torch.empty((batch, heads, dim, dim), dtype=f32, device=call.device)
         L = _native.lib()
-        nbytes = L.pm_gated_delta_bwd_workspace_bytes(batch, seq, heads, dim, _code(cdt))
+        wsf = L.pm_kda_delta_bwd_workspace_bytes if per_channel else L.pm_gated_delta_bwd_workspace_bytes
+        nbytes = wsf(batch, seq, heads, dim, _code(cdt))
         ws = torch.empty(((nbytes + 3) // 4,), dtype=f32, device=call.device) if nbytes else None
-        rc = L.pm_gated_delta_bwd(
+        rc = (L.pm_kda_delta_bwd if per_channel else L.pm_gated_delta_bwd)(
             _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(gd), _ptr(sd), _ptr(god), _ptr(gsd),
             _ptr(gq), _ptr(gk), _ptr(gv), _ptr(gb), _ptr(gg), _ptr(gs0),
             batch, seq, heads, dim, _code(cdt), _ptr(ws), nbytes, _stream(call.device),
@@ -638,15 +652,17 @@ def chunked_gated_delta_rule_bwd(residual: _GatedDeltaResidual, grads):
 
 
 class _ChunkedGatedDeltaRule(torch.autograd.Function):
-    """``chunked_gated_delta_rule`` as a differentiable op: the gated forward kernel and
-    ``chunked_gated_delta_rule_bwd`` as its backward (gradients for q, k, v, beta, g and
-    the state, in each input's dtype and device)."""
+    """``chunked_gated_delta_rule`` (``per_channel``: ``chunked_kda_rule``) as a
+    differentiable op: the gated forward kernel and ``chunked_gated_delta_rule_bwd``
+    (``chunked_kda_rule_bwd``) as its backward (gradients for q, k, v, beta, g and the
+    state, in each input's dtype and device)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, beta, g, state, chunk, out_dtype):
-        call, (qd, kd, vd, bd, gd, sd), o, s = _gated_forward(q, k, v, beta, g, state, out_dtype)
+    def forward(ctx, q, k, v, beta, g, state, chunk, out_dtype, per_channel=False):
+        call, (qd, kd, vd, bd, gd, sd), o, s = _gated_forward(q, k, v, beta, g, state, out_dtype, per_channel)
         ctx.save_for_backward(qd, kd, vd, bd, gd, sd)
         ctx.chunk = chunk
+        ctx.per_channel = per_channel
         ctx.like = [(x.dtype, x.device) if isinstance(x, torch.Tensor) else None
                     for x in (q, k, v, beta, g, state)]
         ctx.knobs = _native.knobs()
@@ -657,11 +673,11 @@ class _ChunkedGatedDeltaRule(torch.autograd.Function):
         qd, kd, vd, bd, gd, sd = ctx.saved_tensors
         res = _GatedDeltaResidual(q=qd, k=kd, v=vd, beta=bd, g=gd, state0=sd, chunk=ctx.chunk)
         with _native.use_knobs(*ctx.knobs):
-            grads = chunked_gated_delta_rule_bwd(res, (go, gs))
+            grads = _gated_bwd(res, (go, gs), ctx.per_channel)
         out = []
         for gr, like, need in zip(grads, ctx.like, ctx.needs_input_grad[:6]):
             out.append(gr.to(device=like[1], dtype=like[0]) if (like is not None and need) else None)
-        return (*out, None, None)
+        return (*out, None, None, None)
 
 
 def chunked_gated_delta_rule(q, k, v, beta, g, state=None, config=None, *, out_dtype=None):
@@ -687,8 +703,12 @@ def chunked_gated_delta_rule(q, k, v, beta, g, state=None, config=None, *, out_d
 
 def chunked_gated_delta_rule_fwd(q, k, v, beta, g, state, config, *, out_dtype=None):
     """Explicit forward of the gated VJP pair: ``((output, next_state), _GatedDeltaResidual)``."""
+    return _gated_fwd_pair(q, k, v, beta, g, state, config, out_dtype, per_channel=False)
+
+
+def _gated_fwd_pair(q, k, v, beta, g, state, config, out_dtype, per_channel):
     chunk = _check_chunk(config)
-    call, (qd, kd, vd, bd, gd, sd), o, s = _gated_forward(q, k, v, beta, g, state, out_dtype)
+    call, (qd, kd, vd, bd, gd, sd), o, s = _gated_forward(q, k, v, beta, g, state, out_dtype, per_channel)
     if call.host_numpy:
         residual = _GatedDeltaResidual(
             q=np.asarray(q, dtype=np.float32), k=np.asarray(k, dtype=np.float32),
@@ -708,15 +728,22 @@ def chunked_kda_rule(q, k, v, beta, g, state=None, config=None, *, out_dtype=Non
     ``chunked_delta_rule``; g: (batch, seq, heads, dim) fp32 log-gates, one per
     key channel (g constant along dim gives ``chunked_gated_delta_rule``). Runs the
     fp32 per-token kernel (``pm_kda_delta_fwd``) for every dtype and dim up to 256.
-    Forward only: a call that autograd would record raises ``KernelError``.
+    Differentiable: when autograd records and a torch input (the gates included)
+    requires grad, the backward runs ``chunked_kda_rule_bwd``.
     """
     cfg = LinearAttnConfig() if config is None else config
-    _check_chunk(cfg)
+    chunk = _check_chunk(cfg)
     if _wants_grad(q, k, v, beta, g, state):
-        raise KernelError("chunked_kda_rule has no backward; call it under torch.no_grad() "
-                          "or on inputs that do not require grad")
+        _validate(q, k, v, beta, state)
+        return _ChunkedGatedDeltaRule.apply(q, k, v, beta, g, state, chunk, out_dtype, True)
     call, _, o, s = _gated_forward(q, k, v, beta, g, state, out_dtype, per_channel=True)
     return call.out(o), call.out(s)
+
+
+def chunked_kda_rule_fwd(q, k, v, beta, g, state, config, *, out_dtype=None):
+    """Explicit forward of the KDA VJP pair: ``((output, next_state), residual)`` for
+    ``chunked_kda_rule_bwd``."""
+    return _gated_fwd_pair(q, k, v, beta, g, state, config, out_dtype, per_channel=True)
 
 
 def gated_delta_rule_step(q, k, v, beta, g, state):
@@ -772,6 +799,8 @@ __all__ = [
     "chunked_delta_rule_varlen",
     "check_varlen",
     "chunked_kda_rule",
+    "chunked_kda_rule_fwd",
+    "chunked_kda_rule_bwd",
     "kda_delta_rule_step",
     "delta_rule_step",
     "chunked_gated_delta_rule",

@@ -520,6 +520,30 @@ def test_knobs_read_and_scoped_set():
     assert _native.knobs() == base
 
 
+def test_kda_backward_workspace_and_checks():
+    """pm_kda_delta_bwd_workspace_bytes: the per-token backward's workspace plus, with
+    several column tiles (D > 32), a partial sum of dL/dg per channel and tile; null
+    gates are refused before any launch, and so is path 2."""
+    lib = _native.lib()
+    f32, bf16 = _native.DTYPE_F32, _native.DTYPE_BF16
+    for b, t, h, d in [(1, 1, 1, 3), (2, 130, 3, 64), (4, 4096, 16, 128), (1, 70, 2, 48), (1, 20, 2, 160)]:
+        base = _per_token_ws(b, t, h, d)
+        n_tiles = 1 if d <= 32 else ((d + 31) // 32 if d <= 128 else (d + 15) // 16)
+        extra = 4 * b * t * h * d * n_tiles if n_tiles > 1 else 0
+        for dt in (f32, bf16):
+            assert lib.pm_kda_delta_bwd_workspace_bytes(b, t, h, d, dt) == base + extra
+    assert lib.pm_kda_delta_bwd_workspace_bytes(1, 4, 1, 257, f32) == 0
+    p = ctypes.c_void_p(256)
+    rc = lib.pm_kda_delta_bwd(p, p, p, p, None, None, p, p, p, p, p, p, p, p, 1, 4, 1, 8, f32, p, 1 << 20, None)
+    assert rc == _native.E_NULL and b"g and gg" in lib.pm_last_error()
+    old = _native.set_path(2)
+    try:
+        rc = lib.pm_kda_delta_bwd(p, p, p, p, p, None, p, p, p, p, p, p, p, p, 1, 4, 1, 64, bf16, p, 1 << 24, None)
+        assert rc == _native.E_UNSUPPORTED and b"per-token" in lib.pm_last_error()
+    finally:
+        _native.set_path(old)
+
+
 def test_gated_backward_workspace_and_checks():
     """pm_gated_delta_bwd_workspace_bytes: the per-token backward's workspace plus the
     partial sums of dL/dg over column tiles (D > 32), for bf16 inputs as well (the gated

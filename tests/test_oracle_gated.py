@@ -303,3 +303,99 @@ def test_kda_planted_mistakes_are_caught():
     for kind in ("columns", "after", "sign"):
         assert np.abs(mutant(kind) - o[0, :, 0]).max() > 1e-3, kind
     np.testing.assert_allclose(mutant("correct"), o[0, :, 0], rtol=1e-12, atol=1e-12)
+
+
+# --- the KDA reverse mode (kda_vjp) ---
+
+
+def _kda_loss(q, k, v, beta, g, s0, go, gs):
+    o, s = gref.kda_delta_rule(q, k, v, beta, g, s0)
+    return float(np.sum(o * go) + np.sum(s * gs))
+
+
+def test_kda_vjp_channel_constant_gate_is_the_gated_vjp():
+    """g constant along D: gq, gk, gv, gbeta and gstate0 are gated_vjp's, and gg summed
+    over the channels is gated_vjp's gg."""
+    rng = np.random.default_rng(31)
+    q, k, v, beta, g, s0 = _problem(rng, (2, 8, 2, 5))
+    go = rng.standard_normal(q.shape)
+    gs = rng.standard_normal(s0.shape) * 0.1
+    got = gref.kda_vjp(q, k, v, beta, np.repeat(g[..., None], 5, axis=-1), go, gs, s0)
+    want = gref.gated_vjp(q, k, v, beta, g, go, gs, s0)
+    for name, a, b in zip(("gq", "gk", "gv", "gbeta", "gs0"), got[:4] + got[5:], want[:4] + want[5:]):
+        np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12, err_msg=name)
+    np.testing.assert_allclose(got[4].sum(axis=-1), want[4], rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("gate_scale", [0.05, 0.5, 2.0])
+def test_kda_vjp_finite_differences(gate_scale):
+    rng = np.random.default_rng(40 + int(gate_scale * 10))
+    q, k, v, beta, g, s0 = _kda_problem(rng, (1, 6, 2, 4), gate_scale)
+    go = rng.standard_normal(q.shape)
+    gs = rng.standard_normal(s0.shape)
+    grads = gref.kda_vjp(q, k, v, beta, g, go, gs, s0)
+    args = {"q": q, "k": k, "v": v, "beta": beta, "g": g, "s0": s0}
+    eps = 1e-6
+    for name, gx in zip(("q", "k", "v", "beta", "g", "s0"), grads):
+        d = rng.standard_normal(args[name].shape)
+        plus, minus = dict(args), dict(args)
+        plus[name], minus[name] = args[name] + eps * d, args[name] - eps * d
+        fd = (_kda_loss(**plus, go=go, gs=gs) - _kda_loss(**minus, go=go, gs=gs)) / (2 * eps)
+        np.testing.assert_allclose(np.sum(gx * d), fd, rtol=1e-6, atol=1e-8, err_msg=name)
+
+
+def test_kda_vjp_pure_decay_closed_form():
+    """beta = 0, go = 0: S_T = Diag(exp(sum_t g_t)) S_0, so dL/dg_t[d] = <gs[d, :], S_T[d, :]>
+    for every t and dL/dS_0 = Diag(exp(sum_t g_t)) gs."""
+    rng = np.random.default_rng(32)
+    q, k, v, _, g, s0 = _kda_problem(rng, (1, 5, 2, 3))
+    gs = rng.standard_normal(s0.shape)
+    _, _, _, _, gg, gs0 = gref.kda_vjp(q, k, v, np.zeros(g.shape[:3]), g, None, gs, s0)
+    dec = np.exp(g.sum(axis=1))[..., None]  # (B, H, D, 1)
+    want = np.einsum("bhde,bhde->bhd", gs, dec * s0)
+    np.testing.assert_allclose(gg, np.repeat(want[:, None], g.shape[1], axis=1), rtol=1e-12)
+    np.testing.assert_allclose(gs0, dec * gs, rtol=1e-12)
+
+
+def test_kda_vjp_planted_mistakes_are_caught():
+    """The channel gradient summed over the wrong axis (columns instead of rows), G
+    scaled along its columns, and the gate's gradient taken before the downdate each
+    differ from finite differences."""
+    rng = np.random.default_rng(33)
+    q, k, v, beta, g, s0 = _kda_problem(rng, (1, 5, 1, 4), 0.5)
+    go = rng.standard_normal(q.shape)
+    gs = rng.standard_normal(s0.shape)
+    eps = 1e-6
+    d = rng.standard_normal(g.shape)
+    fd = (_kda_loss(q, k, v, beta, g + eps * d, s0, go, gs)
+          - _kda_loss(q, k, v, beta, g - eps * d, s0, go, gs)) / (2 * eps)
+
+    def mutant(kind):
+        t = q.shape[1]
+        G, s = gs.copy(), s0.copy()
+        hist, us = [s], []
+        for i in range(t):
+            p = np.exp(g[:, i])[..., None] * s
+            u = v[:, i] - np.einsum("bhd,bhde->bhe", k[:, i], p)
+            s = p + beta[:, i][..., None, None] * np.einsum("bhd,bhe->bhde", k[:, i], u)
+            hist.append(s)
+            us.append(u)
+        gg = np.zeros(g.shape)
+        for i in range(t - 1, -1, -1):
+            a = np.exp(g[:, i])
+            p = a[..., None] * hist[i]
+            G = G + np.einsum("bhd,bhe->bhde", q[:, i], go[:, i])
+            w = np.einsum("bhde,bhd->bhe", G, k[:, i])
+            if kind == "before_downdate":
+                gg[:, i] = np.einsum("bhde,bhde->bhd", G, p)
+            G = G - beta[:, i][..., None, None] * np.einsum("bhd,bhe->bhde", k[:, i], w)
+            if kind == "column_sums":
+                gg[:, i] = np.einsum("bhde,bhde->bhe", G, p)
+            elif kind != "before_downdate":
+                gg[:, i] = np.einsum("bhde,bhde->bhd", G, p)
+            G = a[..., None, :] * G if kind == "scaled_columns" else a[..., None] * G
+        return float(np.sum(gg * d))
+
+    for kind in ("column_sums", "scaled_columns", "before_downdate"):
+        assert abs(mutant(kind) - fd) > 1e-4 * max(1.0, abs(fd)), kind
+    assert abs(mutant("correct") - fd) < 1e-6 * max(1.0, abs(fd))

@@ -18,8 +18,9 @@ the same run and reported under ``decode`` (with the same batch through a
 serving state cache under ``decode.state_cache``), the backward at cfg1
 under ``backward``, the model's linear attention at the cfg1 shape
 under ``model_linear_attention``, the cfg1 forward with fp32 q/k/v (the
-fp32 chunked forward, and the per-token kernel beside it) under ``fp32_forward``, and the gated variant at cfg1
-under ``gated``.
+fp32 chunked forward, and the per-token kernel beside it) under ``fp32_forward``, the gated variant at cfg1
+under ``gated``, and KDA (a log-gate per key channel: the chunked form, and the per-token
+kernel beside it) at cfg1 under ``kda``.
 """
 
 from __future__ import annotations
@@ -238,7 +239,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--decode-steps", type=int, default=64)
     ap.add_argument("--gated-calls", type=int, default=10,
-                    help="timed pm_gated_delta_fwd calls at cfg1 (0 skips)")
+                    help="timed pm_gated_delta_fwd and pm_kda_delta_fwd calls at cfg1 (0 skips)")
     ap.add_argument("--model-calls", type=int, default=2,
                     help="timed pm_linear_attention calls at the cfg1 shape (0 skips)")
     ap.add_argument("--bwd-steps", type=int, default=3,
@@ -687,6 +688,58 @@ def main():
         }
         del og, sg, gates
 
+    # KDA at cfg1 (pm_kda_delta_fwd): cfg1's inputs plus log-gates -0.1 |N(0, 1)| per token,
+    # head and key channel; the chunked form (prepass + recurrence) and the per-token kernel
+    kda = None
+    if args.gated_calls > 0:
+        g.manual_seed(9)
+        gates = -0.1 * torch.randn((B, T, H, D), generator=g, device=dev).abs()
+        ok_ = torch.empty((B, T, H, D), device=dev)
+        sk_ = torch.empty((B, H, D, D), device=dev)
+        kws_bytes = lib.pm_kda_delta_workspace_bytes(B, T, H, D, _native.DTYPE_BF16)
+        kws = torch.empty((kws_bytes,), dtype=torch.uint8, device=dev)
+
+        def kfwd(i=0, ws=True):
+            q, k, v, beta = sets[i % 2]
+            rc = lib.pm_kda_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
+                                      gates.data_ptr(), None, ok_.data_ptr(), sk_.data_ptr(), B, T, H, D,
+                                      _native.DTYPE_BF16, _native.DTYPE_F32, kws.data_ptr() if ws else None,
+                                      kws_bytes if ws else 0, stream.cuda_stream)
+            _native.check(rc)
+
+        def time_kda(ws, calls):
+            kfwd(0, ws)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(calls):
+                kfwd(i, ws)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / calls
+
+        k_ms = time_kda(True, args.gated_calls)
+        o_chunk = ok_.clone()
+        kp_ms = time_kda(False, max(1, args.gated_calls // 5))
+        kfwd(args.gated_calls - 1, False)  # the per-token result on the chunked call's inputs
+        torch.cuda.synchronize()
+        rel = float(torch.linalg.vector_norm(o_chunk - ok_) / torch.linalg.vector_norm(ok_))
+        kb_ = fwd_bytes(B, T, H, D) + 4 * B * T * H * D
+        kda = {
+            "workload": "cfg1 KDA (log-gates -0.1|N(0,1)| per key channel), bf16 q/k/v, fp32 O",
+            "calls": args.gated_calls,
+            "ms_per_call": k_ms,
+            "tokens_per_s": tokens / (k_ms * 1e-3),
+            "workspace_bytes": kws_bytes,
+            "algorithmic_bytes": kb_,
+            "roofline": {"bound": "hbm", "achieved": kb_ / (k_ms * 1e-3) / 1e9,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": kb_ / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+            "per_token": {"ms_per_call": kp_ms, "tokens_per_s": tokens / (kp_ms * 1e-3)},
+            "chunked_vs_per_token_rel_l2": rel,
+        }
+        del ok_, sk_, gates, kws, o_chunk
+
     # backward at cfg1 (chunked_delta_rule_bwd through the C ABI): bf16 q/k/v, zero S0,
     # random go and gS, fp32 gradients
     backward = None
@@ -803,6 +856,7 @@ def main():
         "model_linear_attention": model_la,
         "fp32_forward": fp32_fwd,
         "gated": gated,
+        "kda": kda,
         "backward": backward,
     }
     print(json.dumps(line), flush=True)

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PM_DELTA_ABI_VERSION 12
+#define PM_DELTA_ABI_VERSION 13
 
 /* element types */
 #define PM_DTYPE_F32 0
@@ -165,14 +165,27 @@ int pm_gated_delta_step(float* s_inout, const void* q, const void* k, const void
  *   S_t = (I - beta_t k_t k_t^T) Diag(alpha_t) S_{t-1} + beta_t k_t v_t^T,  o_t = q_t S_t,
  * alpha_t = exp(g_t) with g (B, T, H, D) fp32 (one log-gate per key channel,
  * i.e. per row of S), NULL only when B*T*H == 0.  With g constant along D
- * this is pm_gated_delta_fwd.  Runs the fp32 per-token kernel for every
- * in_dtype and D <= 256 (row d of S is decayed by alpha_t[d] before the
- * token's dot products); path 2 (chunked kernel required) returns
- * PM_E_UNSUPPORTED.  Everything else as pm_delta_fwd.
+ * this is pm_gated_delta_fwd.
+ *   * bf16 q/k/v with D in {64, 128}, 16-byte aligned q/k/v/o, and a workspace of
+ *     pm_kda_delta_workspace_bytes (16-byte aligned): the chunked WY form on bf16
+ *     MFMA (a parallel pass writes every chunk's decayed operands, T and P into the
+ *     workspace, then the chunk recurrence).  It clamps each log-gate into [-10, 1]
+ *     (alpha >= 4.5e-5: a difference below bf16 resolution).
+ *   * otherwise, without a large enough workspace, and under path 1: the fp32
+ *     per-token kernel, every in_dtype and D <= 256, g as given.
+ * Path 2 or 3 (chunked kernel required) returns PM_E_UNSUPPORTED for inputs the
+ * chunked form does not take and PM_E_WORKSPACE without the workspace.
+ * Everything else as pm_delta_fwd.
  */
 int pm_kda_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
                      const float* g, const float* s0, void* o, float* s_out, int B, int T, int H,
-                     int D, int in_dtype, int out_dtype, void* stream);
+                     int D, int in_dtype, int out_dtype, void* workspace, size_t ws_bytes,
+                     void* stream);
+
+/* Workspace bytes of pm_kda_delta_fwd's chunked form (0 where the call runs the
+ * per-token kernel): 61 KiB (D = 128) or 37 KiB (D = 64) per 64-token chunk of every
+ * (b, h). */
+size_t pm_kda_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype);
 
 /*
  * One KDA step: S' = (I - beta k k^T) Diag(exp(g)) S + beta k v^T, o = q S',

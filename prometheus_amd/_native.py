@@ -18,7 +18,7 @@ import torch  # noqa: F401  (see module docstring: must precede CDLL)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpmdelta.so")
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 MAX_D = 256
@@ -51,6 +51,7 @@ EXPORTS = (
     "pm_gated_delta_bwd",
     "pm_gated_delta_bwd_workspace_bytes",
     "pm_kda_delta_fwd",
+    "pm_kda_delta_workspace_bytes",
     "pm_kda_delta_step",
     "pm_kda_delta_bwd",
     "pm_kda_delta_bwd_workspace_bytes",
@@ -94,7 +95,9 @@ def lib() -> ctypes.CDLL:
         L.pm_gated_delta_fwd.restype = i
         L.pm_gated_delta_step.argtypes = [vp] * 7 + [i] * 4 + [vp]
         L.pm_gated_delta_step.restype = i
-        L.pm_kda_delta_fwd.argtypes = [vp] * 8 + [i] * 6 + [vp]
+        L.pm_kda_delta_fwd.argtypes = [vp] * 8 + [i] * 6 + [vp, sz, vp]
+        L.pm_kda_delta_workspace_bytes.argtypes = [i] * 5
+        L.pm_kda_delta_workspace_bytes.restype = sz
         L.pm_kda_delta_fwd.restype = i
         L.pm_kda_delta_step.argtypes = [vp] * 7 + [i] * 4 + [vp]
         L.pm_kda_delta_step.restype = i

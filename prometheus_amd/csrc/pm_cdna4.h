@@ -262,28 +262,19 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // GATED scalings (called through a function instead, it compiled to 5 more VGPRs and
 // about 190 more instructions, in its most time-critical role); for plain inputs the two
 // give equal bits.
-template <int D>
-__device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const float (&bc)[4],
-                                         const f32x4_t (&br4)[4], int lane, f32x4_t (&tb)[10]) {
+//
+// t_from_gram is the part after the Gram matrix, for a Gram that need not be symmetric
+// (the per-channel decayed one): with A'[t][s] the matrix whose strict lower part times
+// diag(beta) is A, gd[b] holds diagonal block b as accumulator tile (lane (g, l16):
+// A'[16b + 4g + r][16b + l16]), gdt[b] the same block transposed (A'[16b + l16][16b + 4g
+// + r]), and gu[x] the off-diagonal block (k, i), k < i, in the order (0,1) (0,2) (1,2)
+// (0,3) (1,3) (2,3), as the tile of A'[16i + l16][16k + 4g + r] at (g, l16).  t_blocks
+// passes K K^T (gdt = gd).
+__device__ __forceinline__ void t_from_gram(const f32x4_t (&gd)[4], const f32x4_t (&gdt)[4],
+                                            const f32x4_t (&gu)[6], const float (&bc)[4],
+                                            const f32x4_t (&br4)[4], int lane, f32x4_t (&tb)[10]) {
     const int l16 = lane & 15, lg = lane >> 4;
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-    // G = K K^T: diagonal tiles gd[b] and upper tiles gu(k, i), k < i
-    f32x4_t gd[4], gu[6];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) gd[b] = zero;
-#pragma unroll
-    for (int x = 0; x < 6; ++x) gu[x] = zero;
-#pragma unroll
-    for (int kb = 0; kb < D / 32; ++kb) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b) gd[b] = mfma32(f[b][kb], f[b][kb], gd[b]);
-        gu[0] = mfma32(f[0][kb], f[1][kb], gu[0]);  // (0,1)
-        gu[1] = mfma32(f[0][kb], f[2][kb], gu[1]);  // (0,2)
-        gu[2] = mfma32(f[1][kb], f[2][kb], gu[2]);  // (1,2)
-        gu[3] = mfma32(f[0][kb], f[3][kb], gu[3]);  // (0,3)
-        gu[4] = mfma32(f[1][kb], f[3][kb], gu[4]);  // (1,3)
-        gu[5] = mfma32(f[2][kb], f[3][kb], gu[5]);  // (2,3)
-    }
     const EyeBits eyeb = eye_bits(lane);
     // diagonal inverses D_b = (I+N)(I+N^2)(I+N^4)(I+N^8), N = -L_b (dd = D_b, ddt = D_b^T),
     // one level at a time over the four independent blocks
@@ -295,7 +286,7 @@ __device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const f
         for (int r = 0; r < 4; ++r) {
             const int row = 4 * lg + r;
             n[r] = (row > l16) ? -br4[b][r] * gd[b][r] : 0.f;   // N[row][l16]
-            nt[r] = (l16 > row) ? -bc[b] * gd[b][r] : 0.f;      // N[l16][row]
+            nt[r] = (l16 > row) ? -bc[b] * gdt[b][r] : 0.f;     // N[l16][row]
         }
         cn[b] = cvt4(n);
         cnt[b] = cvt4(nt);
@@ -375,6 +366,30 @@ __device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const f
     tb[2] = ddt[1];
     tb[5] = ddt[2];
     tb[9] = ddt[3];
+}
+
+template <int D>
+__device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const float (&bc)[4],
+                                         const f32x4_t (&br4)[4], int lane, f32x4_t (&tb)[10]) {
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    // G = K K^T: diagonal tiles gd[b] and upper tiles gu(k, i), k < i
+    f32x4_t gd[4], gu[6];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) gd[b] = zero;
+#pragma unroll
+    for (int x = 0; x < 6; ++x) gu[x] = zero;
+#pragma unroll
+    for (int kb = 0; kb < D / 32; ++kb) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) gd[b] = mfma32(f[b][kb], f[b][kb], gd[b]);
+        gu[0] = mfma32(f[0][kb], f[1][kb], gu[0]);  // (0,1)
+        gu[1] = mfma32(f[0][kb], f[2][kb], gu[1]);  // (0,2)
+        gu[2] = mfma32(f[1][kb], f[2][kb], gu[2]);  // (1,2)
+        gu[3] = mfma32(f[0][kb], f[3][kb], gu[3]);  // (0,3)
+        gu[4] = mfma32(f[1][kb], f[3][kb], gu[4]);  // (1,3)
+        gu[5] = mfma32(f[2][kb], f[3][kb], gu[5]);  // (2,3)
+    }
+    t_from_gram(gd, gd, gu, bc, br4, lane, tb);
 }
 
 // t_blocks for one chunk by one wave from LDS: K token rows in the swizzled tile at

@@ -635,19 +635,58 @@ int pm_gated_delta_fwd(const void* q, const void* k, const void* v, const float*
                    static_cast<hipStream_t>(stream), g);
 }
 
+size_t pm_kda_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype) {
+    if (B < 0 || T < 0 || H < 0 || in_dtype != PM_DTYPE_BF16 || !pm::chunked_supported(D, H) || g_path == 1)
+        return 0;
+    if (static_cast<long>(B) * H > (1L << 30)) return 0;
+    return pm::kda_chunked_ws_bytes(B, T, H, D);
+}
+
 int pm_kda_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
                      const float* g, const float* s0, void* o, float* s_out, int B, int T, int H,
-                     int D, int in_dtype, int out_dtype, void* stream) {
+                     int D, int in_dtype, int out_dtype, void* workspace, size_t ws_bytes, void* stream) {
     g_err[0] = '\0';
     if (B < 0 || T < 0 || H < 0)
         return fail(PM_E_SHAPE, "B, T, H must be >= 0 (got %d, %d, %d)", B, T, H);
     if (D < 1 || D > PM_DELTA_MAX_D)
         return fail(PM_E_SHAPE, "D must be in [1, %d] (got %d)", PM_DELTA_MAX_D, D);
     if (int rc = check_dtypes(in_dtype, out_dtype)) return rc;
-    if (static_cast<long>(B) * T * H > 0 && !g) return fail(PM_E_NULL, "g is NULL");
+    const long n_pairs = static_cast<long>(B) * H, n_tok = static_cast<long>(B) * T;
+    if (n_pairs * T > 0 && !g) return fail(PM_E_NULL, "g is NULL");
     if (g && !aligned(g, 4)) return fail(PM_E_ALIGN, "g must be 4-byte aligned");
-    return forward(q, k, v, beta, s0, o, s_out, nullptr, B, T, 0, H, D, in_dtype, out_dtype, 64,
-                   static_cast<hipStream_t>(stream), nullptr, nullptr, 0, g);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // the chunked form (bf16 q/k/v, D in {64, 128}) with the caller's workspace; otherwise,
+    // and always under path 1, the per-token kernel
+    const bool can_chunked = in_dtype == PM_DTYPE_BF16 && pm::chunked_supported(D, H) && aligned(q, 16) &&
+                             aligned(k, 16) && aligned(v, 16) &&
+                             (out_dtype == PM_DTYPE_F32 ? aligned(o, 16) : aligned(o, 8));
+    if (g_path != 1 && can_chunked && n_pairs > 0 && n_tok > 0 && n_pairs <= (1L << 30)) {
+        if (!s_out || !q || !k || !v || !beta || !o) return fail(PM_E_NULL, "q, k, v, beta, o and s_out must be non-NULL");
+        if (!aligned(beta, 4) || !aligned(s_out, 4) || (s0 && !aligned(s0, 4)))
+            return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
+        const size_t need = pm::kda_chunked_ws_bytes(B, T, H, D);
+        if (workspace && ws_bytes >= need && aligned(workspace, 16)) {
+            pm::KdaChunkedArgs a{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                 static_cast<const uint16_t*>(v), beta, g, s0, o, s_out, B, T, H, D,
+                                 out_dtype == PM_DTYPE_BF16, workspace};
+            hipError_t e = pm::launch_kda_chunked(a, st);
+            return e == hipSuccess ? 0 : hip_fail(e, "KDA chunked forward launch");
+        }
+        if (g_path >= 2)
+            return fail(PM_E_WORKSPACE, "the KDA chunked forward needs a 16-byte aligned workspace of %zu bytes "
+                        "(got %zu)", need, workspace ? ws_bytes : static_cast<size_t>(0));
+    } else if (g_path >= 2 && n_pairs > 0 && n_tok > 0) {
+        return fail(PM_E_UNSUPPORTED,
+                    "the KDA chunked forward needs bf16 q/k/v, D in {64, 128} and 16-byte aligned q/k/v/o "
+                    "(got in_dtype %d, D %d)", in_dtype, D);
+    }
+    // per-token kernel: forward() with the per-channel gates, as path 1
+    const int old = g_path;
+    g_path = 1;
+    const int rc = forward(q, k, v, beta, s0, o, s_out, nullptr, B, T, 0, H, D, in_dtype, out_dtype, 64, st,
+                           nullptr, nullptr, 0, g);
+    g_path = old;
+    return rc;
 }
 
 int pm_kda_delta_step(float* s_inout, const void* q, const void* k, const void* v,

@@ -82,6 +82,26 @@ hipError_t launch_chunked(const ChunkedArgs& a, hipStream_t st);
 // bytes, 16-byte aligned), then the chunk recurrence loads it instead of building it.
 // Same algebra as the single-stage kernel, rounded differently (bf16 parity).
 size_t chunked_split_ws_bytes(bool varlen, int n_seq, int T, int H);
+
+// The per-channel gated (KDA) forward in chunked form (kda_chunked.hip): bf16 q/k/v, D in
+// {64, 128}, fixed length; g (B, T, H, D) fp32 log-gates, clamped into [-10, 1].  A
+// parallel pass writes every chunk's decayed operands, T'' and P into `workspace`
+// (kda_chunked_ws_bytes, 16-byte aligned), then the chunk recurrence copies them in.
+struct KdaChunkedArgs {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const float* beta;
+    const float* g;
+    const float* s0;  // nullable
+    void* o;
+    float* s_out;
+    int B, T, H, D;
+    bool out_bf16;
+    void* workspace;
+};
+size_t kda_chunked_ws_bytes(int B, int T, int H, int D);
+hipError_t launch_kda_chunked(const KdaChunkedArgs& a, hipStream_t st);
 hipError_t launch_chunked_split(const ChunkedArgs& a, int dv, void* t_ws, hipStream_t st);
 // Chunked forward for fp32 q/k/v on fp32 MFMA (delta_chunked_f32.hip), D in {64, 128},
 // plain (no norm, no gates): a parallel pass writes every 16-token chunk's (T'')^T and

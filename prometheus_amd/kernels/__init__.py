@@ -584,11 +584,19 @@ def _gated_forward(q, k, v, beta, g, state, out_dtype, per_channel=False):
         sd = call.dev(state, torch.float32)
         o = torch.empty((batch, seq, heads, dim), dtype=odt, device=call.device)
         s_out = torch.empty((batch, heads, dim, dim), dtype=torch.float32, device=call.device)
-        fwd = _native.lib().pm_kda_delta_fwd if per_channel else _native.lib().pm_gated_delta_fwd
-        rc = fwd(
-            _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(gd), _ptr(sd), _ptr(o), _ptr(s_out),
-            batch, seq, heads, dim, _code(cdt), _code(odt), _stream(call.device),
-        )
+        L = _native.lib()
+        if per_channel:
+            nbytes = L.pm_kda_delta_workspace_bytes(batch, seq, heads, dim, _code(cdt))
+            ws = torch.empty((nbytes,), dtype=torch.uint8, device=call.device) if nbytes else None
+            rc = L.pm_kda_delta_fwd(
+                _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(gd), _ptr(sd), _ptr(o), _ptr(s_out),
+                batch, seq, heads, dim, _code(cdt), _code(odt), _ptr(ws), nbytes, _stream(call.device),
+            )
+        else:
+            rc = L.pm_gated_delta_fwd(
+                _ptr(qd), _ptr(kd), _ptr(vd), _ptr(bd), _ptr(gd), _ptr(sd), _ptr(o), _ptr(s_out),
+                batch, seq, heads, dim, _code(cdt), _code(odt), _stream(call.device),
+            )
         _native.check(rc)
         if sd is None:
             sd = torch.zeros((batch, heads, dim, dim), dtype=torch.float32, device=call.device)
@@ -726,8 +734,10 @@ def chunked_kda_rule(q, k, v, beta, g, state=None, config=None, *, out_dtype=Non
     ``S_t = (I - beta_t k_t k_t^T) Diag(exp(g_t)) S_{t-1} + beta_t k_t v_t^T``,
     ``o_t = q_t S_t``. q, k, v, beta, state and the return value as
     ``chunked_delta_rule``; g: (batch, seq, heads, dim) fp32 log-gates, one per
-    key channel (g constant along dim gives ``chunked_gated_delta_rule``). Runs the
-    fp32 per-token kernel (``pm_kda_delta_fwd``) for every dtype and dim up to 256.
+    key channel (g constant along dim gives ``chunked_gated_delta_rule``). bf16 q/k/v
+    with dim 64 or 128 run the chunked WY form on bf16 MFMA (``pm_kda_delta_fwd`` with
+    a workspace; log-gates clamped into [-10, 1] there); other inputs run the fp32
+    per-token kernel for every dim up to 256.
     Differentiable: when autograd records and a torch input (the gates included)
     requires grad, the backward runs ``chunked_kda_rule_bwd``.
     """

@@ -422,13 +422,28 @@ def test_kda_validation_without_gpu():
                                     np.zeros((1, 2, 8, 8), np.float32))
     lib = _native.lib()
     p = ctypes.c_void_p(256)
-    assert lib.pm_kda_delta_fwd(p, p, p, p, None, None, p, p, 1, 4, 2, 8, 0, 0, None) == _native.E_NULL
+    assert lib.pm_kda_delta_fwd(p, p, p, p, None, None, p, p, 1, 4, 2, 8, 0, 0, None, 0, None) == _native.E_NULL
     assert lib.pm_kda_delta_fwd(p, p, p, p, ctypes.c_void_p(2), None, p, p, 1, 4, 2, 8, 0, 0,
-                                None) == _native.E_ALIGN
-    assert lib.pm_kda_delta_fwd(p, p, p, p, p, None, p, p, 1, 4, 2, 300, 0, 0, None) == _native.E_SHAPE
-    assert lib.pm_kda_delta_fwd(p, p, p, p, p, None, p, p, 1, 4, 2, 8, 0, 7, None) == _native.E_DTYPE
+                                None, 0, None) == _native.E_ALIGN
+    assert lib.pm_kda_delta_fwd(p, p, p, p, p, None, p, p, 1, 4, 2, 300, 0, 0, None, 0, None) == _native.E_SHAPE
+    assert lib.pm_kda_delta_fwd(p, p, p, p, p, None, p, p, 1, 4, 2, 8, 0, 7, None, 0, None) == _native.E_DTYPE
     assert lib.pm_kda_delta_step(p, p, p, p, p, None, p, 1, 2, 8, 0, None) == _native.E_NULL
     assert lib.pm_kda_delta_step(p, p, p, p, p, p, p, 1, 2, 300, 0, None) == _native.E_SHAPE
+    # the chunked form's workspace: 61 KiB (D = 128) or 37 KiB (D = 64) per chunk, bf16 only
+    bf16 = _native.DTYPE_BF16
+    for b, t, h, d, per in [(4, 4096, 16, 128, 61), (2, 130, 3, 64, 37), (1, 1, 1, 128, 61)]:
+        assert lib.pm_kda_delta_workspace_bytes(b, t, h, d, bf16) == b * h * (-(-t // 64)) * per * 1024
+    assert lib.pm_kda_delta_workspace_bytes(1, 64, 1, 128, _native.DTYPE_F32) == 0
+    assert lib.pm_kda_delta_workspace_bytes(1, 64, 1, 48, bf16) == 0
+    with _native.use_knobs(1, 0):
+        assert lib.pm_kda_delta_workspace_bytes(1, 64, 1, 128, bf16) == 0
+    # path 2: the chunked form required; fp32 inputs refused, a missing workspace too
+    al = ctypes.c_void_p(1 << 20)
+    with _native.use_knobs(2, 0):
+        assert lib.pm_kda_delta_fwd(al, al, al, al, al, None, al, al, 1, 4, 2, 64, 0, 0, None, 0,
+                                    None) == _native.E_UNSUPPORTED
+        assert lib.pm_kda_delta_fwd(al, al, al, al, al, None, al, al, 1, 4, 2, 64, 1, 0, None, 0,
+                                    None) == _native.E_WORKSPACE
 
 
 def test_selection_knobs_are_per_thread():

@@ -142,15 +142,26 @@ def _time_calls(torch, stream, f, calls):
     return e0.elapsed_time(e1) / calls
 
 
+def _time_rounds(torch, stream, fns, calls, rounds=3):
+    """Median ms per call of each of `fns`, timed in `rounds` interleaved rounds (each fn
+    `calls` back-to-back calls per round, after 2 untimed), so that clock and cache
+    warm-up fall on every candidate alike."""
+    res = [[] for _ in fns]
+    for _ in range(rounds):
+        for j, f in enumerate(fns):
+            res[j].append(_time_calls(torch, stream, f, calls))
+    return [sorted(r)[len(r) // 2] for r in res]
+
+
 def _roofline(nbytes, ms):
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}
 
 
-def time_cfg3(torch, lib, _native, dev, stream, calls=8):
+def time_cfg3(torch, lib, _native, dev, stream, calls=4):
     """cfg3, the long-context single-GPU share: B1 H32 T32768 D128 bf16 with S0 ~ N(0, 0.02).
     The default path (with the workspace the Python layer passes) and the single-stage
-    kernel forced (path 2); two input sets alternate."""
+    kernel forced (path 2), in interleaved rounds; two input sets alternate."""
     B, T, H, D = 1, 32768, 32, 128
     print(f"[bench] cfg3 B{B} T{T} H{H} D{D}", file=sys.stderr, flush=True)
     sets = [make_inputs(torch, B, T, H, D, seed, dev) for seed in (31, 32)]
@@ -170,12 +181,14 @@ def time_cfg3(torch, lib, _native, dev, stream, calls=8):
                               stream.cuda_stream)
         _native.check(rc)
 
-    ms_default = _time_calls(torch, stream, f, calls)
-    old = _native.set_path(2)
-    try:
-        ms_single = _time_calls(torch, stream, lambda i: f(i, False), calls)
-    finally:
-        _native.set_path(old)
+    def single(i):
+        old = _native.set_path(2)
+        try:
+            f(i, False)
+        finally:
+            _native.set_path(old)
+
+    ms_default, ms_single = _time_rounds(torch, stream, [f, single], calls)
     nb = fwd_bytes(B, T, H, D, s0=True)
     tile = 16 if B * H * (D // 32) < 256 else 32  # the chunked kernel's d_v tile rule
     return {

@@ -58,38 +58,81 @@ def short_name(name: str) -> str:
     return name if len(name) <= 110 else name[:107] + "..."
 
 
+def _bench_line(path: str) -> str:
+    """One sentence with every leg's timing from a bench.py JSON line."""
+    d = None
+    for ln in open(path):
+        if ln.startswith("{"):
+            d = json.loads(ln)
+    if d is None:
+        return ""
+    parts = [f"headline kernel_us (HIP events over the timed launches, per launch) = {d['kernel_us']:.1f}",
+             f"value = {d['value']:.4g} {d['unit']}"]
+    if d.get("bf16_out"):
+        b = d["bf16_out"]
+        parts.append(f"bf16-O kernel_us = {b['kernel_us']:.1f} (fp32-O {b['fp32_out_kernel_us_same_rounds']:.1f} "
+                     f"in the same rounds)")
+    for key in ("cfg3", "cfg2"):
+        if d.get(key):
+            c = d[key]
+            extra = f", single-stage {c['single_stage']['kernel_us']:.1f}" if c.get("single_stage") else ""
+            parts.append(f"{key} kernel_us = {c['kernel_us']:.1f} ({c['path']}{extra})")
+    if d.get("decode"):
+        parts.append(f"decode us_per_step = {d['decode']['us_per_step']:.1f}")
+    for key, label in (("fp32_forward", "fp32 forward"), ("gated", "gated forward"), ("kda", "KDA forward")):
+        if d.get(key):
+            parts.append(f"{label} = {d[key]['ms_per_call']:.3f} ms")
+    if d.get("kda") and d["kda"].get("per_token"):
+        parts.append(f"KDA per-token = {d['kda']['per_token']['ms_per_call']:.3f} ms")
+    if d.get("model_linear_attention"):
+        m = d["model_linear_attention"]
+        parts.append(f"model linear attention bf16 / fp32 = {m['bf16']['ms_per_call']:.3f} / "
+                     f"{m['fp32']['ms_per_call']:.3f} ms")
+    if d.get("backward"):
+        b = d["backward"]
+        parts.append(f"backward bf16 = {b['ms_per_call']:.3f} ms" +
+                     (f", fp32 = {b['fp32']['ms_per_call']:.3f} ms" if b.get("fp32") else ""))
+    return "bench.py line from the same run: " + "; ".join(parts) + "."
+
+
 def stats(args) -> None:
-    path = _one(os.path.join(args.dir, "**", "*kernel_stats.csv"))
-    with open(path) as f:
-        rows = list(csv.DictReader(f))
-    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    """Per-kernel durations.  With the kernel trace present, one row per (kernel, grid size),
+    so that launches of one kernel at different shapes (cfg1 and a varlen batch, say)
+    are told apart; otherwise rocprofv3's own per-kernel statistics."""
     out = ["# rocprofv3 kernel statistics", "", "Command:", "", "```", args.cmd, "```", ""]
     if args.bench_log:
-        for ln in open(args.bench_log):
-            if ln.startswith("{"):
-                d = json.loads(ln)
-                extra = ""
-                for key, label in (("fp32_forward", "fp32 forward"), ("gated", "gated forward")):
-                    if d.get(key):
-                        extra += f"; {label} = {d[key]['ms_per_call']:.3f} ms"
-                if d.get("model_linear_attention"):
-                    m = d["model_linear_attention"]
-                    extra += (f"; model linear attention bf16 / fp32 = {m['bf16']['ms_per_call']:.3f} / "
-                              f"{m['fp32']['ms_per_call']:.3f} ms")
-                if d.get("backward"):
-                    b = d["backward"]
-                    extra += f"; backward bf16 = {b['ms_per_call']:.3f} ms"
-                    if b.get("fp32"):
-                        extra += f", fp32 = {b['fp32']['ms_per_call']:.3f} ms"
-                out += [f"bench.py line from the same run: kernel_us (HIP events over the timed launches, per launch) = "
-                        f"{d['kernel_us']:.1f}; decode us_per_step = "
-                        f"{d['decode']['us_per_step']:.1f}; value = {d['value']:.4g} {d['unit']}{extra}", ""]
-    out += ["| kernel | calls | avg us | min us | max us | total % |",
-            "|---|---:|---:|---:|---:|---:|"]
-    for r in rows[: args.top]:
-        out.append(f"| `{short_name(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
-                   f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
-                   f"{float(r['Percentage']):.1f} |")
+        out += [_bench_line(args.bench_log), ""]
+    hits = sorted(glob.glob(os.path.join(args.dir, "**", "*kernel_trace.csv"), recursive=True))
+    if hits:
+        groups: dict[tuple[str, int], list[float]] = {}
+        with open(hits[0]) as f:
+            for r in csv.DictReader(f):
+                grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+                wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+                dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                groups.setdefault((short_name(r["Kernel_Name"]), grid // max(wg, 1)), []).append(dur)
+        total = sum(sum(v) for v in groups.values())
+        rows = sorted(groups.items(), key=lambda kv: -sum(kv[1]))
+        if args.prefix:
+            rows = [kv for kv in rows if kv[0][0].startswith(args.prefix)]
+            out += [f"Kernels named {args.prefix}* only (the rest are the bench's own torch set-up and "
+                    f"reference work); total % is of every kernel's time.", ""]
+        out += ["| kernel | workgroups | calls | avg us | min us | max us | total % |",
+                "|---|---:|---:|---:|---:|---:|---:|"]
+        for (name, n_wg), v in rows[: args.top]:
+            out.append(f"| `{name}` | {n_wg} | {len(v)} | {sum(v) / len(v):.1f} | {min(v):.1f} | {max(v):.1f} | "
+                       f"{100 * sum(v) / total:.1f} |")
+    else:
+        path = _one(os.path.join(args.dir, "**", "*kernel_stats.csv"))
+        with open(path) as f:
+            rows = list(csv.DictReader(f))
+        rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+        out += ["| kernel | calls | avg us | min us | max us | total % |",
+                "|---|---:|---:|---:|---:|---:|"]
+        for r in rows[: args.top]:
+            out.append(f"| `{short_name(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                       f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
+                       f"{float(r['Percentage']):.1f} |")
     text = "\n".join(out) + "\n"
     with open(args.out, "w") as f:
         f.write(text)
@@ -222,7 +265,8 @@ def main(argv=None) -> None:
     s.add_argument("dir")
     s.add_argument("--cmd", required=True)
     s.add_argument("--bench-log")
-    s.add_argument("--top", type=int, default=8)
+    s.add_argument("--top", type=int, default=40)
+    s.add_argument("--prefix", default=None, help="list only kernels whose name starts with this")
     s.add_argument("-o", "--out", required=True)
     t = sub.add_parser("traffic")
     t.add_argument("fetch_dir")

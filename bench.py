@@ -153,6 +153,46 @@ def _time_rounds(torch, stream, fns, calls, rounds=3):
     return [sorted(r)[len(r) // 2] for r in res]
 
 
+SPLIT_SWEEP_SHAPES = [(4, 4096, 16, 128), (2, 4096, 16, 128), (1, 4096, 16, 128), (1, 32768, 32, 128),
+                      (2, 8192, 8, 128), (1, 1024, 4, 128), (4, 4096, 16, 64), (1, 8192, 16, 64),
+                      (8, 2048, 16, 128), (16, 512, 16, 128)]
+
+
+def split_sweep(torch, lib, _native, dev, stream, calls=10):
+    """The forward's two chunked forms (single-stage: pm_delta_set_path 2; split: 3) at the
+    shapes of SPLIT_SWEEP_SHAPES, bf16 q/k/v, fp32 O, in interleaved rounds; and which form
+    path 0 takes there (it takes the split form exactly when it asks for a workspace).
+    One JSON line per shape."""
+    for (B, T, H, D) in SPLIT_SWEEP_SHAPES:
+        sets = [make_inputs(torch, B, T, H, D, seed, dev) for seed in (1, 2)]
+        o = torch.empty((B, T, H, D), dtype=torch.float32, device=dev)
+        s = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+        auto_ws = lib.pm_delta_workspace_bytes(B, T, H, D, _native.DTYPE_BF16)
+        old = _native.set_path(3)
+        nws = lib.pm_delta_workspace_bytes(B, T, H, D, _native.DTYPE_BF16)
+        _native.set_path(old)
+        ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+
+        def run(path):
+            def f(i):
+                q, k, v, beta = sets[i % 2]
+                old = _native.set_path(path)
+                try:
+                    _native.check(lib.pm_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), None,
+                                                   o.data_ptr(), s.data_ptr(), B, T, H, D, _native.DTYPE_BF16,
+                                                   _native.DTYPE_F32, CHUNK, ws.data_ptr(), nws, stream.cuda_stream))
+                finally:
+                    _native.set_path(old)
+            return f
+
+        single, split = _time_rounds(torch, stream, [run(2), run(3)], calls)
+        tile = 16 if B * H * (D // 32) < 256 else 32
+        print(json.dumps({"shape": {"B": B, "T": T, "H": H, "D": D}, "d_v_tile": tile,
+                          "single_stage_us": single * 1e3, "split_us": split * 1e3, "split_over_single": split / single,
+                          "path0_takes": "split" if auto_ws else "single-stage"}), flush=True)
+        del sets, o, s, ws
+
+
 def _roofline(nbytes, ms):
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}
@@ -271,6 +311,9 @@ def main():
                     help="also run 3 launches of a plain 1 GiB fp32 elementwise copy (torch.neg, "
                          "4 GiB read+written in all) so that rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE "
                          "runs can be scaled to bytes")
+    ap.add_argument("--split-sweep", action="store_true",
+                    help="only time the forward's single-stage and split forms at a list of shapes "
+                         "(one JSON line per shape) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
@@ -289,6 +332,9 @@ def main():
     lib = _native.lib()
     if args.tile:
         _native.set_tile(args.tile)
+    if args.split_sweep:
+        split_sweep(torch, lib, _native, dev, torch.cuda.current_stream(dev))
+        return
 
     B, T, H, D = 4, 4096, 16, 128
     print(f"[bench] cfg1 inputs B{B} T{T} H{H} D{D}", file=sys.stderr, flush=True)

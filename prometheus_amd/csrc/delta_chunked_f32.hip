@@ -38,28 +38,17 @@
 #include <type_traits>
 
 #include "pm_cdna4.h"
+#include "pm_f32mfma.h"
 #include "pm_internal.h"
 
 namespace pm {
 namespace {
 
-constexpr int kC16 = 16;          // tokens per chunk
+constexpr int kBwdRec = kF32BwdRec;  // floats per chunk of the backward's record: T, K K^T, beta
 // workspace floats per chunk: (T'')^T, then (normalised mode) the 16 keys' 1 / max(||k||, 1e-6)
 template <bool NORM>
 constexpr int ws_floats() { return NORM ? 256 + 16 : 256; }
 
-__device__ __forceinline__ f32x4_t mfma4(float a, float b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-// Left * Right over a 16-token contraction, given the accumulators of Left^T and Right
-// (plus c), in two accumulators.
-__device__ __forceinline__ f32x4_t mm16(f32x4_t lt, f32x4_t r, f32x4_t c = f32x4_t{0.f, 0.f, 0.f, 0.f}) {
-    const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-    f32x4_t a0 = mfma4(lt[0], r[0], c), a1 = mfma4(lt[1], r[1], z);
-    a0 = mfma4(lt[2], r[2], a0);
-    a1 = mfma4(lt[3], r[3], a1);
-    return a0 + a1;
-}
 
 // Workspace slots (16-token chunks), as the split form's: fixed length, row = pair, slot
 // = c; varlen, row = h and slot = floor(tok0 / 16) + seq + c (consecutive sequences never
@@ -68,22 +57,14 @@ __host__ __device__ inline int f32_n_slot(bool varlen, int T, int n_seq) {
     return varlen ? (T + kC16 - 1) / kC16 + n_seq : (T + kC16 - 1) / kC16;
 }
 
-// LDS tile of 16 fp32 token rows of D values: the 16-byte chunk p of row t is stored at
-// chunk t * (D / 4) + (p ^ t).  With it the float4 operand reads (lane (g, r): row r,
-// chunk 4 m + g) and the column reads of K^T (lane (g, r): row 4 g + v, element 16 m + r)
-// fall in distinct banks across each quarter wave.
-template <int D>
-__device__ __forceinline__ int f32_chunk(int t, int p) {
-    return t * (D / 4) + (p ^ t);
-}
 
 // ---------------------------------------------------------------- K7p
-template <int D, bool NORM>
+template <int D, bool NORM, bool BWD = false>
 __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __restrict__ k,
                                                              const float* __restrict__ beta,
                                                              const int32_t* __restrict__ cu_seqlens,
                                                              int n_seq, int T, int H, int n_slot, long n_items,
-                                                             float* __restrict__ ws) {
+                                                             float* __restrict__ ws, float* __restrict__ ws_b = nullptr) {
     constexpr int NJ = D / 16;
     const int lane = threadIdx.x & 63;
     const long item = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -181,6 +162,15 @@ __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __rest
     for (int v = 0; v < 4; ++v) tw[v] = -bt[v] * Tt[v];  // (T'')^T[i][j] = -beta_i T[j][i]
     float* out = ws + (static_cast<size_t>(row) * n_slot + slot) * ws_floats<NORM>();
     *reinterpret_cast<f32x4_t*>(out + lane * 4) = tw;
+    if constexpr (BWD) {
+        // the backward's record: T (accumulator registers: T[4 g + v][r]), the Gram matrix
+        // K K^T (symmetric, so its registers are also those of its transpose) and beta
+        const f32x4_t Tacc = mm16(F2t, eye + N8);  // (I+N)(I+N^2)(I+N^4) (I+N^8)
+        float* ob = ws_b + (static_cast<size_t>(row) * n_slot + slot) * kBwdRec;
+        *reinterpret_cast<f32x4_t*>(ob + lane * 4) = Tacc;
+        *reinterpret_cast<f32x4_t*>(ob + 256 + lane * 4) = G;
+        if (g == 0) ob[512 + r] = bc;
+    }
     if constexpr (NORM) {
         if (g == 0) out[256 + r] = sk;
     }
@@ -213,14 +203,21 @@ struct F32Geo {
     static_assert(BYTES <= 160 * 1024 && NCP + NST <= 63, "LDS / vmcnt");
 };
 
-template <int D, int DV, bool OUT_BF16, bool NORM>
+// HIST (the backward's history pass, fixed-length batches): no O and no final state; the
+// chain waves store the state at the start of every kF32Span-th chunk and at the end
+// instead (n_span = the number of spans + 1 states per pair), as accumulator registers:
+// hist[pair][index][column block 16 jb][tile m][lane][4] holds S[16 m + 4 g + v][16 jb + r]
+// at lane 16 g + r, register v.  The copy wave then copies no Q.
+template <int D, int DV, bool OUT_BF16, bool NORM, bool HIST = false>
 __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ s0, void* __restrict__ o_out, float* __restrict__ s_out,
     const int32_t* __restrict__ cu_seqlens, const float* __restrict__ ws, int n_pairs, int T, int H,
-    int n_tiles, int n_slot) {
+    int n_tiles, int n_slot, float* __restrict__ hist = nullptr, int n_span = 0) {
     using G = F32Geo<D, DV, NORM>;
     constexpr int NCW = G::NCW, NT = G::NT;
+    constexpr int NCP = HIST ? G::NCP - G::NI : G::NCP;  // copies per chunk
+    constexpr int NST = HIST ? 0 : G::NST;               // O stores per output wave per chunk
     constexpr int WSF = ws_floats<NORM>();
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
@@ -297,7 +294,7 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
     auto copies = [&](int c) __attribute__((always_inline)) {
         unsigned char* b = buf(c);
         copy_tile(k, c, b + G::B_K);
-        copy_tile(q, c, b + G::B_Q);
+        if constexpr (!HIST) copy_tile(q, c, b + G::B_Q);
         copy_ws(c, b + G::B_T);
 #pragma unroll
         for (int j = 0; j < NCW; ++j) copy_v(c, j, b + G::B_V + 1024 * j);
@@ -306,9 +303,9 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
     // issued after them (this and the last iteration's O stores, the copies of the chunk
     // after next) possibly in flight
     auto wait_next = [&](bool extra_stores, bool extra_copies) __attribute__((always_inline)) {
-        if (extra_copies && extra_stores) wait_vm_n<G::NCP + G::NST>();
-        else if (extra_copies) wait_vm_n<G::NCP>();
-        else if (extra_stores) wait_vm_n<G::NST>();
+        if (extra_copies && extra_stores) wait_vm_n<NCP + NST>();
+        else if (extra_copies) wait_vm_n<NCP>();
+        else if (extra_stores) wait_vm_n<NST>();
         else wait_vm_n<0>();
     };
 
@@ -362,6 +359,14 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
                     for (int m = 0; m < NT; ++m) S[m] = mfma4(kt[e][m], Up[e], S[m]);
             }
             if (!run) break;
+            if constexpr (HIST) {
+                if (i % kF32Span == 0) {
+                    float* hp = hist + ((static_cast<size_t>(pair) * n_span + i / kF32Span) * (D / 16) +
+                                        col0 / 16 + cw) * NT * 256;
+#pragma unroll
+                    for (int m = 0; m < NT; ++m) *reinterpret_cast<f32x4_t*>(hp + m * 256 + 4 * lane) = S[m];
+                }
+            }
             fence();
             if constexpr (!NORM) xa[0] = -vr;  // (negated only here: a use right after the read would wait for it)
             // X = K S - V (accumulator e takes the steps (m, e))
@@ -380,10 +385,12 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
             Up = mm16(tt, X);
             if constexpr (NORM) Up = Up * skc;
             // hand S_i and U_i to the output wave
-            unsigned char* ss = sslot(i, cw);
+            if constexpr (!HIST) {
+                unsigned char* ss = sslot(i, cw);
 #pragma unroll
-            for (int m = 0; m < NT; ++m) st4(ss + 1024 * m + 16 * lane, S[m]);
-            st4(uslot(i, cw) + 16 * lane, Up);
+                for (int m = 0; m < NT; ++m) st4(ss + 1024 * m + 16 * lane, S[m]);
+                st4(uslot(i, cw) + 16 * lane, Up);
+            }
             // K^T operand of chunk i, for the next iteration's state update
             const float* Kf = reinterpret_cast<const float*>(b + G::B_K);
 #pragma unroll
@@ -398,10 +405,24 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
             __builtin_amdgcn_s_waitcnt(0xC07F);
             lds_barrier();
         }
+        if constexpr (!HIST) {
 #pragma unroll
-        for (int m = 0; m < NT; ++m)
+            for (int m = 0; m < NT; ++m)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) s_out[sbase + static_cast<size_t>(16 * m + 4 * g + e) * D + ecol] = S[m][e];
+                for (int e = 0; e < 4; ++e) s_out[sbase + static_cast<size_t>(16 * m + 4 * g + e) * D + ecol] = S[m][e];
+        } else {
+            // the state at the end of the sequence closes the last span
+            float* hp = hist + ((static_cast<size_t>(pair) * n_span + n_span - 1) * (D / 16) + col0 / 16 + cw) * NT * 256;
+#pragma unroll
+            for (int m = 0; m < NT; ++m) *reinterpret_cast<f32x4_t*>(hp + m * 256 + 4 * lane) = S[m];
+        }
+    } else if (HIST && n_chunks > 0) {
+        // the copy wave keeps two chunks ahead; the other output waves only keep the barriers
+        for (int i = 0; i < n_chunks; ++i) {
+            if (copy_wave && i + 2 < n_chunks) copies(i + 2);
+            if (copy_wave && i + 1 < n_chunks) wait_next(false, i + 2 < n_chunks);
+            lds_barrier();
+        }
     } else if (n_chunks > 0) {
         // ============ output waves: O of chunk i - 1 for the columns of chain wave cw ============
         // Iteration i: the P wave builds P^T of chunk i (for the next iteration, into LDS);
@@ -523,7 +544,7 @@ hipError_t launch_f32_t(const ChunkedF32Args& a, float* ws, hipStream_t st) {
     const float *q = a.q, *k = a.k, *v = a.v;
     if (n_items > 0) {
         hipLaunchKernelGGL((delta_f32_prep_kernel<D, NORM>), dim3(static_cast<unsigned>((n_items + 3) / 4)), dim3(256), 0,
-                           st, k, a.beta, a.cu_seqlens, a.n_seq, a.T, a.H, n_slot, n_items, ws);
+                           st, k, a.beta, a.cu_seqlens, a.n_seq, a.T, a.H, n_slot, n_items, ws, nullptr);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -533,7 +554,7 @@ hipError_t launch_f32_t(const ChunkedF32Args& a, float* ws, hipStream_t st) {
     const int n_tiles = D / DV;
     const int slots = (n_pairs + 7) / 8;
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(slots * n_tiles * 8)), dim3(128 * G::NCW), G::BYTES, st, q, k,
-                       v, a.s0, a.o, a.s_out, a.cu_seqlens, ws, n_pairs, a.T, a.H, n_tiles, n_slot);
+                       v, a.s0, a.o, a.s_out, a.cu_seqlens, ws, n_pairs, a.T, a.H, n_tiles, n_slot, nullptr, 0);
     return hipGetLastError();
 }
 
@@ -557,6 +578,39 @@ int chunked_f32_pick_tile(int D, long n_pairs, int requested) {
     if (requested == 16 || requested == 32) return requested;
     if (requested == 64) return 32;
     return n_pairs * (D / 32) >= 256 ? 32 : 16;
+}
+
+namespace {
+template <int D, int DV>
+hipError_t launch_hist_t(const float* k, const float* v, const float* beta, const float* s0, int n_pairs, int T,
+                         int H, float* ws_t2, float* ws_rec, float* s_hist, hipStream_t st) {
+    using G = F32Geo<D, DV, false>;
+    const int n_slot = f32_n_slot(false, T, 0);
+    const long n_items = static_cast<long>(n_pairs) * n_slot;
+    hipLaunchKernelGGL((delta_f32_prep_kernel<D, false, true>), dim3(static_cast<unsigned>((n_items + 3) / 4)),
+                       dim3(256), 0, st, k, beta, nullptr, n_pairs / H, T, H, n_slot, n_items, ws_t2, ws_rec);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = set_lds_f32<delta_f32_kernel<D, DV, false, false, true>>(G::BYTES);
+    if (e != hipSuccess) return e;
+    const int n_tiles = D / DV, slots = (n_pairs + 7) / 8;
+    const int n_state = (n_slot + kF32Span - 1) / kF32Span + 1;  // every span's start, and the end
+    hipLaunchKernelGGL((delta_f32_kernel<D, DV, false, false, true>), dim3(static_cast<unsigned>(slots * n_tiles * 8)),
+                       dim3(128 * G::NCW), G::BYTES, st, nullptr, k, v, s0, nullptr, nullptr, nullptr, ws_t2, n_pairs,
+                       T, H, n_tiles, n_slot, s_hist, n_state);
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_f32_history(const float* k, const float* v, const float* beta, const float* s0, int n_pairs,
+                              int T, int H, int D, float* ws_t2, float* ws_rec, float* s_hist, hipStream_t st) {
+    if (n_pairs == 0 || T == 0) return hipSuccess;
+    const int dv = chunked_f32_pick_tile(D, n_pairs, 0);
+    if (D == 128)
+        return dv == 16 ? launch_hist_t<128, 16>(k, v, beta, s0, n_pairs, T, H, ws_t2, ws_rec, s_hist, st)
+                        : launch_hist_t<128, 32>(k, v, beta, s0, n_pairs, T, H, ws_t2, ws_rec, s_hist, st);
+    return dv == 16 ? launch_hist_t<64, 16>(k, v, beta, s0, n_pairs, T, H, ws_t2, ws_rec, s_hist, st)
+                    : launch_hist_t<64, 32>(k, v, beta, s0, n_pairs, T, H, ws_t2, ws_rec, s_hist, st);
 }
 
 hipError_t launch_chunked_f32(const ChunkedF32Args& a, void* ws, hipStream_t st) {

@@ -6,6 +6,10 @@
 //   K3    delta_step.hip       decode step, HBM-streaming
 //   K4    delta_recurrent.hip  per-token fp32 recurrence (generic shapes)
 //   K5    delta_bwd.hip        reverse mode, fp32, checkpointed
+//   K6    delta_chunked_bwd.hip     chunked reverse mode, bf16 inputs
+//   K7    delta_chunked_f32.hip     chunked forward on fp32 MFMA, fp32 inputs
+//   K8    kda_chunked.hip           chunked forward with a decay per key channel
+//   K9    delta_chunked_f32_bwd.hip chunked reverse mode on fp32 MFMA, fp32 inputs
 // Mirrors the checks of kernels/__init__.py:308-338 (shapes), :613-614 and
 // :676-677 (chunk >= 1); shapes arrive as integers, so the Python layer
 // (prometheus_amd/kernels) raises KernelError for the tensor-level checks
@@ -286,11 +290,16 @@ int step(float* s_inout, const void* q, const void* k, const void* v, const floa
 bool bwd_chunked(int H, int D, int in_dtype) {
     return g_path != 1 && in_dtype == PM_DTYPE_BF16 && pm::chunked_bwd_supported(D, H);
 }
+// ... and the fp32 chunked backward (K9) for fp32 inputs with D in {64, 128}
+bool bwd_chunked_f32(int H, int D, int in_dtype) {
+    return g_path != 1 && in_dtype == PM_DTYPE_F32 && pm::f32_bwd_supported(D, H);
+}
 
 // gm: 0 ungated, 1 gated (a log-gate per token and head), 2 per-channel gated (KDA)
 size_t bwd_ws_bytes(int B, int T, int H, int D, int in_dtype, int gm = 0) {
     const long n_pairs = static_cast<long>(B) * H;
     if (gm == 0 && bwd_chunked(H, D, in_dtype)) return pm::chunked_bwd_ws(n_pairs, T, D).bytes;
+    if (gm == 0 && bwd_chunked_f32(H, D, in_dtype)) return pm::f32_bwd_ws(n_pairs, T, D).bytes;
     return sizeof(float) * pm::bwd_workspace_floats(n_pairs, T, D, gm);
 }
 
@@ -318,11 +327,13 @@ int backward(const void* q, const void* k, const void* v, const float* beta, con
     const void* f32s[] = {beta, g, s0, go, gs, gq, gk, gv, gbeta, gg, gs0, workspace};
     for (const void* p : f32s)
         if (p && !aligned(p, 4)) return fail(PM_E_ALIGN, "fp32 buffers must be 4-byte aligned");
-    const bool chunked = !gated && bwd_chunked(H, D, in_dtype);
+    const bool chunked16 = !gated && bwd_chunked(H, D, in_dtype);
+    const bool chunked32 = !gated && bwd_chunked_f32(H, D, in_dtype);
+    const bool chunked = chunked16 || chunked32;
     if (g_path >= 2 && !chunked)
         return fail(PM_E_UNSUPPORTED,
                     gated ? "the gated backward runs on the per-token kernels only (path 2 asks for the chunked one)"
-                          : "chunked backward needs bf16 inputs and D in {64, 128} (got in_dtype %d, D %d)",
+                          : "chunked backward needs D in {64, 128} (got in_dtype %d, D %d)",
                     in_dtype, D);
     if (chunked && n_tok > 0) {
         const void* v16[] = {q, k, v, go, gq, gk, gv, workspace};
@@ -341,8 +352,9 @@ int backward(const void* q, const void* k, const void* v, const float* beta, con
     a.g = g;
     a.gg = gg;
     a.per_channel = per_channel;
-    hipError_t e = chunked ? pm::launch_bwd_chunked(a, static_cast<hipStream_t>(stream))
-                           : pm::launch_bwd(a, static_cast<hipStream_t>(stream));
+    hipError_t e = chunked16   ? pm::launch_bwd_chunked(a, static_cast<hipStream_t>(stream))
+                   : chunked32 ? pm::launch_bwd_chunked_f32(a, static_cast<hipStream_t>(stream))
+                               : pm::launch_bwd(a, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? 0 : hip_fail(e, "backward launch");
 }
 

@@ -132,6 +132,26 @@ hipError_t launch_chunked_f32(const ChunkedF32Args& a, void* ws, hipStream_t st)
 // s_hist holds n_seq*H x ceil(T/64) x D x D values.
 hipError_t launch_chunked_states(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st);
 
+// The fp32 chunked backward (K9; fixed-length batches, fp32 q/k/v, D in {64, 128}).
+// Chunks of kC16 = 16 tokens; the state S and its gradient G are kept at the start and
+// the end of every span of kF32Span chunks (128 tokens).  Workspace regions (bytes, each
+// 16-byte aligned), per (b, h):
+//   t2     (T'')^T per chunk, 256 floats (the fp32 forward's own workspace layout)
+//   rec    T, K K^T and beta per chunk, kF32BwdRec floats
+//   s_hist S at every span start, g_hist G at every span end: D x D floats per span, as
+//          accumulator registers (column block of 16, tile of 16 rows, lane, register)
+//   w      W = dL/dX per token (B, T, H, D) floats
+constexpr int kF32Span = 8;
+constexpr int kF32BwdRec = 528;
+struct F32BwdWs {
+    size_t t2, rec, s_hist, g_hist, w, bytes;
+};
+F32BwdWs f32_bwd_ws(long n_pairs, int T, int D);
+bool f32_bwd_supported(int D, int H);
+// K9p + K9a: the backward's records and the state history (fixed-length batches).
+hipError_t launch_f32_history(const float* k, const float* v, const float* beta, const float* s0, int n_pairs,
+                              int T, int H, int D, float* ws_t2, float* ws_rec, float* s_hist, hipStream_t st);
+
 // Reverse mode (K5, fp32): fixed-length batch of n_pairs = B*H sequences of
 // T tokens, D <= 256.  workspace holds bwd_workspace_floats(n_pairs, T, D)
 // floats: u (n_pairs x T x D), the checkpoints (n_pairs x ceil(T/8) x D x D),
@@ -177,6 +197,8 @@ struct ChunkedBwdWs {
 ChunkedBwdWs chunked_bwd_ws(long n_pairs, int T, int D);
 bool chunked_bwd_supported(int D, int H);  // chunked_supported and H*D <= 2^23 (fp32 dO rows)
 hipError_t launch_bwd_chunked(const BwdArgs& a, hipStream_t st);
+// K9 (the fp32 chunked backward): a.workspace holds f32_bwd_ws(...).bytes bytes.
+hipError_t launch_bwd_chunked_f32(const BwdArgs& a, hipStream_t st);
 
 // Zero fill (used instead of hipMemsetAsync so callers may graph-capture).
 hipError_t launch_fill_zero(float* p, size_t n, hipStream_t st);

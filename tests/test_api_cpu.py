@@ -116,17 +116,35 @@ def _chunked_ws(b, t, h, d):
     return 2 * b * h * (-(-t // 64)) * (2 * d * d + 64 * d + 9216)
 
 
+def _f32_chunked_ws(b, t, h, d):
+    # (T'')^T and the T / K K^T / beta record per 16-token chunk, S at every 128-token span
+    # start and at the end, G at every span end, W per token; each region 256-byte aligned
+    n_ch = -(-t // 16)
+    n_span = -(-n_ch // 8)
+    n = b * h
+    al = lambda x: -(-x // 256) * 256
+    size = al(n * n_ch * 256 * 4)
+    size = al(size + n * n_ch * 528 * 4)
+    size = al(size + n * (n_span + 1) * d * d * 4)
+    size = al(size + n * n_span * d * d * 4)
+    return al(size + n * t * d * 4)
+
+
 def test_bwd_workspace_bytes():
     lib = _native.lib()
     f32, bf16 = _native.DTYPE_F32, _native.DTYPE_BF16
     for b, t, h, d in [(1, 1, 1, 3), (2, 130, 3, 64), (4, 4096, 16, 128), (1, 0, 2, 8), (1, 70, 2, 48)]:
-        assert lib.pm_delta_bwd_workspace_bytes(b, t, h, d, f32) == _per_token_ws(b, t, h, d)
+        want = _f32_chunked_ws(b, t, h, d) if d in (64, 128) else _per_token_ws(b, t, h, d)
+        assert lib.pm_delta_bwd_workspace_bytes(b, t, h, d, f32) == want
         want = _chunked_ws(b, t, h, d) if d in (64, 128) else _per_token_ws(b, t, h, d)
         assert lib.pm_delta_bwd_workspace_bytes(b, t, h, d, bf16) == want
+    # the cfg1 shape's fp32 chunked workspace stays under 0.5 GB
+    assert lib.pm_delta_bwd_workspace_bytes(4, 4096, 16, 128, f32) < 500_000_000
     # path 1 (per-token kernel) applies to the backward as well
     old = _native.set_path(1)
     try:
         assert lib.pm_delta_bwd_workspace_bytes(2, 130, 3, 64, bf16) == _per_token_ws(2, 130, 3, 64)
+        assert lib.pm_delta_bwd_workspace_bytes(2, 130, 3, 64, f32) == _per_token_ws(2, 130, 3, 64)
     finally:
         _native.set_path(old)
     assert lib.pm_delta_bwd_workspace_bytes(1, 4, 1, 257, f32) == 0

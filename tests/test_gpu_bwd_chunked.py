@@ -114,9 +114,12 @@ def test_path_two_requires_the_chunked_kernel():
     try:
         got = kernels.chunked_delta_rule_bwd(res, (_dev(go), _dev(gs)))
         _check(got, ref.delta_vjp(x.q, x.k, x.v, x.beta, go, gs, None), "path 2")
-        r32 = kernels._DeltaResidual(q=_dev(x.q), k=_dev(x.k), v=_dev(x.v), beta=_dev(x.beta),
-                                     state0=_dev(np.zeros((1, 1, 64, 64), np.float32)), chunk=64)
+        # fp32 q/k/v with D = 48: no chunked backward serves it (fp32 D in {64, 128} runs the
+        # fp32 chunked one, tests/test_gpu_bwd_f32_chunked.py)
+        x48, go48, _, _ = _problem((1, 40, 1, 48), seed=3, state=False)
+        r32 = kernels._DeltaResidual(q=_dev(x48.q), k=_dev(x48.k), v=_dev(x48.v), beta=_dev(x48.beta),
+                                     state0=_dev(np.zeros((1, 1, 48, 48), np.float32)), chunk=64)
         with pytest.raises(_native.NativeError):
-            kernels.chunked_delta_rule_bwd(r32, (_dev(go), None))
+            kernels.chunked_delta_rule_bwd(r32, (_dev(go48), None))
     finally:
         _native.set_path(old)

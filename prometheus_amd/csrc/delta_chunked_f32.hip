@@ -177,26 +177,29 @@ __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __rest
 }
 
 // ---------------------------------------------------------------- K7
-template <int D, int DV, bool NORM>
+// HIST (the history mode) keeps no Q and no hand-off slots, and three chunk buffers
+// (the chain's, the one in flight, the one being copied): 33 KiB at D = 128, DV = 32, so
+// that a workgroup of the backward's sweep fits beside it on a CU.
+template <int D, int DV, bool NORM, bool HIST = false>
 struct F32Geo {
     static constexpr int NCW = DV / 16;            // chain waves 0 .. NCW-1, output waves NCW ..
     static constexpr int NT = D / 16;              // S accumulator tiles per chain wave
     static constexpr int NI = kC16 * D * 4 / 1024; // 1 KiB copies per K or Q tile
-    static constexpr int NB = 4;                   // rotating chunk buffers
+    static constexpr int NB = HIST ? 3 : 4;        // rotating chunk buffers
     // one chunk buffer: K rows, Q rows, (T'')^T, V columns of each chain wave
     static constexpr int B_K = 0;
     static constexpr int B_Q = B_K + kC16 * D * 4;
-    static constexpr int B_T = B_Q + kC16 * D * 4;
+    static constexpr int B_T = B_Q + (HIST ? 0 : kC16 * D * 4);
     static constexpr int B_V = B_T + (NORM ? 2048 : 1024);  // (T'')^T, then the keys' scales
     static constexpr int BUF = B_V + NCW * 1024;
-    static constexpr int OFF_S = NB * BUF;                     // 2 slots x NCW x NT KiB: S_i
-    static constexpr int OFF_U = OFF_S + 2 * NCW * NT * 1024;  // 2 slots x NCW KiB: U_i
-    static constexpr int PSLOT = NORM ? 1024 + 64 : 1024;      // P^T, then the queries' scales
-    static constexpr int OFF_P = OFF_U + 2 * NCW * 1024;       // 2 slots: P^T of a chunk
-    static constexpr int BYTES = OFF_P + 2 * PSLOT;
+    static constexpr int OFF_S = NB * BUF;                                  // 2 slots x NCW x NT KiB: S_i
+    static constexpr int OFF_U = OFF_S + (HIST ? 0 : 2 * NCW * NT * 1024);  // 2 slots x NCW KiB: U_i
+    static constexpr int PSLOT = NORM ? 1024 + 64 : 1024;                   // P^T, then the queries' scales
+    static constexpr int OFF_P = OFF_U + (HIST ? 0 : 2 * NCW * 1024);       // 2 slots: P^T of a chunk
+    static constexpr int BYTES = OFF_P + (HIST ? 0 : 2 * PSLOT);
     // the last output wave (the copy wave) issues every copy of a chunk: K and Q rows,
     // (T'')^T and the V columns of each chain wave
-    static constexpr int NCP = 2 * NI + 1 + NCW + (NORM ? 1 : 0);
+    static constexpr int NCP = (HIST ? NI : 2 * NI) + 1 + NCW + (NORM ? 1 : 0);
     static constexpr int NST = 4;  // O stores per output wave per chunk
     static_assert(D == 64 || D == 128, "D");
     static_assert(DV == 16 || DV == 32, "DV");
@@ -214,9 +217,9 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
     const float* __restrict__ s0, void* __restrict__ o_out, float* __restrict__ s_out,
     const int32_t* __restrict__ cu_seqlens, const float* __restrict__ ws, int n_pairs, int T, int H,
     int n_tiles, int n_slot, float* __restrict__ hist = nullptr, int n_span = 0) {
-    using G = F32Geo<D, DV, NORM>;
+    using G = F32Geo<D, DV, NORM, HIST>;
     constexpr int NCW = G::NCW, NT = G::NT;
-    constexpr int NCP = HIST ? G::NCP - G::NI : G::NCP;  // copies per chunk
+    constexpr int NCP = G::NCP;                          // copies per chunk
     constexpr int NST = HIST ? 0 : G::NST;               // O stores per output wave per chunk
     constexpr int WSF = ws_floats<NORM>();
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -582,16 +585,11 @@ int chunked_f32_pick_tile(int D, long n_pairs, int requested) {
 
 namespace {
 template <int D, int DV>
-hipError_t launch_hist_t(const float* k, const float* v, const float* beta, const float* s0, int n_pairs, int T,
-                         int H, float* ws_t2, float* ws_rec, float* s_hist, hipStream_t st) {
-    using G = F32Geo<D, DV, false>;
+hipError_t launch_hist_t(const float* k, const float* v, const float* s0, int n_pairs, int T, int H,
+                         const float* ws_t2, float* s_hist, hipStream_t st) {
+    using G = F32Geo<D, DV, false, true>;
     const int n_slot = f32_n_slot(false, T, 0);
-    const long n_items = static_cast<long>(n_pairs) * n_slot;
-    hipLaunchKernelGGL((delta_f32_prep_kernel<D, false, true>), dim3(static_cast<unsigned>((n_items + 3) / 4)),
-                       dim3(256), 0, st, k, beta, nullptr, n_pairs / H, T, H, n_slot, n_items, ws_t2, ws_rec);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    e = set_lds_f32<delta_f32_kernel<D, DV, false, false, true>>(G::BYTES);
+    hipError_t e = set_lds_f32<delta_f32_kernel<D, DV, false, false, true>>(G::BYTES);
     if (e != hipSuccess) return e;
     const int n_tiles = D / DV, slots = (n_pairs + 7) / 8;
     const int n_state = (n_slot + kF32Span - 1) / kF32Span + 1;  // every span's start, and the end
@@ -602,15 +600,30 @@ hipError_t launch_hist_t(const float* k, const float* v, const float* beta, cons
 }
 }  // namespace
 
-hipError_t launch_f32_history(const float* k, const float* v, const float* beta, const float* s0, int n_pairs,
-                              int T, int H, int D, float* ws_t2, float* ws_rec, float* s_hist, hipStream_t st) {
+hipError_t launch_f32_bwd_prep(const float* k, const float* beta, int n_pairs, int T, int H, int D, float* ws_t2,
+                               float* ws_rec, hipStream_t st) {
+    if (n_pairs == 0 || T == 0) return hipSuccess;
+    const int n_slot = f32_n_slot(false, T, 0);
+    const long n_items = static_cast<long>(n_pairs) * n_slot;
+    const dim3 grid(static_cast<unsigned>((n_items + 3) / 4));
+    if (D == 128)
+        hipLaunchKernelGGL((delta_f32_prep_kernel<128, false, true>), grid, dim3(256), 0, st, k, beta, nullptr,
+                           n_pairs / H, T, H, n_slot, n_items, ws_t2, ws_rec);
+    else
+        hipLaunchKernelGGL((delta_f32_prep_kernel<64, false, true>), grid, dim3(256), 0, st, k, beta, nullptr,
+                           n_pairs / H, T, H, n_slot, n_items, ws_t2, ws_rec);
+    return hipGetLastError();
+}
+
+hipError_t launch_f32_history(const float* k, const float* v, const float* s0, int n_pairs, int T, int H, int D,
+                              const float* ws_t2, float* s_hist, hipStream_t st) {
     if (n_pairs == 0 || T == 0) return hipSuccess;
     const int dv = chunked_f32_pick_tile(D, n_pairs, 0);
     if (D == 128)
-        return dv == 16 ? launch_hist_t<128, 16>(k, v, beta, s0, n_pairs, T, H, ws_t2, ws_rec, s_hist, st)
-                        : launch_hist_t<128, 32>(k, v, beta, s0, n_pairs, T, H, ws_t2, ws_rec, s_hist, st);
-    return dv == 16 ? launch_hist_t<64, 16>(k, v, beta, s0, n_pairs, T, H, ws_t2, ws_rec, s_hist, st)
-                    : launch_hist_t<64, 32>(k, v, beta, s0, n_pairs, T, H, ws_t2, ws_rec, s_hist, st);
+        return dv == 16 ? launch_hist_t<128, 16>(k, v, s0, n_pairs, T, H, ws_t2, s_hist, st)
+                        : launch_hist_t<128, 32>(k, v, s0, n_pairs, T, H, ws_t2, s_hist, st);
+    return dv == 16 ? launch_hist_t<64, 16>(k, v, s0, n_pairs, T, H, ws_t2, s_hist, st)
+                    : launch_hist_t<64, 32>(k, v, s0, n_pairs, T, H, ws_t2, s_hist, st);
 }
 
 hipError_t launch_chunked_f32(const ChunkedF32Args& a, void* ws, hipStream_t st) {

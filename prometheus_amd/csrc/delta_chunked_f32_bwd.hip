@@ -33,6 +33,8 @@
 // products that contract over d_v inside a chunk (dO U^T, W U^T) are summed over the
 // waves in LDS, in a fixed order.
 
+#include <mutex>
+
 #include "pm_cdna4.h"
 #include "pm_f32mfma.h"
 #include "pm_internal.h"
@@ -65,14 +67,14 @@ struct SwGeo {
     static_assert(BYTES <= 160 * 1024 && NCP + NST <= 63, "LDS / vmcnt");
 };
 
-// Waves 0 and 1 (chain) carry G for the columns col0 + 16 w + [0, 16) as NT accumulator
-// tiles (rows 16 m ..).  Iteration i runs chunk c = n - i on the chain (i >= 1): Y = K G,
-// dU = Y + P^T dO, W = T^T dU, and G += Q^T dO - K^T diag(beta) W, with Q^T dO and P
-// built one iteration earlier by waves 2 and 3 (helper 2 + w serves chain wave w; helper
-// 2 also builds P).  The helpers store the W and dV rows the chain handed over through
-// LDS one iteration later (iteration n + 1 stores chunk 0's); wave 3 copies chunk
-// n - 3 - i (two iterations ahead of its first use).  One LDS-only barrier per
-// iteration 0 .. n.
+// Waves 2 and 3 (chain) carry G for the columns col0 + 16 (w - 2) + [0, 16) as NT
+// accumulator tiles (rows 16 m ..).  Iteration i runs chunk c = n - i on the chain
+// (i >= 1): Y = K G, dU = Y + P^T dO, W = T^T dU, and G += Q^T dO - K^T diag(beta) W,
+// with Q^T dO and P built one iteration earlier by waves 0 and 1 (helper w serves chain
+// wave 2 + w; helper 0 also builds P).  The helpers store the W and dV rows the chain
+// handed over through LDS one iteration later (iteration n + 1 stores chunk 0's); wave 1
+// copies chunk n - 3 - i (two iterations ahead of its first use).  One LDS-only barrier
+// per iteration 0 .. n.
 template <int D>
 __global__ __launch_bounds__(256) void f32_bwd_sweep_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ go,
@@ -95,8 +97,12 @@ __global__ __launch_bounds__(256) void f32_bwd_sweep_kernel(
     const int lane = threadIdx.x & 63;
     const int w = static_cast<int>(uniform(static_cast<unsigned>(threadIdx.x >> 6)));
     const int r = lane & 15, g = lane >> 4;
+    // roles: waves 2 and 3 chain, 0 and 1 helpers (wave 1 copies), so that beside a
+    // workgroup of the history pass (chain waves 0 and 1) the four chains of a CU spread
+    // over its four SIMDs (waves of a workgroup go to the SIMDs in turn)
+    const bool chain_wave = w >= 2;
     const int cw = w & 1;  // the 16 columns col0 + 16 cw + [0, 16) this wave works on
-    const bool copy_wave = w == 3;
+    const bool copy_wave = w == 1;
     const size_t tstride = static_cast<size_t>(H) * D;
     const size_t sbase = static_cast<size_t>(pair) * D * D;
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
@@ -155,7 +161,7 @@ __global__ __launch_bounds__(256) void f32_bwd_sweep_kernel(
     }
     if (n_ch > 0) lds_barrier();  // B0
 
-    if (w < 2) {
+    if (chain_wave) {
         // ============ chain wave ============
         const int ecol = col0 + 16 * cw + r;
         f32x4_t Gm[NT];
@@ -223,7 +229,7 @@ __global__ __launch_bounds__(256) void f32_bwd_sweep_kernel(
             for (int e = 0; e < 4; ++e) gs0[sbase + static_cast<size_t>(16 * m + 4 * g + e) * D + ecol] = Gm[m][e];
     } else if (n_ch > 0) {
         // ============ helper waves ============
-        const int hw = w - 2;
+        const int hw = w;
         for (int i = 0; i <= n_ch + 1; ++i) {
             const bool cp = copy_wave && n_ch - 3 - i >= 0;
             if (cp) copies(n_ch - 3 - i);
@@ -358,23 +364,23 @@ __global__ __launch_bounds__(D * 4) void f32_bwd_span_kernel(
     const size_t tstride = static_cast<size_t>(H) * D;
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
 
-    auto buf = [&](int f) { return smem + (f & 1) * G::BUF; };
-    auto uh = [&](int m) { return smem + G::OFF_U + m * G::TILE; };
-    auto col_read = [&](const unsigned char* tileb, int t, int d) {  // X[t][d] of a row tile
+    auto buf = [=](int f) { return smem + (f & 1) * G::BUF; };
+    auto uh = [=](int m) { return smem + G::OFF_U + m * G::TILE; };
+    auto col_read = [=](const unsigned char* tileb, int t, int d) {  // X[t][d] of a row tile
         return reinterpret_cast<const float*>(tileb)[4 * f32_chunk<D>(t, d >> 2) + (d & 3)];
     };
-    auto row_read = [&](const unsigned char* tileb, int i) {  // X[r][16 i + 4 g ..]
+    auto row_read = [=](const unsigned char* tileb, int i) {  // X[r][16 i + 4 g ..]
         return ld4(tileb + 16 * f32_chunk<D>(r, 4 * i + g));
     };
-    auto row0_of = [&](int m, int col) {
+    auto row0_of = [=](int m, int col) {
         return static_cast<size_t>(tok0 + (c0 + m) * kC16) * tstride + static_cast<size_t>(h) * D + col;
     };
-    auto bytes_of = [&](int m, int row_floats) {
+    auto bytes_of = [=](int m, int row_floats) {
         const int clen = min(kC16, T - (c0 + m) * kC16);
         return static_cast<unsigned>(((clen - 1) * tstride + row_floats) * 4);
     };
     // copy number x of a chunk's list; wave w issues x = w, w + NW, ...
-    auto copy_one = [&](int m, bool fwd, int x, unsigned char* b) __attribute__((always_inline)) {
+    auto copy_one = [=](int m, bool fwd, int x, unsigned char* b) __attribute__((always_inline)) {
         const size_t cslot = static_cast<size_t>(pair) * n_ch + c0 + m;
         if (fwd) {
             if (x < G::NI) {
@@ -387,12 +393,21 @@ __global__ __launch_bounds__(D * 4) void f32_bwd_span_kernel(
             return;
         }
         if (x < 4 * G::NI) {
+            // one branch per source (a selected pointer would become a table in scratch)
             const int which = x / G::NI, i = x % G::NI;
-            const float* base = which == 0 ? k : which == 1 ? q : which == 2 ? go : w_in;
-            const int off = which == 0 ? G::B_K : which == 1 ? G::B_Q : which == 2 ? G::B_O : G::B_W;
-            const __amdgpu_buffer_rsrc_t rs = make_rsrc(base ? base + row0_of(m, 0) : base, base ? bytes_of(m, D) : 0u);
             const int qc = 64 * i + lane, t = qc / (D / 4), p = (qc % (D / 4)) ^ t;
-            dma16_asm(rs, uniform_ptr(b + off + 1024 * i), static_cast<unsigned>(t * tstride * 4 + 16 * p));
+            const unsigned vo = static_cast<unsigned>(t * tstride * 4 + 16 * p);
+            if (which == 0) {
+                dma16_asm(make_rsrc(k + row0_of(m, 0), bytes_of(m, D)), uniform_ptr(b + G::B_K + 1024 * i), vo);
+            } else if (which == 1) {
+                dma16_asm(make_rsrc(q + row0_of(m, 0), bytes_of(m, D)), uniform_ptr(b + G::B_Q + 1024 * i), vo);
+            } else if (which == 2) {
+                // a null dO reads zeros (a zero-length range)
+                dma16_asm(make_rsrc(go ? go + row0_of(m, 0) : go, go ? bytes_of(m, D) : 0u),
+                          uniform_ptr(b + G::B_O + 1024 * i), vo);
+            } else {
+                dma16_asm(make_rsrc(w_in + row0_of(m, 0), bytes_of(m, D)), uniform_ptr(b + G::B_W + 1024 * i), vo);
+            }
         } else if (x == 4 * G::NI) {
             dma16_asm(make_rsrc(rec + cslot * kF32BwdRec + 256, 1024), uniform_ptr(b + G::B_G),
                       static_cast<unsigned>(16 * lane));
@@ -402,7 +417,7 @@ __global__ __launch_bounds__(D * 4) void f32_bwd_span_kernel(
         }
     };
     // staged chunk f of the span's sequence: forward m = f (f < nm), reverse m = 2 nm - 1 - f
-    auto issue = [&](int f) __attribute__((always_inline)) {
+    auto issue = [=](int f) __attribute__((always_inline)) {
         if (f >= 2 * nm) return;
         const bool fwd = f < nm;
         const int m = fwd ? f : 2 * nm - 1 - f;
@@ -411,7 +426,7 @@ __global__ __launch_bounds__(D * 4) void f32_bwd_span_kernel(
         for (int x = w; x < n; x += NW) copy_one(m, fwd, x, b);
     };
     // this wave's V and W columns of forward chunk m: X[4 g + e][16 w + r]
-    auto load_cols = [&](const float* base, int m) {
+    auto load_cols = [=](const float* base, int m) {
         f32x4_t x = zero;
         if (!base || m >= nm) return x;
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + row0_of(m, 16 * w), bytes_of(m, 16));
@@ -620,6 +635,33 @@ hipError_t set_lds(Kern kern, int bytes) {
     return hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
+// The history pass (K9a) and the sweep (K9b) are independent (both read only the
+// records of K9p), and one workgroup of each fits on a CU (33 + 122 KiB of LDS at
+// D = 128): K9a runs on a side stream of the library's (default priority, one per
+// device, created on first use) between two events, forked from and joined back to the
+// caller's stream, which also keeps the pair capturable in a graph.  The enqueueing is
+// serialised across host threads; without the side stream the two run in order.
+struct Side {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    bool ok = false, tried = false;
+};
+std::mutex g_side_mu;
+Side g_side[64];
+
+Side* side_for_current_device() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    Side& sd = g_side[dev];
+    if (!sd.tried) {
+        sd.tried = true;
+        sd.ok = hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) == hipSuccess &&
+                hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) == hipSuccess &&
+                hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) == hipSuccess;
+    }
+    return sd.ok ? &sd : nullptr;
+}
+
 template <int D>
 hipError_t launch_d(const BwdArgs& a, hipStream_t st) {
     const int n_ch = (a.T + kC16 - 1) / kC16;
@@ -635,16 +677,30 @@ hipError_t launch_d(const BwdArgs& a, hipStream_t st) {
     const float* k = static_cast<const float*>(a.k);
     const float* v = static_cast<const float*>(a.v);
     hipError_t e;
-    if (n_ch > 0 && (e = launch_f32_history(k, v, a.beta, a.s0, a.n_pairs, a.T, a.H, D, t2, rec, s_hist, st)) !=
-                        hipSuccess)
-        return e;
-    const int n_tiles = D / 32, slots = (a.n_pairs + 7) / 8;
     if ((e = set_lds(f32_bwd_sweep_kernel<D>, SwGeo<D>::BYTES)) != hipSuccess) return e;
-    hipLaunchKernelGGL(f32_bwd_sweep_kernel<D>, dim3(static_cast<unsigned>(slots * n_tiles * 8)), dim3(256),
-                       SwGeo<D>::BYTES, st, q, k, a.go, a.gs, a.gv, a.gs0, rec, w_ws, g_hist, a.n_pairs, a.T, a.H,
-                       n_tiles, n_ch, n_span);
-    if ((e = hipGetLastError()) != hipSuccess || n_ch == 0) return e;
     if ((e = set_lds(f32_bwd_span_kernel<D>, SpGeo<D>::BYTES)) != hipSuccess) return e;
+    if (n_ch > 0 && (e = launch_f32_bwd_prep(k, a.beta, a.n_pairs, a.T, a.H, D, t2, rec, st)) != hipSuccess) return e;
+    const int n_tiles = D / 32, slots = (a.n_pairs + 7) / 8;
+    {
+        std::lock_guard<std::mutex> lock(g_side_mu);
+        Side* sd = n_ch > 0 ? side_for_current_device() : nullptr;
+        if (sd) {
+            if ((e = hipEventRecord(sd->fork, st)) != hipSuccess) return e;
+            if ((e = hipStreamWaitEvent(sd->s, sd->fork, 0)) != hipSuccess) return e;
+        }
+        if (n_ch > 0 && (e = launch_f32_history(k, v, a.s0, a.n_pairs, a.T, a.H, D, t2, s_hist, sd ? sd->s : st)) !=
+                            hipSuccess)
+            return e;
+        hipLaunchKernelGGL(f32_bwd_sweep_kernel<D>, dim3(static_cast<unsigned>(slots * n_tiles * 8)), dim3(256),
+                           SwGeo<D>::BYTES, st, q, k, a.go, a.gs, a.gv, a.gs0, rec, w_ws, g_hist, a.n_pairs, a.T, a.H,
+                           n_tiles, n_ch, n_span);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (sd) {
+            if ((e = hipEventRecord(sd->join, sd->s)) != hipSuccess) return e;
+            if ((e = hipStreamWaitEvent(st, sd->join, 0)) != hipSuccess) return e;
+        }
+    }
+    if (n_ch == 0) return hipSuccess;
     hipLaunchKernelGGL(f32_bwd_span_kernel<D>, dim3(static_cast<unsigned>(a.n_pairs * n_span)), dim3(D * 4),
                        SpGeo<D>::BYTES, st, q, k, v, a.go, t2, rec, s_hist, g_hist, w_ws, a.gq, a.gk, a.gbeta, a.T,
                        a.H, n_ch, n_span);

@@ -148,9 +148,12 @@ struct F32BwdWs {
 };
 F32BwdWs f32_bwd_ws(long n_pairs, int T, int D);
 bool f32_bwd_supported(int D, int H);
-// K9p + K9a: the backward's records and the state history (fixed-length batches).
-hipError_t launch_f32_history(const float* k, const float* v, const float* beta, const float* s0, int n_pairs,
-                              int T, int H, int D, float* ws_t2, float* ws_rec, float* s_hist, hipStream_t st);
+// K9p: the backward's records ((T'')^T, and T, K K^T, beta); K9a: the state history
+// (fixed-length batches; reads the (T'')^T that K9p wrote).
+hipError_t launch_f32_bwd_prep(const float* k, const float* beta, int n_pairs, int T, int H, int D, float* ws_t2,
+                               float* ws_rec, hipStream_t st);
+hipError_t launch_f32_history(const float* k, const float* v, const float* s0, int n_pairs, int T, int H, int D,
+                              const float* ws_t2, float* s_hist, hipStream_t st);
 
 // Reverse mode (K5, fp32): fixed-length batch of n_pairs = B*H sequences of
 // T tokens, D <= 256.  workspace holds bwd_workspace_floats(n_pairs, T, D)

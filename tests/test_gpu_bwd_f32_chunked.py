@@ -113,3 +113,40 @@ def test_unsupported_shapes_keep_the_per_token_kernel():
     with pytest.raises(_native.NativeError) as ei:
         _bwd(x, go, gs, path=2)
     assert ei.value.code == _native.E_UNSUPPORTED
+
+
+def test_graph_capture_of_the_forked_launches_replays():
+    """The history pass runs on the library's side stream, forked from and joined back to
+    the caller's stream: captured in a HIP graph, every replay (with eager work and
+    synchronisations between them) gives the eager call's bits."""
+    shape = (2, 300, 2, 64)
+    x, go, gs = _case(shape, 31)
+    b, t, h, d = shape
+    q, k, v, beta, s0, god, gsd = (_dev(a) for a in (x.q, x.k, x.v, x.beta, x.s0, go, gs))
+    outs = [torch.empty_like(q) for _ in range(3)] + [torch.empty_like(beta), torch.empty_like(s0)]
+    L = _native.lib()
+    nb = L.pm_delta_bwd_workspace_bytes(b, t, h, d, _native.DTYPE_F32)
+    ws = torch.empty((nb,), dtype=torch.uint8, device="cuda")
+    ptrs = [z.data_ptr() for z in (q, k, v, beta, s0, god, gsd, *outs)]
+    stream = torch.cuda.Stream()
+
+    def call():
+        _native.check(L.pm_delta_bwd(*ptrs, b, t, h, d, _native.DTYPE_F32, ws.data_ptr(), nb, stream.cuda_stream))
+
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        call()
+    stream.synchronize()
+    eager = [o.clone() for o in outs]
+    _check([_np(o) for o in eager], ref.delta_vjp(x.q, x.k, x.v, x.beta, go, gs, x.s0), "eager")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        call()
+    for _ in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, o, e in zip(NAMES, outs, eager):
+            assert torch.equal(o, e), name

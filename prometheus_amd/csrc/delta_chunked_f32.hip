@@ -44,7 +44,7 @@
 namespace pm {
 namespace {
 
-constexpr int kBwdRec = kF32BwdRec;  // floats per chunk of the backward's record: T, K K^T, beta
+constexpr int kBwdRec = kF32BwdRec;  // floats per chunk of the backward's record: T, K K^T, beta, P
 // workspace floats per chunk: (T'')^T, then (normalised mode) the 16 keys' 1 / max(||k||, 1e-6)
 template <bool NORM>
 constexpr int ws_floats() { return NORM ? 256 + 16 : 256; }
@@ -64,7 +64,8 @@ __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __rest
                                                              const float* __restrict__ beta,
                                                              const int32_t* __restrict__ cu_seqlens,
                                                              int n_seq, int T, int H, int n_slot, long n_items,
-                                                             float* __restrict__ ws, float* __restrict__ ws_b = nullptr) {
+                                                             float* __restrict__ ws, float* __restrict__ ws_b = nullptr,
+                                                             const float* __restrict__ q = nullptr) {
     constexpr int NJ = D / 16;
     const int lane = threadIdx.x & 63;
     const long item = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -164,12 +165,26 @@ __global__ __launch_bounds__(256) void delta_f32_prep_kernel(const float* __rest
     *reinterpret_cast<f32x4_t*>(out + lane * 4) = tw;
     if constexpr (BWD) {
         // the backward's record: T (accumulator registers: T[4 g + v][r]), the Gram matrix
-        // K K^T (symmetric, so its registers are also those of its transpose) and beta
+        // K K^T (symmetric, so its registers are also those of its transpose), beta and P
         const f32x4_t Tacc = mm16(F2t, eye + N8);  // (I+N)(I+N^2)(I+N^4) (I+N^8)
         float* ob = ws_b + (static_cast<size_t>(row) * n_slot + slot) * kBwdRec;
         *reinterpret_cast<f32x4_t*>(ob + lane * 4) = Tacc;
         *reinterpret_cast<f32x4_t*>(ob + 256 + lane * 4) = G;
         if (g == 0) ob[512 + r] = bc;
+        // P = lower_incl(Q K^T): P[4 g + v][r] = q_{4 g + v} . k_r, kept for r <= 4 g + v
+        const __amdgpu_buffer_rsrc_t rq = make_rsrc(q + row0, nb);
+        f32x4_t pa[4] = {zero, zero, zero, zero};
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const unsigned vo = static_cast<unsigned>((r * tstride + 16 * j + 4 * g) * 4);
+            const f32x4_t qf = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rq, vo, 0, 0));
+#pragma unroll
+            for (int v = 0; v < 4; ++v) pa[v] = mfma4(qf[v], kf[j][v], pa[v]);
+        }
+        f32x4_t P = (pa[0] + pa[1]) + (pa[2] + pa[3]);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) P[v] = (r <= 4 * g + v) ? P[v] : 0.f;
+        *reinterpret_cast<f32x4_t*>(ob + 528 + lane * 4) = P;
     }
     if constexpr (NORM) {
         if (g == 0) out[256 + r] = sk;
@@ -547,7 +562,7 @@ hipError_t launch_f32_t(const ChunkedF32Args& a, float* ws, hipStream_t st) {
     const float *q = a.q, *k = a.k, *v = a.v;
     if (n_items > 0) {
         hipLaunchKernelGGL((delta_f32_prep_kernel<D, NORM>), dim3(static_cast<unsigned>((n_items + 3) / 4)), dim3(256), 0,
-                           st, k, a.beta, a.cu_seqlens, a.n_seq, a.T, a.H, n_slot, n_items, ws, nullptr);
+                           st, k, a.beta, a.cu_seqlens, a.n_seq, a.T, a.H, n_slot, n_items, ws, nullptr, nullptr);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -600,18 +615,18 @@ hipError_t launch_hist_t(const float* k, const float* v, const float* s0, int n_
 }
 }  // namespace
 
-hipError_t launch_f32_bwd_prep(const float* k, const float* beta, int n_pairs, int T, int H, int D, float* ws_t2,
-                               float* ws_rec, hipStream_t st) {
+hipError_t launch_f32_bwd_prep(const float* q, const float* k, const float* beta, int n_pairs, int T, int H, int D,
+                               float* ws_t2, float* ws_rec, hipStream_t st) {
     if (n_pairs == 0 || T == 0) return hipSuccess;
     const int n_slot = f32_n_slot(false, T, 0);
     const long n_items = static_cast<long>(n_pairs) * n_slot;
     const dim3 grid(static_cast<unsigned>((n_items + 3) / 4));
     if (D == 128)
         hipLaunchKernelGGL((delta_f32_prep_kernel<128, false, true>), grid, dim3(256), 0, st, k, beta, nullptr,
-                           n_pairs / H, T, H, n_slot, n_items, ws_t2, ws_rec);
+                           n_pairs / H, T, H, n_slot, n_items, ws_t2, ws_rec, q);
     else
         hipLaunchKernelGGL((delta_f32_prep_kernel<64, false, true>), grid, dim3(256), 0, st, k, beta, nullptr,
-                           n_pairs / H, T, H, n_slot, n_items, ws_t2, ws_rec);
+                           n_pairs / H, T, H, n_slot, n_items, ws_t2, ws_rec, q);
     return hipGetLastError();
 }
 

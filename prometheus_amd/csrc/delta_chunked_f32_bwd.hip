@@ -17,7 +17,7 @@
 // Only G travels backwards from chunk to chunk, only S forwards.
 //
 // Launches (on the caller's stream):
-//   K9p + K9a (delta_chunked_f32.hip): (T'')^T, T, K K^T and beta per chunk; the forward
+//   K9p + K9a (delta_chunked_f32.hip): (T'')^T, T, K K^T, beta and P per chunk; the forward
 //     in its history mode, storing S at the start of every span of kF32Span chunks and
 //     at the end of the sequence.
 //   K9b (sweep, one workgroup per (b, h, 32 columns of d_v)): the G recurrence backwards
@@ -56,13 +56,13 @@ struct SwGeo {
     static constexpr int B_Q = B_K + kC16 * D * 4; // Q rows
     static constexpr int B_O = B_Q + kC16 * D * 4; // dO columns of the tile: two [16 t][16] blocks
     static constexpr int B_T = B_O + 2048;         // T, accumulator registers
-    static constexpr int B_B = B_T + 1024;         // beta (64 bytes; the copy fills 1 KiB)
+    static constexpr int B_P = B_T + 1024;         // P, accumulator registers
+    static constexpr int B_B = B_P + 1024;         // beta (64 bytes; the copy fills 1 KiB)
     static constexpr int BUF = B_B + 1024;
-    static constexpr int OFF_P = NB * BUF;                   // 2 slots: P, accumulator registers
-    static constexpr int OFF_H = OFF_P + 2 * 1024;           // 2 slots x 2 chain waves: Q^T dO (NT tiles)
+    static constexpr int OFF_H = NB * BUF;                   // 2 slots x 2 chain waves: Q^T dO (NT tiles)
     static constexpr int OFF_W = OFF_H + 2 * 2 * NT * 1024;  // 2 slots x 2 chain waves: W, -beta W
     static constexpr int BYTES = OFF_W + 2 * 2 * 2048;
-    static constexpr int NCP = 2 * NI + 4;  // the copy wave's copies per chunk
+    static constexpr int NCP = 2 * NI + 5;  // the copy wave's copies per chunk
     static constexpr int NST = 2;           // ... and its stores (W and dV rows)
     static_assert(BYTES <= 160 * 1024 && NCP + NST <= 63, "LDS / vmcnt");
 };
@@ -70,8 +70,8 @@ struct SwGeo {
 // Waves 2 and 3 (chain) carry G for the columns col0 + 16 (w - 2) + [0, 16) as NT
 // accumulator tiles (rows 16 m ..).  Iteration i runs chunk c = n - i on the chain
 // (i >= 1): Y = K G, dU = Y + P^T dO, W = T^T dU, and G += Q^T dO - K^T diag(beta) W,
-// with Q^T dO and P built one iteration earlier by waves 0 and 1 (helper w serves chain
-// wave 2 + w; helper 0 also builds P).  The helpers store the W and dV rows the chain
+// with Q^T dO built one iteration earlier by waves 0 and 1 (helper w serves chain wave
+// 2 + w) and P, T, beta taken from the prep's record.  The helpers store the W and dV rows the chain
 // handed over through LDS one iteration later (iteration n + 1 stores chunk 0's); wave 1
 // copies chunk n - 3 - i (two iterations ahead of its first use).  One LDS-only barrier
 // per iteration 0 .. n.
@@ -108,7 +108,6 @@ __global__ __launch_bounds__(256) void f32_bwd_sweep_kernel(
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
 
     auto buf = [&](int c) { return smem + (c % G::NB) * G::BUF; };
-    auto pslot = [&](int c) { return smem + G::OFF_P + (c & 1) * 1024; };
     auto hslot = [&](int c, int which) { return smem + G::OFF_H + ((c & 1) * 2 + which) * NT * 1024; };
     auto wslot = [&](int c, int which) { return smem + G::OFF_W + ((c & 1) * 2 + which) * 2048; };
     auto col_read = [&](const unsigned char* tileb, int t, int d) {  // X[t][d] of a row tile
@@ -147,6 +146,7 @@ __global__ __launch_bounds__(256) void f32_bwd_sweep_kernel(
         }
         const float* rc = rec + (static_cast<size_t>(pair) * n_ch + c) * kF32BwdRec;
         dma16_asm(make_rsrc(rc, 1024), uniform_ptr(b + G::B_T), static_cast<unsigned>(16 * lane));
+        dma16_asm(make_rsrc(rc + 528, 1024), uniform_ptr(b + G::B_P), static_cast<unsigned>(16 * lane));
         dma16_asm(make_rsrc(rc + 512, 64), uniform_ptr(b + G::B_B), static_cast<unsigned>(16 * lane));
     };
 
@@ -172,41 +172,45 @@ __global__ __launch_bounds__(256) void f32_bwd_sweep_kernel(
                 Gm[m][e] = gs ? gs[sbase + static_cast<size_t>(16 * m + 4 * g + e) * D + ecol] : 0.f;
         // vmcnt(0) as the intrinsic: the gs loads settle here, not inside the loop
         __builtin_amdgcn_s_waitcnt(0x0F70);
+        // Iteration i runs chunk n - i from operands read from its buffer in iteration i - 1
+        // (that buffer has landed by then: the helpers use it in iteration i - 1), so that no
+        // LDS latency starts the chain's chunk; only Q^T dO (built in iteration i - 1) is read
+        // in iteration i.
+        f32x4_t kf[NT], dOc = zero, ta = zero, b4 = zero, pp = zero;
+        float kt[4][NT];
+        auto fetch = [&](int c) __attribute__((always_inline)) {
+            const unsigned char* b = buf(c);
+#pragma unroll
+            for (int m = 0; m < NT; ++m) kf[m] = ld4(b + G::B_K + 16 * f32_chunk<D>(r, 4 * m + g));
+            const float* Of = reinterpret_cast<const float*>(b + G::B_O + 1024 * cw);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dOc[e] = Of[(4 * g + e) * 16 + r];
+            ta = ld4(b + G::B_T + 16 * lane);
+            b4 = ld4(b + G::B_B + 16 * g);
+            pp = ld4(b + G::B_P + 16 * lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int m = 0; m < NT; ++m) kt[e][m] = col_read(b + G::B_K, 4 * g + e, 16 * m + r);
+        };
         for (int i = 0; i <= n_ch; ++i) {
             if (i >= 1) {
                 const int c = n_ch - i;
-                const unsigned char* b = buf(c);
                 if (c == n_ch - 1 || c % kF32Span == kF32Span - 1) {
                     float* hp = g_hist + ((static_cast<size_t>(pair) * n_span + c / kF32Span) * (D / 16) + col0 / 16 +
                                           cw) * NT * 256;
 #pragma unroll
                     for (int m = 0; m < NT; ++m) *reinterpret_cast<f32x4_t*>(hp + m * 256 + 4 * lane) = Gm[m];
                 }
-                f32x4_t kf[NT], dOc;
+                f32x4_t hq[NT];
 #pragma unroll
-                for (int m = 0; m < NT; ++m) kf[m] = ld4(b + G::B_K + 16 * f32_chunk<D>(r, 4 * m + g));
-                const float* Of = reinterpret_cast<const float*>(b + G::B_O + 1024 * cw);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) dOc[e] = Of[(4 * g + e) * 16 + r];
-                const f32x4_t ta = ld4(b + G::B_T + 16 * lane);
-                const f32x4_t b4 = ld4(b + G::B_B + 16 * g);
-                const f32x4_t pp = ld4(pslot(c) + 16 * lane);
-                fence();
+                for (int m = 0; m < NT; ++m) hq[m] = ld4(hslot(c, cw) + 1024 * m + 16 * lane);
                 // Y = K G (accumulator e takes the steps (m, e))
                 f32x4_t ya[4] = {zero, zero, zero, zero};
 #pragma unroll
                 for (int m = 0; m < NT; ++m)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) ya[e] = mfma4(kf[m][e], Gm[m][e], ya[e]);
-                // K^T operands and this chunk's Q^T dO, read while the products run
-                float kt[4][NT];
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-#pragma unroll
-                    for (int m = 0; m < NT; ++m) kt[e][m] = col_read(b + G::B_K, 4 * g + e, 16 * m + r);
-                f32x4_t hq[NT];
-#pragma unroll
-                for (int m = 0; m < NT; ++m) hq[m] = ld4(hslot(c, cw) + 1024 * m + 16 * lane);
                 const f32x4_t dU = mm16(pp, dOc, (ya[0] + ya[1]) + (ya[2] + ya[3]));  // + P^T dO
                 const f32x4_t W = mm16(ta, dU);                                        // T^T dU
                 const f32x4_t nbW = -(W * b4);                                         // -diag(beta) W
@@ -220,6 +224,7 @@ __global__ __launch_bounds__(256) void f32_bwd_sweep_kernel(
 #pragma unroll
                 for (int m = 0; m < NT; ++m) Gm[m] += hq[m];
             }
+            if (n_ch - 1 - i >= 0) fetch(n_ch - 1 - i);
             // (iteration n_ch too: the helpers store its W after one more barrier)
             if (n_ch > 0) lds_barrier();
         }
@@ -253,21 +258,6 @@ __global__ __launch_bounds__(256) void f32_bwd_sweep_kernel(
                 }
 #pragma unroll
                 for (int m = 0; m < NT; ++m) st4(hslot(ch, hw) + 1024 * m + 16 * lane, hq[m]);
-                if (hw == 0) {
-                    // P = lower_incl(Q K^T): lane (g, r) register v holds P[4 g + v][r]
-                    f32x4_t pa[4] = {zero, zero, zero, zero};
-#pragma unroll
-                    for (int m = 0; m < NT; ++m) {
-                        const f32x4_t qf = ld4(b + G::B_Q + 16 * f32_chunk<D>(r, 4 * m + g));
-                        const f32x4_t kf = ld4(b + G::B_K + 16 * f32_chunk<D>(r, 4 * m + g));
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) pa[e] = mfma4(qf[e], kf[e], pa[e]);
-                    }
-                    f32x4_t P = (pa[0] + pa[1]) + (pa[2] + pa[3]);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) P[e] = (r <= 4 * g + e) ? P[e] : 0.f;
-                    st4(pslot(ch) + 16 * lane, P);
-                }
             }
             // the W and dV rows of the chunk the chain ran in the last iteration: lane
             // (t, p) stores columns 4 p .. 4 p + 3 of row t
@@ -679,7 +669,7 @@ hipError_t launch_d(const BwdArgs& a, hipStream_t st) {
     hipError_t e;
     if ((e = set_lds(f32_bwd_sweep_kernel<D>, SwGeo<D>::BYTES)) != hipSuccess) return e;
     if ((e = set_lds(f32_bwd_span_kernel<D>, SpGeo<D>::BYTES)) != hipSuccess) return e;
-    if (n_ch > 0 && (e = launch_f32_bwd_prep(k, a.beta, a.n_pairs, a.T, a.H, D, t2, rec, st)) != hipSuccess) return e;
+    if (n_ch > 0 && (e = launch_f32_bwd_prep(q, k, a.beta, a.n_pairs, a.T, a.H, D, t2, rec, st)) != hipSuccess) return e;
     const int n_tiles = D / 32, slots = (a.n_pairs + 7) / 8;
     {
         std::lock_guard<std::mutex> lock(g_side_mu);

@@ -137,12 +137,12 @@ hipError_t launch_chunked_states(const ChunkedArgs& a, uint16_t* s_hist, hipStre
 // the end of every span of kF32Span chunks (128 tokens).  Workspace regions (bytes, each
 // 16-byte aligned), per (b, h):
 //   t2     (T'')^T per chunk, 256 floats (the fp32 forward's own workspace layout)
-//   rec    T, K K^T and beta per chunk, kF32BwdRec floats
+//   rec    T, K K^T, beta and P = lower_incl(Q K^T) per chunk, kF32BwdRec floats
 //   s_hist S at every span start, g_hist G at every span end: D x D floats per span, as
 //          accumulator registers (column block of 16, tile of 16 rows, lane, register)
 //   w      W = dL/dX per token (B, T, H, D) floats
 constexpr int kF32Span = 8;
-constexpr int kF32BwdRec = 528;
+constexpr int kF32BwdRec = 784;
 struct F32BwdWs {
     size_t t2, rec, s_hist, g_hist, w, bytes;
 };
@@ -150,8 +150,8 @@ F32BwdWs f32_bwd_ws(long n_pairs, int T, int D);
 bool f32_bwd_supported(int D, int H);
 // K9p: the backward's records ((T'')^T, and T, K K^T, beta); K9a: the state history
 // (fixed-length batches; reads the (T'')^T that K9p wrote).
-hipError_t launch_f32_bwd_prep(const float* k, const float* beta, int n_pairs, int T, int H, int D, float* ws_t2,
-                               float* ws_rec, hipStream_t st);
+hipError_t launch_f32_bwd_prep(const float* q, const float* k, const float* beta, int n_pairs, int T, int H, int D,
+                               float* ws_t2, float* ws_rec, hipStream_t st);
 hipError_t launch_f32_history(const float* k, const float* v, const float* s0, int n_pairs, int T, int H, int D,
                               const float* ws_t2, float* s_hist, hipStream_t st);
 

@@ -53,6 +53,18 @@ def fwd_flops(B, T, H, D, chunk=CHUNK) -> float:
     return B * H * (n_full * per(chunk) + (per(rem) if rem else 0.0))
 
 
+def bwd32_flops(B, T, H, D, chunk=16) -> float:
+    """Algorithmic flops of the fp32 chunked backward in 16-token chunks: per (b, h) chunk
+    8 products of D x D size (the forward state K S and K^T U; the gradient sweep K G,
+    Q^T dO and K^T diag(beta) W; dO S^T, U G^T and diag(beta) W S^T over d_v), 2 c D^2 each,
+    and 11 of chunk size (K K^T, T'' X, Q K^T, P^T dO, T^T dU, dO U^T, W U^T, dP K, dP^T Q,
+    dA K, dA^T K), 2 c^2 D each: 16 c D^2 + 22 c^2 D.  What the kernels recompute (the
+    span's forward, S rebuilt backwards, the G recurrence inside each span) is not counted."""
+    n_full, rem = divmod(T, chunk)
+    per = lambda c: 16 * c * D * D + 22 * c * c * D  # noqa: E731
+    return B * H * (n_full * per(chunk) + (per(rem) if rem else 0.0))
+
+
 def fwd_bytes(B, T, H, D, s_in=2, s_out=4, s0=False) -> float:
     """Algorithmic HBM bytes: q, k, v in + beta + O out + S out (+ S0 in)."""
     E = B * T * H * D
@@ -841,7 +853,8 @@ def main():
                          "frac": bb / (bwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
         }
         del ws
-        # the same backward with fp32 q/k/v (the reference's dtype): the per-token kernels
+        # the same backward with fp32 q/k/v (the reference's dtype): the fp32 chunked backward
+        # on fp32 MFMA, and the per-token kernel (path 1) beside it
         q, k, v = (x.float() for x in (q, k, v))
         ws_bytes = lib.pm_delta_bwd_workspace_bytes(B, T, H, D, _native.DTYPE_F32)
         ws = torch.empty(((ws_bytes + 3) // 4,), device=dev)
@@ -861,13 +874,31 @@ def main():
         e1.record(stream)
         torch.cuda.synchronize()
         b32_ms = e0.elapsed_time(e1) / args.bwd_steps
+        f32 = bwd32_flops(B, T, H, D)
         backward["fp32"] = {
-            "workload": "cfg1 backward with fp32 q/k/v (per-token fp32 kernels)",
+            "workload": "cfg1 backward with fp32 q/k/v (fp32 chunked backward on fp32 MFMA)",
             "calls": args.bwd_steps,
             "ms_per_call": b32_ms,
             "tokens_per_s": tokens / (b32_ms * 1e-3),
             "workspace_bytes": ws_bytes,
+            "roofline": {"bound": "mfma", "achieved": f32 / (b32_ms * 1e-3) / 1e12,
+                         "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": f32 / (b32_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+                         "flops": f32},
         }
+        del ws
+        with _native.use_knobs(1, 0):
+            ws_bytes = lib.pm_delta_bwd_workspace_bytes(B, T, H, D, _native.DTYPE_F32)
+            ws = torch.empty(((ws_bytes + 3) // 4,), device=dev)
+            bwd32()
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(max(1, args.bwd_steps // 2)):
+                bwd32()
+            e1.record(stream)
+            torch.cuda.synchronize()
+        backward["fp32"]["per_token_ms_per_call"] = e0.elapsed_time(e1) / max(1, args.bwd_steps // 2)
+        backward["fp32"]["per_token_workspace_bytes"] = ws_bytes
         del go, gs, gq, gk, gv, gb, gs0, ws, q, k, v
 
     if args.calib_copy:

@@ -313,10 +313,11 @@ def chunked_delta_rule_bwd(residual: _DeltaResidual, grads):
     ``:638-653``). Returns ``(gq, gk, gv, gbeta, gstate)``, all fp32, shaped
     like ``q, k, v, beta, state0``: the gradients of the reference's
     ``_delta_vjp_np`` / ``_delta_vjp_jax`` (``:460-588``). Head dimension up
-    to 256. As in the forward, bf16 q/k/v with head dimension 64 or 128 run
-    the chunked backward on bf16 MFMA (bf16 parity); everything else runs the
-    fp32 per-token reverse-mode kernel with state checkpoints (fp32 parity).
-    Neither keeps the reference's per-token state history.
+    to 256. As in the forward, head dimension 64 or 128 runs a chunked
+    backward: on bf16 MFMA for bf16 q/k/v (bf16 parity), on fp32 MFMA for
+    fp32 q/k/v (fp32 parity); everything else runs the fp32 per-token
+    reverse-mode kernel with state checkpoints (fp32 parity). None keeps the
+    reference's per-token state history.
     """
     go, gs = grads
     q, k, v, beta, s0 = residual.q, residual.k, residual.v, residual.beta, residual.state0

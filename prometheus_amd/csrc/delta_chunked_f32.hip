@@ -225,19 +225,20 @@ struct F32Geo {
 // chain waves store the state at the start of every kF32Span-th chunk and at the end
 // instead (n_span = the number of spans + 1 states per pair), as accumulator registers:
 // hist[pair][index][column block 16 jb][tile m][lane][4] holds S[16 m + 4 g + v][16 jb + r]
-// at lane 16 g + r, register v.  The copy wave then copies no Q.
-template <int D, int DV, bool OUT_BF16, bool NORM, bool HIST = false>
-__global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
+// at lane 16 g + r, register v; and every chunk's U as rows (u_out, laid out like v).  The
+// copy wave then copies no Q.
+template <int D, int DV, bool OUT_BF16, bool NORM, bool HIST>
+__device__ __forceinline__ void f32_fwd_body(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ s0, void* __restrict__ o_out, float* __restrict__ s_out,
     const int32_t* __restrict__ cu_seqlens, const float* __restrict__ ws, int n_pairs, int T, int H,
-    int n_tiles, int n_slot, float* __restrict__ hist = nullptr, int n_span = 0) {
+    int n_tiles, int n_slot, float* __restrict__ hist, int n_span, unsigned char* __restrict__ smem, int w,
+    float* __restrict__ u_out = nullptr) {
     using G = F32Geo<D, DV, NORM, HIST>;
     constexpr int NCW = G::NCW, NT = G::NT;
     constexpr int NCP = G::NCP;                          // copies per chunk
     constexpr int NST = HIST ? 0 : G::NST;               // O stores per output wave per chunk
     constexpr int WSF = ws_floats<NORM>();
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
     // XCD-aware placement: the n_tiles workgroups of a pair share bid % 8
     const int bid = blockIdx.x;
@@ -263,7 +264,6 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
     const int ws_slot0 = cu_seqlens ? static_cast<int>(tok0 / kC16) + seq : 0;
 
     const int lane = threadIdx.x & 63;
-    const int w = static_cast<int>(uniform(static_cast<unsigned>(threadIdx.x >> 6)));
     const int r = lane & 15, g = lane >> 4;
     const bool chain = w < NCW;
     const int cw = chain ? w : w - NCW;  // the 16 columns this wave works on
@@ -402,6 +402,18 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
             // U = T'' X (normalised mode: the state update and P U take diag(s) U)
             Up = mm16(tt, X);
             if constexpr (NORM) Up = Up * skc;
+            if constexpr (HIST) {
+                // U's rows for the backward, from U^T = X^T T''^T: lane (g, r) holds
+                // U[r][col0 + 16 cw + 4 g ..] (rows past the end dropped by the range)
+                const f32x4_t Ut = mm16(X, tt);
+                const int clen = min(kC16, len - i * kC16);
+                const size_t rowu = static_cast<size_t>(tok0 + i * kC16) * tstride + static_cast<size_t>(h) * D +
+                                    col0 + 16 * cw;
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(u32x4_t, Ut),
+                    make_rsrc(u_out + rowu, static_cast<unsigned>(((clen - 1) * tstride + 16) * 4)),
+                    static_cast<unsigned>((r * tstride + 4 * g) * 4), 0, 0);
+            }
             // hand S_i and U_i to the output wave
             if constexpr (!HIST) {
                 unsigned char* ss = sslot(i, cw);
@@ -538,6 +550,300 @@ __global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
     }
 }
 
+template <int D, int DV, bool OUT_BF16, bool NORM, bool HIST = false>
+__global__ __launch_bounds__(DV == 32 ? 256 : 128) void delta_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ s0, void* __restrict__ o_out, float* __restrict__ s_out,
+    const int32_t* __restrict__ cu_seqlens, const float* __restrict__ ws, int n_pairs, int T, int H,
+    int n_tiles, int n_slot, float* __restrict__ hist = nullptr, int n_span = 0) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    f32_fwd_body<D, DV, OUT_BF16, NORM, HIST>(q, k, v, s0, o_out, s_out, cu_seqlens, ws, n_pairs, T, H, n_tiles,
+                                              n_slot, hist, n_span, smem,
+                                              static_cast<int>(uniform(static_cast<unsigned>(threadIdx.x >> 6))));
+}
+
+// ---------------------------------------------------------------- K9b: the backward's gradient sweep
+template <int D>
+struct SwGeo {
+    static constexpr int NT = D / 16;              // G accumulator tiles per chain wave
+    static constexpr int NI = kC16 * D * 4 / 1024; // 1 KiB copies per K or Q tile
+    static constexpr int NB = 4;                   // rotating chunk buffers
+    static constexpr int B_K = 0;                  // K rows (f32_chunk)
+    static constexpr int B_Q = B_K + kC16 * D * 4; // Q rows
+    static constexpr int B_O = B_Q + kC16 * D * 4; // dO columns of the tile: two [16 t][16] blocks
+    static constexpr int B_T = B_O + 2048;         // T, accumulator registers
+    static constexpr int B_P = B_T + 1024;         // P, accumulator registers
+    static constexpr int B_B = B_P + 1024;         // beta (64 bytes; the copy fills 1 KiB)
+    static constexpr int BUF = B_B + 1024;
+    static constexpr int OFF_H = NB * BUF;                   // 2 slots x 2 chain waves: Q^T dO (NT tiles)
+    static constexpr int OFF_W = OFF_H + 2 * 2 * NT * 1024;  // 2 slots x 2 chain waves: W, -beta W
+    static constexpr int BYTES = OFF_W + 2 * 2 * 2048;
+    static constexpr int NCP = 2 * NI + 5;  // the copy wave's copies per chunk
+    static constexpr int NST = 2;           // ... and its stores (W and dV rows)
+    static_assert(BYTES <= 160 * 1024 && NCP + NST <= 63, "LDS / vmcnt");
+};
+
+// Waves 2 and 3 (chain) carry G for the columns col0 + 16 (w - 2) + [0, 16) as NT
+// accumulator tiles (rows 16 m ..).  Iteration i runs chunk c = n - i on the chain
+// (i >= 1): Y = K G, dU = Y + P^T dO, W = T^T dU, and G += Q^T dO - K^T diag(beta) W,
+// with Q^T dO built one iteration earlier by waves 0 and 1 (helper w serves chain wave
+// 2 + w) and P, T, beta taken from the prep's record.  The helpers store the W and dV rows the chain
+// handed over through LDS one iteration later (iteration n + 1 stores chunk 0's); wave 1
+// copies chunk n - 3 - i (two iterations ahead of its first use).  One LDS-only barrier
+// per iteration 0 .. n.
+template <int D>
+__device__ __forceinline__ void f32_sweep_body(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ go,
+    const float* __restrict__ gs, float* __restrict__ gv, float* __restrict__ gs0, const float* __restrict__ rec,
+    float* __restrict__ w_out, float* __restrict__ g_hist, int n_pairs, int T, int H, int n_tiles, int n_ch,
+    int n_span, unsigned char* __restrict__ smem, int w) {
+    using G = SwGeo<D>;
+    constexpr int NT = G::NT;
+    auto ld4 = [](const unsigned char* p) { return *reinterpret_cast<const f32x4_t*>(p); };
+    auto st4 = [](unsigned char* p, f32x4_t x) { *reinterpret_cast<f32x4_t*>(p) = x; };
+
+    // XCD-aware placement: the n_tiles workgroups of a pair share bid % 8
+    const int bid = blockIdx.x;
+    const int xcd = bid & 7, bslot = bid >> 3;
+    const int tile = bslot % n_tiles;
+    const int pair = (bslot / n_tiles) * 8 + xcd;
+    if (pair >= n_pairs) return;
+    const int seq = pair / H, h = pair % H;
+    const long tok0 = static_cast<long>(seq) * T;
+    const int col0 = tile * 32;
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15, g = lane >> 4;
+    // roles: waves 2 and 3 chain, 0 and 1 helpers (wave 1 copies), so that beside a
+    // workgroup of the history pass (chain waves 0 and 1) the four chains of a CU spread
+    // over its four SIMDs (waves of a workgroup go to the SIMDs in turn)
+    const bool chain_wave = w >= 2;
+    const int cw = w & 1;  // the 16 columns col0 + 16 cw + [0, 16) this wave works on
+    const bool copy_wave = w == 1;
+    const size_t tstride = static_cast<size_t>(H) * D;
+    const size_t sbase = static_cast<size_t>(pair) * D * D;
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+
+    auto buf = [&](int c) { return smem + (c % G::NB) * G::BUF; };
+    auto hslot = [&](int c, int which) { return smem + G::OFF_H + ((c & 1) * 2 + which) * NT * 1024; };
+    auto wslot = [&](int c, int which) { return smem + G::OFF_W + ((c & 1) * 2 + which) * 2048; };
+    auto col_read = [&](const unsigned char* tileb, int t, int d) {  // X[t][d] of a row tile
+        return reinterpret_cast<const float*>(tileb)[4 * f32_chunk<D>(t, d >> 2) + (d & 3)];
+    };
+
+    // ---- HBM -> LDS copies of chunk c ----
+    auto row0_of = [&](int c, int col) {
+        return static_cast<size_t>(tok0 + c * kC16) * tstride + static_cast<size_t>(h) * D + col;
+    };
+    auto bytes_of = [&](int c, int row_floats) {
+        const int clen = min(kC16, T - c * kC16);
+        return static_cast<unsigned>(((clen - 1) * tstride + row_floats) * 4);
+    };
+    auto copy_tile = [&](const float* base, int c, unsigned char* dst) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + row0_of(c, 0), bytes_of(c, D));
+        unsigned char* d0 = uniform_ptr(dst);
+#pragma unroll
+        for (int i = 0; i < G::NI; ++i) {
+            const int qc = 64 * i + lane;
+            const int t = qc / (D / 4), p = (qc % (D / 4)) ^ t;
+            dma16_asm(rs, d0 + 1024 * i, static_cast<unsigned>(t * tstride * 4 + 16 * p));
+        }
+    };
+    auto copies = [&](int c) __attribute__((always_inline)) {
+        unsigned char* b = buf(c);
+        copy_tile(k, c, b + G::B_K);
+        copy_tile(q, c, b + G::B_Q);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            // a null dO reads zeros (a zero-length range)
+            const __amdgpu_buffer_rsrc_t rs =
+                make_rsrc(go ? go + row0_of(c, col0 + 16 * j) : go, go ? bytes_of(c, 16) : 0u);
+            const int t = lane >> 2, p = lane & 3;
+            dma16_asm(rs, uniform_ptr(b + G::B_O + 1024 * j), static_cast<unsigned>(t * tstride * 4 + 16 * p));
+        }
+        const float* rc = rec + (static_cast<size_t>(pair) * n_ch + c) * kF32BwdRec;
+        dma16_asm(make_rsrc(rc, 1024), uniform_ptr(b + G::B_T), static_cast<unsigned>(16 * lane));
+        dma16_asm(make_rsrc(rc + 528, 1024), uniform_ptr(b + G::B_P), static_cast<unsigned>(16 * lane));
+        dma16_asm(make_rsrc(rc + 512, 64), uniform_ptr(b + G::B_B), static_cast<unsigned>(16 * lane));
+    };
+
+    if (n_ch > 0 && copy_wave) {
+        copies(n_ch - 1);
+        if (n_ch > 1) {
+            copies(n_ch - 2);
+            wait_vm_n<G::NCP>();
+        } else {
+            wait_vm_n<0>();
+        }
+    }
+    if (n_ch > 0) lds_barrier();  // B0
+
+    if (chain_wave) {
+        // ============ chain wave ============
+        const int ecol = col0 + 16 * cw + r;
+        f32x4_t Gm[NT];
+#pragma unroll
+        for (int m = 0; m < NT; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                Gm[m][e] = gs ? gs[sbase + static_cast<size_t>(16 * m + 4 * g + e) * D + ecol] : 0.f;
+        // vmcnt(0) as the intrinsic: the gs loads settle here, not inside the loop
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        // Iteration i runs chunk n - i from operands read from its buffer in iteration i - 1
+        // (that buffer has landed by then: the helpers use it in iteration i - 1), so that no
+        // LDS latency starts the chain's chunk; only Q^T dO (built in iteration i - 1) is read
+        // in iteration i.
+        f32x4_t kf[NT], dOc = zero, ta = zero, b4 = zero, pp = zero;
+        float kt[4][NT];
+        auto fetch = [&](int c) __attribute__((always_inline)) {
+            const unsigned char* b = buf(c);
+#pragma unroll
+            for (int m = 0; m < NT; ++m) kf[m] = ld4(b + G::B_K + 16 * f32_chunk<D>(r, 4 * m + g));
+            const float* Of = reinterpret_cast<const float*>(b + G::B_O + 1024 * cw);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dOc[e] = Of[(4 * g + e) * 16 + r];
+            ta = ld4(b + G::B_T + 16 * lane);
+            b4 = ld4(b + G::B_B + 16 * g);
+            pp = ld4(b + G::B_P + 16 * lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int m = 0; m < NT; ++m) kt[e][m] = col_read(b + G::B_K, 4 * g + e, 16 * m + r);
+        };
+        for (int i = 0; i <= n_ch; ++i) {
+            if (i >= 1) {
+                const int c = n_ch - i;
+                if (c == n_ch - 1 || c % kF32Span == kF32Span - 1) {
+                    float* hp = g_hist + ((static_cast<size_t>(pair) * n_span + c / kF32Span) * (D / 16) + col0 / 16 +
+                                          cw) * NT * 256;
+#pragma unroll
+                    for (int m = 0; m < NT; ++m) *reinterpret_cast<f32x4_t*>(hp + m * 256 + 4 * lane) = Gm[m];
+                }
+                f32x4_t hq[NT];
+#pragma unroll
+                for (int m = 0; m < NT; ++m) hq[m] = ld4(hslot(c, cw) + 1024 * m + 16 * lane);
+                // Y = K G (accumulator e takes the steps (m, e))
+                f32x4_t ya[4] = {zero, zero, zero, zero};
+#pragma unroll
+                for (int m = 0; m < NT; ++m)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ya[e] = mfma4(kf[m][e], Gm[m][e], ya[e]);
+                const f32x4_t dU = mm16(pp, dOc, (ya[0] + ya[1]) + (ya[2] + ya[3]));  // + P^T dO
+                const f32x4_t W = mm16(ta, dU);                                        // T^T dU
+                const f32x4_t nbW = -(W * b4);                                         // -diag(beta) W
+                st4(wslot(c, cw) + 16 * lane, W);
+                st4(wslot(c, cw) + 1024 + 16 * lane, nbW);
+                // G += Q^T dO - K^T diag(beta) W
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int m = 0; m < NT; ++m) Gm[m] = mfma4(kt[e][m], nbW[e], Gm[m]);
+#pragma unroll
+                for (int m = 0; m < NT; ++m) Gm[m] += hq[m];
+            }
+            if (n_ch - 1 - i >= 0) fetch(n_ch - 1 - i);
+            // (iteration n_ch too: the helpers store its W after one more barrier)
+            if (n_ch > 0) lds_barrier();
+        }
+#pragma unroll
+        for (int m = 0; m < NT; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) gs0[sbase + static_cast<size_t>(16 * m + 4 * g + e) * D + ecol] = Gm[m][e];
+    } else if (n_ch > 0) {
+        // ============ helper waves ============
+        const int hw = w;
+        for (int i = 0; i <= n_ch + 1; ++i) {
+            const bool cp = copy_wave && n_ch - 3 - i >= 0;
+            if (cp) copies(n_ch - 3 - i);
+            const int ch = n_ch - 1 - i;
+            if (ch >= 0) {
+                const unsigned char* b = buf(ch);
+                const float* Of = reinterpret_cast<const float*>(b + G::B_O + 1024 * hw);
+                f32x4_t dOc;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dOc[e] = Of[(4 * g + e) * 16 + r];
+                // Q^T dO for chain wave hw's columns: tile m = rows 16 m .. of d
+                f32x4_t hq[NT];
+#pragma unroll
+                for (int m = 0; m < NT; ++m) {
+                    float qt[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) qt[e] = col_read(b + G::B_Q, 4 * g + e, 16 * m + r);
+                    hq[m] = zero;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) hq[m] = mfma4(qt[e], dOc[e], hq[m]);
+                }
+#pragma unroll
+                for (int m = 0; m < NT; ++m) st4(hslot(ch, hw) + 1024 * m + 16 * lane, hq[m]);
+            }
+            // the W and dV rows of the chunk the chain ran in the last iteration: lane
+            // (t, p) stores columns 4 p .. 4 p + 3 of row t
+            const int cs = n_ch - i + 1;
+            const bool st = i >= 2;
+            if (st) {
+                const float* wsrc = reinterpret_cast<const float*>(wslot(cs, hw));
+                const int t = lane >> 2, p = lane & 3;
+                f32x4_t wv, dv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int ln = 16 * (t >> 2) + 4 * p + e;
+                    wv[e] = wsrc[4 * ln + (t & 3)];
+                    dv[e] = -wsrc[256 + 4 * ln + (t & 3)];
+                }
+                const size_t row0 = row0_of(cs, col0 + 16 * hw);
+                const unsigned nb = bytes_of(cs, 16);
+                const unsigned off = static_cast<unsigned>((t * tstride + 4 * p) * 4);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, wv), make_rsrc(w_out + row0, nb),
+                                                       off, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, dv), make_rsrc(gv + row0, nb),
+                                                       off, 0, 0);
+            }
+            if (i <= n_ch) {
+                // the copies of chunk ch - 1 (the helpers' next) have landed; the newer copies
+                // and this iteration's stores may still be in flight
+                if (copy_wave && ch - 1 >= 0) {
+                    if (cp && st) wait_vm_n<G::NCP + G::NST>();
+                    else if (cp) wait_vm_n<G::NCP>();
+                    else if (st) wait_vm_n<G::NST>();
+                    else wait_vm_n<0>();
+                }
+                lds_barrier();
+            }
+        }
+    }
+}
+
+
+// K9a + K9b in one workgroup of eight waves per (b, h, 32 columns of d_v): waves 0-3 run
+// the forward in its history mode, waves 4-7 the gradient sweep, two independent
+// recurrences over the same chunks in opposite directions.  Waves w and w + 4 share a
+// SIMD, so the four chain waves (0, 1, 6, 7) take the four SIMDs.  The two halves share
+// the workgroup's barriers: the sweep passes one more (n + 2 against n + 1), which the
+// history half adds at its end.  LDS: the history half's 33 KiB, then the sweep's.
+template <int D>
+__global__ __launch_bounds__(512) void f32_hist_sweep_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ s0, const float* __restrict__ go, const float* __restrict__ gs, float* __restrict__ gv,
+    float* __restrict__ gs0, const float* __restrict__ t2, const float* __restrict__ rec, float* __restrict__ w_out,
+    float* __restrict__ s_hist, float* __restrict__ g_hist, float* __restrict__ u_out, int n_pairs, int T, int H,
+    int n_ch, int n_span) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    using GH = F32Geo<D, 32, false, true>;
+    constexpr int OFF2 = (GH::BYTES + 255) & ~255;
+    constexpr int n_tiles = D / 32;
+    const int w8 = static_cast<int>(uniform(static_cast<unsigned>(threadIdx.x >> 6)));
+    if (w8 < 4) {
+        f32_fwd_body<D, 32, false, false, true>(nullptr, k, v, s0, nullptr, nullptr, nullptr, t2, n_pairs, T, H,
+                                                n_tiles, n_ch, s_hist, n_span + 1, smem, w8, u_out);
+        const int bslot = static_cast<int>(blockIdx.x) >> 3;
+        const int pair = (bslot / n_tiles) * 8 + (static_cast<int>(blockIdx.x) & 7);
+        if (pair < n_pairs && n_ch > 0) lds_barrier();
+    } else {
+        f32_sweep_body<D>(q, k, go, gs, gv, gs0, rec, w_out, g_hist, n_pairs, T, H, n_tiles, n_ch, n_span,
+                          smem + OFF2, w8 - 4);
+    }
+}
+
+
 // The dynamic-LDS limit is a per-device function attribute, set once per device for each
 // kernel (KERN: one static flag array per kernel, not per signature).
 template <auto KERN>
@@ -598,23 +904,6 @@ int chunked_f32_pick_tile(int D, long n_pairs, int requested) {
     return n_pairs * (D / 32) >= 256 ? 32 : 16;
 }
 
-namespace {
-template <int D, int DV>
-hipError_t launch_hist_t(const float* k, const float* v, const float* s0, int n_pairs, int T, int H,
-                         const float* ws_t2, float* s_hist, hipStream_t st) {
-    using G = F32Geo<D, DV, false, true>;
-    const int n_slot = f32_n_slot(false, T, 0);
-    hipError_t e = set_lds_f32<delta_f32_kernel<D, DV, false, false, true>>(G::BYTES);
-    if (e != hipSuccess) return e;
-    const int n_tiles = D / DV, slots = (n_pairs + 7) / 8;
-    const int n_state = (n_slot + kF32Span - 1) / kF32Span + 1;  // every span's start, and the end
-    hipLaunchKernelGGL((delta_f32_kernel<D, DV, false, false, true>), dim3(static_cast<unsigned>(slots * n_tiles * 8)),
-                       dim3(128 * G::NCW), G::BYTES, st, nullptr, k, v, s0, nullptr, nullptr, nullptr, ws_t2, n_pairs,
-                       T, H, n_tiles, n_slot, s_hist, n_state);
-    return hipGetLastError();
-}
-}  // namespace
-
 hipError_t launch_f32_bwd_prep(const float* q, const float* k, const float* beta, int n_pairs, int T, int H, int D,
                                float* ws_t2, float* ws_rec, hipStream_t st) {
     if (n_pairs == 0 || T == 0) return hipSuccess;
@@ -630,15 +919,31 @@ hipError_t launch_f32_bwd_prep(const float* q, const float* k, const float* beta
     return hipGetLastError();
 }
 
-hipError_t launch_f32_history(const float* k, const float* v, const float* s0, int n_pairs, int T, int H, int D,
-                              const float* ws_t2, float* s_hist, hipStream_t st) {
-    if (n_pairs == 0 || T == 0) return hipSuccess;
-    const int dv = chunked_f32_pick_tile(D, n_pairs, 0);
-    if (D == 128)
-        return dv == 16 ? launch_hist_t<128, 16>(k, v, s0, n_pairs, T, H, ws_t2, s_hist, st)
-                        : launch_hist_t<128, 32>(k, v, s0, n_pairs, T, H, ws_t2, s_hist, st);
-    return dv == 16 ? launch_hist_t<64, 16>(k, v, s0, n_pairs, T, H, ws_t2, s_hist, st)
-                    : launch_hist_t<64, 32>(k, v, s0, n_pairs, T, H, ws_t2, s_hist, st);
+namespace {
+template <int D>
+hipError_t launch_hist_sweep_t(const BwdArgs& a, const float* t2, const float* rec, float* w_out, float* s_hist,
+                               float* g_hist, float* u_out, hipStream_t st) {
+    constexpr int OFF2 = (F32Geo<D, 32, false, true>::BYTES + 255) & ~255;
+    constexpr int BYTES = OFF2 + SwGeo<D>::BYTES;
+    static_assert(BYTES <= 160 * 1024, "LDS");
+    hipError_t e = set_lds_f32<f32_hist_sweep_kernel<D>>(BYTES);
+    if (e != hipSuccess) return e;
+    const int n_ch = (a.T + kC16 - 1) / kC16;
+    const int n_span = (n_ch + kF32Span - 1) / kF32Span;
+    const int slots = (a.n_pairs + 7) / 8;
+    hipLaunchKernelGGL(f32_hist_sweep_kernel<D>, dim3(static_cast<unsigned>(slots * (D / 32) * 8)), dim3(512), BYTES,
+                       st, static_cast<const float*>(a.q), static_cast<const float*>(a.k),
+                       static_cast<const float*>(a.v), a.s0, a.go, a.gs, a.gv, a.gs0, t2, rec, w_out, s_hist, g_hist,
+                       u_out, a.n_pairs, a.T, a.H, n_ch, n_span);
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_f32_hist_sweep(const BwdArgs& a, const float* t2, const float* rec, float* w_out, float* s_hist,
+                                 float* g_hist, float* u_out, hipStream_t st) {
+    if (a.n_pairs == 0) return hipSuccess;
+    return a.D == 128 ? launch_hist_sweep_t<128>(a, t2, rec, w_out, s_hist, g_hist, u_out, st)
+                      : launch_hist_sweep_t<64>(a, t2, rec, w_out, s_hist, g_hist, u_out, st);
 }
 
 hipError_t launch_chunked_f32(const ChunkedF32Args& a, void* ws, hipStream_t st) {

@@ -134,26 +134,24 @@ hipError_t launch_chunked_states(const ChunkedArgs& a, uint16_t* s_hist, hipStre
 
 // The fp32 chunked backward (K9; fixed-length batches, fp32 q/k/v, D in {64, 128}).
 // Chunks of kC16 = 16 tokens; the state S and its gradient G are kept at the start and
-// the end of every span of kF32Span chunks (128 tokens).  Workspace regions (bytes, each
-// 16-byte aligned), per (b, h):
+// the end of every span of kF32Span chunks (256 tokens).  Workspace regions (bytes, each
+// 256-byte aligned), per (b, h):
 //   t2     (T'')^T per chunk, 256 floats (the fp32 forward's own workspace layout)
 //   rec    T, K K^T, beta and P = lower_incl(Q K^T) per chunk, kF32BwdRec floats
-//   s_hist S at every span start, g_hist G at every span end: D x D floats per span, as
-//          accumulator registers (column block of 16, tile of 16 rows, lane, register)
-//   w      W = dL/dX per token (B, T, H, D) floats
-constexpr int kF32Span = 8;
+//   s_hist S at every span start and at the end, g_hist G at every span end: D x D floats
+//          each, as accumulator registers (column block of 16, tile of 16 rows, lane,
+//          register)
+//   w, u   W = dL/dX and U per token, (B, T, H, D) floats each
+constexpr int kF32Span = 16;
 constexpr int kF32BwdRec = 784;
 struct F32BwdWs {
-    size_t t2, rec, s_hist, g_hist, w, bytes;
+    size_t t2, rec, s_hist, g_hist, w, u, bytes;
 };
 F32BwdWs f32_bwd_ws(long n_pairs, int T, int D);
 bool f32_bwd_supported(int D, int H);
-// K9p: the backward's records ((T'')^T, and T, K K^T, beta); K9a: the state history
-// (fixed-length batches; reads the (T'')^T that K9p wrote).
+// K9p: the backward's records ((T'')^T, and T, K K^T, beta, P; fixed-length batches).
 hipError_t launch_f32_bwd_prep(const float* q, const float* k, const float* beta, int n_pairs, int T, int H, int D,
                                float* ws_t2, float* ws_rec, hipStream_t st);
-hipError_t launch_f32_history(const float* k, const float* v, const float* s0, int n_pairs, int T, int H, int D,
-                              const float* ws_t2, float* s_hist, hipStream_t st);
 
 // Reverse mode (K5, fp32): fixed-length batch of n_pairs = B*H sequences of
 // T tokens, D <= 256.  workspace holds bwd_workspace_floats(n_pairs, T, D)
@@ -201,6 +199,10 @@ ChunkedBwdWs chunked_bwd_ws(long n_pairs, int T, int D);
 bool chunked_bwd_supported(int D, int H);  // chunked_supported and H*D <= 2^23 (fp32 dO rows)
 hipError_t launch_bwd_chunked(const BwdArgs& a, hipStream_t st);
 // K9 (the fp32 chunked backward): a.workspace holds f32_bwd_ws(...).bytes bytes.
+// K9a + K9b in one launch: the state history (s_hist, U into u_out) and the gradient sweep
+// (gv, gs0, W into w_out, g_hist), from K9p's records.
+hipError_t launch_f32_hist_sweep(const BwdArgs& a, const float* t2, const float* rec, float* w_out, float* s_hist,
+                                 float* g_hist, float* u_out, hipStream_t st);
 hipError_t launch_bwd_chunked_f32(const BwdArgs& a, hipStream_t st);
 
 // Zero fill (used instead of hipMemsetAsync so callers may graph-capture).

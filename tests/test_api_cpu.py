@@ -117,16 +117,17 @@ def _chunked_ws(b, t, h, d):
 
 
 def _f32_chunked_ws(b, t, h, d):
-    # (T'')^T and the T / K K^T / beta / P record per 16-token chunk, S at every 128-token span
-    # start and at the end, G at every span end, W per token; each region 256-byte aligned
+    # (T'')^T and the T / K K^T / beta / P record per 16-token chunk, S at every 256-token span
+    # start and at the end, G at every span end, W and U per token; each region 256-byte aligned
     n_ch = -(-t // 16)
-    n_span = -(-n_ch // 8)
+    n_span = -(-n_ch // 16)
     n = b * h
     al = lambda x: -(-x // 256) * 256
     size = al(n * n_ch * 256 * 4)
     size = al(size + n * n_ch * 784 * 4)
     size = al(size + n * (n_span + 1) * d * d * 4)
     size = al(size + n * n_span * d * d * 4)
+    size = al(size + n * t * d * 4)
     return al(size + n * t * d * 4)
 
 

@@ -32,12 +32,9 @@
  *
  * All launches are asynchronous on `stream` (a hipStream_t; NULL is the
  * default stream).  The library never synchronises the host and allocates
- * no device memory (pm_delta_bwd_noalloc's scratch is a static array).  The
- * fp32 chunked backward runs one of its launches on a side stream the library
- * creates per device on first use (default priority), forked from `stream`
- * and joined back to it by two events, so the call stays ordered on `stream`
- * and capturable in a graph.  Inputs and outputs must not alias, except that
- * pm_delta_step updates s_inout in place by design.
+ * no device memory (pm_delta_bwd_noalloc's scratch is a static array).
+ * Inputs and outputs must not alias, except that pm_delta_step updates
+ * s_inout in place by design.
  */
 #ifndef PM_DELTA_H
 #define PM_DELTA_H
@@ -285,9 +282,10 @@ size_t pm_delta_varlen_workspace_bytes(int n_seqs, int total_T, int H, int D, in
  *     (16-token chunks; fp32 parity).  q, k, v, go, gq, gk, gv and workspace
  *     16-byte aligned.  Workspace (fp32, each region rounded up to 256
  *     bytes), per (b, h): 256 + 784 values per 16-token chunk (the chunk's
- *     T and P factors), D * D values per 128-token span and one more (the
+ *     T and P factors), D * D values per 256-token span and one more (the
  *     state at every span start and at the end), D * D per span (the state
- *     gradient at every span end) and T * D (W); 475 MB at B4 T4096 H16 D128.
+ *     gradient at every span end) and 2 * T * D (W and U); 475 MB at B4
+ *     T4096 H16 D128.
  *   - otherwise the per-token fp32 backward (fp32 parity).  Workspace:
  *     per-token u = v - S^T k and the state every 8 tokens, 4 * B * H *
  *     (T * D + ceil(T / 8) * D * D) bytes, and for D > 32 the partial sums

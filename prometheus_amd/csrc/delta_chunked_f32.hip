@@ -227,13 +227,19 @@ struct F32Geo {
 // hist[pair][index][column block 16 jb][tile m][lane][4] holds S[16 m + 4 g + v][16 jb + r]
 // at lane 16 g + r, register v; and every chunk's U as rows (u_out, laid out like v).  The
 // copy wave then copies no Q.
-template <int D, int DV, bool OUT_BF16, bool NORM, bool HIST>
+// Work a caller adds to the history mode's non-chain waves, once per chunk i (before
+// the chunk's barrier): none by default.
+struct NoExtra {
+    __device__ void operator()(int, int) const {}
+};
+
+template <int D, int DV, bool OUT_BF16, bool NORM, bool HIST, typename Extra = NoExtra>
 __device__ __forceinline__ void f32_fwd_body(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ s0, void* __restrict__ o_out, float* __restrict__ s_out,
     const int32_t* __restrict__ cu_seqlens, const float* __restrict__ ws, int n_pairs, int T, int H,
     int n_tiles, int n_slot, float* __restrict__ hist, int n_span, unsigned char* __restrict__ smem, int w,
-    float* __restrict__ u_out = nullptr) {
+    float* __restrict__ u_out = nullptr, Extra extra = Extra{}) {
     using G = F32Geo<D, DV, NORM, HIST>;
     constexpr int NCW = G::NCW, NT = G::NT;
     constexpr int NCP = G::NCP;                          // copies per chunk
@@ -450,6 +456,7 @@ __device__ __forceinline__ void f32_fwd_body(
         // the copy wave keeps two chunks ahead; the other output waves only keep the barriers
         for (int i = 0; i < n_chunks; ++i) {
             if (copy_wave && i + 2 < n_chunks) copies(i + 2);
+            extra(i, w);
             if (copy_wave && i + 1 < n_chunks) wait_next(false, i + 2 < n_chunks);
             lds_barrier();
         }
@@ -591,7 +598,38 @@ struct SwGeo {
 // handed over through LDS one iteration later (iteration n + 1 stores chunk 0's); wave 1
 // copies chunk n - 3 - i (two iterations ahead of its first use).  One LDS-only barrier
 // per iteration 0 .. n.
+// Q^T dO of chunk ch for chain wave c's 16 columns, tiles m0 .. m1 - 1 (rows 16 m .. of d),
+// from the chunk's buffer into its slot (sw: the sweep's LDS).
 template <int D>
+__device__ __forceinline__ void sweep_qtdo(unsigned char* sw, int ch, int c, int m0, int m1) {
+    using G = SwGeo<D>;
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const unsigned char* b = sw + (ch % G::NB) * G::BUF;
+    const float* Of = reinterpret_cast<const float*>(b + G::B_O + 1024 * c);
+    const float* Qf = reinterpret_cast<const float*>(b + G::B_Q);
+    f32x4_t dOc;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dOc[e] = Of[(4 * g + e) * 16 + r];
+    unsigned char* slot = sw + G::OFF_H + ((ch & 1) * 2 + c) * G::NT * 1024;
+#pragma unroll
+    for (int m = 0; m < G::NT; ++m) {
+        if (m < m0 || m >= m1) continue;
+        float qt[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = 4 * g + e, d = 16 * m + r;
+            qt[e] = Qf[4 * f32_chunk<D>(t, d >> 2) + (d & 3)];
+        }
+        f32x4_t hq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hq = mfma4(qt[e], dOc[e], hq);
+        *reinterpret_cast<f32x4_t*>(slot + 1024 * m + 16 * lane) = hq;
+    }
+}
+
+// SPLIT: the helper forms the first half of its chain's Q^T dO tiles (the caller's other
+// waves form the second half in the same iteration).
+template <int D, bool SPLIT = false>
 __device__ __forceinline__ void f32_sweep_body(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ go,
     const float* __restrict__ gs, float* __restrict__ gv, float* __restrict__ gs0, const float* __restrict__ rec,
@@ -755,26 +793,8 @@ __device__ __forceinline__ void f32_sweep_body(
             const bool cp = copy_wave && n_ch - 3 - i >= 0;
             if (cp) copies(n_ch - 3 - i);
             const int ch = n_ch - 1 - i;
-            if (ch >= 0) {
-                const unsigned char* b = buf(ch);
-                const float* Of = reinterpret_cast<const float*>(b + G::B_O + 1024 * hw);
-                f32x4_t dOc;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) dOc[e] = Of[(4 * g + e) * 16 + r];
-                // Q^T dO for chain wave hw's columns: tile m = rows 16 m .. of d
-                f32x4_t hq[NT];
-#pragma unroll
-                for (int m = 0; m < NT; ++m) {
-                    float qt[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) qt[e] = col_read(b + G::B_Q, 4 * g + e, 16 * m + r);
-                    hq[m] = zero;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) hq[m] = mfma4(qt[e], dOc[e], hq[m]);
-                }
-#pragma unroll
-                for (int m = 0; m < NT; ++m) st4(hslot(ch, hw) + 1024 * m + 16 * lane, hq[m]);
-            }
+            // Q^T dO for chain wave hw's columns: tile m = rows 16 m .. of d
+            if (ch >= 0) sweep_qtdo<D>(smem, ch, hw, 0, SPLIT ? NT / 2 : NT);
             // the W and dV rows of the chunk the chain ran in the last iteration: lane
             // (t, p) stores columns 4 p .. 4 p + 3 of row t
             const int cs = n_ch - i + 1;
@@ -832,14 +852,22 @@ __global__ __launch_bounds__(512) void f32_hist_sweep_kernel(
     constexpr int n_tiles = D / 32;
     const int w8 = static_cast<int>(uniform(static_cast<unsigned>(threadIdx.x >> 6)));
     if (w8 < 4) {
+        // the history half's two non-chain waves (2, 3: SIMDs 2, 3, beside the sweep's chains
+        // on waves 6, 7) form the second half of each sweep chain's Q^T dO, the sweep's
+        // helpers (4, 5: SIMDs 0, 1, beside the history's chains) the first
+        unsigned char* sw = smem + OFF2;
+        auto extra = [=](int i, int wl) {
+            const int ch = n_ch - 1 - i;
+            if (wl >= 2 && ch >= 0) sweep_qtdo<D>(sw, ch, wl - 2, SwGeo<D>::NT / 2, SwGeo<D>::NT);
+        };
         f32_fwd_body<D, 32, false, false, true>(nullptr, k, v, s0, nullptr, nullptr, nullptr, t2, n_pairs, T, H,
-                                                n_tiles, n_ch, s_hist, n_span + 1, smem, w8, u_out);
+                                                n_tiles, n_ch, s_hist, n_span + 1, smem, w8, u_out, extra);
         const int bslot = static_cast<int>(blockIdx.x) >> 3;
         const int pair = (bslot / n_tiles) * 8 + (static_cast<int>(blockIdx.x) & 7);
         if (pair < n_pairs && n_ch > 0) lds_barrier();
     } else {
-        f32_sweep_body<D>(q, k, go, gs, gv, gs0, rec, w_out, g_hist, n_pairs, T, H, n_tiles, n_ch, n_span,
-                          smem + OFF2, w8 - 4);
+        f32_sweep_body<D, true>(q, k, go, gs, gv, gs0, rec, w_out, g_hist, n_pairs, T, H, n_tiles, n_ch, n_span,
+                                smem + OFF2, w8 - 4);
     }
 }
 

@@ -354,18 +354,20 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const uint16_t* __restric
                 v = frag(arr == 0 ? KAs : QAs, 16 * m + l16, kb, kCvH + m);
             } else {
                 // lane (g, l16): K-[K0 + 4g + i][d] (slots 0-3) and K-[K0 + 16 + 4g + i][d]
-                // (slots 4-7), d = s_row_d(md, l16); K- = k r cB(block)
+                // (slots 4-7), d = s_row_d(md, l16); K- = k r cB(block).  The k r values come
+                // from two transposing reads of the K r tile, 16 rows apart (the swizzle
+                // repeats every 16 rows): lanes 4 j + cc of group g address row K0 + 4 g + j,
+                // d = 32 kb + 8 cc + 4 h + [0, 4) (md = 2 kb + h); then one channel value
+                // per lane for each 16-token block.
                 const int md = blk / 2, k0 = 32 * (blk % 2);
                 const int d = s_row_d(md, l16);
-                float e[8];
-#pragma unroll
-                for (int s2 = 0; s2 < 8; ++s2) {
-                    const int t = k0 + (s2 < 4 ? 4 * lg + s2 : 16 + 4 * lg + s2 - 4), b = t / 16;
-                    const int pos = t * D + 8 * ((d / 8) ^ kda_swz<D>(t)) + d % 8;
-                    const float kr = __uint_as_float(static_cast<unsigned>(KRs[pos]) << 16);
-                    e[s2] = kr * Cv[(kCvB + b) * D + d];
-                }
-                const u32x4_t o = {pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7])};
+                const int jj = (lane >> 2) & 3, cc = lane & 3, t = k0 + 4 * lg + jj;
+                const unsigned ad = lds_addr(KRs + t * D + 8 * ((4 * (md >> 1) + cc) ^ kda_swz<D>(t)) + 4 * (md & 1));
+                u32x2_t lo = lds_tr16_issue<0>(ad), hi = lds_tr16_issue<16 * D * 2>(ad);
+                const float c0 = Cv[(kCvB + k0 / 16) * D + d], c1 = Cv[(kCvB + k0 / 16 + 1) * D + d];
+                __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo), "+v"(hi) : : "memory");
+                const f32x4_t e0 = widen4(lo) * c0, e1 = widen4(hi) * c1;
+                const u32x4_t o = {pack2(e0.x, e0.y), pack2(e0.z, e0.w), pack2(e1.x, e1.y), pack2(e1.z, e1.w)};
                 v = __builtin_bit_cast(bf16x8_t, o);
             }
             const int base = arr == 0 ? W::KH : arr == 1 ? W::QH : W::KT;

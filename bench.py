@@ -29,6 +29,7 @@ import argparse
 import json
 import os
 import platform
+import statistics
 import sys
 import time
 
@@ -272,15 +273,23 @@ def time_cfg2(torch, lib, _native, synth, dev, stream, calls=10):
     nws = lib.pm_delta_varlen_workspace_bytes(n_seqs, N, H, D, _native.DTYPE_BF16)
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
 
-    def f(i):
+    def call(i, use_ws):
         q, k, v, beta = sets[i % 2]
+        w = use_ws and nws > 0
         rc = lib.pm_delta_fwd_varlen(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), cu.data_ptr(),
                                      n_seqs, N, None, o.data_ptr(), s.data_ptr(), H, D, _native.DTYPE_BF16,
-                                     _native.DTYPE_F32, CHUNK, ws.data_ptr() if nws else None, nws,
+                                     _native.DTYPE_F32, CHUNK, ws.data_ptr() if w else None, nws if w else 0,
                                      stream.cuda_stream)
         _native.check(rc)
 
-    ms = _time_calls(torch, stream, f, calls)
+    # the default call (workspace from pm_delta_varlen_workspace_bytes) and, beside it, the
+    # same call without a workspace (the single-stage kernel in cu_seqlens order), in
+    # interleaved rounds
+    ms_rounds, nat_rounds = [], []
+    for _ in range(3):
+        ms_rounds.append(_time_calls(torch, stream, lambda i: call(i, True), calls))
+        nat_rounds.append(_time_calls(torch, stream, lambda i: call(i, False), calls))
+    ms, ms_nat = statistics.median(ms_rounds), statistics.median(nat_rounds)
     E = N * H * D
     nb = 3 * E * 2 + 4 * N * H + 4 * E + 4 * n_seqs * H * D * D + 4 * (n_seqs + 1)
     return {
@@ -288,12 +297,16 @@ def time_cfg2(torch, lib, _native, synth, dev, stream, calls=10):
                     f"(lengths U[64, 4096], seed 2), cu_seqlens int32 on the device",
         "calls": calls,
         "kernel_us": ms * 1e3,
-        "path": "split form" if nws else "single-stage chunked kernel",
+        "path": ("single-stage chunked kernel, sequences longest first" if nws == 4 * n_seqs
+                 else "split form" if nws else "single-stage chunked kernel"),
         "lengths": [int(x) for x in lens],
         "longest": int(max(lens)),
         "tokens_per_s": N / (ms * 1e-3),
         "algorithmic_bytes": nb,
         "roofline": _roofline(nb, ms),
+        "no_workspace": {"path": "single-stage chunked kernel, sequences in cu_seqlens order",
+                         "kernel_us": ms_nat * 1e3, "roofline": _roofline(nb, ms_nat)},
+        "rounds": 3,
     }
 
 

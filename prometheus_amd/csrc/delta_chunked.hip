@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const uint16_t* __restrict__ v, const float* __restrict__ beta,
     const float* __restrict__ s0, void* __restrict__ o_out, float* __restrict__ s_out,
     uint16_t* __restrict__ s_hist, const int32_t* __restrict__ cu_seqlens, int n_pairs, int T,
-    int H, int n_tiles, const float* __restrict__ gate) {
+    int H, int n_tiles, const float* __restrict__ gate, const int32_t* __restrict__ seq_order) {
     static_assert(!(GATED && (HIST || NORM)), "gated forward only");
     using G = Geo<D, DV, GATED>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -145,9 +145,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int bid = blockIdx.x;
     const int xcd = bid & 7, slot = bid >> 3;
     const int tile = slot % n_tiles;
-    const int pair = (slot / n_tiles) * 8 + xcd;
-    if (pair >= n_pairs) return;
-    const int seq = pair / H, h = pair % H;
+    const int vpair = (slot / n_tiles) * 8 + xcd;
+    if (vpair >= n_pairs) return;
+    // packed batches: workgroups are dispatched in block order, so the sequences are taken
+    // in the order seq_order gives (longest first) when the caller provides one
+    const int h = vpair % H;
+    const int seq = seq_order ? seq_order[vpair / H] : vpair / H;
+    const int pair = seq * H + h;
     long tok0;
     int len;
     if (cu_seqlens) {
@@ -831,7 +835,8 @@ hipError_t launch_t(const ChunkedArgs& a, uint16_t* s_hist, hipStream_t st) {
     const int slots = (n_pairs + 7) / 8;
     const dim3 grid(static_cast<unsigned>(slots * 8 * n_tiles));
     hipLaunchKernelGGL(kern, grid, dim3(256), kBytes, st, a.q, a.k, a.v, a.beta, a.s0, a.o,
-                       a.s_out, s_hist, a.cu_seqlens, n_pairs, a.T, a.H, n_tiles, a.g);
+                       a.s_out, s_hist, a.cu_seqlens, n_pairs, a.T, a.H, n_tiles, a.g,
+                       a.cu_seqlens ? a.seq_order : nullptr);
     return hipGetLastError();
 }
 

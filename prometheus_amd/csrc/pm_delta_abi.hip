@@ -78,6 +78,43 @@ hipError_t launch_varlen_check(const int32_t* cu, int n_seqs, int total, int32_t
     return hipGetLastError();
 }
 
+// The order in which the chunked forward takes the sequences of a packed batch: its
+// workgroups are dispatched in block order, one per CU, and a long sequence whose blocks
+// come late starts only when earlier, shorter ones have finished.  Ranked by chunk count
+// (the recurrence walks chunks in order), largest first, ties in index order, so the
+// ranks are a permutation and every order slot is written once.  One thread per
+// sequence, the counts compared through LDS in tiles of 1024.
+__global__ __launch_bounds__(256) void varlen_order_kernel(const int32_t* __restrict__ cu, int n_seqs,
+                                                           int total, int32_t* __restrict__ order) {
+    constexpr int kTile = 1024;
+    __shared__ int nc[kTile];
+    auto chunks = [&](int j) {  // clamped as the chunked kernels clamp the offsets
+        const int a = min(max(cu[j], 0), total);
+        const int z = min(max(cu[j + 1], a), total);
+        return (z - a + 63) / 64;  // 64-token chunks
+    };
+    const int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    const int mine = i < n_seqs ? chunks(i) : 0;
+    int rank = 0;
+    for (int j0 = 0; j0 < n_seqs; j0 += kTile) {
+        const int m = min(kTile, n_seqs - j0);
+        __syncthreads();
+        for (int t = static_cast<int>(threadIdx.x); t < m; t += 256) nc[t] = chunks(j0 + t);
+        __syncthreads();
+        if (i < n_seqs) {
+            for (int t = 0; t < m; ++t) rank += nc[t] > mine || (nc[t] == mine && j0 + t < i);
+        }
+    }
+    if (i < n_seqs) order[rank] = i;
+}
+
+hipError_t launch_varlen_order(const int32_t* cu, int n_seqs, int total, int32_t* order, hipStream_t st) {
+    if (n_seqs <= 0 || n_seqs > kVarlenOrderMax) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(varlen_order_kernel, dim3(static_cast<unsigned>((n_seqs + 255) / 256)), dim3(256), 0, st,
+                       cu, n_seqs, total, order);
+    return hipGetLastError();
+}
+
 hipError_t launch_copy_f32(float* dst, const float* src, size_t n, hipStream_t st) {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(copy_f32_kernel, dim3(grid_for(n)), dim3(256), 0, st, dst, src, n);
@@ -236,6 +273,14 @@ int forward(const void* q, const void* k, const void* v, const float* beta, cons
                 return fail(PM_E_WORKSPACE, "path 3 needs a 16-byte aligned workspace of %zu bytes (got %zu)",
                             need, workspace ? ws_bytes : static_cast<size_t>(0));
         }
+        // packed batches: the sequences go longest first where the workspace holds the order
+        if (varlen && !g && n_seq >= 2 && n_seq <= pm::kVarlenOrderMax && workspace &&
+            ws_bytes >= static_cast<size_t>(n_seq) * 4 && aligned(workspace, 4)) {
+            int32_t* order = static_cast<int32_t*>(workspace);
+            hipError_t e = pm::launch_varlen_order(cu, n_seq, total_T, order, st);
+            if (e != hipSuccess) return hip_fail(e, "sequence order launch");
+            a.seq_order = order;
+        }
         hipError_t e = pm::launch_chunked(a, st);
         return e == hipSuccess ? 0 : hip_fail(e, "chunked forward launch");
     }
@@ -358,15 +403,19 @@ int backward(const void* q, const void* k, const void* v, const float* beta, con
     return e == hipSuccess ? 0 : hip_fail(e, "backward launch");
 }
 
-// The forward's workspace: the split form's T blocks (bf16 inputs, where split_chosen), or
-// the fp32 chunked forward's (T'')^T and P^T (fp32 inputs); 0 where the call runs neither.
+// The forward's workspace: the split form's T blocks (bf16 inputs, where split_chosen), the
+// fp32 chunked forward's (T'')^T and P^T (fp32 inputs), or a packed batch's sequence order
+// for the single-stage kernel (bf16 inputs, 2 to kVarlenOrderMax sequences); else 0.
 size_t fwd_ws_bytes(bool varlen, int n_seq, int T, int H, int D, int in_dtype) {
     if (n_seq < 0 || T < 0 || H < 0 || !pm::chunked_supported(D, H) || g_path == 1) return 0;
     const long n_pairs = static_cast<long>(n_seq) * H;
     if (n_pairs > (1L << 30)) return 0;
     if (in_dtype == PM_DTYPE_F32) return pm::chunked_f32_ws_bytes(varlen, n_seq, T, H);
-    if (in_dtype != PM_DTYPE_BF16 || !split_chosen(g_path, D, n_pairs)) return 0;
-    return pm::chunked_split_ws_bytes(varlen, n_seq, T, H);
+    if (in_dtype != PM_DTYPE_BF16) return 0;
+    if (split_chosen(g_path, D, n_pairs)) return pm::chunked_split_ws_bytes(varlen, n_seq, T, H);
+    // the single-stage kernel: a packed batch's sequence order (longest first)
+    if (varlen && n_seq >= 2 && n_seq <= pm::kVarlenOrderMax) return static_cast<size_t>(n_seq) * 4;
+    return 0;
 }
 
 }  // namespace

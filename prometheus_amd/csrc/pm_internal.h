@@ -71,6 +71,10 @@ struct ChunkedArgs {
     // Gated variant (not with norm): log-gates per (token, head), alpha = exp(g)
     // (g <= 0 keeps every in-chunk decay factor at most 1).
     const float* g = nullptr;
+    // Packed batches (cu_seqlens): a permutation of the n_seq sequences, longest first
+    // (launch_varlen_order), in which the workgroups take them; nullptr keeps their order.
+    // Only the schedule changes: every sequence's results are the same bits either way.
+    const int32_t* seq_order = nullptr;
 };
 bool chunked_supported(int D, int H);  // D in {64, 128}, H*D <= 2^24
 // d_v columns per workgroup of the chunked forward: 32 (two chain waves) unless that
@@ -210,5 +214,9 @@ hipError_t launch_fill_zero(float* p, size_t n, hipStream_t st);
 hipError_t launch_copy_f32(float* dst, const float* src, size_t n, hipStream_t st);
 // One workgroup checks a packed batch's offsets and ORs error bits into *flag.
 hipError_t launch_varlen_check(const int32_t* cu, int n_seqs, int total, int32_t* flag, hipStream_t st);
+// order[r] = the sequence of rank r by chunk count, largest first, ties in index order
+// (cu_seqlens clamped as the chunked kernels clamp them); at most kVarlenOrderMax sequences
+constexpr int kVarlenOrderMax = 8192;
+hipError_t launch_varlen_order(const int32_t* cu, int n_seqs, int total, int32_t* order, hipStream_t st);
 
 }  // namespace pm

@@ -282,14 +282,29 @@ def time_cfg2(torch, lib, _native, synth, dev, stream, calls=10):
                                      stream.cuda_stream)
         _native.check(rc)
 
-    # the default call (workspace from pm_delta_varlen_workspace_bytes) and, beside it, the
-    # same call without a workspace (the single-stage kernel in cu_seqlens order), in
-    # interleaved rounds
-    ms_rounds, nat_rounds = [], []
-    for _ in range(3):
-        ms_rounds.append(_time_calls(torch, stream, lambda i: call(i, True), calls))
-        nat_rounds.append(_time_calls(torch, stream, lambda i: call(i, False), calls))
-    ms, ms_nat = statistics.median(ms_rounds), statistics.median(nat_rounds)
+    # the default call (with the workspace pm_delta_varlen_workspace_bytes asks for, none
+    # at cfg2), medians of three rounds
+    ms = statistics.median(_time_calls(torch, stream, lambda i: call(i, True), calls) for _ in range(3))
+    # the schedule: one batch of 60 x 192 tokens and one 4096-token sequence, packed with the
+    # long sequence first and with it last; the forward takes sequences longest first, so
+    # the two orders should time the same (in cu_seqlens order the late long sequence
+    # starts only when the short ones have freed CUs)
+    sched = {}
+    for name, sl in (("long_first", [4096] + [192] * 60), ("long_last", [192] * 60 + [4096])):
+        cu2 = torch.from_numpy(synth.cu_seqlens(np.array(sl))).to(dev)
+        n2, N2 = len(sl), sum(sl)
+        assert N2 <= N
+        q2, k2, v2, b2 = (x[:, :N2].contiguous() for x in sets[0])
+        o2 = torch.empty((1, N2, H, D), dtype=torch.float32, device=dev)
+        s2 = torch.empty((n2, H, D, D), dtype=torch.float32, device=dev)
+
+        def call2(i):
+            rc = lib.pm_delta_fwd_varlen(q2.data_ptr(), k2.data_ptr(), v2.data_ptr(), b2.data_ptr(), cu2.data_ptr(),
+                                         n2, N2, None, o2.data_ptr(), s2.data_ptr(), H, D, _native.DTYPE_BF16,
+                                         _native.DTYPE_F32, CHUNK, None, 0, stream.cuda_stream)
+            _native.check(rc)
+
+        sched[name + "_us"] = statistics.median(_time_calls(torch, stream, call2, calls) for _ in range(3)) * 1e3
     E = N * H * D
     nb = 3 * E * 2 + 4 * N * H + 4 * E + 4 * n_seqs * H * D * D + 4 * (n_seqs + 1)
     return {
@@ -297,16 +312,17 @@ def time_cfg2(torch, lib, _native, synth, dev, stream, calls=10):
                     f"(lengths U[64, 4096], seed 2), cu_seqlens int32 on the device",
         "calls": calls,
         "kernel_us": ms * 1e3,
-        "path": ("single-stage chunked kernel, sequences longest first" if nws == 4 * n_seqs
-                 else "split form" if nws else "single-stage chunked kernel"),
+        "path": ("split form" if nws > 4 * n_seqs else
+                 "single-stage chunked kernel, sequences longest first"
+                 + (" (order from the rank kernel)" if nws else " (ranked in the kernel)")),
         "lengths": [int(x) for x in lens],
         "longest": int(max(lens)),
         "tokens_per_s": N / (ms * 1e-3),
         "algorithmic_bytes": nb,
         "roofline": _roofline(nb, ms),
-        "no_workspace": {"path": "single-stage chunked kernel, sequences in cu_seqlens order",
-                         "kernel_us": ms_nat * 1e3, "roofline": _roofline(nb, ms_nat)},
         "rounds": 3,
+        "schedule": {"batch": "60 x 192 tokens and one of 4096, H16 D128 bf16, packed with the long "
+                              "sequence first or last", **sched},
     }
 
 

@@ -100,10 +100,11 @@ int pm_delta_fwd(const void* q, const void* k, const void* v, const float* beta,
  * chunked_delta_rule calls (kernels/__init__.py:591-619) with B=1.
  * s0 may be NULL (zeros) or (n_seqs, H, D, D).
  * workspace/ws_bytes as pm_delta_fwd, sized by pm_delta_varlen_workspace_bytes.
- * Where the single-stage bf16 kernel runs, the workspace holds the order in
- * which its workgroups take the sequences (longest first, by chunk count,
- * computed on the device); without it they go in cu_seqlens order.  Only the
- * schedule changes: the results are the same bits either way.
+ * Where the single-stage bf16 kernel runs, its workgroups take the sequences
+ * longest first (by chunk count, ties in index order): up to 64 sequences
+ * ranked inside the kernel; beyond that the workspace holds the order
+ * (computed on the device), and without it they go in cu_seqlens order.
+ * Only the schedule changes: the results are the same bits either way.
  */
 int pm_delta_fwd_varlen(const void* q, const void* k, const void* v, const float* beta,
                         const int32_t* cu_seqlens, int n_seqs, int total_T,
@@ -262,7 +263,7 @@ size_t pm_delta_workspace_bytes(int B, int T, int H, int D, int in_dtype);
 /* The same for pm_delta_fwd_varlen (per head: 6 KiB per slot, with
  * ceil(total_T / 64) + n_seqs slots; fp32: 1 KiB per slot, with
  * ceil(total_T / 16) + n_seqs slots; the single-stage bf16 kernel: 4 bytes
- * per sequence for 2 to 8192 sequences, the sequence order). */
+ * per sequence for 65 to 8192 sequences, the sequence order). */
 size_t pm_delta_varlen_workspace_bytes(int n_seqs, int total_T, int H, int D, int in_dtype);
 
 /*

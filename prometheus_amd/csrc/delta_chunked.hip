@@ -147,10 +147,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int tile = slot % n_tiles;
     const int vpair = (slot / n_tiles) * 8 + xcd;
     if (vpair >= n_pairs) return;
-    // packed batches: workgroups are dispatched in block order, so the sequences are taken
-    // in the order seq_order gives (longest first) when the caller provides one
+    // Packed batches: workgroups are dispatched in block order, one per CU, so the sequences
+    // are taken longest first (by chunk count, ties in index order): from seq_order where
+    // the caller computed it, and up to 64 sequences ranked here, one lane per sequence,
+    // by every wave for itself (one load of the offsets, n readlanes, a ballot)
     const int h = vpair % H;
-    const int seq = seq_order ? seq_order[vpair / H] : vpair / H;
+    int seq = vpair / H;
+    if (seq_order) {
+        seq = seq_order[seq];
+    } else if (cu_seqlens && n_pairs / H <= 64) {
+        const int n = n_pairs / H, lane_ = threadIdx.x & 63;
+        int nc = -1;
+        if (lane_ < n) {
+            const int a = min(max(cu_seqlens[lane_], 0), T);
+            const int z = min(max(cu_seqlens[lane_ + 1], a), T);
+            nc = (z - a + kC - 1) / kC;
+        }
+        int rank = 0;
+        for (int j = 0; j < n; ++j) {
+            const int o = __builtin_amdgcn_readlane(nc, j);
+            rank += o > nc || (o == nc && j < lane_);
+        }
+        // ranks are a permutation of [0, n): exactly one lane holds rank seq
+        seq = __builtin_ctzll(__ballot(lane_ < n && rank == seq));
+    }
     const int pair = seq * H + h;
     long tok0;
     int len;

@@ -273,8 +273,9 @@ int forward(const void* q, const void* k, const void* v, const float* beta, cons
                 return fail(PM_E_WORKSPACE, "path 3 needs a 16-byte aligned workspace of %zu bytes (got %zu)",
                             need, workspace ? ws_bytes : static_cast<size_t>(0));
         }
-        // packed batches: the sequences go longest first where the workspace holds the order
-        if (varlen && !g && n_seq >= 2 && n_seq <= pm::kVarlenOrderMax && workspace &&
+        // packed batches: the sequences go longest first, ranked inside the kernel up to 64
+        // sequences and, beyond, through an order the rank kernel writes into the workspace
+        if (varlen && !g && n_seq > 64 && n_seq <= pm::kVarlenOrderMax && workspace &&
             ws_bytes >= static_cast<size_t>(n_seq) * 4 && aligned(workspace, 4)) {
             int32_t* order = static_cast<int32_t*>(workspace);
             hipError_t e = pm::launch_varlen_order(cu, n_seq, total_T, order, st);
@@ -405,7 +406,7 @@ int backward(const void* q, const void* k, const void* v, const float* beta, con
 
 // The forward's workspace: the split form's T blocks (bf16 inputs, where split_chosen), the
 // fp32 chunked forward's (T'')^T and P^T (fp32 inputs), or a packed batch's sequence order
-// for the single-stage kernel (bf16 inputs, 2 to kVarlenOrderMax sequences); else 0.
+// for the single-stage kernel (bf16 inputs, 65 to kVarlenOrderMax sequences); else 0.
 size_t fwd_ws_bytes(bool varlen, int n_seq, int T, int H, int D, int in_dtype) {
     if (n_seq < 0 || T < 0 || H < 0 || !pm::chunked_supported(D, H) || g_path == 1) return 0;
     const long n_pairs = static_cast<long>(n_seq) * H;
@@ -413,8 +414,9 @@ size_t fwd_ws_bytes(bool varlen, int n_seq, int T, int H, int D, int in_dtype) {
     if (in_dtype == PM_DTYPE_F32) return pm::chunked_f32_ws_bytes(varlen, n_seq, T, H);
     if (in_dtype != PM_DTYPE_BF16) return 0;
     if (split_chosen(g_path, D, n_pairs)) return pm::chunked_split_ws_bytes(varlen, n_seq, T, H);
-    // the single-stage kernel: a packed batch's sequence order (longest first)
-    if (varlen && n_seq >= 2 && n_seq <= pm::kVarlenOrderMax) return static_cast<size_t>(n_seq) * 4;
+    // the single-stage kernel: a packed batch's sequence order (longest first) beyond the 64
+    // sequences the kernel ranks itself
+    if (varlen && n_seq > 64 && n_seq <= pm::kVarlenOrderMax) return static_cast<size_t>(n_seq) * 4;
     return 0;
 }
 

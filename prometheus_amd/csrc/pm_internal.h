@@ -72,8 +72,9 @@ struct ChunkedArgs {
     // (g <= 0 keeps every in-chunk decay factor at most 1).
     const float* g = nullptr;
     // Packed batches (cu_seqlens): a permutation of the n_seq sequences, longest first
-    // (launch_varlen_order), in which the workgroups take them; nullptr keeps their order.
-    // Only the schedule changes: every sequence's results are the same bits either way.
+    // (launch_varlen_order), in which the workgroups take them; nullptr: the kernel ranks
+    // up to 64 sequences itself and keeps cu_seqlens order beyond.  Only the schedule
+    // changes: every sequence's results are the same bits either way.
     const int32_t* seq_order = nullptr;
 };
 bool chunked_supported(int D, int H);  // D in {64, 128}, H*D <= 2^24

@@ -303,10 +303,11 @@ def test_forward_workspace_sizes_and_checks():
     assert lib.pm_delta_varlen_workspace_bytes(3, 100, 2, 128, f32) == 2 * (7 + 3) * 1024
     # varlen: H x (ceil(total / 64) + n_seqs) slots
     assert lib.pm_delta_varlen_workspace_bytes(3, 1000, 4, 128, bf16) == 4 * (16 + 3) * per
-    # the single-stage kernel on a packed batch: the sequence order (4 bytes per sequence,
-    # 2 to 8192 sequences); cfg2 (8 sequences here) runs 32-column tiles
-    assert lib.pm_delta_varlen_workspace_bytes(8, 16384, 16, 128, bf16) == 8 * 4
-    assert lib.pm_delta_varlen_workspace_bytes(1, 16384, 64, 128, bf16) == 0  # one sequence
+    # the single-stage kernel on a packed batch: the sequence order (4 bytes per sequence)
+    # for 65 to 8192 sequences; up to 64 the kernel ranks them itself
+    assert lib.pm_delta_varlen_workspace_bytes(8, 16384, 16, 128, bf16) == 0  # cfg2: 32-col tiles
+    assert lib.pm_delta_varlen_workspace_bytes(64, 16384, 16, 128, bf16) == 0
+    assert lib.pm_delta_varlen_workspace_bytes(65, 16384, 16, 128, bf16) == 65 * 4
     assert lib.pm_delta_varlen_workspace_bytes(8192, 16384, 16, 128, bf16) == 8192 * 4
     assert lib.pm_delta_varlen_workspace_bytes(8193, 16384, 16, 128, bf16) == 0
     assert lib.pm_delta_workspace_bytes(8, 2048, 16, 128, bf16) == 0  # fixed length: no order

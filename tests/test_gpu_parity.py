@@ -494,6 +494,60 @@ def test_cfg2_varlen_vs_c_oracle():
         assert_bf16_parity(s_np[i], e_s[0], f"cfg2 segment {i} S")
 
 
+def _varlen_abi(q, k, v, b, cu_d, n_seqs, s0, ws=None, nws=0):
+    n, H, D = q.shape
+    o = torch.full((n, H, D), float("nan"), device="cuda")
+    s = torch.full((n_seqs, H, D, D), float("nan"), device="cuda")
+    rc = _native.lib().pm_delta_fwd_varlen(q.data_ptr(), k.data_ptr(), v.data_ptr(), b.data_ptr(), cu_d.data_ptr(),
+                                           n_seqs, n, s0.data_ptr(), o.data_ptr(), s.data_ptr(), H, D,
+                                           _native.DTYPE_BF16, _native.DTYPE_F32, 64,
+                                           None if ws is None else ws.data_ptr(), nws,
+                                           torch.cuda.current_stream().cuda_stream)
+    _native.check(rc)
+    return o, s
+
+
+def _varlen_lens_case(lens, seed):
+    lens = np.array(lens)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    n, H, D = int(cu[-1]), 2, 128
+    x, (q, k, v, b, _) = _bf16_case((n, H, D), seed=seed)
+    rng = np.random.default_rng(seed + 1)
+    s0 = torch.from_numpy((0.02 * rng.standard_normal((lens.size, H, D, D))).astype(np.float32)).cuda()
+    return lens, cu, x, (q, k, v, b), s0
+
+
+@pytest.mark.parametrize("lens", [
+    [3, 64, 0, 65, 700, 64, 130, 4000],             # longest last, ties (64 and 3: one chunk each), an empty one
+    [4000, 700, 130, 65, 64, 3, 0],                 # already longest first
+    [1] * 40 + [300] * 23 + [900],                  # 64 sequences, the most the kernel ranks itself
+])
+def test_varlen_longest_first_in_kernel_rank(lens):
+    """Up to 64 sequences the single-stage varlen forward ranks them inside the kernel
+    (longest first): no workspace is asked for, and every sequence's O rows and final state
+    equal a standalone single-stage call on it (with its own initial state) bit for bit, so
+    each workgroup found its own sequence; the longest and the shortest also against the
+    oracle."""
+    lens, cu, x, (q, k, v, b), s0 = _varlen_lens_case(lens, seed=44)
+    n, H, D = q.shape
+    with _path(2):  # the single-stage form at any shape
+        assert _native.lib().pm_delta_varlen_workspace_bytes(lens.size, n, H, D, _native.DTYPE_BF16) == 0
+        o, s = _varlen_abi(q, k, v, b, torch.from_numpy(cu).cuda(), lens.size, s0)
+        for i in range(lens.size):
+            a, z = int(cu[i]), int(cu[i + 1])
+            oi, si = kernels.chunked_delta_rule(q[None, a:z], k[None, a:z], v[None, a:z], b[None, a:z], s0[i:i + 1])
+            assert torch.equal(o[a:z], oi[0]), f"sequence {i} [{a}, {z}) O"
+            assert torch.equal(s[i], si[0]), f"sequence {i} state"
+    o_np, s_np = _np(o), _np(s)
+    for i in (int(np.argmax(lens)), int(np.argmin(lens))):
+        a, z = int(cu[i]), int(cu[i + 1])
+        e_o, e_s = ref.wy_chunked_fwd(x.q[None, a:z], x.k[None, a:z], x.v[None, a:z], x.beta[None, a:z],
+                                      _np(s0[i:i + 1]), chunk=64, dtype=np.float64)
+        if z > a:
+            assert_bf16_parity(o_np[a:z], e_o[0], f"ordered varlen sequence {i} O")
+        assert_bf16_parity(s_np[i], e_s[0], f"ordered varlen sequence {i} S")
+
+
 def _expected_order(cu, total):
     """Sequences by chunk count, largest first, ties in index order (offsets clamped as the
     kernels clamp them)."""
@@ -504,52 +558,33 @@ def _expected_order(cu, total):
 
 
 @pytest.mark.parametrize("lens", [
-    [3, 64, 0, 65, 700, 64, 130, 4000],            # longest last, ties (64 and 3: one chunk each), an empty one
-    [4000, 700, 130, 65, 64, 3, 0],                # already longest first
-    [200] * 5 + [1] * 300 + [2000],                 # 306 sequences: two workgroups of the order kernel
+    [1] * 40 + [300] * 24 + [900],                  # 65 sequences: the order through the workspace
+    [200] * 5 + [1] * 300 + [2000],                 # 306 sequences: two workgroups of the rank kernel
 ])
-def test_varlen_longest_first_order_is_bitwise_neutral(lens):
-    """The single-stage varlen forward takes its sequences longest first when the workspace
-    (pm_delta_varlen_workspace_bytes) holds the order: the workspace then holds that
-    permutation, and O and every final state equal the call without a workspace (cu_seqlens
-    order) bit for bit, with an initial state per sequence."""
-    lens = np.array(lens)
-    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
-    n, H, D = int(cu[-1]), 2, 128
-    x, (q, k, v, b, _) = _bf16_case((n, H, D), seed=44)
-    rng = np.random.default_rng(45)
-    s0 = torch.from_numpy((0.02 * rng.standard_normal((lens.size, H, D, D))).astype(np.float32)).cuda()
+def test_varlen_longest_first_order_table(lens):
+    """Beyond 64 sequences the order comes from the rank kernel through the workspace
+    (pm_delta_varlen_workspace_bytes): the workspace then holds the expected permutation,
+    and O and every final state equal the call without a workspace (cu_seqlens order) bit
+    for bit, with an initial state per sequence."""
+    lens, cu, x, (q, k, v, b), s0 = _varlen_lens_case(lens, seed=46)
+    n, H, D = q.shape
     cu_d = torch.from_numpy(cu).cuda()
-    lib = _native.lib()
-    st = torch.cuda.current_stream().cuda_stream
-    with _path(2):  # the single-stage form at any shape
-        nws = lib.pm_delta_varlen_workspace_bytes(lens.size, n, H, D, _native.DTYPE_BF16)
+    with _path(2):
+        nws = _native.lib().pm_delta_varlen_workspace_bytes(lens.size, n, H, D, _native.DTYPE_BF16)
         assert nws == 4 * lens.size
         ws = torch.full((nws // 4,), -7, dtype=torch.int32, device="cuda")
-        outs = []
-        for w in (None, ws):
-            o = torch.full((n, H, D), float("nan"), device="cuda")
-            s = torch.full((lens.size, H, D, D), float("nan"), device="cuda")
-            rc = lib.pm_delta_fwd_varlen(q.data_ptr(), k.data_ptr(), v.data_ptr(), b.data_ptr(), cu_d.data_ptr(),
-                                         lens.size, n, s0.data_ptr(), o.data_ptr(), s.data_ptr(), H, D,
-                                         _native.DTYPE_BF16, _native.DTYPE_F32, 64,
-                                         None if w is None else w.data_ptr(), 0 if w is None else nws, st)
-            _native.check(rc)
-            outs.append((o, s))
+        o0, s0_ = _varlen_abi(q, k, v, b, cu_d, lens.size, s0)
+        o1, s1_ = _varlen_abi(q, k, v, b, cu_d, lens.size, s0, ws, nws)
         torch.cuda.synchronize()
     assert np.array_equal(ws.cpu().numpy(), _expected_order(cu, n))
-    (o0, s0_), (o1, s1_) = outs
     assert not torch.isnan(o0).any() and not torch.isnan(s0_).any()
     assert torch.equal(o0, o1) and torch.equal(s0_, s1_)
-    # and the ordered call against the oracle on the longest and an empty sequence
-    o_np, s_np = _np(o1), _np(s1_)
-    for i in (int(np.argmax(lens)), int(np.argmin(lens))):
-        a, z = int(cu[i]), int(cu[i + 1])
-        e_o, e_s = ref.wy_chunked_fwd(x.q[None, a:z], x.k[None, a:z], x.v[None, a:z], x.beta[None, a:z],
-                                      _np(s0[i:i + 1]), chunk=64, dtype=np.float64)
-        if z > a:
-            assert_bf16_parity(o_np[a:z], e_o[0], f"ordered varlen sequence {i} O")
-        assert_bf16_parity(s_np[i], e_s[0], f"ordered varlen sequence {i} S")
+    i = int(np.argmax(lens))
+    a, z = int(cu[i]), int(cu[i + 1])
+    e_o, e_s = ref.wy_chunked_fwd(x.q[None, a:z], x.k[None, a:z], x.v[None, a:z], x.beta[None, a:z],
+                                  _np(s0[i:i + 1]), chunk=64, dtype=np.float64)
+    assert_bf16_parity(_np(o1)[a:z], e_o[0], f"ordered varlen sequence {i} O")
+    assert_bf16_parity(_np(s1_)[i], e_s[0], f"ordered varlen sequence {i} S")
 
 
 # ---------------------------------------------------------------------------

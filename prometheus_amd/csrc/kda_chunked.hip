@@ -121,7 +121,7 @@ __device__ __forceinline__ u32x4_t kda_mul8(u32x4_t x, const float (&f)[8]) {
 // all of them; wave 1 the off-diagonal Gram tiles (handed to wave 0 through LDS); waves 2
 // and 3 the ten P tiles; waves 1-3 the recurrence's operand blocks; wave 0 exp(G_C).
 template <int D>
-__global__ __launch_bounds__(256) void kda_prep_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void kda_prep_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                        const float* __restrict__ beta, const float* __restrict__ gate,
                                                        int T, int H, int n_chunks, long n_items,
                                                        unsigned char* __restrict__ ws) {
@@ -163,12 +163,24 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const uint16_t* __restric
             pk[i] = t < cl ? *reinterpret_cast<const u32x4_t*>(k + r0 + t * tstride + 8 * ch) : z;
             pq[i] = t < cl ? *reinterpret_cast<const u32x4_t*>(q + r0 + t * tstride + 8 * ch) : z;
         }
-#pragma unroll
-        for (int j = 0; j < SEG; ++j) {
-            const int t = gsg * SEG + j;
-            pgv[j] = t < cl ? gate[r0 + t * tstride + gd_] : 0.f;
-        }
         if (tid < kC) pb = tid < cl ? beta[static_cast<size_t>(t0 + tid) * H + pr % H] : 0.f;
+    };
+    // An item's log-gates, at the item's start: through a buffer resource whose range ends
+    // at the chunk's last valid row (later rows read as zeros), with the token's offset a
+    // wave-uniform scalar and the channel the lane's (per-token 64-bit addresses, hoisted
+    // out of the item loop, had held 64 VGPRs through the whole kernel)
+    auto load_gates = [&](long it) __attribute__((always_inline)) {
+        const int pr = static_cast<int>(it / n_chunks), cc = static_cast<int>(it % n_chunks);
+        const long t0 = static_cast<long>(pr / H) * T + static_cast<long>(cc) * kC;
+        const int cl = min(kC, T - cc * kC);
+        const size_t r0 = static_cast<size_t>(t0) * tstride + static_cast<size_t>(pr % H) * D;
+        const __amdgpu_buffer_rsrc_t rg =
+            make_rsrc(gate + r0, static_cast<unsigned>(((cl - 1) * tstride + D) * 4));
+        const int seg0 = static_cast<int>(uniform(static_cast<unsigned>(gsg))) * SEG;
+#pragma unroll
+        for (int j = 0; j < SEG; ++j)
+            pgv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                rg, static_cast<unsigned>(gd_ * 4), static_cast<unsigned>((seg0 + j) * tstride * 4), 0));
     };
 
     long item = blockIdx.x;
@@ -176,6 +188,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const uint16_t* __restric
     prefetch(item);
     for (; item < n_items; item += gridDim.x) {
     unsigned char* out = ws + static_cast<size_t>(item) * W::BYTES;
+    load_gates(item);
 
     // ---- stage the item: beta and the prefix sums G of the log-gates (K and Q stay in
     // registers until the scaled tiles are formed) ----
@@ -202,17 +215,24 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const uint16_t* __restric
 
     // ---- the scaled tiles K a, K r, Q a (bf16) over G's storage, and the channel vectors ----
     {
+        // the tiles are formed into registers while G is still in LDS, and written over it
+        // after the barrier (element chunk i of a thread lies in block i)
         constexpr int NE = NV / 256;  // 8-element chunks per thread
-        float gv[NE][8], gm[NE][8];
+        u32x4_t tka[NE], tkr[NE], tqa[NE];
 #pragma unroll
         for (int i = 0; i < NE; ++i) {
             const int x = tid + 256 * i, t = x / NCH, ch = x % NCH, b = t / 16;
+            float av[8], rv[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int d = 8 * ch + j;
-                gv[i][j] = Gs[t * D + d];
-                gm[i][j] = Gs[(16 * b + 7) * D + d];
+                const float gv = Gs[t * D + d], gm = Gs[(16 * b + 7) * D + d];
+                av[j] = exp2_hw(gv - gm);
+                rv[j] = exp2_hw(gm - gv);
             }
+            tka[i] = kda_mul8(pk[i], av);
+            tkr[i] = kda_mul8(pk[i], rv);
+            tqa[i] = kda_mul8(pq[i], av);
         }
         for (int x = tid; x < L::NCV * D; x += 256) {
             const int v = x / D, d = x % D;
@@ -232,21 +252,13 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const uint16_t* __restric
 #pragma unroll
         for (int i = 0; i < NE; ++i) {
             const int x = tid + 256 * i, t = x / NCH, ch = x % NCH;
-            float av[8], rv[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                av[j] = exp2_hw(gv[i][j] - gm[i][j]);
-                rv[j] = exp2_hw(gm[i][j] - gv[i][j]);
-            }
             const int pos = t * D + 8 * (ch ^ kda_swz<D>(t));
-            *reinterpret_cast<u32x4_t*>(KAs + pos) = kda_mul8(pk[i], av);
-            *reinterpret_cast<u32x4_t*>(KRs + pos) = kda_mul8(pk[i], rv);
-            *reinterpret_cast<u32x4_t*>(QAs + pos) = kda_mul8(pq[i], av);
+            *reinterpret_cast<u32x4_t*>(KAs + pos) = tka[i];
+            *reinterpret_cast<u32x4_t*>(KRs + pos) = tkr[i];
+            *reinterpret_cast<u32x4_t*>(QAs + pos) = tqa[i];
         }
     }
     __syncthreads();
-    // the next item's loads, in flight through this item's work
-    if (item + gridDim.x < n_items) prefetch(item + gridDim.x);
 
     auto cvec = [&](int v, int kb) { return Cv + v * D + 32 * kb + 8 * lg; };
     auto frag = [&](const uint16_t* X, int t, int kb, int v) {
@@ -374,6 +386,9 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(const uint16_t* __restric
             *reinterpret_cast<bf16x8_t*>(out + base + blk * 1024 + lane * 16) = v;
         }
     }
+    // the next item's K, Q and beta, issued after this item's heavy phases (registers held
+    // through them cost two workgroups per CU); the gates load at the item's start
+    if (item + gridDim.x < n_items) prefetch(item + gridDim.x);
     __syncthreads();  // every read of this item's LDS is done before the next item is staged
     }
 }

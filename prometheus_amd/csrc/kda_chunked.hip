@@ -23,7 +23,7 @@
 // below bf16 resolution.  The per-token kernel (delta_recurrent.hip) takes g as given.
 //
 // K8p (prepass, 256-thread workgroups, two per CU, each walking (b, h, chunk) items with
-// the next item's inputs loaded during the current one; all chunks independent):
+// the next item's K and Q loaded during the current one; all chunks independent):
 // the clamped prefix sums G (LDS), then T'' = -T diag(beta) (the decayed Gram blocks on
 // waves 0 and 1, t_from_gram on wave 0), P (waves 2 and 3) and the recurrence's operands
 // K^, Q^, K-^T and exp(G_C), all written to the workspace in MFMA operand order (1 KiB
@@ -146,9 +146,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int NKQ = NV / 256, NSEG = 256 / D, SEG = kC / NSEG;
     const int gd_ = tid % D, gsg = tid / D;  // this thread's channel and token segment of G
 
-    // An item's inputs (K and Q rows, zeros past the chunk's end; its log-gates; beta),
-    // loaded one whole item ahead into registers, so that they arrive during the
-    // previous item's work (the workgroup walks items blockIdx.x, + gridDim.x, ...).
+    // An item's K and Q rows (zeros past the chunk's end) and beta, loaded one whole item
+    // ahead into registers, so that they arrive during the previous item's work (the
+    // workgroup walks items blockIdx.x, + gridDim.x, ...); its log-gates load at its start.
     u32x4_t pk[NKQ], pq[NKQ];
     float pgv[SEG], pb = 0.f;
     auto prefetch = [&](long it) __attribute__((always_inline)) {
@@ -258,6 +258,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             *reinterpret_cast<u32x4_t*>(QAs + pos) = tqa[i];
         }
     }
+    // the next item's K, Q and beta, in flight through this item's work (the gates load at
+    // the item's start: held as well, they would not fit two workgroups per CU)
+    if (item + gridDim.x < n_items) prefetch(item + gridDim.x);
     __syncthreads();
 
     auto cvec = [&](int v, int kb) { return Cv + v * D + 32 * kb + 8 * lg; };
@@ -386,9 +389,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             *reinterpret_cast<bf16x8_t*>(out + base + blk * 1024 + lane * 16) = v;
         }
     }
-    // the next item's K, Q and beta, issued after this item's heavy phases (registers held
-    // through them cost two workgroups per CU); the gates load at the item's start
-    if (item + gridDim.x < n_items) prefetch(item + gridDim.x);
     __syncthreads();  // every read of this item's LDS is done before the next item is staged
     }
 }

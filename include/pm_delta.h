@@ -282,8 +282,8 @@ size_t pm_delta_varlen_workspace_bytes(int n_seqs, int total_T, int H, int D, in
  *     (the forward's chunked kernel in reverse; bf16 parity, rel-L2 <= 2e-2
  *     against the fp32 reference).  q, k, v, go, gq, gk, gv and
  *     workspace 16-byte aligned.  Workspace, per (b, h) and 64-token chunk: the chunk's start
- *     state and end state gradient and W (bf16), and three packed 64x64
- *     operands: 2 * B * H * ceil(T / 64) * (2 * D * D + 64 * D + 9216) bytes.
+ *     state and end state gradient and W (bf16), and the packed 64x64 T:
+ *     2 * B * H * ceil(T / 64) * (2 * D * D + 64 * D + 3072) bytes.
  *   - fp32 q/k/v with D in {64, 128}: the chunked backward on fp32 MFMA
  *     (16-token chunks; fp32 parity).  q, k, v, go, gq, gk, gv and workspace
  *     16-byte aligned.  Workspace (fp32, each region rounded up to 256

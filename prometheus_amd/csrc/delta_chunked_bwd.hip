@@ -16,17 +16,17 @@
 //     dbeta_t = W_t . (v_t - S^T k_t) + sum_{s<t} dA_ts (k_t . k_s)
 // (dT = dU X^T and dA = -T^T dT T^T = -W U^T.)  Only the state gradient G
 // is carried from chunk to chunk; everything else is local to a chunk once
-// its start state S and end gradient G are known.  Four launches:
+// its start state S and end gradient G are known.  Three launches:
 //   1. the forward kernel in its state-history mode writes every chunk's S
 //      (bf16, as rows of S^T);
-//   2. bwd_prep_kernel, one workgroup per chunk: T (the forward's builder), and
-//      T^T and P^T, in packed MFMA operand order;
-//   3. bwd_rev_kernel walks the chunks backwards per (b, h, 32 columns of
+//   2. bwd_rev_kernel walks the chunks backwards per (b, h, 32 columns of
 //      d_v) carrying G in fp32 MFMA accumulators (the columns of G are
-//      independent) in two waves, while two more waves copy the next chunk;
-//      it writes G_c and W (bf16, in the packed order below), dV and
-//      finally dS_0;
-//   4. bwd_grad_kernel, all chunks in parallel (one persistent workgroup
+//      independent) in two waves, while a third copies K, Q and beta of the
+//      chunks ahead and builds their T^T and P^T (T by the forward's
+//      builder) in packed MFMA operand order and a fourth copies dO and
+//      stores dV; it writes G_c and W (bf16, in the packed order below),
+//      the packed T, dV and finally dS_0;
+//   3. bwd_grad_kernel, all chunks in parallel (one persistent workgroup
 //      per CU, the next chunk's inputs fetched during the last two phases):
 //      dQ, dK and dbeta from S_c, G_c, W and the chunk's q/k/v/beta.
 // Numerics as in the forward: bf16 operands, fp32 accumulation; G and the
@@ -139,134 +139,28 @@ __device__ __forceinline__ void copy_flat(__amdgpu_buffer_rsrc_t rs, unsigned ch
 }
 
 // ---------------------------------------------------------------------------
-// 2. prep: packed T, T^T and P^T of one chunk (one workgroup of four waves)
-// ---------------------------------------------------------------------------
-template <int D>
-struct PrepGeo {
-    static constexpr int KS = 0;
-    static constexpr int QS = KS + kC * D * 2;
-    static constexpr int BS = QS + kC * D * 2;
-    static constexpr int TP = BS + kC * 4;
-    static constexpr int BYTES = TP + kPacked * 2;
-};
-
-// The four waves copy K, Q and beta; then wave 0 builds T (K1's builder) while waves
-// 1-3 form the P^T blocks; after a barrier all four gather T^T from the packed T.
-// (One wave per chunk, four chunks per CU by LDS, took 45 us at cfg1.)
-template <int D>
-__global__ __launch_bounds__(256) void bwd_prep_kernel(const uint16_t* __restrict__ q,
-                                                       const uint16_t* __restrict__ k,
-                                                       const float* __restrict__ beta,
-                                                       uint16_t* __restrict__ tp_ws, int T, int H,
-                                                       int n_ch) {
-    using G = PrepGeo<D>;
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    const int pair = blockIdx.x / n_ch, c = blockIdx.x % n_ch;
-    const int seq = pair / H, h = pair % H;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = static_cast<int>(uniform(static_cast<unsigned>(tid >> 6)));
-    const int l16 = lane & 15, lg = lane >> 4;
-    const int base = c * kC, clen = min(kC, T - base);
-    const size_t tstride = static_cast<size_t>(H) * D;
-    const size_t row0 = (static_cast<size_t>(seq) * T + base) * tstride + static_cast<size_t>(h) * D;
-    const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
-    const unsigned n_b = static_cast<unsigned>(((clen - 1) * H + 1) * 4);
-    copy_rows<D>(make_rsrc(k + row0, n_kq), smem + G::KS, kC * D * 2 / 1024,
-                 static_cast<unsigned>(tstride * 2), w, 4, lane);
-    copy_rows<D>(make_rsrc(q + row0, n_kq), smem + G::QS, kC * D * 2 / 1024,
-                 static_cast<unsigned>(tstride * 2), w, 4, lane);
-    if (w == 3)
-        copy_to_lds(make_rsrc(beta + (static_cast<size_t>(seq) * T + base) * H + h, n_b), smem + G::BS, 4,
-                    static_cast<unsigned>(lane * H * 4));
-    wait_copies();
-    __syncthreads();
-
-    uint16_t* Tp = reinterpret_cast<uint16_t*>(smem + G::TP);
-    uint16_t* out = tp_ws + (static_cast<size_t>(pair) * n_ch + c) * 3 * kPacked;
-    if (w == 0) {
-        build_t_packed<D, G::KS, G::BS>(smem, Tp, lane);
-        // packed T as built (a wave's LDS accesses complete in order)
-#pragma unroll
-        for (int x = 0; x < 6; ++x)
-            *reinterpret_cast<u32x4_t*>(out + x * 512 + lane * 8) =
-                *reinterpret_cast<const u32x4_t*>(Tp + x * 512 + lane * 8);
-    } else {
-        // packed P^T: the accumulator tile of Q_j K_i^T (lane: P[16j + 4g + r][16i + l16])
-        // is block (i, j) of P^T in the form the packed store takes; the ten blocks i <= j,
-        // numbered row by row, go to waves 1-3 by number mod 3
-        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(smem + G::KS);
-        const uint16_t* Qs = reinterpret_cast<const uint16_t*>(smem + G::QS);
-        uint16_t* pt = out + 2 * kPacked;
-        const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-        int idx = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int j = i; j < 4; ++j, ++idx) {
-                if (idx % 3 != w - 1) continue;
-                f32x4_t acc = zero;
-#pragma unroll
-                for (int kb = 0; kb < D / 32; ++kb)
-                    acc = mfma32(lds_op_kq<D>(Qs, 16 * j + l16, kb, lg), lds_op_kq<D>(Ks, 16 * i + l16, kb, lg), acc);
-                if (i == j) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[r] = (4 * lg + r >= l16) ? acc[r] : 0.f;
-                }
-                *reinterpret_cast<u32x2_t*>(pt + qblk_u(i, j >> 1) * 512 + lane * 8 + 4 * (j & 1)) = cvt4(acc);
-            }
-        }
-        if (w == 1) {
-            const u32x2_t z2 = {0u, 0u};
-            *reinterpret_cast<u32x2_t*>(pt + qblk_u(1, 0) * 512 + lane * 8) = z2;  // t < 16 <= s
-            *reinterpret_cast<u32x2_t*>(pt + qblk_u(3, 1) * 512 + lane * 8) = z2;  // t < 48 <= s
-        }
-    }
-    __syncthreads();  // the packed T is in LDS
-
-    // packed T^T: lane (g, l16), slot x of block (m, kb) = T[32kb + o(g, x)][16m + l16];
-    // wave w takes blocks w and w + 4
-    auto t_at = [&](int i, int kk) -> uint16_t {  // T[i][kk] from the packed T (0 above the diagonal)
-        if (kk > i) return 0;
-        const int gg = (kk & 15) >> 2, x = (kk & 3) + 4 * ((kk >> 4) & 1);
-        return Tp[qblk(i >> 4, kk >> 5) * 512 + (16 * gg + (i & 15)) * 8 + x];
-    };
-    const int mk[6][2] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}, {2, 1}, {3, 1}};
-#pragma unroll
-    for (int b = 0; b < 6; ++b) {
-        if ((b & 3) != w) continue;
-        const int m = mk[b][0], kb = mk[b][1];
-        const int s = 16 * m + l16;
-        unsigned wds[4];
-#pragma unroll
-        for (int x = 0; x < 8; x += 2) {
-            const int t0 = 32 * kb + (x < 4 ? 4 * lg + x : 12 + 4 * lg + x);
-            wds[x / 2] = static_cast<unsigned>(t_at(t0, s)) | (static_cast<unsigned>(t_at(t0 + 1, s)) << 16);
-        }
-        const u32x4_t v = {wds[0], wds[1], wds[2], wds[3]};
-        *reinterpret_cast<u32x4_t*>(out + kPacked + qblk_u(m, kb) * 512 + lane * 8) = v;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// 3. reverse sweep over chunks: G, W, dV, dS_0
+// 2. reverse sweep over chunks: G, W, T, dV, dS_0
 // ---------------------------------------------------------------------------
 template <int D>
 struct RevGeo {
     static constexpr int KS = 0;
     static constexpr int QS = KS + kC * D * 2;
-    static constexpr int TT = QS + kC * D * 2;  // packed T^T, then packed P^T
+    static constexpr int TT = QS + kC * D * 2;  // packed T^T, then packed P^T (built here)
     static constexpr int PT = TT + kPacked * 2;
     static constexpr int NC = 32;                // columns per workgroup (16 per chain wave)
     static constexpr int DO = PT + kPacked * 2;  // dO tile, fp32 [t][NC], 16-byte chunks swizzled
     static constexpr int BS = DO + kC * NC * 4;
     static constexpr int BUF = BS + kC * 4;
     static constexpr int NBUF = 3;  // the loaders run two chunks ahead
-    static constexpr int BYTES = NBUF * BUF;
-    // copy instructions one loader wave issues per chunk (loader 1 adds beta's)
-    static constexpr int N_KQ = kC * D * 2 / 1024, N_TP = 4 * kPacked / 1024, N_DO = kC * NC * 4 / 1024;
-    static constexpr int COPIES = N_KQ / 2 * 2 + N_TP / 2 + N_DO / 2;
-    static_assert(N_KQ % 2 == 0 && N_TP % 2 == 0 && N_DO % 2 == 0, "copies split evenly");
-    static_assert(COPIES + 1 <= 63, "vmcnt range");
+    // two ints: the oldest chunk whose K and beta, and whose Q, have landed in LDS
+    static constexpr int FLAG = NBUF * BUF;
+    static constexpr int BYTES = FLAG + 16;
+    static constexpr int THREADS = 320;  // five waves
+    // copy instructions per chunk: K, Q and beta (wave 2), dO (wave 4)
+    static constexpr int N_KQ = kC * D * 2 / 1024, N_DO = kC * NC * 4 / 1024;
+    // most memory operations a wave has in flight (vmcnt counts to 63): wave 2 one chunk's
+    // copies, wave 4 two chunks' dO copies and one chunk's dV stores
+    static_assert(2 * N_KQ + 1 <= 63 && 3 * N_DO <= 63, "vmcnt range");
     static_assert(BUF % 16 == 0 && BYTES <= 160 * 1024, "layout");
 };
 // dO tile (rows of 32 fp32 = 128 bytes, half the banks): 16-byte chunk p of token row t
@@ -276,9 +170,9 @@ struct RevGeo {
 __device__ __forceinline__ int fdo(int t) { return 4 * ((t >> 2) & 1); }
 
 template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_rev_kernel(
+__global__ __launch_bounds__(320) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_rev_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const float* __restrict__ beta,
-    const float* __restrict__ go, const float* __restrict__ gs, const uint16_t* __restrict__ tp_ws,
+    const float* __restrict__ go, const float* __restrict__ gs, uint16_t* __restrict__ t_ws,
     uint16_t* __restrict__ g_hist, uint16_t* __restrict__ w_hist, float* __restrict__ gv,
     float* __restrict__ gs0, int n_pairs, int T, int H, int n_ch, int n_tiles) {
     using G = RevGeo<D>;
@@ -294,51 +188,137 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = static_cast<int>(uniform(static_cast<unsigned>(tid >> 6)));
     const int l16 = lane & 15, lg = lane >> 4;
-    // waves 0 and 1 carry G (16 columns each) and store; waves 2 and 3 only copy the next
-    // chunk into LDS and wait for it, so no wave waits on the others' stores
-    const bool chain = w < 2;
+    // waves 0 and 1 (the chain) carry G (16 columns each) and store G and W.  For the chunks
+    // ahead, wave 2 copies K, Q and beta and marks each chunk whose copies have landed in an
+    // LDS flag; wave 3 then builds the chunk's T^T (and T), wave 4 its P^T, and wave 4 also
+    // copies dO and stores dV.  No chain wave waits on a copy, a build or a dV store, and no
+    // builder's MFMA work queues behind its own copies.
     const int j = tile * G::NC + 16 * (w & 1) + l16;  // this lane's column of G (chain waves)
     const int jt = j >> 4;                             // its 16-column tile
     const size_t tstride = static_cast<size_t>(H) * D;
     const size_t sbase = static_cast<size_t>(pair) * D * D;
 
-    f32x4_t Gm[D / 16];
-#pragma unroll
-    for (int md = 0; md < D / 16; ++md)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            Gm[md][r] = (chain && gs) ? gs[sbase + static_cast<size_t>(s_row_d(md, 4 * lg + r)) * D + j] : 0.f;
-    bf16x8_t Gb[D / 32];
-#pragma unroll
-    for (int kb = 0; kb < D / 32; ++kb) Gb[kb] = acc_to_b(Gm[2 * kb], Gm[2 * kb + 1]);
-
     const int col0 = tile * G::NC;
     auto buf = [&](int c) { return smem + ((n_ch - 1 - c) % G::NBUF) * G::BUF; };
-    auto issue = [&](int c) {
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    auto put = [&](uint16_t* dst, int x, f32x4_t lo, f32x4_t hi) {
+        *reinterpret_cast<bf16x8_t*>(dst + x * 512 + lane * 8) = acc_to_b(lo, hi);
+    };
+    // Wave 2 copies K, beta and then Q of chunk c; wave 4 its dO (rows past the chunk's end
+    // fall outside the buffer ranges and read as zeros)
+    auto issue_kq = [&](int c) {
         const int base = c * kC, clen = min(kC, T - base);
         const size_t row0 = (tok0 + base) * tstride + static_cast<size_t>(h) * D;
         const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
         unsigned char* b = uniform_ptr(buf(c));
-        const int lw = w - 2;  // loader index
-        copy_rows<D>(make_rsrc(k + row0, n_kq), b + G::KS, kC * D * 2 / 1024,
-                     static_cast<unsigned>(tstride * 2), lw, 2, lane);
-        copy_rows<D>(make_rsrc(q + row0, n_kq), b + G::QS, kC * D * 2 / 1024,
-                     static_cast<unsigned>(tstride * 2), lw, 2, lane);
-        copy_flat(make_rsrc(tp_ws + (static_cast<size_t>(pair) * n_ch + c) * 3 * kPacked + kPacked,
-                            4 * kPacked),
-                  b + G::TT, 4 * kPacked / 1024, lw, 2, lane);
+        copy_rows<D>(make_rsrc(k + row0, n_kq), b + G::KS, G::N_KQ, static_cast<unsigned>(tstride * 2), 0, 1, lane);
+        copy_to_lds(make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4)),
+                    b + G::BS, 4, static_cast<unsigned>(lane * H * 4));
+        copy_rows<D>(make_rsrc(q + row0, n_kq), b + G::QS, G::N_KQ, static_cast<unsigned>(tstride * 2), 0, 1, lane);
+    };
+    auto issue_do = [&](int c) {
+        const int base = c * kC, clen = min(kC, T - base);
+        const size_t row0 = (tok0 + base) * tstride + static_cast<size_t>(h) * D;
+        unsigned char* b = uniform_ptr(buf(c));
         // dO (fp32): rows of NC values from column col0; a NULL go reads as zeros
         const unsigned n_do = go ? static_cast<unsigned>(((clen - 1) * tstride + G::NC) * 4) : 0u;
         const __amdgpu_buffer_rsrc_t rd = make_rsrc(go ? go + row0 + col0 : go, n_do);
-        for (int ii = lw; ii < kC * G::NC * 4 / 1024; ii += 2) {
+        for (int ii = 0; ii < G::N_DO; ++ii) {
             const int pos = 1024 * ii + 16 * lane;  // byte in the LDS tile
             const int r = pos / (G::NC * 4), p = (pos % (G::NC * 4)) / 16;
             copy_to_lds(rd, b + G::DO + 1024 * ii, 16,
                         static_cast<unsigned>(r * tstride * 4) + 16u * static_cast<unsigned>(p ^ fdo(r)));
         }
-        if (lw == 1)
-            copy_to_lds(make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4)),
-                        b + G::BS, 4, static_cast<unsigned>(lane * H * 4));
+    };
+    // Wave 3: T^T of chunk c, from its K and beta in LDS, into the chunk's buffer in packed
+    // operand order, and T itself (packed, the gradient kernel's operand) into tp.  The
+    // forward's builder gives T's blocks both
+    // transposed (tb, for T) and not (tn): T^T's packed block (m, kb) is T_(2kb, m) over
+    // T_(2kb+1, m) as untransposed tiles, a zero tile where 2kb < m.
+    auto build_t = [&](int c, u32x4_t (&tp)[6]) {
+        unsigned char* b = uniform_ptr(buf(c));
+        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(b + G::KS);
+        const float* Bs = reinterpret_cast<const float*>(b + G::BS);
+        bf16x8_t f[4][D / 32];
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) f[r][kb] = lds_op_kq<D>(Ks, 16 * r + l16, kb, lg);
+        f32x4_t br4[4];
+        float bc[4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            br4[x] = *reinterpret_cast<const f32x4_t*>(Bs + 16 * x + 4 * lg);
+            bc[x] = Bs[16 * x + l16];
+        }
+        f32x4_t tb[10], tn[10];
+        t_blocks<D>(f, bc, br4, lane, tb, tn);
+        // block (i, j), j <= i, is number i (i + 1) / 2 + j of tb and tn
+        uint16_t* TTp = reinterpret_cast<uint16_t*>(b + G::TT);
+        put(TTp, qblk_u(0, 0), tn[0], tn[1]);  // T00, T10
+        put(TTp, qblk_u(0, 1), tn[3], tn[6]);  // T20, T30
+        put(TTp, qblk_u(1, 0), zero, tn[2]);   // T01 = 0, T11
+        put(TTp, qblk_u(1, 1), tn[4], tn[7]);  // T21, T31
+        put(TTp, qblk_u(2, 1), tn[5], tn[8]);  // T22, T32
+        put(TTp, qblk_u(3, 1), zero, tn[9]);   // T23 = 0, T33
+        // packed T (block q = qblk(i, kb) holds T_(i, 2kb) and T_(i, 2kb+1) transposed)
+        auto pk = [](f32x4_t lo, f32x4_t hi) { return __builtin_bit_cast(u32x4_t, acc_to_b(lo, hi)); };
+        tp[qblk(0, 0)] = pk(tb[0], zero);
+        tp[qblk(1, 0)] = pk(tb[1], tb[2]);
+        tp[qblk(2, 0)] = pk(tb[3], tb[4]);
+        tp[qblk(2, 1)] = pk(tb[5], zero);
+        tp[qblk(3, 0)] = pk(tb[6], tb[7]);
+        tp[qblk(3, 1)] = pk(tb[8], tb[9]);
+    };
+    // the first tile's workgroup writes T of chunk c for the gradient kernel
+    auto store_t = [&](int c, const u32x4_t (&tp)[6]) {
+        if (tile != 0) return;
+        uint16_t* dst = t_ws + (static_cast<size_t>(pair) * n_ch + c) * kPacked;
+#pragma unroll
+        for (int x = 0; x < 6; ++x) *reinterpret_cast<u32x4_t*>(dst + x * 512 + lane * 8) = tp[x];
+    };
+    // Wave 4: P^T of chunk c from its K and Q in LDS.  The accumulator tile of Q_j K_i^T
+    // (lane: P[16j + 4g + r][16i + l16]) is the (i, j) part of P^T's packed block (i, j / 2);
+    // parts with j < i are zero.  Two column blocks j at a time, stored as soon as formed.
+    auto build_p = [&](int c) {
+        unsigned char* b = uniform_ptr(buf(c));
+        const uint16_t* Ks = reinterpret_cast<const uint16_t*>(b + G::KS);
+        const uint16_t* Qs = reinterpret_cast<const uint16_t*>(b + G::QS);
+        uint16_t* PTp = reinterpret_cast<uint16_t*>(b + G::PT);
+        bf16x8_t f[4][D / 32];
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) f[r][kb] = lds_op_kq<D>(Ks, 16 * r + l16, kb, lg);
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) {
+            f32x4_t pa[4][2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pa[i][0] = pa[i][1] = zero;
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int j = 2 * jb + jj;
+#pragma unroll
+                for (int kb = 0; kb < D / 32; ++kb) {
+                    const bf16x8_t qa = lds_op_kq<D>(Qs, 16 * j + l16, kb, lg);
+#pragma unroll
+                    for (int i = 0; i <= j; ++i) pa[i][jj] = mfma32(qa, f[i][kb], pa[i][jj]);
+                }
+            }
+#pragma unroll
+            for (int i = 2 * jb; i < 2 * jb + 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) pa[i][i - 2 * jb][r] = (4 * lg + r >= l16) ? pa[i][i - 2 * jb][r] : 0.f;
+            if (jb == 0) {
+                put(PTp, qblk_u(0, 0), pa[0][0], pa[0][1]);
+                put(PTp, qblk_u(1, 0), zero, pa[1][1]);
+            } else {
+                put(PTp, qblk_u(0, 1), pa[0][0], pa[0][1]);
+                put(PTp, qblk_u(1, 1), pa[1][0], pa[1][1]);
+                put(PTp, qblk_u(2, 1), pa[2][0], pa[2][1]);
+                put(PTp, qblk_u(3, 1), zero, pa[3][1]);
+            }
+        }
     };
     // dO as a B operand over tokens 32kb + {4g..4g+3, 16+4g..16+4g+3}, column j
     const int jl = 16 * (w & 1) + l16;  // column within the tile
@@ -353,75 +333,140 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         return as_b(v);
     };
 
-    // One LDS-only barrier per chunk: by then the loaders have waited for the copies of the
-    // chunk the chain takes next, and the chain's stores need not complete.  The loaders
-    // keep the chunk after that in flight: a loader wave issues only these copies and,
-    // before them, its dV stores, so waiting until G::COPIES (+1 for the beta copy) are
-    // outstanding completes at least the older chunk's copies (loads complete in order).
-    auto wait_older = [&] {
-        if (w == 3)
-            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(G::COPIES + 1) : "memory");
-        else
-            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(G::COPIES) : "memory");
-    };
-    if (n_ch > 0) {
-        if (!chain) {
-            issue(n_ch - 1);
-            if (n_ch > 1) {
-                issue(n_ch - 2);
-                wait_older();
-            } else {
-                wait_copies();
-            }
-        }
-        lds_barrier();
-    }
-    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-    // Stores that scatter over many rows stall a chain wave while the loaders' copies are in
-    // flight.  So G and W go out in packed order (one contiguous block per instruction), W
-    // at the start of the next iteration next to G; and dV, whose rows are 64 bytes per
-    // chain wave, is staged in the chunk's dO space (dead once the chain has its dO
-    // operands; each wave overwrites only the bytes of its own dO columns) and stored by the
-    // loader waves in whole 128-byte rows in the next iteration, before that buffer is
-    // refilled.
+    // Stores that scatter over many rows stall a chain wave while copies are in flight.  So
+    // G and W go out in packed order (one contiguous block per instruction), W at the start
+    // of the next iteration next to G; and dV, whose rows are 64 bytes per chain wave, is
+    // staged in the chunk's dO space (dead once the chain has its dO operands; each wave
+    // overwrites only the bytes of its own dO columns) and stored by wave 4 in whole 128-byte
+    // rows in the next iteration, before that buffer is refilled.
     u32x2_t w_pend[4];
     uint16_t* wp_pend = nullptr;
     auto store_w = [&] {
 #pragma unroll
         for (int m = 0; m < 4; ++m) *reinterpret_cast<u32x2_t*>(wp_pend + m * 256) = w_pend[m];
     };
-    // dV of chunk cc from its staging tile (rows of 32 fp32 in the dO tile's order) to gv;
-    // rows past the chunk's end fall outside the buffer range and are dropped (offsets
-    // fit 32 bits since H D <= 2^23)
-    auto store_dv = [&](int cc) {
+    // dV of chunk cc from its staging tile (rows of 32 fp32 in the dO tile's order) to gv, in
+    // two steps so that copies into the same buffer can be issued between them (the reads
+    // complete first); rows past the chunk's end fall outside the buffer range and are
+    // dropped (offsets fit 32 bits since H D <= 2^23)
+    auto read_dv = [&](int cc, u32x4_t (&x)[G::N_DO]) {
+        const float* Ds = reinterpret_cast<const float*>(buf(cc) + G::DO);
+#pragma unroll
+        for (int ii = 0; ii < G::N_DO; ++ii) {
+            const int r = 8 * ii + (lane >> 3), p = lane & 7;
+            x[ii] = *reinterpret_cast<const u32x4_t*>(Ds + r * G::NC + 4 * (p ^ fdo(r)));
+        }
+        lds_wait_all();
+#pragma unroll
+        for (int ii = 0; ii < G::N_DO; ++ii) tie(x[ii]);
+    };
+    auto write_dv = [&](int cc, const u32x4_t (&x)[G::N_DO]) {
         const int cb = cc * kC, cl = min(kC, T - cb);
         const __amdgpu_buffer_rsrc_t rv =
             make_rsrc(gv + (tok0 + cb) * tstride + static_cast<size_t>(h) * D + col0,
                       static_cast<unsigned>(((cl - 1) * tstride + G::NC) * 4));
-        const float* Ds = reinterpret_cast<const float*>(buf(cc) + G::DO);
 #pragma unroll
-        for (int ii = w - 2; ii < kC * G::NC * 4 / 1024; ii += 2) {
+        for (int ii = 0; ii < G::N_DO; ++ii) {
             const int r = 8 * ii + (lane >> 3), p = lane & 7;
-            const u32x4_t x = *reinterpret_cast<const u32x4_t*>(Ds + r * G::NC + 4 * (p ^ fdo(r)));
-            __builtin_amdgcn_raw_buffer_store_b128(x, rv, static_cast<unsigned>((r * tstride + 4 * p) * 4), 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(x[ii], rv, static_cast<unsigned>((r * tstride + 4 * p) * 4), 0, 0);
         }
     };
-    for (int c = n_ch - 1; c >= 0; --c) {
-        if (!chain) {
-            if (c > 0) {  // make chunk c - 1 ready; put c - 2 in flight
-                if (c < n_ch - 1) store_dv(c + 1);  // staged in the last iteration; c + 1 and c - 2 share a buffer
-                if (c >= 2) {
-                    issue(c - 2);
-                    wait_older();
-                } else {
-                    wait_copies();
-                }
-                lds_barrier();
-            } else if (n_ch > 1) {
-                store_dv(1);
-            }
-            continue;
+    // One LDS-only barrier per chunk: by then the chunk the chain takes next is in LDS with
+    // its T^T and P^T, and the chain's stores need not complete.  In iteration c (the chain
+    // on chunk c) wave 2 waits for chunk c - 1's copies (issued an iteration earlier),
+    // marking K and beta as soon as they have landed and then Q, and issues chunk c - 2's;
+    // wave 3 waits for the first mark and builds chunk c - 1's T^T, wave 4 for the second
+    // and builds its P^T.  The iteration before the chain's first (c = n_ch) does the
+    // same for chunk n_ch - 1.  Each role runs its own loop, with the same barriers, so that
+    // no value of the chain is live through the builders' code.
+    // (an LDS pointer, so that its accesses are ds_ reads and writes, not flat ones, which
+    // would wait on the vector memory counter too)
+    typedef __attribute__((address_space(3))) volatile int lds_int;
+    lds_int* flag = (lds_int*)(smem + G::FLAG);  // [0]: K and beta, [1]: Q
+    if (w == 2 && lane < 2) flag[lane] = n_ch;   // nothing landed yet
+    lds_barrier();
+    // Waves 3 and 4: wait until chunk c's K, Q and beta have landed.  Wave 2 marks every
+    // chunk in turn, after its vmcnt wait for the copies and before the barrier that ends
+    // the iteration, so the wait ends; its bound only keeps it finite by construction.
+    auto wait_mark = [&](int c, int which) {
+        for (int spin = 0; spin < (1 << 20); ++spin) {
+            if (__builtin_amdgcn_readfirstlane(flag[which]) <= c) break;
+            __builtin_amdgcn_s_sleep(1);
         }
+    };
+    if (w == 2) {
+        if (n_ch > 0) issue_kq(n_ch - 1);
+        for (int c = n_ch; c > 0; --c) {
+            wait_vm_n<G::N_KQ>();            // chunk c - 1's K and beta (its Q copies follow)
+            if (lane == 0) flag[0] = c - 1;
+            wait_copies();                   // and its Q
+            if (lane == 0) flag[1] = c - 1;
+            if (c >= 2) issue_kq(c - 2);     // into chunk c + 1's buffer
+            lds_barrier();
+        }
+        if (n_ch > 0) lds_barrier();
+        return;
+    }
+    if (w == 3) {
+        u32x4_t tp[6];
+        for (int c = n_ch; c > 0; --c) {
+            wait_mark(c - 1, 0);
+            build_t(c - 1, tp);
+            wait_copies();                   // the last chunk's T stores, long complete
+            store_t(c - 1, tp);
+            lds_barrier();
+        }
+        if (n_ch > 0) lds_barrier();
+        return;
+    }
+    if (w == 4) {
+        u32x4_t x[G::N_DO];
+        if (n_ch > 0) issue_do(n_ch - 1);
+        for (int c = n_ch; c > 0; --c) {
+            if (c <= n_ch - 2) {             // dV of chunk c + 1, whose buffer chunk c - 2 takes
+                read_dv(c + 1, x);
+                if (c >= 2) issue_do(c - 2);
+                write_dv(c + 1, x);
+            } else if (c >= 2) {
+                issue_do(c - 2);
+            }
+            wait_mark(c - 1, 1);
+            build_p(c - 1);
+            // chunk c - 1's dO (issued an iteration earlier): issued after it only chunk c - 2's
+            // copies, then chunk c + 1's dV stores (they complete in issue order)
+            const bool dv = c <= n_ch - 2;
+            if (c >= 2 && dv)
+                wait_vm_n<2 * G::N_DO>();
+            else if (c >= 2 || dv)
+                wait_vm_n<G::N_DO>();
+            else
+                wait_copies();
+            lds_barrier();
+        }
+        if (n_ch > 1) {
+            read_dv(1, x);
+            write_dv(1, x);
+        }
+        if (n_ch > 0) {
+            lds_barrier();  // chunk 0's dV is staged
+            read_dv(0, x);
+            write_dv(0, x);
+        }
+        return;
+    }
+    // chain waves
+    if (n_ch > 0) lds_barrier();  // chunk n_ch - 1 is ready
+    f32x4_t Gm[D / 16];
+#pragma unroll
+    for (int md = 0; md < D / 16; ++md)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            Gm[md][r] = gs ? gs[sbase + static_cast<size_t>(s_row_d(md, 4 * lg + r)) * D + j] : 0.f;
+    bf16x8_t Gb[D / 32];
+#pragma unroll
+    for (int kb = 0; kb < D / 32; ++kb) Gb[kb] = acc_to_b(Gm[2 * kb], Gm[2 * kb + 1]);
+
+    for (int c = n_ch - 1; c >= 0; --c) {
         unsigned char* b = buf(c);
         const uint16_t* Ks = reinterpret_cast<const uint16_t*>(b + G::KS);
         const uint16_t* Qs = reinterpret_cast<const uint16_t*>(b + G::QS);
@@ -528,22 +573,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     if (n_ch > 0) {
         lds_barrier();  // chunk 0's dV is staged
-        if (chain)
-            store_w();
-        else
-            store_dv(0);
+        store_w();
     }
-    if (chain) {
 #pragma unroll
-        for (int md = 0; md < D / 16; ++md)
+    for (int md = 0; md < D / 16; ++md)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                gs0[sbase + static_cast<size_t>(s_row_d(md, 4 * lg + r)) * D + j] = Gm[md][r];
-    }
+        for (int r = 0; r < 4; ++r) gs0[sbase + static_cast<size_t>(s_row_d(md, 4 * lg + r)) * D + j] = Gm[md][r];
 }
 
 // ---------------------------------------------------------------------------
-// 4. per-chunk gradients dQ, dK, dbeta (all chunks in parallel)
+// 3. per-chunk gradients dQ, dK, dbeta (all chunks in parallel)
 // ---------------------------------------------------------------------------
 template <int D>
 struct GradGeo {
@@ -655,7 +694,7 @@ __global__ __launch_bounds__(256) void bwd_grad_kernel(
         copy_flat(make_rsrc(w_hist + r.cidx * D * kC, D * kC * 2), smem + G::WT, D * kC * 2 / 1024, w, 4, lane);
     };
     auto copy_t = [&](const Ref& r) {
-        copy_flat(make_rsrc(tp_ws + r.cidx * 3 * kPacked, kPacked * 2), smem + G::TP, kPacked * 2 / 1024, w, 4, lane);
+        copy_flat(make_rsrc(tp_ws + r.cidx * kPacked, kPacked * 2), smem + G::TP, kPacked * 2 / 1024, w, 4, lane);
     };
     // K and beta, copied while phase 2 runs: K over the K that phase 1 read last, beta into
     // the other buffer (phase 3 still reads the current one)
@@ -1051,15 +1090,11 @@ hipError_t launch_d(const BwdArgs& a, hipStream_t st) {
     if (n_ch > 0) {
         ChunkedArgs f{q, k, v, a.beta, a.s0, nullptr, nullptr, nullptr, a.n_pairs / a.H, a.T, a.H, D, false, 0};
         if ((e = launch_chunked_states(f, s_hist, st)) != hipSuccess) return e;
-        if ((e = set_lds(bwd_prep_kernel<D>, PrepGeo<D>::BYTES)) != hipSuccess) return e;
-        hipLaunchKernelGGL(bwd_prep_kernel<D>, dim3(static_cast<unsigned>(a.n_pairs) * n_ch), dim3(256),
-                           PrepGeo<D>::BYTES, st, q, k, a.beta, tp, a.T, a.H, n_ch);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     const int n_tiles = D / RevGeo<D>::NC;
     const int slots = (a.n_pairs + 7) / 8;
     if ((e = set_lds(bwd_rev_kernel<D>, RevGeo<D>::BYTES)) != hipSuccess) return e;
-    hipLaunchKernelGGL(bwd_rev_kernel<D>, dim3(static_cast<unsigned>(slots * 8 * n_tiles)), dim3(256),
+    hipLaunchKernelGGL(bwd_rev_kernel<D>, dim3(static_cast<unsigned>(slots * 8 * n_tiles)), dim3(RevGeo<D>::THREADS),
                        RevGeo<D>::BYTES, st, q, k, a.beta, a.go, a.gs, tp, g_hist, w_hist, a.gv, a.gs0,
                        a.n_pairs, a.T, a.H, n_ch, n_tiles);
     if ((e = hipGetLastError()) != hipSuccess || n_ch == 0) return e;
@@ -1087,7 +1122,7 @@ ChunkedBwdWs chunked_bwd_ws(long n_pairs, int T, int D) {
     w.g_hist = w.s_hist + n * D * D * 2;
     w.w_hist = w.g_hist + n * D * D * 2;
     w.tp = w.w_hist + n * D * kC * 2;
-    w.bytes = w.tp + n * 3 * kPacked * 2;
+    w.bytes = w.tp + n * kPacked * 2;
     return w;
 }
 

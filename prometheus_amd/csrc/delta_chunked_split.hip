@@ -120,8 +120,8 @@ __global__ __launch_bounds__(256) void delta_t_prep_kernel(const uint16_t* __res
             br4[b][r] = __uint_as_float(
                 __builtin_amdgcn_raw_buffer_load_b32(rb, static_cast<unsigned>((16 * b + 4 * lg + r) * H * 4), 0, 0));
     }
-    f32x4_t tb[10];
-    t_blocks<D>(f, bc, br4, lane, tb);
+    f32x4_t tb[10], tn[10];
+    t_blocks<D>(f, bc, br4, lane, tb, tn);
     // T'' = -T diag(beta): block (i, j) holds T[16i + l16][16j + 4g + r] in this lane, so its
     // columns scale by -beta of token 16j + 4g + r
     {

@@ -340,8 +340,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             bc[b] = Bs[16 * b + l16];
             br4[b] = *reinterpret_cast<const f32x4_t*>(Bs + 16 * b + 4 * lg);
         }
-        f32x4_t tb[10];
-        t_from_gram(gd, gdt, gu, bc, br4, lane, tb);
+        f32x4_t tb[10], tn[10];
+        t_from_gram(gd, gdt, gu, bc, br4, lane, tb, tn);
         // block (i, j) holds T[16i + l16][16j + 4g + r] in this lane
         constexpr int ib[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3}, jb[10] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
         uint16_t* tt = reinterpret_cast<uint16_t*>(out + W::TT);

@@ -269,10 +269,15 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // A'[16b + 4g + r][16b + l16]), gdt[b] the same block transposed (A'[16b + l16][16b + 4g
 // + r]), and gu[x] the off-diagonal block (k, i), k < i, in the order (0,1) (0,2) (1,2)
 // (0,3) (1,3) (2,3), as the tile of A'[16i + l16][16k + 4g + r] at (g, l16).  t_blocks
-// passes K K^T (gdt = gd).
+// passes K K^T (gdt = gd).  tn gets the same blocks untransposed (lane (g, l16) holds
+// T[16i + 4g + r][16j + l16], the diagonal blocks with exact zeros above the diagonal):
+// two of those stacked, T_{2kb, m} over T_{2kb+1, m}, are block (m, kb) of T^T in packed
+// operand order (acc_to_b).  Callers that do not read tn leave its products to dead-code
+// elimination.
 __device__ __forceinline__ void t_from_gram(const f32x4_t (&gd)[4], const f32x4_t (&gdt)[4],
                                             const f32x4_t (&gu)[6], const float (&bc)[4],
-                                            const f32x4_t (&br4)[4], int lane, f32x4_t (&tb)[10]) {
+                                            const f32x4_t (&br4)[4], int lane, f32x4_t (&tb)[10],
+                                            f32x4_t (&tn)[10]) {
     const int l16 = lane & 15, lg = lane >> 4;
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
     const EyeBits eyeb = eye_bits(lane);
@@ -366,11 +371,24 @@ __device__ __forceinline__ void t_from_gram(const f32x4_t (&gd)[4], const f32x4_
     tb[2] = ddt[1];
     tb[5] = ddt[2];
     tb[9] = ddt[3];
+    // mfma(cdt_i, Z_ij) = T_ij: the products above with the operands swapped (the same
+    // products summed in the same order, so each element has the bits of tb's)
+    tn[1] = mfma16(cdt1, z10, zero);
+    tn[4] = mfma16(cdt2, z21, zero);
+    tn[8] = mfma16(cdt3, z32, zero);
+    tn[3] = mfma16(cdt2, z20, zero);
+    tn[7] = mfma16(cdt3, z31, zero);
+    tn[6] = mfma16(cdt3, z30, zero);
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tn[b * (b + 3) / 2][r] = (4 * lg + r >= l16) ? dd[b][r] : 0.f;
 }
 
 template <int D>
 __device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const float (&bc)[4],
-                                         const f32x4_t (&br4)[4], int lane, f32x4_t (&tb)[10]) {
+                                         const f32x4_t (&br4)[4], int lane, f32x4_t (&tb)[10],
+                                         f32x4_t (&tn)[10]) {
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
     // G = K K^T: diagonal tiles gd[b] and upper tiles gu(k, i), k < i
     f32x4_t gd[4], gu[6];
@@ -389,7 +407,7 @@ __device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const f
         gu[4] = mfma32(f[1][kb], f[3][kb], gu[4]);  // (1,3)
         gu[5] = mfma32(f[2][kb], f[3][kb], gu[5]);  // (2,3)
     }
-    t_from_gram(gd, gd, gu, bc, br4, lane, tb);
+    t_from_gram(gd, gd, gu, bc, br4, lane, tb, tn);
 }
 
 // t_blocks for one chunk by one wave from LDS: K token rows in the swizzled tile at
@@ -412,8 +430,8 @@ __device__ __forceinline__ void build_t_packed(const unsigned char* rb, uint16_t
         br4[b] = *reinterpret_cast<const f32x4_t*>(Bs + 16 * b + 4 * lg);
         bc[b] = Bs[16 * b + l16];
     }
-    f32x4_t tb[10];
-    t_blocks<D>(f, bc, br4, lane, tb);
+    f32x4_t tb[10], tn[10];
+    t_blocks<D>(f, bc, br4, lane, tb, tn);
     store_packed_t(Tp, 0, 0, tb[0], lane);
     store_packed_t(Tp, 1, 0, tb[1], lane);
     store_packed_t(Tp, 1, 1, tb[2], lane);

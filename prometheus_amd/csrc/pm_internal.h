@@ -196,7 +196,7 @@ hipError_t launch_bwd(const BwdArgs& a, hipStream_t st);
 // H).  a.workspace is a byte buffer of chunked_bwd_ws(...).bytes bytes (16-byte
 // aligned) holding, per chunk of every (b, h), the start state and the end
 // gradient of the state (bf16 rows of S^T and G^T), W (bf16 rows of W^T) and
-// the packed T, T^T, P^T.
+// the packed T.
 struct ChunkedBwdWs {
     size_t s_hist, g_hist, w_hist, tp, bytes;
 };

@@ -113,7 +113,7 @@ def _per_token_ws(b, t, h, d):
 
 
 def _chunked_ws(b, t, h, d):
-    return 2 * b * h * (-(-t // 64)) * (2 * d * d + 64 * d + 9216)
+    return 2 * b * h * (-(-t // 64)) * (2 * d * d + 64 * d + 3072)
 
 
 def _f32_chunked_ws(b, t, h, d):

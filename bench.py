@@ -8,6 +8,10 @@ B=4 H=16 T=4096 d_k=d_v=128, bf16 q/k/v (q, k L2-normalised), fp32 beta,
 zero initial state, fp32 O and final S, chunk 64. Inputs are resident in
 HBM before timing starts; two input sets alternate so that consecutive
 steps never find their 201 MB of inputs in the 256 MB Infinity Cache.
+The shader clock ramps up over the first ~150 calls after the GPU idles, so
+the default warm-up (200 steps) and each later leg's own warm-up run past
+it, and the CPU work (the baseline and the parity replays) runs after every
+GPU leg, from host copies of the outputs it checks.
 
 Prints ONE JSON line (the driver's contract) with ``roofline`` for the
 forward kernel (HBM-bound at this shape: 340.8 MB vs 47.6 GFLOP) and
@@ -329,14 +333,16 @@ def time_cfg2(torch, lib, _native, synth, dev, stream, calls=10):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    # the shader clock ramps up over the first ~150 calls after idle (measured: rounds of 10
+    # calls at 128-137 us, settling at 109-110 us), so the default warm-up covers the ramp
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--decode-steps", type=int, default=64)
     ap.add_argument("--gated-calls", type=int, default=10,
                     help="timed pm_gated_delta_fwd and pm_kda_delta_fwd calls at cfg1 (0 skips)")
     ap.add_argument("--model-calls", type=int, default=2,
                     help="timed pm_linear_attention calls at the cfg1 shape (0 skips)")
-    ap.add_argument("--bwd-steps", type=int, default=3,
+    ap.add_argument("--bwd-steps", type=int, default=10,
                     help="timed calls of the backward at cfg1 (0 skips it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-long-configs", dest="long_configs", action="store_false",
@@ -499,48 +505,12 @@ def main():
         cfg2 = time_cfg2(torch, lib, _native, synth, dev, stream)
     launch(last)  # the output the parity check reads
     torch.cuda.synchronize()
-
-    # parity of the timed output against the C restatement (which is also the CPU baseline)
-    cpu = None
-    parity = None
+    # host copies for the CPU baseline and its parity check, which run after every GPU leg
+    # (an idle GPU drops its clock, and the legs after a long CPU phase would time the ramp)
+    host_o = host_s = None
     if not args.no_cpu_baseline:
-        from oracle import cref
-
-        q, k, v, beta = sets[last]
-        hq, hk, hv, hb = bits(q), bits(k), bits(v), beta.cpu().numpy()
-        threads = cpu_threads()
-        print(f"[bench] CPU baseline on {threads} threads", file=sys.stderr, flush=True)
-        cref.delta_fwd(hq[:, :64], hk[:, :64], hv[:, :64], hb[:, :64], None, threads=threads)
-        # the full batch, repeated for about CPU_SAMPLE_S seconds of CPU work
-        t1 = time.perf_counter()
-        e_o, e_s = cref.delta_fwd(hq, hk, hv, hb, None, threads=threads)
-        reps = 1
-        while time.perf_counter() - t1 < CPU_SAMPLE_S and reps < 1000:
-            cref.delta_fwd(hq, hk, hv, hb, None, threads=threads)
-            reps += 1
-        cpu_s = (time.perf_counter() - t1) / reps
-        got_o, got_s = o.cpu().numpy(), s.cpu().numpy()
-        rel = lambda a, b: float(np.linalg.norm((a - b).ravel()) / np.linalg.norm(b.ravel()))  # noqa
-        parity = {"rel_l2_o": rel(got_o, e_o), "rel_l2_s": rel(got_s, e_s), "bound": 2e-2}
-        parity["ok"] = parity["rel_l2_o"] <= 2e-2 and parity["rel_l2_s"] <= 2e-2
-        cpu = {"value": tokens / cpu_s, "unit": "tokens/s", "cores": threads, "kind": "port",
-               "sample": f"full cfg1 batch (B4 T4096 H16 D128, bf16 inputs upcast to fp32), "
-                         f"{reps} repeats, {cpu_s:.3f} s each; C restatement of the reference's per-token rank-1 "
-                         f"recurrence (oracle/delta_ref.c), OpenMP over 64 (b,h) sequences",
-               "cpu_model": cpu_model(),
-               "affinity_cpus": len(os.sched_getaffinity(0)),
-               "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
-               "threads_used": threads,
-               "threads_rule": "OMP_NUM_THREADS when set (the box's CPU share), else the affinity count"}
-        # the other BASELINE configurations on the same CPU path, per call / per step
-        x0 = synth.fwd_inputs((1, 256, 4, 64), seed=0, dtype="fp32")
-        t1 = time.perf_counter()
-        reps0 = 0
-        while time.perf_counter() - t1 < 1.0:
-            cref.delta_fwd(x0.q, x0.k, x0.v, x0.beta, None, threads=threads)
-            reps0 += 1
-        cpu["cfg0_ms_per_call"] = (time.perf_counter() - t1) * 1e3 / reps0
-        cpu["cfg0_tokens_per_s"] = 256 / ((time.perf_counter() - t1) / reps0)
+        host_o, host_s = o.cpu().numpy(), s.cpu().numpy()
+        host_in = tuple(bits(x) for x in sets[last][:3]) + (sets[last][3].cpu().numpy(),)
 
     # decode step, cfg4: B256 H32 D128, fp32 state updated in place, 64 steps
     Bd, Hd = 256, 32
@@ -587,27 +557,10 @@ def main():
                      "frac": dbytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                      "traffic": dtraffic},
     }
-    if state0_host is not None:
-        # every step the GPU ran (4 untimed + the timed ones), replayed on the C restatement
-        from oracle import cref
-
-        threads = cpu_threads()
-        s_ref = state0_host
-        htoks = [(bits(a), bits(b_), bits(c_), d_.cpu().numpy()) for a, b_, c_, d_ in toks]
-        n_all = 4 + args.decode_steps
-        t1 = time.perf_counter()
-        for i in range(n_all):
-            e_od = cref.delta_step(s_ref, *htoks[i % 2], threads=threads)
-        cpu_step_s = (time.perf_counter() - t1) / n_all
-        rel = lambda a, b: float(np.linalg.norm((a - b).ravel()) / np.linalg.norm(b.ravel()))  # noqa
-        decode["parity"] = {"steps_checked": n_all, "rel_l2_final_state": rel(state.cpu().numpy(), s_ref),
-                            "rel_l2_last_o": rel(od.cpu().numpy(), e_od), "bound": 1e-5}
-        decode["parity"]["ok"] = (decode["parity"]["rel_l2_final_state"] <= 1e-5
-                                  and decode["parity"]["rel_l2_last_o"] <= 1e-5)
-        if cpu is not None:
-            cpu["cfg4_ms_per_step"] = cpu_step_s * 1e3
-            cpu["cfg4_tokens_per_s"] = Bd / cpu_step_s
-        del s_ref
+    decode_host = None
+    if state0_host is not None:  # replayed on the C restatement after every GPU leg
+        decode_host = (state0_host, [(bits(a), bits(b_), bits(c_), d_.cpu().numpy()) for a, b_, c_, d_ in toks],
+                       state.cpu().numpy(), od.cpu().numpy())
 
     # the same decode through a serving state cache: a pool of 2*B slots, the batch's
     # requests on a random half of them (pm_delta_step_slots)
@@ -861,7 +814,8 @@ def main():
                                   _native.DTYPE_BF16, ws.data_ptr(), ws_bytes, stream.cuda_stream)
             _native.check(rc)
 
-        bwd()
+        for _ in range(60):  # warm-up: about 25 ms of calls, past the clock's ramp
+            bwd()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
@@ -895,7 +849,8 @@ def main():
                                   _native.DTYPE_F32, ws.data_ptr(), ws_bytes, stream.cuda_stream)
             _native.check(rc)
 
-        bwd32()
+        for _ in range(20):  # warm-up, as above
+            bwd32()
         torch.cuda.synchronize()
         e0.record(stream)
         for _ in range(args.bwd_steps):
@@ -938,6 +893,69 @@ def main():
             torch.neg(x, out=y)
         torch.cuda.synchronize()
         del x, y
+
+    # parity of the timed output against the C restatement (which is also the CPU baseline)
+    cpu = None
+    parity = None
+    if not args.no_cpu_baseline:
+        from oracle import cref
+
+        hq, hk, hv, hb = host_in
+        threads = cpu_threads()
+        print(f"[bench] CPU baseline on {threads} threads", file=sys.stderr, flush=True)
+        cref.delta_fwd(hq[:, :64], hk[:, :64], hv[:, :64], hb[:, :64], None, threads=threads)
+        # the full batch, repeated for about CPU_SAMPLE_S seconds of CPU work
+        t1 = time.perf_counter()
+        e_o, e_s = cref.delta_fwd(hq, hk, hv, hb, None, threads=threads)
+        reps = 1
+        while time.perf_counter() - t1 < CPU_SAMPLE_S and reps < 1000:
+            cref.delta_fwd(hq, hk, hv, hb, None, threads=threads)
+            reps += 1
+        cpu_s = (time.perf_counter() - t1) / reps
+        got_o, got_s = host_o, host_s
+        rel = lambda a, b: float(np.linalg.norm((a - b).ravel()) / np.linalg.norm(b.ravel()))  # noqa
+        parity = {"rel_l2_o": rel(got_o, e_o), "rel_l2_s": rel(got_s, e_s), "bound": 2e-2}
+        parity["ok"] = parity["rel_l2_o"] <= 2e-2 and parity["rel_l2_s"] <= 2e-2
+        cpu = {"value": tokens / cpu_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": f"full cfg1 batch (B4 T4096 H16 D128, bf16 inputs upcast to fp32), "
+                         f"{reps} repeats, {cpu_s:.3f} s each; C restatement of the reference's per-token rank-1 "
+                         f"recurrence (oracle/delta_ref.c), OpenMP over 64 (b,h) sequences",
+               "cpu_model": cpu_model(),
+               "affinity_cpus": len(os.sched_getaffinity(0)),
+               "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
+               "threads_used": threads,
+               "threads_rule": "OMP_NUM_THREADS when set (the box's CPU share), else the affinity count"}
+        # the other BASELINE configurations on the same CPU path, per call / per step
+        x0 = synth.fwd_inputs((1, 256, 4, 64), seed=0, dtype="fp32")
+        t1 = time.perf_counter()
+        reps0 = 0
+        while time.perf_counter() - t1 < 1.0:
+            cref.delta_fwd(x0.q, x0.k, x0.v, x0.beta, None, threads=threads)
+            reps0 += 1
+        cpu["cfg0_ms_per_call"] = (time.perf_counter() - t1) * 1e3 / reps0
+        cpu["cfg0_tokens_per_s"] = 256 / ((time.perf_counter() - t1) / reps0)
+
+    if decode_host is not None:
+        # every decode step the GPU ran (4 untimed + the timed ones), replayed on the C
+        # restatement
+        from oracle import cref
+
+        threads = cpu_threads()
+        s_ref, htoks, got_state, got_od = decode_host
+        n_all = 4 + args.decode_steps
+        t1 = time.perf_counter()
+        for i in range(n_all):
+            e_od = cref.delta_step(s_ref, *htoks[i % 2], threads=threads)
+        cpu_step_s = (time.perf_counter() - t1) / n_all
+        rel = lambda a, b: float(np.linalg.norm((a - b).ravel()) / np.linalg.norm(b.ravel()))  # noqa
+        decode["parity"] = {"steps_checked": n_all, "rel_l2_final_state": rel(got_state, s_ref),
+                            "rel_l2_last_o": rel(got_od, e_od), "bound": 1e-5}
+        decode["parity"]["ok"] = (decode["parity"]["rel_l2_final_state"] <= 1e-5
+                                  and decode["parity"]["rel_l2_last_o"] <= 1e-5)
+        if cpu is not None:
+            cpu["cfg4_ms_per_step"] = cpu_step_s * 1e3
+            cpu["cfg4_tokens_per_s"] = Bd / cpu_step_s
+        del s_ref
 
     line = {
         "metric": "delta-rule fwd tokens/s + % MFMA/HBM roofline, B4·H16·T4096·d128 bf16",

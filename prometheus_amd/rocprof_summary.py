@@ -117,11 +117,16 @@ def stats(args) -> None:
             rows = [kv for kv in rows if kv[0][0].startswith(args.prefix)]
             out += [f"Kernels named {args.prefix}* only (the rest are the bench's own torch set-up and "
                     f"reference work); total % is of every kernel's time.", ""]
-        out += ["| kernel | workgroups | calls | avg us | min us | max us | total % |",
-                "|---|---:|---:|---:|---:|---:|---:|"]
+        if args.skip:
+            out += [f"`avg us` leaves out the first {args.skip} launches of a row that has more (the "
+                    f"headline's warm-up, during which the shader clock ramps up); `avg all` is over every "
+                    f"launch.", ""]
+        out += ["| kernel | workgroups | calls | avg us | avg all | min us | max us | total % |",
+                "|---|---:|---:|---:|---:|---:|---:|---:|"]
         for (name, n_wg), v in rows[: args.top]:
-            out.append(f"| `{name}` | {n_wg} | {len(v)} | {sum(v) / len(v):.1f} | {min(v):.1f} | {max(v):.1f} | "
-                       f"{100 * sum(v) / total:.1f} |")
+            w = v[args.skip:] if args.skip and len(v) > args.skip else v
+            out.append(f"| `{name}` | {n_wg} | {len(v)} | {sum(w) / len(w):.1f} | {sum(v) / len(v):.1f} | "
+                       f"{min(v):.1f} | {max(v):.1f} | {100 * sum(v) / total:.1f} |")
     else:
         path = _one(os.path.join(args.dir, "**", "*kernel_stats.csv"))
         with open(path) as f:
@@ -267,6 +272,8 @@ def main(argv=None) -> None:
     s.add_argument("--bench-log")
     s.add_argument("--top", type=int, default=40)
     s.add_argument("--prefix", default=None, help="list only kernels whose name starts with this")
+    s.add_argument("--skip", type=int, default=0,
+                   help="leave the first N launches of rows with more than N out of `avg us`")
     s.add_argument("-o", "--out", required=True)
     t = sub.add_parser("traffic")
     t.add_argument("fetch_dir")

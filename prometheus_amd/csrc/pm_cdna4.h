@@ -410,41 +410,5 @@ __device__ __forceinline__ void t_blocks(const bf16x8_t (&f)[4][D / 32], const f
     t_from_gram(gd, gd, gu, bc, br4, lane, tb, tn);
 }
 
-// t_blocks for one chunk by one wave from LDS: K token rows in the swizzled tile at
-// rb + R_KS, beta (fp32) at rb + R_BS; T lands in Tp in the packed operand layout
-// (6 blocks of 1 KiB).  The backward's prep kernel calls this.
-template <int D, int R_KS, int R_BS>
-__device__ __forceinline__ void build_t_packed(const unsigned char* rb, uint16_t* Tp, int lane) {
-    const uint16_t* Ks = reinterpret_cast<const uint16_t*>(rb + R_KS);
-    const float* Bs = reinterpret_cast<const float*>(rb + R_BS);
-    const int l16 = lane & 15, lg = lane >> 4;
-    bf16x8_t f[4][D / 32];
-#pragma unroll
-    for (int kb = 0; kb < D / 32; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) f[r][kb] = lds_op_kq<D>(Ks, 16 * r + l16, kb, lg);
-    f32x4_t br4[4];
-    float bc[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        br4[b] = *reinterpret_cast<const f32x4_t*>(Bs + 16 * b + 4 * lg);
-        bc[b] = Bs[16 * b + l16];
-    }
-    f32x4_t tb[10], tn[10];
-    t_blocks<D>(f, bc, br4, lane, tb, tn);
-    store_packed_t(Tp, 0, 0, tb[0], lane);
-    store_packed_t(Tp, 1, 0, tb[1], lane);
-    store_packed_t(Tp, 1, 1, tb[2], lane);
-    store_packed_t(Tp, 2, 0, tb[3], lane);
-    store_packed_t(Tp, 2, 1, tb[4], lane);
-    store_packed_t(Tp, 2, 2, tb[5], lane);
-    store_packed_t(Tp, 3, 0, tb[6], lane);
-    store_packed_t(Tp, 3, 1, tb[7], lane);
-    store_packed_t(Tp, 3, 2, tb[8], lane);
-    store_packed_t(Tp, 3, 3, tb[9], lane);
-    zero_upper_half(Tp, qblk(0, 0), lane);
-    zero_upper_half(Tp, qblk(2, 1), lane);
-}
-
 }  // namespace
 }  // namespace pm

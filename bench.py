@@ -47,6 +47,7 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, vendor figure
 FP32_VALU_PEAK_TFLOPS = 157.3  # MI355X fp32 vector, vendor figure (packed FMA; half without)
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA, vendor figure
 CHUNK = 64
+WARM_CALLS = 5  # untimed calls before each later leg's timed ones (fresh output buffers)
 CALIB_COPY_BYTES = 1 << 30  # bytes read (and written) by one calibration copy launch
 CPU_SAMPLE_S = 10.0  # seconds of CPU work timed for cpu_baseline (whole cfg1 batches)
 
@@ -417,6 +418,22 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     last = (args.steps - 1) % 2
 
+    def spin_up(ms=25.0):
+        """Untimed forward calls for about `ms` of GPU time before a leg: the shader clock
+        drops while the GPU waits on host work (copies, allocations) and ramps up again
+        over ~150 calls."""
+        w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0.record(stream)
+        n = 0
+        while True:
+            for _ in range(10):
+                launch(n)
+                n += 1
+            w1.record(stream)
+            w1.synchronize()
+            if w0.elapsed_time(w1) >= ms:
+                return
+
     tokens = B * T
     flops = fwd_flops(B, T, H, D)
     nbytes = fwd_bytes(B, T, H, D)
@@ -512,6 +529,95 @@ def main():
         host_o, host_s = o.cpu().numpy(), s.cpu().numpy()
         host_in = tuple(bits(x) for x in sets[last][:3]) + (sets[last][3].cpu().numpy(),)
 
+    # The gated and KDA forwards run next to the other bf16 forward legs: after the heavy
+    # fp32 legs the same calls took 3-25% longer for a while (0.118-0.142 ms for a gated
+    # call that takes 0.114-0.115 ms in a steady loop)
+    g = torch.Generator(device=dev)
+    # the gated delta rule at cfg1 (pm_gated_delta_fwd): cfg1's inputs plus log-gates
+    # -0.1 |N(0, 1)| per token and head, on the chunked kernel
+    gated = None
+    if args.gated_calls > 0:
+        spin_up()
+        g.manual_seed(8)
+        gates = -0.1 * torch.randn((B, T, H), generator=g, device=dev).abs()
+        og = torch.empty((B, T, H, D), device=dev)
+        sg = torch.empty((B, H, D, D), device=dev)
+
+        def gfwd(i=0):  # the two input sets alternate, as in the headline loop
+            q, k, v, beta = sets[i % 2]
+            rc = lib.pm_gated_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
+                                        gates.data_ptr(), None, og.data_ptr(), sg.data_ptr(), B, T, H,
+                                        D, _native.DTYPE_BF16, _native.DTYPE_F32, stream.cuda_stream)
+            _native.check(rc)
+
+        # after the heavy fp32 legs, 20 untimed calls, then the median of 5 rounds
+        for i in range(20):
+            gfwd(i)
+        g_ms = float(np.median([time_launches(stream, gfwd, args.gated_calls) for _ in range(5)]))
+        gb = fwd_bytes(B, T, H, D) + 4 * B * T * H
+        gated = {
+            "workload": "cfg1 gated delta rule (log-gates -0.1|N(0,1)|), bf16 q/k/v, chunked kernel",
+            "calls": args.gated_calls,
+            "timing": "median of 5 rounds of the calls, after 20 untimed",
+            "ms_per_call": g_ms,
+            "tokens_per_s": tokens / (g_ms * 1e-3),
+            "roofline": {"bound": "hbm", "achieved": gb / (g_ms * 1e-3) / 1e9,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gb / (g_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        }
+        del og, sg, gates
+
+    # KDA at cfg1 (pm_kda_delta_fwd): cfg1's inputs plus log-gates -0.1 |N(0, 1)| per token,
+    # head and key channel; the chunked form (prepass + recurrence) and the per-token kernel
+    kda = None
+    if args.gated_calls > 0:
+        spin_up()
+        g.manual_seed(9)
+        gates = -0.1 * torch.randn((B, T, H, D), generator=g, device=dev).abs()
+        ok_ = torch.empty((B, T, H, D), device=dev)
+        sk_ = torch.empty((B, H, D, D), device=dev)
+        kws_bytes = lib.pm_kda_delta_workspace_bytes(B, T, H, D, _native.DTYPE_BF16)
+        kws = torch.empty((kws_bytes,), dtype=torch.uint8, device=dev)
+
+        def kfwd(i=0, ws=True):
+            q, k, v, beta = sets[i % 2]
+            rc = lib.pm_kda_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
+                                      gates.data_ptr(), None, ok_.data_ptr(), sk_.data_ptr(), B, T, H, D,
+                                      _native.DTYPE_BF16, _native.DTYPE_F32, kws.data_ptr() if ws else None,
+                                      kws_bytes if ws else 0, stream.cuda_stream)
+            _native.check(rc)
+
+        def time_kda(ws, calls):
+            # as for the gated leg: untimed calls, then the median of rounds (one round for
+            # the slow per-token kernel)
+            for i in range(20 if ws else 1):
+                kfwd(i, ws)
+            return float(np.median([time_launches(stream, lambda i: kfwd(i, ws), calls)
+                                    for _ in range(5 if ws else 1)]))
+
+        k_ms = time_kda(True, args.gated_calls)
+        o_chunk = ok_.clone()
+        kp_ms = time_kda(False, max(1, args.gated_calls // 5))
+        kfwd(args.gated_calls - 1, False)  # the per-token result on the chunked call's inputs
+        torch.cuda.synchronize()
+        rel = float(torch.linalg.vector_norm(o_chunk - ok_) / torch.linalg.vector_norm(ok_))
+        kb_ = fwd_bytes(B, T, H, D) + 4 * B * T * H * D
+        kda = {
+            "workload": "cfg1 KDA (log-gates -0.1|N(0,1)| per key channel), bf16 q/k/v, fp32 O",
+            "calls": args.gated_calls,
+            "timing": "median of 5 rounds of the calls, after 20 untimed",
+            "ms_per_call": k_ms,
+            "tokens_per_s": tokens / (k_ms * 1e-3),
+            "workspace_bytes": kws_bytes,
+            "algorithmic_bytes": kb_,
+            "roofline": {"bound": "hbm", "achieved": kb_ / (k_ms * 1e-3) / 1e9,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": kb_ / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+            "per_token": {"ms_per_call": kp_ms, "tokens_per_s": tokens / (kp_ms * 1e-3)},
+            "chunked_vs_per_token_rel_l2": rel,
+        }
+        del ok_, sk_, gates, kws, o_chunk
+
     # decode step, cfg4: B256 H32 D128, fp32 state updated in place, 64 steps
     Bd, Hd = 256, 32
     g = torch.Generator(device=dev)
@@ -537,6 +643,7 @@ def main():
 
     # the state before any step, for the parity check of the whole in-place sequence
     state0_host = state.cpu().numpy() if not args.no_cpu_baseline else None
+    spin_up()
     for i in range(4):
         step(i)
     torch.cuda.synchronize()
@@ -575,6 +682,7 @@ def main():
                                      Bd, Hd, D, _native.DTYPE_BF16, stream.cuda_stream)
         _native.check(rc)
 
+    spin_up()
     for i in range(4):
         step_slots(i)
     torch.cuda.synchronize()
@@ -614,6 +722,7 @@ def main():
     # reference model's dtype) on the fp32 chunked forward, with the per-token kernel beside
     model_la = None
     if args.model_calls > 0:
+        spin_up()
         model_la = {"workload": "cfg1 shape, model.linear_attention (beta 1, L2-normalised q/k)"}
         g.manual_seed(7)
         om = torch.empty((B, T, H, D), device=dev)
@@ -631,7 +740,8 @@ def main():
                                                 stream.cuda_stream)
                 _native.check(rc)
 
-            la(0)
+            for i in range(WARM_CALLS):  # first touches of fresh output buffers are slower
+                la(i)
             calls = args.model_calls * (10 if name == "bf16" else 5)
             la_ms = time_launches(stream, la, calls)
             lb = fwd_bytes(B, T, H, D, s_in=s_in, s_out=4) - 4 * B * T * H  # no beta array
@@ -670,7 +780,8 @@ def main():
             _native.check(rc)
 
         def time_ffwd(ws, calls):
-            ffwd(ws)
+            for i in range(WARM_CALLS if ws is not None else 1):  # first touches of fresh output buffers are slower
+                ffwd(ws, i)
             return time_launches(stream, lambda i: ffwd(ws, i), calls)
 
         calls = args.model_calls * 5
@@ -704,99 +815,11 @@ def main():
         }
         del fsets, of, sf, wsf
 
-    # the gated delta rule at cfg1 (pm_gated_delta_fwd): cfg1's inputs plus log-gates
-    # -0.1 |N(0, 1)| per token and head, on the chunked kernel
-    gated = None
-    if args.gated_calls > 0:
-        g.manual_seed(8)
-        gates = -0.1 * torch.randn((B, T, H), generator=g, device=dev).abs()
-        og = torch.empty((B, T, H, D), device=dev)
-        sg = torch.empty((B, H, D, D), device=dev)
-
-        def gfwd(i=0):  # the two input sets alternate, as in the headline loop
-            q, k, v, beta = sets[i % 2]
-            rc = lib.pm_gated_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
-                                        gates.data_ptr(), None, og.data_ptr(), sg.data_ptr(), B, T, H,
-                                        D, _native.DTYPE_BF16, _native.DTYPE_F32, stream.cuda_stream)
-            _native.check(rc)
-
-        gfwd()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(args.gated_calls):
-            gfwd(i)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        g_ms = e0.elapsed_time(e1) / args.gated_calls
-        gb = fwd_bytes(B, T, H, D) + 4 * B * T * H
-        gated = {
-            "workload": "cfg1 gated delta rule (log-gates -0.1|N(0,1)|), bf16 q/k/v, chunked kernel",
-            "calls": args.gated_calls,
-            "ms_per_call": g_ms,
-            "tokens_per_s": tokens / (g_ms * 1e-3),
-            "roofline": {"bound": "hbm", "achieved": gb / (g_ms * 1e-3) / 1e9,
-                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": gb / (g_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
-        }
-        del og, sg, gates
-
-    # KDA at cfg1 (pm_kda_delta_fwd): cfg1's inputs plus log-gates -0.1 |N(0, 1)| per token,
-    # head and key channel; the chunked form (prepass + recurrence) and the per-token kernel
-    kda = None
-    if args.gated_calls > 0:
-        g.manual_seed(9)
-        gates = -0.1 * torch.randn((B, T, H, D), generator=g, device=dev).abs()
-        ok_ = torch.empty((B, T, H, D), device=dev)
-        sk_ = torch.empty((B, H, D, D), device=dev)
-        kws_bytes = lib.pm_kda_delta_workspace_bytes(B, T, H, D, _native.DTYPE_BF16)
-        kws = torch.empty((kws_bytes,), dtype=torch.uint8, device=dev)
-
-        def kfwd(i=0, ws=True):
-            q, k, v, beta = sets[i % 2]
-            rc = lib.pm_kda_delta_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
-                                      gates.data_ptr(), None, ok_.data_ptr(), sk_.data_ptr(), B, T, H, D,
-                                      _native.DTYPE_BF16, _native.DTYPE_F32, kws.data_ptr() if ws else None,
-                                      kws_bytes if ws else 0, stream.cuda_stream)
-            _native.check(rc)
-
-        def time_kda(ws, calls):
-            kfwd(0, ws)
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for i in range(calls):
-                kfwd(i, ws)
-            e1.record(stream)
-            torch.cuda.synchronize()
-            return e0.elapsed_time(e1) / calls
-
-        k_ms = time_kda(True, args.gated_calls)
-        o_chunk = ok_.clone()
-        kp_ms = time_kda(False, max(1, args.gated_calls // 5))
-        kfwd(args.gated_calls - 1, False)  # the per-token result on the chunked call's inputs
-        torch.cuda.synchronize()
-        rel = float(torch.linalg.vector_norm(o_chunk - ok_) / torch.linalg.vector_norm(ok_))
-        kb_ = fwd_bytes(B, T, H, D) + 4 * B * T * H * D
-        kda = {
-            "workload": "cfg1 KDA (log-gates -0.1|N(0,1)| per key channel), bf16 q/k/v, fp32 O",
-            "calls": args.gated_calls,
-            "ms_per_call": k_ms,
-            "tokens_per_s": tokens / (k_ms * 1e-3),
-            "workspace_bytes": kws_bytes,
-            "algorithmic_bytes": kb_,
-            "roofline": {"bound": "hbm", "achieved": kb_ / (k_ms * 1e-3) / 1e9,
-                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": kb_ / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
-            "per_token": {"ms_per_call": kp_ms, "tokens_per_s": tokens / (kp_ms * 1e-3)},
-            "chunked_vs_per_token_rel_l2": rel,
-        }
-        del ok_, sk_, gates, kws, o_chunk
-
     # backward at cfg1 (chunked_delta_rule_bwd through the C ABI): bf16 q/k/v, zero S0,
     # random go and gS, fp32 gradients
     backward = None
     if args.bwd_steps > 0:
+        spin_up()
         q, k, v, beta = sets[last]
         g.manual_seed(5)
         go = torch.randn((B, T, H, D), generator=g, device=dev)

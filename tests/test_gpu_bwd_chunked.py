@@ -58,8 +58,11 @@ def _check(got, exp, what):
         assert_bf16_parity(g, e, f"{what} {name}")
 
 
+# chunk counts 1 to 5 (the reverse sweep's first and last iterations take their own
+# branches of its copy and build schedule), full and ragged last chunks, D = 64 and 128
 @pytest.mark.parametrize("shape", [(1, 1, 1, 64), (1, 37, 2, 64), (2, 64, 1, 64), (2, 150, 2, 64),
-                                   (1, 63, 1, 128), (2, 130, 3, 128), (1, 257, 1, 128)])
+                                   (1, 63, 1, 128), (2, 130, 3, 128), (1, 257, 1, 128),
+                                   (1, 128, 2, 128), (1, 192, 1, 64), (2, 200, 1, 128)])
 @pytest.mark.parametrize("state", [True, False])
 def test_against_oracle(shape, state):
     x, go, gs, res = _problem(shape, seed=sum(shape) + 7 * state, state=state)

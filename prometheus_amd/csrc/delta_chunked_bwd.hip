@@ -156,11 +156,11 @@ struct RevGeo {
     static constexpr int FLAG = NBUF * BUF;
     static constexpr int BYTES = FLAG + 16;
     static constexpr int THREADS = 320;  // five waves
-    // copy instructions per chunk: K, Q and beta (wave 2), dO (wave 4)
+    // copy instructions per chunk (all by wave 2): K, Q, beta and dO
     static constexpr int N_KQ = kC * D * 2 / 1024, N_DO = kC * NC * 4 / 1024;
-    // most memory operations a wave has in flight (vmcnt counts to 63): wave 2 one chunk's
-    // copies, wave 4 two chunks' dO copies and one chunk's dV stores
-    static_assert(2 * N_KQ + 1 <= 63 && 3 * N_DO <= 63, "vmcnt range");
+    // most memory operations wave 2 has in flight (vmcnt counts to 63): a chunk's dV stores,
+    // the next chunk's copies and the one after's, and that one's dV stores
+    static_assert(2 * N_KQ + 1 + N_DO + 2 * N_DO <= 63, "vmcnt range");
     static_assert(BUF % 16 == 0 && BYTES <= 160 * 1024, "layout");
 };
 // dO tile (rows of 32 fp32 = 128 bytes, half the banks): 16-byte chunk p of token row t
@@ -189,10 +189,10 @@ __global__ __launch_bounds__(320) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int w = static_cast<int>(uniform(static_cast<unsigned>(tid >> 6)));
     const int l16 = lane & 15, lg = lane >> 4;
     // waves 0 and 1 (the chain) carry G (16 columns each) and store G and W.  For the chunks
-    // ahead, wave 2 copies K, Q and beta and marks each chunk whose copies have landed in an
-    // LDS flag; wave 3 then builds the chunk's T^T (and T), wave 4 its P^T, and wave 4 also
-    // copies dO and stores dV.  No chain wave waits on a copy, a build or a dV store, and no
-    // builder's MFMA work queues behind its own copies.
+    // ahead, wave 2 copies K, beta, Q and dO, marks in an LDS flag each chunk whose copies
+    // have landed, and stores dV; wave 3 then builds the chunk's T^T (and T), wave 4 its
+    // P^T.  No chain wave waits on a copy, a build or a dV store, and no builder's MFMA work
+    // queues behind memory instructions.
     const int j = tile * G::NC + 16 * (w & 1) + l16;  // this lane's column of G (chain waves)
     const int jt = j >> 4;                             // its 16-column tile
     const size_t tstride = static_cast<size_t>(H) * D;
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(320) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     auto put = [&](uint16_t* dst, int x, f32x4_t lo, f32x4_t hi) {
         *reinterpret_cast<bf16x8_t*>(dst + x * 512 + lane * 8) = acc_to_b(lo, hi);
     };
-    // Wave 2 copies K, beta and then Q of chunk c; wave 4 its dO (rows past the chunk's end
+    // Wave 2 copies K, beta and then Q of chunk c, and its dO (rows past the chunk's end
     // fall outside the buffer ranges and read as zeros)
     auto issue_kq = [&](int c) {
         const int base = c * kC, clen = min(kC, T - base);
@@ -337,7 +337,7 @@ __global__ __launch_bounds__(320) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // G and W go out in packed order (one contiguous block per instruction), W at the start
     // of the next iteration next to G; and dV, whose rows are 64 bytes per chain wave, is
     // staged in the chunk's dO space (dead once the chain has its dO operands; each wave
-    // overwrites only the bytes of its own dO columns) and stored by wave 4 in whole 128-byte
+    // overwrites only the bytes of its own dO columns) and stored by wave 2 in whole 128-byte
     // rows in the next iteration, before that buffer is refilled.
     u32x2_t w_pend[4];
     uint16_t* wp_pend = nullptr;
@@ -395,16 +395,49 @@ __global__ __launch_bounds__(320) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     };
     if (w == 2) {
-        if (n_ch > 0) issue_kq(n_ch - 1);
+        // chunk c's copies in issue order: K and beta, Q, dO; in iteration c they are waited
+        // for one part at a time (each mark as soon as its part has landed), with chunk
+        // c + 2's dV stores (issued last in the iteration before, when there was one) still
+        // in flight behind them
+        if (n_ch > 0) {
+            issue_kq(n_ch - 1);
+            issue_do(n_ch - 1);
+        }
         for (int c = n_ch; c > 0; --c) {
-            wait_vm_n<G::N_KQ>();            // chunk c - 1's K and beta (its Q copies follow)
-            if (lane == 0) flag[0] = c - 1;
-            wait_copies();                   // and its Q
-            if (lane == 0) flag[1] = c - 1;
+            if (c <= n_ch - 3) {             // chunk c + 2's dV stores issued last
+                wait_vm_n<G::N_KQ + 2 * G::N_DO>();
+                if (lane == 0) flag[0] = c - 1;
+                wait_vm_n<2 * G::N_DO>();
+                if (lane == 0) flag[1] = c - 1;
+                wait_vm_n<G::N_DO>();        // its dO
+            } else {
+                wait_vm_n<G::N_KQ + G::N_DO>();
+                if (lane == 0) flag[0] = c - 1;
+                wait_vm_n<G::N_DO>();
+                if (lane == 0) flag[1] = c - 1;
+                wait_copies();               // its dO
+            }
             if (c >= 2) issue_kq(c - 2);     // into chunk c + 1's buffer
+            if (c <= n_ch - 2) {             // dV of chunk c + 1, whose buffer chunk c - 2 takes
+                u32x4_t x[G::N_DO];
+                read_dv(c + 1, x);
+                if (c >= 2) issue_do(c - 2);
+                write_dv(c + 1, x);
+            } else if (c >= 2) {
+                issue_do(c - 2);
+            }
             lds_barrier();
         }
-        if (n_ch > 0) lds_barrier();
+        u32x4_t x[G::N_DO];
+        if (n_ch > 1) {
+            read_dv(1, x);
+            write_dv(1, x);
+        }
+        if (n_ch > 0) {
+            lds_barrier();  // chunk 0's dV is staged
+            read_dv(0, x);
+            write_dv(0, x);
+        }
         return;
     }
     if (w == 3) {
@@ -420,38 +453,12 @@ __global__ __launch_bounds__(320) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         return;
     }
     if (w == 4) {
-        u32x4_t x[G::N_DO];
-        if (n_ch > 0) issue_do(n_ch - 1);
         for (int c = n_ch; c > 0; --c) {
-            if (c <= n_ch - 2) {             // dV of chunk c + 1, whose buffer chunk c - 2 takes
-                read_dv(c + 1, x);
-                if (c >= 2) issue_do(c - 2);
-                write_dv(c + 1, x);
-            } else if (c >= 2) {
-                issue_do(c - 2);
-            }
             wait_mark(c - 1, 1);
             build_p(c - 1);
-            // chunk c - 1's dO (issued an iteration earlier): issued after it only chunk c - 2's
-            // copies, then chunk c + 1's dV stores (they complete in issue order)
-            const bool dv = c <= n_ch - 2;
-            if (c >= 2 && dv)
-                wait_vm_n<2 * G::N_DO>();
-            else if (c >= 2 || dv)
-                wait_vm_n<G::N_DO>();
-            else
-                wait_copies();
             lds_barrier();
         }
-        if (n_ch > 1) {
-            read_dv(1, x);
-            write_dv(1, x);
-        }
-        if (n_ch > 0) {
-            lds_barrier();  // chunk 0's dV is staged
-            read_dv(0, x);
-            write_dv(0, x);
-        }
+        if (n_ch > 0) lds_barrier();
         return;
     }
     // chain waves

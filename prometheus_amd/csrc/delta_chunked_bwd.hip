@@ -206,15 +206,20 @@ __global__ __launch_bounds__(320) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
     // Wave 2 copies K, beta and then Q of chunk c, and its dO (rows past the chunk's end
     // fall outside the buffer ranges and read as zeros)
-    auto issue_kq = [&](int c) {
+    auto issue_kq = [&](int c, bool kpart, bool qpart) {
         const int base = c * kC, clen = min(kC, T - base);
         const size_t row0 = (tok0 + base) * tstride + static_cast<size_t>(h) * D;
         const unsigned n_kq = static_cast<unsigned>(((clen - 1) * tstride + D) * 2);
         unsigned char* b = uniform_ptr(buf(c));
-        copy_rows<D>(make_rsrc(k + row0, n_kq), b + G::KS, G::N_KQ, static_cast<unsigned>(tstride * 2), 0, 1, lane);
-        copy_to_lds(make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4)),
-                    b + G::BS, 4, static_cast<unsigned>(lane * H * 4));
-        copy_rows<D>(make_rsrc(q + row0, n_kq), b + G::QS, G::N_KQ, static_cast<unsigned>(tstride * 2), 0, 1, lane);
+        if (kpart) {
+            copy_rows<D>(make_rsrc(k + row0, n_kq), b + G::KS, G::N_KQ, static_cast<unsigned>(tstride * 2), 0, 1,
+                         lane);
+            copy_to_lds(make_rsrc(beta + (tok0 + base) * H + h, static_cast<unsigned>(((clen - 1) * H + 1) * 4)),
+                        b + G::BS, 4, static_cast<unsigned>(lane * H * 4));
+        }
+        if (qpart)
+            copy_rows<D>(make_rsrc(q + row0, n_kq), b + G::QS, G::N_KQ, static_cast<unsigned>(tstride * 2), 0, 1,
+                         lane);
     };
     auto issue_do = [&](int c) {
         const int base = c * kC, clen = min(kC, T - base);
@@ -400,24 +405,45 @@ __global__ __launch_bounds__(320) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // c + 2's dV stores (issued last in the iteration before, when there was one) still
         // in flight behind them
         if (n_ch > 0) {
-            issue_kq(n_ch - 1);
+            issue_kq(n_ch - 1, true, true);
             issue_do(n_ch - 1);
         }
+        constexpr int NK = G::N_KQ + 1, NQ = G::N_KQ, ND = G::N_DO;  // copies of K + beta, Q, dO
         for (int c = n_ch; c > 0; --c) {
-            if (c <= n_ch - 3) {             // chunk c + 2's dV stores issued last
-                wait_vm_n<G::N_KQ + 2 * G::N_DO>();
+            // The newer chunk's K and beta go out as soon as the older chunk's have landed, and
+            // its Q once the older Q has: each wait counts what was issued after the part it
+            // waits for.  In flight at the top: chunk c - 1's K + beta, Q, dO, then chunk c + 2's
+            // dV stores when the last iteration stored (c <= n_ch - 3).
+            const bool more = c >= 2;
+            if (c <= n_ch - 3) {
+                wait_vm_n<NQ + 2 * ND>();
                 if (lane == 0) flag[0] = c - 1;
-                wait_vm_n<2 * G::N_DO>();
-                if (lane == 0) flag[1] = c - 1;
-                wait_vm_n<G::N_DO>();        // its dO
+                if (more) {
+                    issue_kq(c - 2, true, false);
+                    wait_vm_n<2 * ND + NK>();
+                    if (lane == 0) flag[1] = c - 1;
+                    issue_kq(c - 2, false, true);
+                    wait_vm_n<ND + NK + NQ>();  // its dO
+                } else {
+                    wait_vm_n<2 * ND>();
+                    if (lane == 0) flag[1] = c - 1;
+                    wait_vm_n<ND>();
+                }
             } else {
-                wait_vm_n<G::N_KQ + G::N_DO>();
+                wait_vm_n<NQ + ND>();
                 if (lane == 0) flag[0] = c - 1;
-                wait_vm_n<G::N_DO>();
-                if (lane == 0) flag[1] = c - 1;
-                wait_copies();               // its dO
+                if (more) {
+                    issue_kq(c - 2, true, false);
+                    wait_vm_n<ND + NK>();
+                    if (lane == 0) flag[1] = c - 1;
+                    issue_kq(c - 2, false, true);
+                    wait_vm_n<NK + NQ>();       // its dO
+                } else {
+                    wait_vm_n<ND>();
+                    if (lane == 0) flag[1] = c - 1;
+                    wait_copies();
+                }
             }
-            if (c >= 2) issue_kq(c - 2);     // into chunk c + 1's buffer
             if (c <= n_ch - 2) {             // dV of chunk c + 1, whose buffer chunk c - 2 takes
                 u32x4_t x[G::N_DO];
                 read_dv(c + 1, x);
